@@ -1,0 +1,256 @@
+"""The extension module of the reference, re-implemented over libbevk.so.
+
+Same module name, function names and argument order as the reference's pybind11
+module (naotic/bev-kernels csrc/binding.cpp:142-191), plus the MSDA ``forward`` /
+``backward`` of its MUSA module (csrc_musa/msda/binding_musa.mu:545-557) and the fused
+NHWC entry point ``dcn_fused_fwd_nhwc``. Outputs are caller-allocated, as in the
+reference (MSDA forward allocates and returns its output).
+
+Unlike the reference launchers these wrappers check device, contiguity, dtype and
+element counts against the integer sizes before launching, and raise RuntimeError on
+a mismatch, so a kernel never indexes past a buffer.
+
+The backward entry points are kept as names only: the backward kernels are not part
+of this build and raise RuntimeError.
+"""
+from __future__ import annotations
+
+import torch
+
+import _bevk as _b
+
+__all__ = [
+    "modulated_deformable_im2col_cuda",
+    "modulated_deformable_col2im_cuda",
+    "modulated_deformable_im2col_opt_cuda",
+    "modulated_deformable_col2im_opt_cuda",
+    "modulated_deformable_col2im_smem_cuda",
+    "modulated_deformable_col2im_coord_cuda",
+    "modulated_deformable_col2im_coord_opt_cuda",
+    "modulated_deformable_im2col_nhwc_cuda",
+    "modulated_deformable_fused_im2col_nhwc_cuda",
+    "modulated_deformable_col2im_nhwc_cuda",
+    "modulated_deformable_col2im_coord_nhwc_cuda",
+    "modulated_deformable_gradx_smem_nhwc_cuda",
+    "modulated_deformable_gradx_gather_nhwc_cuda",
+    "modulated_deformable_col2im_fused_smem_nhwc_cuda",
+    "modulated_deformable_col2im_perelem_nhwc_cuda",
+    "modulated_deformable_col2im_perelem_smem_nhwc_cuda",
+    "dcn_fused_fwd_nhwc",
+    "forward",
+    "backward",
+]
+
+
+def _im2col_nchw(entry, fn, data_im, data_offset, data_mask, batch_size, channels, height_im,
+                 width_im, height_col, width_col, kernel_h, kernel_w, pad_h, pad_w, stride_h,
+                 stride_w, dilation_h, dilation_w, deformable_group, data_col):
+    _b.require_device(fn, data_im, data_offset, data_mask, data_col)
+    _b.require_contiguous(fn, data_im=data_im, data_offset=data_offset, data_mask=data_mask,
+                          data_col=data_col)
+    _b.require_dtype(fn, data_im, data_offset=data_offset, data_mask=data_mask,
+                     data_col=data_col)
+    if deformable_group <= 0:
+        raise RuntimeError(f"{fn}: deformable_group must be positive")
+    taps = kernel_h * kernel_w
+    plane = height_col * width_col
+    _b.require_numel(fn, "data_im", data_im, batch_size * channels * height_im * width_im)
+    _b.require_numel(fn, "data_offset", data_offset,
+                     batch_size * deformable_group * 2 * taps * plane)
+    _b.require_numel(fn, "data_mask", data_mask, batch_size * deformable_group * taps * plane)
+    _b.require_numel(fn, "data_col", data_col, channels * taps * batch_size * plane)
+    _b.call(entry, _b.dtype_code(data_im), _b.ptr(data_im), _b.ptr(data_offset),
+            _b.ptr(data_mask), batch_size, channels, height_im, width_im, height_col, width_col,
+            kernel_h, kernel_w, pad_h, pad_w, stride_h, stride_w, dilation_h, dilation_w,
+            deformable_group, _b.ptr(data_col), _b.stream_of(data_im))
+
+
+def modulated_deformable_im2col_cuda(data_im, data_offset, data_mask, batch_size, channels,
+                                     height_im, width_im, height_col, width_col, kernel_h,
+                                     kernel_w, pad_h, pad_w, stride_h, stride_w, dilation_h,
+                                     dilation_w, deformable_group, data_col):
+    """NCHW modulated im2col into data_col [C*kh*kw, B, Ho, Wo] (binding.cpp:5-11)."""
+    _im2col_nchw("bevk_modulated_deformable_im2col", "modulated_deformable_im2col_cuda",
+                 data_im, data_offset, data_mask, batch_size, channels, height_im, width_im,
+                 height_col, width_col, kernel_h, kernel_w, pad_h, pad_w, stride_h, stride_w,
+                 dilation_h, dilation_w, deformable_group, data_col)
+
+
+def modulated_deformable_im2col_opt_cuda(data_im, data_offset, data_mask, batch_size,
+                                         channels, height_im, width_im, height_col, width_col,
+                                         kernel_h, kernel_w, pad_h, pad_w, stride_h, stride_w,
+                                         dilation_h, dilation_w, deformable_group, data_col):
+    """Tiled NCHW modulated im2col, same contract (binding.cpp:21-27)."""
+    _im2col_nchw("bevk_modulated_deformable_im2col_opt", "modulated_deformable_im2col_opt_cuda",
+                 data_im, data_offset, data_mask, batch_size, channels, height_im, width_im,
+                 height_col, width_col, kernel_h, kernel_w, pad_h, pad_w, stride_h, stride_w,
+                 dilation_h, dilation_w, deformable_group, data_col)
+
+
+def modulated_deformable_im2col_nhwc_cuda(data_im, data_offset, data_mask, batch_size,
+                                          channels, height_im, width_im, height_col,
+                                          width_col, kernel_h, kernel_w, pad_h, pad_w,
+                                          stride_h, stride_w, dilation_h, dilation_w,
+                                          deformable_group, data_col):
+    """NHWC deformable gather into data_col [B*Ho*Wo, T*C] (binding.cpp:64-70).
+
+    data_offset's last dim selects the form: 2T = offsets with a separate mask,
+    3T = raw offset-conv output (offsets, then the pre-sigmoid mask)."""
+    fn = "modulated_deformable_im2col_nhwc_cuda"
+    if deformable_group != 1:
+        raise RuntimeError("NHWC fused path supports deformable_group == 1 only")
+    _b.require_device(fn, data_im, data_offset, data_mask, data_col)
+    _b.require_contiguous(fn, data_im=data_im, data_offset=data_offset, data_mask=data_mask,
+                          data_col=data_col)
+    taps = kernel_h * kernel_w
+    last = data_offset.size(-1)
+    fused_y = last == 3 * taps
+    _b.require_dtype(fn, data_im, data_offset=data_offset, data_col=data_col,
+                     data_mask=None if fused_y else data_mask)
+    m = batch_size * height_col * width_col
+    _b.require_numel(fn, "data_im", data_im, batch_size * height_im * width_im * channels)
+    _b.require_numel(fn, "data_offset", data_offset, m * last)
+    if not fused_y:
+        _b.require_numel(fn, "data_mask", data_mask, m * taps)
+    _b.require_numel(fn, "data_col", data_col, m * taps * channels)
+    _b.call("bevk_modulated_deformable_im2col_nhwc", _b.dtype_code(data_im), _b.ptr(data_im),
+            _b.ptr(data_offset), last, _b.ptr(data_mask), batch_size, channels, height_im,
+            width_im, height_col, width_col, kernel_h, kernel_w, pad_h, pad_w, stride_h,
+            stride_w, dilation_h, dilation_w, deformable_group, _b.ptr(data_col),
+            _b.stream_of(data_im))
+
+
+def dcn_fused_fwd_nhwc(data_im, data_offset, data_mask, weight_kc, bias, batch_size, channels,
+                       height_im, width_im, height_col, width_col, channels_out, kernel_h,
+                       kernel_w, pad_h, pad_w, stride_h, stride_w, dilation_h, dilation_w, out):
+    """Fused NHWC DCNv2 forward into out [B, Ho, Wo, Cout] with no column buffer.
+
+    weight_kc is the main weight as [Cout, kh, kw, C] (weight.permute(0, 2, 3, 1));
+    bias is [Cout] in the input dtype or None; data_offset follows the 2T / 3T rule of
+    modulated_deformable_im2col_nhwc_cuda."""
+    fn = "dcn_fused_fwd_nhwc"
+    _b.require_device(fn, data_im, data_offset, data_mask, weight_kc, bias, out)
+    _b.require_contiguous(fn, data_im=data_im, data_offset=data_offset, data_mask=data_mask,
+                          weight_kc=weight_kc, bias=bias, out=out)
+    taps = kernel_h * kernel_w
+    last = data_offset.size(-1)
+    fused_y = last == 3 * taps
+    _b.require_dtype(fn, data_im, data_offset=data_offset, weight_kc=weight_kc, bias=bias,
+                     out=out, data_mask=None if fused_y else data_mask)
+    m = batch_size * height_col * width_col
+    _b.require_numel(fn, "data_im", data_im, batch_size * height_im * width_im * channels)
+    _b.require_numel(fn, "data_offset", data_offset, m * last)
+    if not fused_y:
+        _b.require_numel(fn, "data_mask", data_mask, m * taps)
+    _b.require_numel(fn, "weight_kc", weight_kc, channels_out * taps * channels)
+    if bias is not None:
+        _b.require_numel(fn, "bias", bias, channels_out)
+    _b.require_numel(fn, "out", out, m * channels_out)
+    _b.call("bevk_dcn_fused_fwd_nhwc", _b.dtype_code(data_im), _b.ptr(data_im),
+            _b.ptr(data_offset), last, _b.ptr(data_mask), _b.ptr(weight_kc), _b.ptr(bias),
+            batch_size, channels, height_im, width_im, height_col, width_col, channels_out,
+            kernel_h, kernel_w, pad_h, pad_w, stride_h, stride_w, dilation_h, dilation_w,
+            _b.ptr(out), _b.stream_of(data_im))
+
+
+def _backward_absent(name):
+    def fn(*args, **kwargs):
+        raise RuntimeError(
+            f"{name}: the backward kernels are not part of this build (forward operators only)")
+    fn.__name__ = name
+    fn.__doc__ = "Backward entry point of the reference; not implemented in this build."
+    return fn
+
+
+modulated_deformable_col2im_cuda = _backward_absent("modulated_deformable_col2im_cuda")
+modulated_deformable_col2im_opt_cuda = _backward_absent("modulated_deformable_col2im_opt_cuda")
+modulated_deformable_col2im_smem_cuda = _backward_absent("modulated_deformable_col2im_smem_cuda")
+modulated_deformable_col2im_coord_cuda = _backward_absent(
+    "modulated_deformable_col2im_coord_cuda")
+modulated_deformable_col2im_coord_opt_cuda = _backward_absent(
+    "modulated_deformable_col2im_coord_opt_cuda")
+modulated_deformable_col2im_nhwc_cuda = _backward_absent("modulated_deformable_col2im_nhwc_cuda")
+modulated_deformable_col2im_coord_nhwc_cuda = _backward_absent(
+    "modulated_deformable_col2im_coord_nhwc_cuda")
+modulated_deformable_gradx_smem_nhwc_cuda = _backward_absent(
+    "modulated_deformable_gradx_smem_nhwc_cuda")
+modulated_deformable_gradx_gather_nhwc_cuda = _backward_absent(
+    "modulated_deformable_gradx_gather_nhwc_cuda")
+modulated_deformable_col2im_fused_smem_nhwc_cuda = _backward_absent(
+    "modulated_deformable_col2im_fused_smem_nhwc_cuda")
+modulated_deformable_col2im_perelem_nhwc_cuda = _backward_absent(
+    "modulated_deformable_col2im_perelem_nhwc_cuda")
+modulated_deformable_col2im_perelem_smem_nhwc_cuda = _backward_absent(
+    "modulated_deformable_col2im_perelem_smem_nhwc_cuda")
+
+
+def modulated_deformable_fused_im2col_nhwc_cuda(data_im, w_off, b_off, batch_size, channels,
+                                                height_im, width_im, height_col, width_col,
+                                                kernel_h, kernel_w, pad_h, pad_w, stride_h,
+                                                stride_w, dilation_h, dilation_w,
+                                                deformable_group, data_col):
+    """Offset conv + gather in one kernel (binding.cpp:72-78). Not in this build yet."""
+    raise RuntimeError(
+        "modulated_deformable_fused_im2col_nhwc_cuda: the fused offset-conv front end is not "
+        "part of this build; use F.conv2d + modulated_deformable_im2col_nhwc_cuda")
+
+
+# ---------------------------------------------------------------------------------------
+# Multi-scale deformable attention (binding_musa.mu:286-412, :545-557)
+# ---------------------------------------------------------------------------------------
+
+def forward(value, spatial_shapes, level_start_index, sampling_loc, attn_weight,
+            im2col_step=64, force_generic=False):
+    """MSDA forward. value [B, S, heads, D], spatial_shapes [L, 2] int64,
+    level_start_index [L] int64, sampling_loc [B, Lq, heads, L, P, 2],
+    attn_weight [B, Lq, heads, L, P] -> output [B, Lq, heads * D]."""
+    fn = "msda_forward"
+    if value.device.type != "cuda":
+        raise RuntimeError("value must be a HIP device tensor")
+    # binding_musa.mu:292-298
+    if not value.is_contiguous():
+        raise RuntimeError("value must be contiguous")
+    if not spatial_shapes.is_contiguous():
+        raise RuntimeError("spatial_shapes must be contiguous")
+    if not level_start_index.is_contiguous():
+        raise RuntimeError("level_start_index must be contiguous")
+    if not sampling_loc.is_contiguous():
+        raise RuntimeError("sampling_loc must be contiguous")
+    if not attn_weight.is_contiguous():
+        raise RuntimeError("attn_weight must be contiguous")
+    _b.require_device(fn, value, spatial_shapes, level_start_index, sampling_loc, attn_weight)
+    _b.require_dtype(fn, value, sampling_loc=sampling_loc, attn_weight=attn_weight)
+    if spatial_shapes.dtype != torch.int64 or level_start_index.dtype != torch.int64:
+        raise RuntimeError(f"{fn}: spatial_shapes and level_start_index must be int64")
+    if value.dim() != 4 or sampling_loc.dim() != 6 or attn_weight.dim() != 5:
+        raise RuntimeError(
+            f"{fn}: expected value [B,S,heads,D], sampling_loc [B,Lq,heads,L,P,2] and "
+            "attn_weight [B,Lq,heads,L,P]")
+    batch, spatial, heads, channels = value.shape
+    num_levels = spatial_shapes.size(0)
+    num_query = sampling_loc.size(1)
+    num_point = sampling_loc.size(4)
+    if tuple(spatial_shapes.shape) != (num_levels, 2) or \
+            tuple(level_start_index.shape) != (num_levels,):
+        raise RuntimeError(f"{fn}: spatial_shapes must be [L, 2] and level_start_index [L]")
+    if tuple(sampling_loc.shape) != (batch, num_query, heads, num_levels, num_point, 2):
+        raise RuntimeError(f"{fn}: sampling_loc shape {tuple(sampling_loc.shape)} does not match "
+                           f"value {tuple(value.shape)} and {num_levels} levels")
+    if tuple(attn_weight.shape) != (batch, num_query, heads, num_levels, num_point):
+        raise RuntimeError(f"{fn}: attn_weight shape {tuple(attn_weight.shape)} does not match "
+                           f"sampling_loc {tuple(sampling_loc.shape)}")
+    output = torch.empty(batch, num_query, heads * channels, dtype=value.dtype,
+                         device=value.device)
+    _b.call("bevk_msda_forward", _b.dtype_code(value), _b.ptr(value), _b.ptr(spatial_shapes),
+            _b.ptr(level_start_index), _b.ptr(sampling_loc), _b.ptr(attn_weight), batch, spatial,
+            heads, channels, num_levels, num_query, num_point, int(im2col_step),
+            1 if force_generic else 0, _b.ptr(output), _b.stream_of(value))
+    return output
+
+
+def backward(value, spatial_shapes, level_start_index, sampling_loc, attn_weight, grad_output,
+             grad_value, grad_sampling_loc, grad_attn_weight, im2col_step=64,
+             force_generic_col2im=False):
+    """MSDA backward (binding_musa.mu:414-543). Not part of this build."""
+    raise RuntimeError("msda backward: the backward kernels are not part of this build "
+                       "(forward operators only)")

@@ -1,0 +1,46 @@
+// Internal launcher interface between the C ABI (binding.cpp) and the kernel
+// translation units. Arguments are already validated by the caller; each launcher
+// only enqueues work and returns the HIP status of the launch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace bevk {
+
+struct MsdaArgs {
+  const void *value;
+  const int64_t *spatial_shapes;
+  const int64_t *level_start_index;
+  const void *sampling_loc;
+  const void *attn_weight;
+  void *output;
+  int batch, spatial_size, num_heads, channels, num_levels, num_query, num_point;
+};
+
+hipError_t launch_msda_forward(int dtype, const MsdaArgs &a, bool force_generic,
+                               hipStream_t stream);
+
+struct DcnGeom {
+  int batch, channels, height, width, height_col, width_col;
+  int kernel_h, kernel_w, pad_h, pad_w, stride_h, stride_w, dil_h, dil_w;
+  int deformable_group;
+};
+
+// NCHW modulated im2col; `tiled` picks the geometry-reuse kernel (im2col_opt).
+hipError_t launch_im2col_nchw(int dtype, const DcnGeom &g, const void *data_im,
+                              const void *data_offset, const void *data_mask,
+                              void *data_col, bool tiled, hipStream_t stream);
+
+// NHWC gather (dg == 1). fused_y: data_offset is the raw [.., 3T] offset-conv output.
+hipError_t launch_im2col_nhwc(int dtype, const DcnGeom &g, const void *data_im,
+                              const void *data_offset, bool fused_y, const void *data_mask,
+                              void *data_col, hipStream_t stream);
+
+// Fused NHWC implicit-GEMM forward (dg == 1).
+hipError_t launch_dcn_fused_nhwc(int dtype, const DcnGeom &g, int channels_out,
+                                 const void *data_im, const void *data_offset, bool fused_y,
+                                 const void *data_mask, const void *weight_kc,
+                                 const void *bias, void *out, hipStream_t stream);
+
+}  // namespace bevk

@@ -1,0 +1,257 @@
+// C ABI of libbevk.so: argument validation, error reporting and dispatch onto the
+// kernel launchers. The entry points keep the argument order of the reference's
+// pybind11 functions (naotic/bev-kernels csrc/binding.cpp:142-191 and
+// csrc_musa/msda/binding_musa.mu:545-557) with tensors lowered to device pointers.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/bev_kernels.h"
+#include "bevk_launch.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char *fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() { return BEVK_OK; }
+
+int hip_status(hipError_t e, const char *what) {
+  if (e == hipSuccess) return ok();
+  return fail(BEVK_ERR_HIP, "%s: HIP error %d (%s)", what, (int)e, hipGetErrorString(e));
+}
+
+const char *dtype_name(int dtype) {
+  switch (dtype) {
+    case BEVK_F32: return "Float";
+    case BEVK_F16: return "Half";
+    case BEVK_BF16: return "BFloat16";
+    case BEVK_F64: return "Double";
+    default: return "unknown";
+  }
+}
+
+bool valid_dtype(int dtype) { return dtype >= BEVK_F32 && dtype <= BEVK_F64; }
+
+int dtype_size(int dtype) {
+  switch (dtype) {
+    case BEVK_F32: return 4;
+    case BEVK_F16: case BEVK_BF16: return 2;
+    default: return 8;
+  }
+}
+
+// The kernels address one image (or, for the fused kernel, the whole input) through a
+// 32-bit buffer range with an out-of-range sentinel just past its end.
+constexpr long long kMaxBufferBytes = (1LL << 31) - 256;
+
+// Shared geometry checks of the DCN entry points; the output size must follow the
+// convolution formula (modulated_deform_conv.py:364-365).
+int check_geom(const char *fn, const bevk::DcnGeom &g) {
+  if (g.batch < 0 || g.channels < 0 || g.height < 0 || g.width < 0)
+    return fail(BEVK_ERR_INVALID, "%s: negative input size", fn);
+  if (g.kernel_h <= 0 || g.kernel_w <= 0 || g.stride_h <= 0 || g.stride_w <= 0 ||
+      g.dil_h <= 0 || g.dil_w <= 0 || g.pad_h < 0 || g.pad_w < 0)
+    return fail(BEVK_ERR_INVALID,
+                "%s: kernel, stride and dilation must be positive and padding non-negative", fn);
+  if (g.deformable_group <= 0)
+    return fail(BEVK_ERR_INVALID, "%s: deformable_group must be positive", fn);
+  if (g.channels % g.deformable_group != 0)
+    return fail(BEVK_ERR_INVALID, "%s: channels (%d) must be divisible by deformable_group (%d)",
+                fn, g.channels, g.deformable_group);
+  const int ho = (g.height + 2 * g.pad_h - (g.dil_h * (g.kernel_h - 1) + 1)) / g.stride_h + 1;
+  const int wo = (g.width + 2 * g.pad_w - (g.dil_w * (g.kernel_w - 1) + 1)) / g.stride_w + 1;
+  if (g.height_col != ho || g.width_col != wo)
+    return fail(BEVK_ERR_INVALID,
+                "%s: output size (%d, %d) does not match the convolution geometry (%d, %d)", fn,
+                g.height_col, g.width_col, ho, wo);
+  if (ho <= 0 || wo <= 0)
+    return fail(BEVK_ERR_INVALID, "%s: empty output (%d x %d)", fn, ho, wo);
+  return ok();
+}
+
+bevk::DcnGeom make_geom(int batch_size, int channels, int height_im, int width_im,
+                        int height_col, int width_col, int kernel_h, int kernel_w, int pad_h,
+                        int pad_w, int stride_h, int stride_w, int dilation_h, int dilation_w,
+                        int deformable_group) {
+  bevk::DcnGeom g;
+  g.batch = batch_size; g.channels = channels; g.height = height_im; g.width = width_im;
+  g.height_col = height_col; g.width_col = width_col;
+  g.kernel_h = kernel_h; g.kernel_w = kernel_w; g.pad_h = pad_h; g.pad_w = pad_w;
+  g.stride_h = stride_h; g.stride_w = stride_w; g.dil_h = dilation_h; g.dil_w = dilation_w;
+  g.deformable_group = deformable_group;
+  return g;
+}
+
+int im2col_nchw_common(const char *fn, bool tiled, int dtype, const void *data_im,
+                       const void *data_offset, const void *data_mask, const bevk::DcnGeom &g,
+                       void *data_col, void *stream) {
+  g_last_error.clear();
+  if (!valid_dtype(dtype)) return fail(BEVK_ERR_INVALID, "%s: unknown dtype code %d", fn, dtype);
+  if (int rc = check_geom(fn, g)) return rc;
+  const long long cols = (long long)g.channels * g.kernel_h * g.kernel_w * g.batch *
+                         g.height_col * g.width_col;
+  if (cols == 0) return ok();
+  if ((long long)g.channels * g.height * g.width * dtype_size(dtype) > kMaxBufferBytes)
+    return fail(BEVK_ERR_INVALID, "%s: one input image exceeds 2 GiB", fn);
+  if (!data_im || !data_offset || !data_mask || !data_col)
+    return fail(BEVK_ERR_INVALID, "%s: null tensor pointer", fn);
+  return hip_status(bevk::launch_im2col_nchw(dtype, g, data_im, data_offset, data_mask,
+                                             data_col, tiled, (hipStream_t)stream),
+                    fn);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *bevk_last_error(void) { return g_last_error.c_str(); }
+
+const char *bevk_version(void) { return "bevk 0.1.0 gfx950"; }
+
+int bevk_modulated_deformable_im2col(int dtype, const void *data_im, const void *data_offset,
+                                     const void *data_mask, int batch_size, int channels,
+                                     int height_im, int width_im, int height_col, int width_col,
+                                     int kernel_h, int kernel_w, int pad_h, int pad_w,
+                                     int stride_h, int stride_w, int dilation_h, int dilation_w,
+                                     int deformable_group, void *data_col, void *stream) {
+  return im2col_nchw_common(
+      "modulated_deformable_im2col", false, dtype, data_im, data_offset, data_mask,
+      make_geom(batch_size, channels, height_im, width_im, height_col, width_col, kernel_h,
+                kernel_w, pad_h, pad_w, stride_h, stride_w, dilation_h, dilation_w,
+                deformable_group),
+      data_col, stream);
+}
+
+int bevk_modulated_deformable_im2col_opt(
+    int dtype, const void *data_im, const void *data_offset, const void *data_mask,
+    int batch_size, int channels, int height_im, int width_im, int height_col, int width_col,
+    int kernel_h, int kernel_w, int pad_h, int pad_w, int stride_h, int stride_w,
+    int dilation_h, int dilation_w, int deformable_group, void *data_col, void *stream) {
+  return im2col_nchw_common(
+      "modulated_deformable_im2col_opt", true, dtype, data_im, data_offset, data_mask,
+      make_geom(batch_size, channels, height_im, width_im, height_col, width_col, kernel_h,
+                kernel_w, pad_h, pad_w, stride_h, stride_w, dilation_h, dilation_w,
+                deformable_group),
+      data_col, stream);
+}
+
+int bevk_modulated_deformable_im2col_nhwc(
+    int dtype, const void *data_im, const void *data_offset, int offset_last_dim,
+    const void *data_mask, int batch_size, int channels, int height_im, int width_im,
+    int height_col, int width_col, int kernel_h, int kernel_w, int pad_h, int pad_w,
+    int stride_h, int stride_w, int dilation_h, int dilation_w, int deformable_group,
+    void *data_col, void *stream) {
+  const char *fn = "modulated_deformable_im2col_nhwc";
+  g_last_error.clear();
+  // dcn_fused_nhwc_cuda.cu:34-35
+  if (deformable_group != 1)
+    return fail(BEVK_ERR_INVALID, "NHWC fused path supports deformable_group == 1 only");
+  if (!valid_dtype(dtype)) return fail(BEVK_ERR_INVALID, "%s: unknown dtype code %d", fn, dtype);
+  const bevk::DcnGeom g =
+      make_geom(batch_size, channels, height_im, width_im, height_col, width_col, kernel_h,
+                kernel_w, pad_h, pad_w, stride_h, stride_w, dilation_h, dilation_w, 1);
+  if (int rc = check_geom(fn, g)) return rc;
+  const int taps = kernel_h * kernel_w;
+  if (offset_last_dim != 2 * taps && offset_last_dim != 3 * taps)
+    return fail(BEVK_ERR_INVALID, "%s: offset last dim must be 2T (%d) or 3T (%d), got %d", fn,
+                2 * taps, 3 * taps, offset_last_dim);
+  const bool fused_y = offset_last_dim == 3 * taps;  // dcn_fused_nhwc_cuda.cu:54
+  const long long m = (long long)batch_size * height_col * width_col;
+  // dcn_fused_nhwc_cuda.cu:37-40
+  if (m * taps * channels >= 2147483647LL)
+    return fail(BEVK_ERR_INVALID, "NHWC gather: Col element count exceeds int32 range");
+  if (m * taps * channels == 0) return ok();
+  if ((long long)height_im * width_im * channels * dtype_size(dtype) > kMaxBufferBytes)
+    return fail(BEVK_ERR_INVALID, "%s: one input image exceeds 2 GiB", fn);
+  if (!data_im || !data_offset || (!fused_y && !data_mask) || !data_col)
+    return fail(BEVK_ERR_INVALID, "%s: null tensor pointer", fn);
+  return hip_status(bevk::launch_im2col_nhwc(dtype, g, data_im, data_offset, fused_y, data_mask,
+                                             data_col, (hipStream_t)stream),
+                    fn);
+}
+
+int bevk_dcn_fused_fwd_nhwc(int dtype, const void *data_im, const void *data_offset,
+                            int offset_last_dim, const void *data_mask, const void *weight_kc,
+                            const void *bias, int batch_size, int channels, int height_im,
+                            int width_im, int height_col, int width_col, int channels_out,
+                            int kernel_h, int kernel_w, int pad_h, int pad_w, int stride_h,
+                            int stride_w, int dilation_h, int dilation_w, void *out,
+                            void *stream) {
+  const char *fn = "dcn_fused_fwd_nhwc";
+  g_last_error.clear();
+  if (dtype != BEVK_F32 && dtype != BEVK_F16 && dtype != BEVK_BF16)
+    return fail(BEVK_ERR_UNSUPPORTED, "\"%s\" not implemented for '%s'", fn, dtype_name(dtype));
+  const bevk::DcnGeom g =
+      make_geom(batch_size, channels, height_im, width_im, height_col, width_col, kernel_h,
+                kernel_w, pad_h, pad_w, stride_h, stride_w, dilation_h, dilation_w, 1);
+  if (int rc = check_geom(fn, g)) return rc;
+  if (channels_out < 0) return fail(BEVK_ERR_INVALID, "%s: negative channels_out", fn);
+  const int taps = kernel_h * kernel_w;
+  if (offset_last_dim != 2 * taps && offset_last_dim != 3 * taps)
+    return fail(BEVK_ERR_INVALID, "%s: offset last dim must be 2T (%d) or 3T (%d), got %d", fn,
+                2 * taps, 3 * taps, offset_last_dim);
+  const bool fused_y = offset_last_dim == 3 * taps;
+  const long long m = (long long)batch_size * height_col * width_col;
+  if (m * channels_out == 0) return ok();
+  const int vec = 16 / dtype_size(dtype);
+  if (channels <= 0 || channels % vec != 0)
+    return fail(BEVK_ERR_UNSUPPORTED,
+                "%s: channels (%d) must be a positive multiple of %d for '%s'", fn, channels,
+                vec, dtype_name(dtype));
+  if ((long long)batch_size * height_im * width_im * channels * dtype_size(dtype) >
+          kMaxBufferBytes ||
+      (long long)taps * channels * channels_out * dtype_size(dtype) > kMaxBufferBytes ||
+      m >= (1LL << 30))
+    return fail(BEVK_ERR_INVALID, "%s: problem too large for 32-bit buffer offsets", fn);
+  if (!data_im || !data_offset || (!fused_y && !data_mask) || !weight_kc || !out)
+    return fail(BEVK_ERR_INVALID, "%s: null tensor pointer", fn);
+  return hip_status(bevk::launch_dcn_fused_nhwc(dtype, g, channels_out, data_im, data_offset,
+                                                fused_y, data_mask, weight_kc, bias, out,
+                                                (hipStream_t)stream),
+                    fn);
+}
+
+int bevk_msda_forward(int dtype, const void *value, const int64_t *spatial_shapes,
+                      const int64_t *level_start_index, const void *sampling_loc,
+                      const void *attn_weight, int batch, int spatial_size, int num_heads,
+                      int channels, int num_levels, int num_query, int num_point,
+                      int im2col_step, int force_generic, void *output, void *stream) {
+  const char *fn = "msda_forward";
+  g_last_error.clear();
+  if (!valid_dtype(dtype)) return fail(BEVK_ERR_INVALID, "%s: unknown dtype code %d", fn, dtype);
+  if (batch < 0 || spatial_size < 0 || num_heads < 0 || channels < 0 || num_levels < 0 ||
+      num_query < 0 || num_point < 0)
+    return fail(BEVK_ERR_INVALID, "%s: negative size", fn);
+  if (im2col_step <= 0) return fail(BEVK_ERR_INVALID, "%s: im2col_step must be positive", fn);
+  // binding_musa.mu:308-309
+  const int step = batch < im2col_step ? batch : im2col_step;
+  if (step > 0 && batch % step != 0)
+    return fail(BEVK_ERR_INVALID, "batch must divide im2col_step");
+  const long long n = (long long)batch * num_query * num_heads * channels;
+  if (n == 0) return ok();
+  if (!value || !spatial_shapes || !level_start_index || !sampling_loc || !attn_weight ||
+      !output)
+    return fail(BEVK_ERR_INVALID, "%s: null tensor pointer", fn);
+  bevk::MsdaArgs a;
+  a.value = value; a.spatial_shapes = spatial_shapes; a.level_start_index = level_start_index;
+  a.sampling_loc = sampling_loc; a.attn_weight = attn_weight; a.output = output;
+  a.batch = batch; a.spatial_size = spatial_size; a.num_heads = num_heads;
+  a.channels = channels; a.num_levels = num_levels; a.num_query = num_query;
+  a.num_point = num_point;
+  return hip_status(
+      bevk::launch_msda_forward(dtype, a, force_generic != 0, (hipStream_t)stream), fn);
+}
+
+}  // extern "C"

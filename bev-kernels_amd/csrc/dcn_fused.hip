@@ -1,0 +1,331 @@
+// Fused NHWC DCNv2 forward for gfx950: deformable gather + GEMM with no column buffer.
+//
+//   out[m, n] = sum_k A[m, k] * Wkc[n, k] (+ bias[n]),  m = (b, oh, ow), k = t*C + c
+//   A[m, k]   = mask[m, t] * bilinear(x[b], h(m, t), w(m, t))[c]
+// (naotic/bev-kernels fused_tl.py:42-139 is the algorithmic model: A tiles are built
+// on the fly, never written to HBM.)
+//
+// Structure of one workgroup (4 waves) computing a BM x BN tile of `out`:
+//   * K loop in steps of BK. Every thread owns fixed (row, 16-byte k-vector) slots of
+//     the A tile; per slot it keeps the tap geometry (four corner byte offsets and
+//     four mask-folded bilinear weights) and refreshes it only when the slot moves to
+//     a new tap. Corner rows are read with 16-byte buffer loads; invalid corners use
+//     an out-of-range offset and read zero.
+//   * The blended A vectors (fp32 math, one rounding to T) and the weight tile go to
+//     double-buffered LDS; one barrier per K step.
+//   * The next step's global loads are issued before the current step's MFMAs
+//     (v_mfma_f32_32x32x16_{f16,bf16}, or v_mfma_f32_32x32x2_f32 for fp32).
+//   * Epilogue: fp32 accumulators + bias, rounded once to T.
+// M tiles are dealt to XCDs in contiguous bands so that one XCD's L2 holds the rows of
+// the input image its tiles sample.
+#include "bevk_common.h"
+#include "bevk_launch.h"
+
+namespace bevk {
+namespace {
+
+constexpr int kThreads = 256;
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+struct FusedParams {
+  const void *x;
+  const void *off;
+  const void *msk;
+  const void *w;
+  const void *bias;
+  void *out;
+  int B, C, H, W, Ho, Wo, Cout, kh, kw, ph, pw, sh, sw, dh, dw;
+  int M, K;
+  int tiles_m;
+  uint32_t x_bytes, w_bytes;
+};
+
+// MFMA step on one 32x32 tile. A/B fragments are k-contiguous 16-byte LDS vectors.
+template <typename T> struct Mfma;
+template <> struct Mfma<f16> {
+  static constexpr int KSTEP = 16;  // k per instruction
+  __device__ static floatx16 run(const f16 *a, const f16 *b, floatx16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8 *>(a),
+                                                  *reinterpret_cast<const half8 *>(b), c, 0, 0, 0);
+  }
+};
+template <> struct Mfma<bf16> {
+  static constexpr int KSTEP = 16;
+  __device__ static floatx16 run(const bf16 *a, const bf16 *b, floatx16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(*reinterpret_cast<const bf16x8 *>(a),
+                                                   *reinterpret_cast<const bf16x8 *>(b), c, 0, 0, 0);
+  }
+};
+template <> struct Mfma<float> {
+  static constexpr int KSTEP = 2;
+  __device__ static floatx16 run(const float *a, const float *b, floatx16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(*a, *b, c, 0, 0, 0);
+  }
+};
+// Elements of k each lane contributes per instruction (lanes 0-31 take the first
+// chunk, lanes 32-63 the second).
+template <typename T> constexpr int lane_k() { return Mfma<T>::KSTEP / 2; }
+
+template <typename T, int BM, int BN, int BK, int WAVES_M, int WAVES_N, bool FY>
+__global__ void __launch_bounds__(kThreads) dcn_fused_nhwc_kernel(const FusedParams p) {
+  constexpr int VEC = 16 / sizeof(T);
+  constexpr int KV = BK / VEC;                    // 16-byte vectors per tile row per step
+  constexpr int AV = BM * KV / kThreads;          // A vectors per thread per step
+  constexpr int BV = BN * KV / kThreads;          // B vectors per thread per step
+  static_assert(AV >= 1 && BV >= 1, "tile too small for the thread count");
+  static_assert((BM * KV) % kThreads == 0 && (BN * KV) % kThreads == 0, "tile/thread mismatch");
+  constexpr int PAD = VEC;                        // one 16-byte vector of padding per row
+  constexpr int LDA = BK + PAD;
+  constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  static_assert(TM >= 1 && TN >= 1 && WAVES_M * WAVES_N == kThreads / kWave, "wave grid");
+  using V = Vec<T, VEC>;
+
+  __shared__ __attribute__((aligned(16))) T As[2][BM * LDA];
+  __shared__ __attribute__((aligned(16))) T Bs[2][BN * LDA];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid / kWave;
+  const int wm = wave / WAVES_N, wn = wave - (wave / WAVES_N) * WAVES_N;
+
+  // Contiguous band of M tiles per XCD (blocks are dealt round-robin to the 8 XCDs).
+  int tile_m = blockIdx.x;
+  {
+    const int full = (p.tiles_m / 8) * 8;
+    if (tile_m < full) tile_m = (tile_m & 7) * (full / 8) + (tile_m >> 3);
+  }
+  const int m0 = tile_m * BM;
+  const int n0 = blockIdx.y * BN;
+  const int HoWo = p.Ho * p.Wo;
+  const int T_ = p.kh * p.kw;
+
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, p.x_bytes);
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, p.w_bytes);
+  const uint32_t xoob = p.x_bytes;
+  const uint32_t woob = p.w_bytes;
+
+  // ---- per-slot A state -------------------------------------------------------
+  int a_row[AV], a_kv[AV];
+  int a_m[AV];            // output pixel, or -1 past M
+  int a_hb[AV], a_wb[AV]; // oh*sh - ph, ow*sw - pw
+  int a_img[AV];          // b * H * W
+  int a_t[AV], a_c[AV];   // current tap and channel of the slot's vector
+  int a_gt[AV];           // tap of the cached geometry
+  float a_w[AV][4];
+  uint32_t a_o[AV][4];
+#pragma unroll
+  for (int i = 0; i < AV; ++i) {
+    const int a = tid + i * kThreads;
+    a_row[i] = a / KV;
+    a_kv[i] = a - (a / KV) * KV;
+    const int m = m0 + a_row[i];
+    a_m[i] = m < p.M ? m : -1;
+    const int mm = m < p.M ? m : 0;
+    const int b = mm / HoWo;
+    const int r = mm - b * HoWo;
+    const int oh = r / p.Wo, ow = r - (r / p.Wo) * p.Wo;
+    a_hb[i] = oh * p.sh - p.ph;
+    a_wb[i] = ow * p.sw - p.pw;
+    a_img[i] = b * p.H * p.W;
+    const int k = a_kv[i] * VEC;
+    a_t[i] = k / p.C;
+    a_c[i] = k - a_t[i] * p.C;
+    a_gt[i] = -1;  // tap whose geometry is cached: none yet
+  }
+
+  auto refresh_geometry = [&](int i, int t) {
+    const int m = a_m[i];
+    float w1 = 0.f, w2 = 0.f, w3 = 0.f, w4 = 0.f;
+    uint32_t o1 = xoob, o2 = xoob, o3 = xoob, o4 = xoob;
+    if (m >= 0 && t < T_) {
+      float dy, dx, mk;
+      const T *offp = static_cast<const T *>(p.off);
+      if constexpr (FY) {
+        const T *yp = offp + (int64_t)m * 3 * T_;
+        dy = (float)yp[2 * t];
+        dx = (float)yp[2 * t + 1];
+        mk = sigmoid_f32((float)yp[2 * T_ + t]);
+      } else {
+        dy = (float)offp[(int64_t)m * 2 * T_ + 2 * t];
+        dx = (float)offp[(int64_t)m * 2 * T_ + 2 * t + 1];
+        mk = (float)static_cast<const T *>(p.msk)[(int64_t)m * T_ + t];
+      }
+      const int ki = t / p.kw, kj = t - (t / p.kw) * p.kw;
+      const float h = (float)(a_hb[i] + ki * p.dh) + dy;
+      const float w = (float)(a_wb[i] + kj * p.dw) + dx;
+      if (h > -1.f && w > -1.f && h < (float)p.H && w < (float)p.W) {
+        const float fh = floorf(h), fw = floorf(w);
+        const int hl = (int)fh, wl = (int)fw;
+        const float lh = h - fh, lw = w - fw, hh = 1.f - lh, hw = 1.f - lw;
+        const bool y0 = hl >= 0, y1 = hl + 1 <= p.H - 1;
+        const bool x0 = wl >= 0, x1 = wl + 1 <= p.W - 1;
+        const uint32_t row = (uint32_t)p.C * (uint32_t)sizeof(T);
+        const uint32_t base = (uint32_t)(a_img[i] + hl * p.W + wl) * row;
+        if (y0 && x0) { w1 = hh * hw * mk; o1 = base; }
+        if (y0 && x1) { w2 = hh * lw * mk; o2 = base + row; }
+        if (y1 && x0) { w3 = lh * hw * mk; o3 = base + (uint32_t)p.W * row; }
+        if (y1 && x1) { w4 = lh * lw * mk; o4 = base + (uint32_t)(p.W + 1) * row; }
+      }
+    }
+    a_w[i][0] = w1; a_w[i][1] = w2; a_w[i][2] = w3; a_w[i][3] = w4;
+    a_o[i][0] = o1; a_o[i][1] = o2; a_o[i][2] = o3; a_o[i][3] = o4;
+  };
+
+  // Raw global data for one K step, held in registers between issue and use.
+  V ra[AV][4];
+  V rb[BV];
+
+  auto issue_loads = [&](int ks) {
+#pragma unroll
+    for (int i = 0; i < AV; ++i) {
+      // Advance the slot's (t, c) to k = ks*BK + kv*VEC.
+      if (ks > 0) {
+        a_c[i] += BK;
+        while (a_c[i] >= p.C) { a_c[i] -= p.C; ++a_t[i]; }
+      }
+      if (a_t[i] != a_gt[i]) {
+        refresh_geometry(i, a_t[i]);
+        a_gt[i] = a_t[i];
+      }
+      const uint32_t cb = (uint32_t)a_c[i] * (uint32_t)sizeof(T);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t o = a_o[i][q];
+        ra[i][q] = buffer_load_vec<T, VEC>(xr, o == xoob ? xoob : o + cb);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < BV; ++i) {
+      const int v = tid + i * kThreads;
+      const int n = n0 + v / KV;
+      const int k = ks * BK + (v - (v / KV) * KV) * VEC;
+      const bool ok = n < p.Cout && k < p.K;
+      const uint32_t o = ok ? ((uint32_t)n * (uint32_t)p.K + (uint32_t)k) * (uint32_t)sizeof(T) : woob;
+      rb[i] = buffer_load_vec<T, VEC>(wr, o);
+    }
+  };
+
+  auto store_lds = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < AV; ++i) {
+      V o;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float val = a_w[i][0] * (float)ra[i][0].v[e] + a_w[i][1] * (float)ra[i][1].v[e] +
+                          a_w[i][2] * (float)ra[i][2].v[e] + a_w[i][3] * (float)ra[i][3].v[e];
+        o.v[e] = static_cast<T>(val);
+      }
+      store_vec<T, VEC>(&As[buf][a_row[i] * LDA + a_kv[i] * VEC], o);
+    }
+#pragma unroll
+    for (int i = 0; i < BV; ++i) {
+      const int v = tid + i * kThreads;
+      store_vec<T, VEC>(&Bs[buf][(v / KV) * LDA + (v - (v / KV) * KV) * VEC], rb[i]);
+    }
+  };
+
+  floatx16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  const int nk = (p.K + BK - 1) / BK;
+  const int lrow = lane & 31;
+  const int lk = (lane >> 5) * lane_k<T>();
+
+  issue_loads(0);
+  for (int ks = 0; ks < nk; ++ks) {
+    const int buf = ks & 1;
+    store_lds(buf);
+    __syncthreads();
+    if (ks + 1 < nk) issue_loads(ks + 1);
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += Mfma<T>::KSTEP) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const T *a = &As[buf][(wm * WTM + i * 32 + lrow) * LDA + kk + lk];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const T *bp = &Bs[buf][(wn * WTN + j * 32 + lrow) * LDA + kk + lk];
+          acc[i][j] = Mfma<T>::run(a, bp, acc[i][j]);
+        }
+      }
+    }
+  }
+
+  // ---- epilogue: D[row][col], lane holds col = lane%32,
+  //      row = 8*(e/4) + 4*(lane/32) + e%4 for e in [0, 16).
+  T *out = static_cast<T *>(p.out);
+  const T *bias = static_cast<const T *>(p.bias);
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int n = n0 + wn * WTN + j * 32 + lrow;
+    const float bv = (bias != nullptr && n < p.Cout) ? (float)bias[n] : 0.f;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = wm * WTM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        const int m = m0 + row;
+        if (m < p.M && n < p.Cout) out[(int64_t)m * p.Cout + n] = static_cast<T>(acc[i][j][e] + bv);
+      }
+    }
+  }
+}
+
+template <typename T, int BM, int BN, int BK, int WM, int WN>
+hipError_t launch_cfg(const FusedParams &p, bool fy, hipStream_t stream) {
+  dim3 grid(p.tiles_m, (p.Cout + BN - 1) / BN);
+  if (fy)
+    hipLaunchKernelGGL((dcn_fused_nhwc_kernel<T, BM, BN, BK, WM, WN, true>), grid,
+                       dim3(kThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL((dcn_fused_nhwc_kernel<T, BM, BN, BK, WM, WN, false>), grid,
+                       dim3(kThreads), 0, stream, p);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_t(FusedParams p, bool fy, hipStream_t stream) {
+  constexpr int BK = sizeof(T) == 4 ? 16 : 32;
+  constexpr int BM = 64;
+  p.tiles_m = (p.M + BM - 1) / BM;
+  if (p.Cout > 128) return launch_cfg<T, BM, 256, BK, 1, 4>(p, fy, stream);
+  if (p.Cout > 64) return launch_cfg<T, BM, 128, BK, 1, 4>(p, fy, stream);
+  return launch_cfg<T, BM, 64, BK, 2, 2>(p, fy, stream);
+}
+
+}  // namespace
+
+hipError_t launch_dcn_fused_nhwc(int dtype, const DcnGeom &g, int channels_out, const void *x,
+                                 const void *off, bool fused_y, const void *msk,
+                                 const void *w_kc, const void *bias, void *out,
+                                 hipStream_t stream) {
+  FusedParams p;
+  p.x = x; p.off = off; p.msk = msk; p.w = w_kc; p.bias = bias; p.out = out;
+  p.B = g.batch; p.C = g.channels; p.H = g.height; p.W = g.width;
+  p.Ho = g.height_col; p.Wo = g.width_col; p.Cout = channels_out;
+  p.kh = g.kernel_h; p.kw = g.kernel_w; p.ph = g.pad_h; p.pw = g.pad_w;
+  p.sh = g.stride_h; p.sw = g.stride_w; p.dh = g.dil_h; p.dw = g.dil_w;
+  p.M = g.batch * g.height_col * g.width_col;
+  p.K = g.kernel_h * g.kernel_w * g.channels;
+  p.tiles_m = 0;
+  const int es = dtype == 0 ? 4 : 2;
+  p.x_bytes = (uint32_t)((int64_t)g.batch * g.height * g.width * g.channels * es);
+  p.w_bytes = (uint32_t)((int64_t)channels_out * p.K * es);
+  switch (dtype) {
+    case 0: return launch_t<float>(p, fused_y, stream);
+    case 1: return launch_t<f16>(p, fused_y, stream);
+    case 2: return launch_t<bf16>(p, fused_y, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace bevk

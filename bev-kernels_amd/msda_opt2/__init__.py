@@ -1,0 +1,7 @@
+"""Multi-scale deformable attention on MI355X (gfx950)."""
+from .dispatch import ms_deform_attn_backward, ms_deform_attn_forward
+
+__all__ = [
+    "ms_deform_attn_forward",
+    "ms_deform_attn_backward",
+]

@@ -1,0 +1,146 @@
+/*
+ * bev_kernels.h — C ABI of libbevk.so, the MI355X (gfx950) implementation of the
+ * BEVFormer deformable-conv (DCNv2) and multi-scale deformable attention (MSDA)
+ * forward operators.
+ *
+ * Conventions shared by every entry point:
+ *   - All data pointers are DEVICE pointers to dense, contiguous (row-major) buffers.
+ *     The caller allocates every input and output; the library allocates nothing
+ *     that outlives a call.
+ *   - `dtype` selects the element type of the floating-point buffers (bevk_dtype).
+ *   - `stream` is a hipStream_t (NULL = the legacy default stream). Work is
+ *     enqueued asynchronously; nothing synchronises the host.
+ *   - Return value: 0 on success, otherwise a bevk_status code; the message for the
+ *     last failure on the calling thread is returned by bevk_last_error().
+ *   - Arguments are validated before any device work is enqueued; a rejected call
+ *     leaves every output untouched.
+ *
+ * Each entry point names the reference interface it replaces (naotic/bev-kernels,
+ * file:line). The reference exposes these through pybind11 on at::Tensor; here the
+ * same argument order is kept with tensors lowered to (pointer, dtype) pairs.
+ */
+#ifndef BEV_KERNELS_H_
+#define BEV_KERNELS_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  BEVK_F32 = 0,
+  BEVK_F16 = 1,
+  BEVK_BF16 = 2,
+  BEVK_F64 = 3
+} bevk_dtype;
+
+typedef enum {
+  BEVK_OK = 0,
+  BEVK_ERR_INVALID = 1,     /* argument validation failed (RuntimeError in Python) */
+  BEVK_ERR_UNSUPPORTED = 2, /* dtype / shape combination not implemented           */
+  BEVK_ERR_HIP = 3          /* HIP runtime reported an error at launch              */
+} bevk_status;
+
+/* Message describing the most recent failed call on this thread ("" if none). */
+const char *bevk_last_error(void);
+
+/* Library version string, e.g. "bevk 0.1.0 gfx950". */
+const char *bevk_version(void);
+
+/* ------------------------------------------------------------------------- */
+/* DCNv2, NCHW layout                                                         */
+/* ------------------------------------------------------------------------- */
+
+/* Modulated deformable im2col, NCHW.
+ *   data_im     [B, C, H, W]
+ *   data_offset [B, dg*2*kh*kw, Ho, Wo]   (dy, dx) interleaved per tap
+ *   data_mask   [B, dg*kh*kw, Ho, Wo]
+ *   data_col    [C*kh*kw, B, Ho, Wo]      row = c*kh*kw + (i*kw + j); fully written
+ * Replaces binding.cpp:5-11 / :142-144 (modulated_deformable_im2col_cuda, launcher
+ * modulated_deform_conv_cuda.cu:4-30). dtypes: F32, F64, F16, BF16. */
+int bevk_modulated_deformable_im2col(
+    int dtype, const void *data_im, const void *data_offset, const void *data_mask,
+    int batch_size, int channels, int height_im, int width_im, int height_col,
+    int width_col, int kernel_h, int kernel_w, int pad_h, int pad_w, int stride_h,
+    int stride_w, int dilation_h, int dilation_w, int deformable_group,
+    void *data_col, void *stream);
+
+/* Same contract as bevk_modulated_deformable_im2col; the tiled kernel that the
+ * reference's module forward uses.
+ * Replaces binding.cpp:21-27 / :149-151 (modulated_deformable_im2col_opt_cuda,
+ * launcher modulated_deform_conv_cuda.cu:62-115). */
+int bevk_modulated_deformable_im2col_opt(
+    int dtype, const void *data_im, const void *data_offset, const void *data_mask,
+    int batch_size, int channels, int height_im, int width_im, int height_col,
+    int width_col, int kernel_h, int kernel_w, int pad_h, int pad_w, int stride_h,
+    int stride_w, int dilation_h, int dilation_w, int deformable_group,
+    void *data_col, void *stream);
+
+/* ------------------------------------------------------------------------- */
+/* DCNv2, NHWC layout (deformable_group == 1)                                 */
+/* ------------------------------------------------------------------------- */
+
+/* Deformable gather into columns, NHWC.
+ *   data_im     [B, H, W, C]
+ *   data_offset [B, Ho, Wo, offset_last_dim]. offset_last_dim == 2T: offsets
+ *               (dy, dx per tap) and data_mask [B, Ho, Wo, T] holds the mask.
+ *               offset_last_dim == 3T: the raw offset-conv output y; offsets are
+ *               y[..., :2T] and mask = sigmoid(y[..., 2T:]); data_mask is ignored.
+ *   data_col    [B*Ho*Wo, T*C], k = t*C + c; fully written.
+ * Replaces binding.cpp:64-70 / :164-166 (modulated_deformable_im2col_nhwc_cuda,
+ * launcher dcn_fused_nhwc_cuda.cu:27-87, fused-y rule at :54). */
+int bevk_modulated_deformable_im2col_nhwc(
+    int dtype, const void *data_im, const void *data_offset, int offset_last_dim,
+    const void *data_mask, int batch_size, int channels, int height_im, int width_im,
+    int height_col, int width_col, int kernel_h, int kernel_w, int pad_h, int pad_w,
+    int stride_h, int stride_w, int dilation_h, int dilation_w, int deformable_group,
+    void *data_col, void *stream);
+
+/* Fused NHWC DCNv2 forward: bilinear x mask taps are produced straight into LDS
+ * and multiplied on the matrix cores; no column buffer touches HBM.
+ *   data_im     [B, H, W, C]
+ *   data_offset [B, Ho, Wo, offset_last_dim] with the same 2T / 3T rule as above
+ *   data_mask   [B, Ho, Wo, T] (ignored in the 3T form)
+ *   weight_kc   [Cout, kh, kw, C]  (= torch weight.permute(0, 2, 3, 1)), K-contiguous
+ *   bias        [Cout] in dtype, or NULL
+ *   out         [B, Ho, Wo, Cout]; fully written. fp32 accumulation, one rounding.
+ * Computes fused_tl.fused_dcn_forward_nhwc (fused_tl.py:513-556, algorithm of the
+ * T.gemm kernel at :42-139) and the forward of DCNSplitNHWCFunction
+ * (dcn_split_nhwc.py:158-228) after its offset conv. dtypes: F16, BF16, F32. */
+int bevk_dcn_fused_fwd_nhwc(
+    int dtype, const void *data_im, const void *data_offset, int offset_last_dim,
+    const void *data_mask, const void *weight_kc, const void *bias, int batch_size,
+    int channels, int height_im, int width_im, int height_col, int width_col,
+    int channels_out, int kernel_h, int kernel_w, int pad_h, int pad_w, int stride_h,
+    int stride_w, int dilation_h, int dilation_w, void *out, void *stream);
+
+/* ------------------------------------------------------------------------- */
+/* Multi-scale deformable attention                                            */
+/* ------------------------------------------------------------------------- */
+
+/* MSDA forward.
+ *   value              [B, spatial_size, num_heads, channels]
+ *   spatial_shapes     [num_levels, 2] int64 (H_l, W_l), device memory
+ *   level_start_index  [num_levels]    int64, device memory
+ *   sampling_loc       [B, num_query, num_heads, num_levels, num_point, 2] (x, y) in [0,1]
+ *   attn_weight        [B, num_query, num_heads, num_levels, num_point]
+ *   output             [B, num_query, num_heads*channels]; fully written (samples
+ *                      outside a level contribute zero).
+ * im2col_step keeps the reference's contract (batch % min(batch, step) == 0); the
+ * whole batch is processed by one launch. force_generic selects the
+ * thread-per-output-element kernel.
+ * Replaces _msda_opt2_musa.forward (binding_musa.mu:286-412, :546-549).
+ * dtypes: F32, F16, BF16 (fp32 accumulation), F64. */
+int bevk_msda_forward(
+    int dtype, const void *value, const int64_t *spatial_shapes,
+    const int64_t *level_start_index, const void *sampling_loc, const void *attn_weight,
+    int batch, int spatial_size, int num_heads, int channels, int num_levels,
+    int num_query, int num_point, int im2col_step, int force_generic, void *output,
+    void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BEV_KERNELS_H_ */

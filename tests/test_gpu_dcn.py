@@ -1,0 +1,261 @@
+"""DCNv2 forward on the GPU vs the float64 CPU oracle (oracle/dcn.py), through the
+reference-shaped APIs: the extension functions (_modulated_deform_conv_ext), the NHWC
+entry points (fused_tl / dcn_split_nhwc) and the modules (modulated_deform_conv).
+
+Full-size ResNet-101 res4/res5 configurations run whole on the GPU; the oracle checks
+the first and last image."""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from _tol import check
+from oracle import dcn as od
+from oracle import inputs
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda")
+HALF = [torch.float16, torch.bfloat16]
+
+
+def _ext():
+    import _modulated_deform_conv_ext
+    return _modulated_deform_conv_ext
+
+
+def _rand_problem(b, cin, cout, h, w, k=3, stride=1, pad=1, dil=1, dg=1, groups=1, seed=0,
+                  off_std=2.0, dtype=torch.float32):
+    g = torch.Generator().manual_seed(seed)
+    ho = od.out_size(h, pad, dil, k, stride)
+    wo = od.out_size(w, pad, dil, k, stride)
+    x = torch.randn(b, cin, h, w, generator=g)
+    off = off_std * torch.randn(b, dg * 2 * k * k, ho, wo, generator=g)
+    # a few taps exactly on integers, half pixels and far outside
+    off.view(-1)[::7] = torch.round(off.view(-1)[::7])
+    off.view(-1)[::11] = torch.round(off.view(-1)[::11]) + 0.5
+    off.view(-1)[::13] = 40.0
+    mask = torch.rand(b, dg * k * k, ho, wo, generator=g)
+    weight = 0.1 * torch.randn(cout, cin // groups, k, k, generator=g)
+    bias = torch.randn(cout, generator=g)
+    r = lambda t: t.to(dtype)
+    return dict(x=r(x), offset=r(off), mask=r(mask), weight=r(weight), bias=r(bias),
+                stride=(stride, stride), padding=(pad, pad), dilation=(dil, dil), dg=dg,
+                groups=groups)
+
+
+# ---------------------------------------------------------------------------------------
+# NCHW columns (ext.modulated_deformable_im2col[_opt]_cuda)
+# ---------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("entry", ["modulated_deformable_im2col_cuda",
+                                   "modulated_deformable_im2col_opt_cuda"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.float16, torch.bfloat16],
+                         ids=["fp32", "fp64", "fp16", "bf16"])
+@pytest.mark.parametrize("geom", [
+    # b, cin, h, w, k, stride, pad, dil, dg
+    (2, 8, 9, 11, 3, 1, 1, 1, 1),
+    (1, 12, 13, 10, 3, 2, 1, 1, 2),
+    (2, 6, 12, 12, 3, 1, 2, 2, 3),
+    (1, 4, 7, 5, 1, 1, 0, 1, 1),
+    (1, 64, 32, 32, 3, 1, 1, 1, 1),
+])
+def test_im2col_nchw(entry, dtype, geom):
+    b, cin, h, w, k, s, p, dl, dg = geom
+    d = _rand_problem(b, cin, 4, h, w, k, s, p, dl, dg, dtype=dtype, seed=sum(geom))
+    ho, wo = od.out_size(h, p, dl, k, s), od.out_size(w, p, dl, k, s)
+    col = torch.full((cin * k * k, b, ho, wo), float("nan"), dtype=dtype, device=DEV)
+    getattr(_ext(), entry)(d["x"].to(DEV), d["offset"].to(DEV), d["mask"].to(DEV), b, cin, h,
+                           w, ho, wo, k, k, p, p, s, s, dl, dl, dg, col)
+    torch.cuda.synchronize()
+    ref = od.im2col_nchw(d["x"].double(), d["offset"].double(), d["mask"].double(), k, k, p, p,
+                         s, s, dl, dl, dg)
+    check(col.cpu(), ref, dtype, f"{entry} {geom}")
+
+
+# ---------------------------------------------------------------------------------------
+# NHWC columns (ext.modulated_deformable_im2col_nhwc_cuda), 2T and raw-y (3T) forms
+# ---------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("fused_y", [False, True], ids=["2T", "3T"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16, torch.float64],
+                         ids=["fp32", "fp16", "bf16", "fp64"])
+@pytest.mark.parametrize("geom", [
+    (2, 16, 9, 11, 1, 1, 1), (1, 24, 8, 13, 2, 1, 1), (1, 256, 12, 10, 1, 1, 1),
+    (2, 5, 7, 6, 1, 1, 1), (1, 40, 10, 9, 1, 2, 2),
+])
+def test_im2col_nhwc(fused_y, dtype, geom):
+    b, cin, h, w, s, p, dl = geom
+    d = inputs.nchw_to_nhwc(_rand_problem(b, cin, 4, h, w, 3, s, p, dl, dtype=dtype,
+                                          seed=sum(geom) + fused_y))
+    ho, wo = od.out_size(h, p, dl, 3, s), od.out_size(w, p, dl, 3, s)
+    x = d["x"]
+    if fused_y:
+        raw = torch.randn(b, ho, wo, 9, generator=torch.Generator().manual_seed(1)).to(dtype)
+        y = torch.cat([d["offset"], raw], -1).contiguous()
+        off_ref, mask_ref = od.split_y_nhwc(y.double(), 9)
+        off_arg, mask_arg = y, y
+    else:
+        off_ref, mask_ref = d["offset"].double(), d["mask"].double()
+        off_arg, mask_arg = d["offset"], d["mask"]
+    col = torch.full((b * ho * wo, 9 * cin), float("nan"), dtype=dtype, device=DEV)
+    _ext().modulated_deformable_im2col_nhwc_cuda(
+        x.to(DEV), off_arg.to(DEV), mask_arg.to(DEV), b, cin, h, w, ho, wo, 3, 3, p, p, s, s,
+        dl, dl, 1, col)
+    torch.cuda.synchronize()
+    ref = od.columns_nhwc(x.double(), off_ref, mask_ref, 3, 3, s, s, p, p, dl, dl)
+    check(col.cpu(), ref, dtype, f"nhwc cols {geom}")
+
+
+# ---------------------------------------------------------------------------------------
+# Fused NHWC implicit GEMM (fused_tl.fused_dcn_forward_nhwc -> ext.dcn_fused_fwd_nhwc)
+# ---------------------------------------------------------------------------------------
+
+def _fused_ref(d, dtype):
+    return od.forward_nhwc(d["x"].double(), d["offset"].double(), d["mask"].double(),
+                           d["weight"].double(), d["bias"].double(), d["stride"], d["padding"],
+                           d["dilation"])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16],
+                         ids=["fp32", "fp16", "bf16"])
+@pytest.mark.parametrize("geom", [
+    # b, cin, cout, h, w, stride, pad, dil
+    (2, 16, 32, 9, 11, 1, 1, 1),
+    (1, 64, 64, 32, 32, 1, 1, 1),
+    (2, 32, 40, 13, 7, 1, 1, 1),      # Cout tail
+    (1, 24, 300, 10, 9, 2, 1, 1),     # stride 2, Cout > 256
+    (1, 128, 96, 6, 20, 1, 2, 2),     # dilation 2
+    (3, 8, 8, 5, 5, 1, 1, 1),
+])
+def test_fused_nhwc(dtype, geom):
+    b, cin, cout, h, w, s, p, dl = geom
+    from modulated_deform_conv import fused_tl
+    d = inputs.nchw_to_nhwc(_rand_problem(b, cin, cout, h, w, 3, s, p, dl, dtype=dtype,
+                                          seed=sum(geom)))
+    out = fused_tl.fused_dcn_forward_nhwc(d["x"].to(DEV), d["offset"].to(DEV),
+                                          d["mask"].to(DEV), d["weight"].to(DEV),
+                                          d["bias"].to(DEV), s, p, dl)
+    torch.cuda.synchronize()
+    check(out.cpu(), _fused_ref(d, dtype), dtype, f"fused {geom}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32],
+                         ids=["fp16", "bf16", "fp32"])
+@pytest.mark.parametrize("cfg", ["dcn_res4", "dcn_res5"])
+def test_fused_nhwc_full_size(cfg, dtype):
+    d = inputs.nchw_to_nhwc(inputs.dcn_inputs(cfg))
+    d = {k: (v.to(dtype) if torch.is_tensor(v) else v) for k, v in d.items()}
+    from modulated_deform_conv import fused_tl
+    out = fused_tl.fused_dcn_forward_nhwc(d["x"].to(DEV), d["offset"].to(DEV),
+                                          d["mask"].to(DEV), d["weight"].to(DEV), None, 1, 1, 1)
+    torch.cuda.synchronize()
+    out = out.cpu()
+    assert torch.isfinite(out.float()).all()
+    for b in (0, d["x"].shape[0] - 1):
+        sub = {k: (v[b:b + 1] if k in ("x", "offset", "mask") else v) for k, v in d.items()}
+        sub["bias"] = None
+        ref = od.forward_nhwc(sub["x"].double(), sub["offset"].double(), sub["mask"].double(),
+                              sub["weight"].double(), None, 1, 1, 1)
+        check(out[b:b + 1], ref, dtype, f"{cfg} image {b}")
+
+
+def test_fused_matches_gather_plus_gemm():
+    """Fused kernel == explicit columns (NHWC gather kernel) @ weight, same inputs."""
+    d = inputs.nchw_to_nhwc(_rand_problem(2, 64, 128, 20, 24, seed=5, dtype=torch.float32))
+    from modulated_deform_conv import fused_tl
+    x, off, m, w = (d[k].to(DEV) for k in ("x", "offset", "mask", "weight"))
+    fused = fused_tl.fused_dcn_forward_nhwc(x, off, m, w, None, 1, 1, 1)
+    cols = fused_tl.dcn_gather_cols_nhwc(x, off, m, 3, 3, 1, 1, 1)
+    split = (cols.double() @ w.permute(2, 3, 1, 0).reshape(-1, 128).double()).view_as(fused)
+    check(fused.cpu(), split.cpu(), torch.float32, "fused vs split")
+
+
+# ---------------------------------------------------------------------------------------
+# Modules and autograd functions
+# ---------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("groups,dg", [(1, 1), (2, 1), (1, 2)])
+def test_modulated_deform_conv2d_nchw(groups, dg):
+    from modulated_deform_conv import modulated_deform_conv2d
+    d = _rand_problem(2, 16, 24, 11, 13, dg=dg, groups=groups, seed=groups * 10 + dg)
+    out = modulated_deform_conv2d(d["x"].to(DEV), d["offset"].to(DEV), d["mask"].to(DEV),
+                                  d["weight"].to(DEV), d["bias"].to(DEV), 1, 1, 1, groups, dg)
+    torch.cuda.synchronize()
+    ref = od.forward_nchw(d["x"].double(), d["offset"].double(), d["mask"].double(),
+                          d["weight"].double(), d["bias"].double(), (1, 1), (1, 1), (1, 1),
+                          groups, dg)
+    check(out.cpu(), ref, torch.float32, f"nchw module g{groups} dg{dg}")
+
+
+def test_config1_nchw_fixture():
+    """BASELINE configs[0] through the module forward vs the committed fixture."""
+    import os
+    from modulated_deform_conv import modulated_deform_conv2d
+    fx = torch.load(os.path.join(os.path.dirname(__file__), "golden", "dcn_c1.pt"),
+                    weights_only=True)
+    d = inputs.dcn_inputs("dcn_c1")
+    for k, v in fx["checksums"].items():
+        assert abs(float(d[k].double().sum() + (d[k].double() ** 2).sum()) - v) < 1e-6 * abs(v)
+    out = modulated_deform_conv2d(d["x"].to(DEV), d["offset"].to(DEV), d["mask"].to(DEV),
+                                  d["weight"].to(DEV), d["bias"].to(DEV), 1, 1, 1, 1, 1)
+    torch.cuda.synchronize()
+    check(out.cpu(), fx["out"], torch.float32, "config1")
+
+
+@pytest.mark.parametrize("cfg", ["dcn_res4", "dcn_res5"])
+def test_nchw_fp32_full_size(cfg):
+    from modulated_deform_conv import modulated_deform_conv2d
+    d = inputs.dcn_inputs(cfg)
+    out = modulated_deform_conv2d(d["x"].to(DEV), d["offset"].to(DEV), d["mask"].to(DEV),
+                                  d["weight"].to(DEV), None, 1, 1, 1, 1, 1)
+    torch.cuda.synchronize()
+    out = out.cpu()
+    b = d["x"].shape[0] - 1
+    ref = od.forward_nchw(d["x"][b:].double(), d["offset"][b:].double(),
+                          d["mask"][b:].double(), d["weight"].double(), None, (1, 1), (1, 1),
+                          (1, 1))
+    check(out[b:], ref, torch.float32, f"{cfg} nchw fp32")
+
+
+@pytest.mark.parametrize("backend", ["fuse_c", "tilelang", "cuda"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["fp32", "fp16"])
+def test_pack_module(backend, dtype):
+    """Pack forward vs the oracle fed with the module's own offset-conv output (the
+    offset conv is a library convolution; the check covers the offset/mask split, the
+    sigmoid and the deformable kernel)."""
+    from modulated_deform_conv import ModulatedDeformConv2dPack
+    torch.manual_seed(0)
+    mod = ModulatedDeformConv2dPack(32, 48, 3, stride=1, padding=1, backend=backend)
+    with torch.no_grad():
+        mod.conv_offset.weight.normal_(0, 0.05)
+        mod.conv_offset.bias.normal_(0, 0.5)
+        mod.bias.normal_()
+    mod = mod.to(dtype).to(DEV)
+    x = torch.randn(2, 32, 14, 17).to(dtype).to(DEV)
+    with torch.no_grad():
+        out = mod(x)
+        y = mod.conv_offset(x)
+    torch.cuda.synchronize()
+    off, msk = od.split_y_nchw(y.double().cpu(), 9)
+    ref = od.forward_nchw(x.double().cpu(), off, msk, mod.weight.double().cpu(),
+                          mod.bias.double().cpu(), (1, 1), (1, 1), (1, 1))
+    check(out.cpu(), ref, dtype, f"pack {backend}")
+
+
+def test_dcn_split_nhwc_bn_relu_epilogue():
+    from modulated_deform_conv import dcn_split_nhwc as dsn
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(2, 10, 12, 32, generator=g)
+    w_off = 0.05 * torch.randn(27, 32, 3, 3, generator=g)
+    b_off = 0.3 * torch.randn(27, generator=g)
+    weight = 0.1 * torch.randn(64, 32, 3, 3, generator=g)
+    bias = torch.randn(64, generator=g)
+    scale = 0.5 + torch.rand(64, generator=g)
+    shift = torch.randn(64, generator=g)
+    out = dsn.dcn_split_nhwc(*(t.to(DEV) for t in (x, w_off, b_off, weight, bias)), 1, 1, 1,
+                             scale.to(DEV), shift.to(DEV), True)
+    torch.cuda.synchronize()
+    y = F.conv2d(x.double().permute(0, 3, 1, 2), w_off.double(), b_off.double(), 1, 1, 1)
+    off, msk = od.split_y_nhwc(y.permute(0, 2, 3, 1), 9)
+    conv = od.forward_nhwc(x.double(), off, msk, weight.double(), bias.double(), 1, 1, 1)
+    ref = torch.relu(conv * scale.double() + shift.double())
+    check(out.cpu(), ref, torch.float32, "bn relu")

@@ -1,0 +1,162 @@
+"""MSDA forward on the GPU vs the float64 CPU oracle (oracle/msda.py), through the
+reference-shaped API (msda_opt2.ms_deform_attn_forward -> _modulated_deform_conv_ext
+.forward -> libbevk.so bevk_msda_forward).
+
+Full-size BASELINE configurations run whole on the GPU and are checked on a random
+subset of queries (each query's output depends only on its own locations/weights), plus
+size-independent properties over the whole output (linearity in value and in attn)."""
+import pytest
+import torch
+
+from _tol import check
+from oracle import inputs
+from oracle import msda as om
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+
+
+def _api():
+    import msda_opt2
+    return msda_opt2
+
+
+def _run(d, dtype, **kw):
+    dev = torch.device("cuda")
+    out = _api().ms_deform_attn_forward(
+        d["value"].to(dtype).to(dev), d["spatial_shapes"].to(dev),
+        d["level_start_index"].to(dev), d["sampling_loc"].to(dtype).to(dev),
+        d["attn_weight"].to(dtype).to(dev), **kw)
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+def _ref(d, dtype, q_idx=None):
+    """Oracle on the dtype-rounded inputs, in float64; optionally on a query subset."""
+    v = d["value"].to(dtype).double()
+    loc = d["sampling_loc"].to(dtype).double()
+    att = d["attn_weight"].to(dtype).double()
+    if q_idx is not None:
+        loc = loc[:, q_idx]
+        att = att[:, q_idx]
+    return om.forward(v, d["spatial_shapes"], d["level_start_index"], loc, att)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=["fp32", "fp16", "bf16"])
+@pytest.mark.parametrize("cfg", ["msda_detr", "msda_tsa", "msda_sca"])
+def test_configs_reduced(cfg, dtype):
+    d = inputs.msda_inputs(cfg, scale_q=0.02)
+    out = _run(d, dtype)
+    assert out.dtype == dtype
+    check(out, _ref(d, dtype), dtype, f"{cfg} {dtype}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=["fp32", "fp16", "bf16"])
+@pytest.mark.parametrize("cfg", ["msda_detr", "msda_tsa", "msda_sca"])
+def test_configs_full_size(cfg, dtype):
+    d = inputs.msda_inputs(cfg)
+    out = _run(d, dtype)
+    nq = d["sampling_loc"].shape[1]
+    g = torch.Generator().manual_seed(123)
+    q_idx = torch.randperm(nq, generator=g)[:400].sort().values
+    q_idx = torch.cat([q_idx, torch.tensor([0, nq - 1])]).unique()
+    check(out[:, q_idx], _ref(d, dtype, q_idx), dtype, f"{cfg} full {dtype}")
+
+
+def test_sca_full_linearity():
+    """Whole-output properties at the full SCA size: out is linear in value and in attn."""
+    d = inputs.msda_inputs("msda_sca")
+    base = _run(d, torch.float32)
+    d2 = dict(d, value=d["value"] * 2.0)
+    torch.testing.assert_close(_run(d2, torch.float32), base * 2.0, rtol=1e-6, atol=1e-6)
+    d3 = dict(d, attn_weight=d["attn_weight"] * 0.5)
+    torch.testing.assert_close(_run(d3, torch.float32), base * 0.5, rtol=1e-6, atol=1e-6)
+    assert torch.isfinite(base).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.float64],
+                         ids=["fp32", "fp16", "fp64"])
+def test_force_generic(dtype):
+    d = inputs.msda_inputs("msda_sca", scale_q=0.01, batch=2)
+    out = _run(d, dtype, force_generic=True)
+    check(out, _ref(d, dtype), dtype, "generic")
+
+
+@pytest.mark.parametrize("geom", [
+    # batch, shapes, num_query, heads, head_dim, points
+    (2, [(7, 9), (4, 5), (2, 3)], 33, 4, 32, 5),      # D=32, runtime L/P
+    (1, [(11, 13)], 17, 8, 16, 3),                     # D=16
+    (3, [(6, 7), (3, 4)], 25, 2, 64, 2),               # D=64
+    (2, [(5, 5), (9, 4)], 9, 3, 128, 4),               # D=128, odd heads
+    (2, [(8, 6)], 13, 5, 24, 3),                       # D=24 -> generic kernel
+    (1, [(1, 1), (2, 1)], 5, 8, 32, 8),                # 1-pixel levels
+])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_geometries(geom, dtype):
+    b, shapes, nq, nh, hd, npnt = geom
+    d = inputs.msda_random(b, shapes, nq, nh, hd, npnt, seed=7, loc_lo=-0.3, loc_hi=1.3)
+    out = _run(d, dtype)
+    check(out, _ref(d, dtype), dtype, f"geom {geom}")
+
+
+def test_edge_locations():
+    """Pixel centres return the pixel, loc 0/1 give half-weight edges, far-out samples
+    are zero, loc exactly at the -1 / H gates."""
+    shapes = [(4, 6), (3, 5)]
+    b, nq, nh, hd, npnt = 1, 8, 8, 32, 4
+    d = inputs.msda_random(b, shapes, nq, nh, hd, npnt, seed=3)
+    loc = d["sampling_loc"]
+    loc[0, 0, :, 0, 0] = torch.tensor([(2 + 0.5) / 6, (1 + 0.5) / 4])   # pixel centre
+    loc[0, 1, :, :, :] = 0.0                                           # corner (x=0, y=0)
+    loc[0, 2, :, :, :] = 1.0                                           # corner (x=1, y=1)
+    loc[0, 3, :, :, :] = 5.0                                           # far outside
+    loc[0, 4, :, :, :] = -5.0
+    loc[0, 5, :, 0, :, 1] = -0.5 / 4                                   # h_im exactly -1
+    loc[0, 6, :, 0, :, 0] = (6 + 0.5) / 6                              # w_im exactly W
+    out = _run(d, torch.float32)
+    check(out, _ref(d, torch.float32), torch.float32, "edges")
+    assert torch.all(out[0, 3] == 0) and torch.all(out[0, 4] == 0)
+
+
+def test_empty_and_single():
+    d = inputs.msda_random(2, [(3, 3)], 1, 8, 32, 4, seed=5)
+    check(_run(d, torch.float32), _ref(d, torch.float32), torch.float32, "Lq=1")
+    d0 = inputs.msda_random(2, [(3, 3)], 1, 8, 32, 4, seed=5)
+    d0["sampling_loc"] = d0["sampling_loc"][:, :0].contiguous()
+    d0["attn_weight"] = d0["attn_weight"][:, :0].contiguous()
+    out = _run(d0, torch.float32)
+    assert out.shape == (2, 0, 256)
+
+
+def test_im2col_step_contract():
+    d = inputs.msda_random(6, [(5, 7), (3, 4)], 11, 8, 32, 4, seed=9)
+    ref = _ref(d, torch.float32)
+    for step in (1, 2, 3, 6, 64):
+        check(_run(d, torch.float32, im2col_step=step), ref, torch.float32, f"step {step}")
+    with pytest.raises(RuntimeError, match="batch must divide im2col_step"):
+        _run(d, torch.float32, im2col_step=4)
+
+
+def test_on_side_stream():
+    """The kernel is enqueued on torch's current stream."""
+    d = inputs.msda_inputs("msda_tsa", scale_q=0.01)
+    dev = torch.device("cuda")
+    args = [d["value"].to(dev), d["spatial_shapes"].to(dev), d["level_start_index"].to(dev),
+            d["sampling_loc"].to(dev), d["attn_weight"].to(dev)]
+    s = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        out = _api().ms_deform_attn_forward(*args)
+    s.synchronize()
+    check(out.cpu(), _ref(d, torch.float32), torch.float32, "side stream")
+
+
+def test_non_contiguous_rejected():
+    d = inputs.msda_random(2, [(3, 3)], 4, 8, 32, 4, seed=5)
+    dev = torch.device("cuda")
+    v = d["value"].to(dev).transpose(1, 2)
+    with pytest.raises(RuntimeError, match="value must be contiguous"):
+        _api().ms_deform_attn_forward(v, d["spatial_shapes"].to(dev),
+                                      d["level_start_index"].to(dev),
+                                      d["sampling_loc"].to(dev), d["attn_weight"].to(dev))
