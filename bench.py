@@ -1,0 +1,322 @@
+"""Benchmark of the bev-kernels hot paths on one MI355X.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--warm] [--no-configs]
+                  [--no-cpu-baseline] [--only NAME]
+
+Prints ONE JSON line. The headline ("step") is one MSDA forward at the BEVFormer
+spatial-cross-attention shape (6 cameras, 4 levels, Len_in 30825,
+Len_q 10000, 8 heads x 32, 8 points), fp32, with inputs resident in HBM:
+  value      algorithmic GB/s = compulsory bytes (value + sampling_loc + attn_weight
+             read once, output written once: 435.15 MB) / mean kernel time
+  roofline   the same figure against 8 TB/s, kernel time from HIP events on the stream
+             the kernel runs on; `traffic` from the committed rocprofv3 counter summary
+  secondary  the fused NHWC DCNv2 res4 fp16 forward in MFMA TFLOP/s (2*M*K*Cout flops)
+  configs    every BASELINE configuration x dtype: us, GB/s or TFLOP/s, roofline fraction
+  cpu_baseline  the CPU oracle (grid_sample form) on the same SCA workload, timed on the
+             host cores of this machine
+Cold-cache protocol (default): a 1 GiB buffer is overwritten before every timed launch so
+L2 and the 256 MB MALL hold none of the inputs; --warm times back-to-back launches.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "bev-kernels_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = {"fp16": 2516.6, "bf16": 2516.6, "fp32": 157.3}
+METRIC = ("MSDA fwd µs + HBM GB/s (BEVFormer SCA); DCNv2 NHWC fwd µs + MFMA TFLOP/s")
+COUNTER_FILE = os.path.join(ROOT, "profiles", "msda_sca_fp32_counters.txt")
+
+
+def parse_args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warm", action="store_true", help="no cache flush between launches")
+    ap.add_argument("--no-configs", action="store_true", help="headline lines only")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", default=None, help="run one configuration (profiling)")
+    return ap.parse_args()
+
+
+def dtype_of(name):
+    import torch
+    return {"fp32": torch.float32, "fp16": torch.float16, "bf16": torch.bfloat16}[name]
+
+
+class Timer:
+    """Times launches of `fn` with HIP events on torch's current stream (the stream the
+    library enqueues on), optionally after a cache-flushing write."""
+
+    def __init__(self, cold: bool):
+        import torch
+        self.torch = torch
+        self.cold = cold
+        self.flush_buf = torch.empty(1 << 28, dtype=torch.float32, device="cuda") if cold else None
+
+    def run(self, fn, steps, warmup):
+        torch = self.torch
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        times = []
+        t0 = time.perf_counter()
+        for i in range(steps):
+            if self.cold:
+                self.flush_buf.fill_(float(i))
+            s = torch.cuda.Event(enable_timing=True)
+            e = torch.cuda.Event(enable_timing=True)
+            s.record()
+            fn()
+            e.record()
+            times.append((s, e))
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) / steps
+        us = [s.elapsed_time(e) * 1e3 for s, e in times]
+        return statistics.mean(us), statistics.median(us), wall * 1e6
+
+
+def msda_case(name, dtype, cache):
+    """Device inputs and the kernel call of one MSDA configuration."""
+    import torch
+    import _modulated_deform_conv_ext as ext
+    from oracle import inputs
+    if name not in cache:
+        cache[name] = inputs.msda_inputs(name)
+    d = cache[name]
+    dev = torch.device("cuda")
+    v = d["value"].to(dtype).to(dev)
+    ss = d["spatial_shapes"].to(dev)
+    lsi = d["level_start_index"].to(dev)
+    loc = d["sampling_loc"].to(dtype).to(dev)
+    att = d["attn_weight"].to(dtype).to(dev)
+    es = v.element_size()
+    nbytes = (v.numel() + loc.numel() + att.numel() + v.shape[0] * loc.shape[1] * v.shape[2]
+              * v.shape[3]) * es
+    return (lambda: ext.forward(v, ss, lsi, loc, att, 64, False)), nbytes
+
+
+def dcn_fused_case(name, dtype, cache):
+    """Fused NHWC kernel call (pre-permuted weight) of one DCN configuration."""
+    import torch
+    import _modulated_deform_conv_ext as ext
+    from oracle import inputs
+    if name not in cache:
+        cache[name] = inputs.nchw_to_nhwc(inputs.dcn_inputs(name))
+    d = cache[name]
+    dev = torch.device("cuda")
+    x = d["x"].to(dtype).to(dev)
+    off = d["offset"].to(dtype).to(dev)
+    msk = d["mask"].to(dtype).to(dev)
+    w_kc = d["weight"].permute(0, 2, 3, 1).contiguous().to(dtype).to(dev)
+    B, H, W, C = x.shape
+    Cout = w_kc.shape[0]
+    out = torch.empty(B, H, W, Cout, dtype=dtype, device=dev)
+    flops = 2.0 * B * H * W * 9 * C * Cout
+    return (lambda: ext.dcn_fused_fwd_nhwc(x, off, msk, w_kc, None, B, C, H, W, H, W, Cout, 3, 3,
+                                           1, 1, 1, 1, 1, 1, out)), flops
+
+
+def dcn_nchw_case(name, cache):
+    """Module-level fp32 NCHW forward (modulated_deform_conv2d)."""
+    import torch
+    from modulated_deform_conv import modulated_deform_conv2d
+    from oracle import inputs
+    key = name + "_nchw"
+    if key not in cache:
+        cache[key] = inputs.dcn_inputs(name)
+    d = cache[key]
+    dev = torch.device("cuda")
+    x, off, msk, w = (d[k].to(dev) for k in ("x", "offset", "mask", "weight"))
+    B, C, H, W = x.shape
+    flops = 2.0 * B * H * W * 9 * C * w.shape[0]
+    return (lambda: modulated_deform_conv2d(x, off, msk, w, None, 1, 1, 1, 1, 1)), flops
+
+
+def read_counters():
+    """FETCH_SIZE / WRITE_SIZE per dispatch of the SCA fp32 kernel and of a plain copy of
+    known size, from the committed rocprofv3 summary (None if absent)."""
+    if not os.path.exists(COUNTER_FILE):
+        return None
+    vals = {}
+    with open(COUNTER_FILE) as f:
+        for line in f:
+            line = line.strip()
+            if "=" in line and not line.startswith("#"):
+                k, v = line.split("=", 1)
+                try:
+                    vals[k.strip()] = float(v.split()[0])
+                except ValueError:
+                    pass
+    try:
+        copy_bytes = vals["copy_bytes_each_way"]
+        rd_scale = copy_bytes / (vals["copy_FETCH_SIZE_KiB"] * 1024.0)
+        wr_scale = copy_bytes / (vals["copy_WRITE_SIZE_KiB"] * 1024.0)
+        traffic = (vals["kernel_FETCH_SIZE_KiB"] * 1024.0 * rd_scale
+                   + vals["kernel_WRITE_SIZE_KiB"] * 1024.0 * wr_scale)
+        return traffic
+    except KeyError:
+        return None
+
+
+def cpu_baseline(cache):
+    """The CPU oracle (grid_sample form of MSDA) on the full SCA fp32 workload, all host
+    threads; 1 warm-up + median of 3."""
+    import torch
+    from oracle import inputs
+    from oracle import msda as om
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    if "msda_sca" not in cache:
+        cache["msda_sca"] = inputs.msda_inputs("msda_sca")
+    d = cache["msda_sca"]
+    nbytes = 4 * (d["value"].numel() + d["sampling_loc"].numel() + d["attn_weight"].numel()
+                  + 6 * 10000 * 256)
+    om.forward_grid_sample(**d)
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        om.forward_grid_sample(**d)
+        ts.append(time.perf_counter() - t0)
+    t = statistics.median(ts)
+    cpu = platform.processor() or platform.machine()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": cores,
+            "kind": "port",
+            "sample": f"full SCA workload (6x10000x8 queries, fp32) through the oracle's "
+                      f"grid_sample form, torch CPU, {cores} threads, median of 3 = "
+                      f"{t * 1e3:.0f} ms, {cpu}"}
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the operators shard over cameras/batch with no communication; see DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import _bevk
+    assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    _bevk.lib()
+    torch.backends.cuda.matmul.allow_tf32 = False
+    timer = Timer(cold=not args.warm)
+    cache = {}
+    steps, warmup = args.steps, args.warmup
+
+    if args.only:
+        kind, _, rest = args.only.partition(":")
+        name, _, dt = rest.partition(":")
+        if kind == "msda":
+            fn, _ = msda_case(name, dtype_of(dt), cache)
+        elif kind == "dcn":
+            fn, _ = dcn_fused_case(name, dtype_of(dt), cache)
+        elif kind == "dcn_nchw":
+            fn, _ = dcn_nchw_case(name, cache)
+        elif kind == "copy":
+            # plain copy of known size: the counter calibration reference
+            n = int(name) if name else 256 << 20
+            src = torch.empty(n // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+            dst = torch.empty_like(src)
+            fn = lambda: dst.copy_(src)  # noqa: E731
+        else:
+            raise SystemExit(f"unknown --only {args.only}")
+        mean_us, med_us, wall_us = timer.run(fn, steps, warmup)
+        print(json.dumps({"only": args.only, "mean_us": round(mean_us, 2),
+                          "median_us": round(med_us, 2)}), flush=True)
+        return
+
+    # ---- headline: MSDA SCA fp32 -------------------------------------------------------
+    fn, nbytes = msda_case("msda_sca", torch.float32, cache)
+    mean_us, med_us, wall_us = timer.run(fn, steps, warmup)
+    gbs = nbytes / (mean_us * 1e-6) / 1e9
+    traffic = read_counters()
+    warm_us = Timer(cold=False).run(fn, steps, warmup)[0]
+
+    # ---- secondary: DCN res4 fp16 fused -----------------------------------------------
+    dfn, flops = dcn_fused_case("dcn_res4", torch.float16, cache)
+    d_mean, d_med, _ = timer.run(dfn, steps, warmup)
+    tflops = flops / (d_mean * 1e-6) / 1e12
+
+    line = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(mean_us / 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (seeded BASELINE distributions)",
+        "config": {"workload": "MSDA forward, BEVFormer spatial cross-attention (BASELINE "
+                               "configs[4]): B=6 cameras, 4 levels (116x200, 58x100, 29x50, "
+                               "15x25), Len_in=30825, Len_q=10000, 8 heads x 32, 8 points",
+                   "cache": "warm" if args.warm else "cold (1 GiB overwrite before each launch)",
+                   "median_us": round(med_us, 2), "warm_mean_us": round(warm_us, 2),
+                   "algorithmic_bytes": nbytes},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": None if traffic is None else round(traffic)},
+        "secondary": {
+            "metric": "DCNv2 NHWC fused forward, res4 (B=6, 256->256, 58x100), fp16",
+            "us": round(d_mean, 2), "value": round(tflops, 2), "unit": "TFLOP/s",
+            "roofline": {"bound": "mfma", "achieved": round(tflops, 2),
+                         "peak": MFMA_PEAK_TFLOPS["fp16"], "unit": "TFLOP/s",
+                         "frac": round(tflops / MFMA_PEAK_TFLOPS["fp16"], 4),
+                         "traffic": None}},
+    }
+
+    if not args.no_configs:
+        rows = []
+        for name in ("msda_sca", "msda_tsa", "msda_detr"):
+            for dt in ("fp32", "fp16", "bf16"):
+                f, nb = msda_case(name, dtype_of(dt), cache)
+                m, _, _ = timer.run(f, max(10, steps // 2), 3)
+                g = nb / (m * 1e-6) / 1e9
+                rows.append({"config": name, "dtype": dt, "us": round(m, 2),
+                             "GB/s": round(g, 1), "frac_hbm": round(g / HBM_PEAK_GBS, 4)})
+        for name in ("dcn_res4", "dcn_res5"):
+            for dt in ("fp16", "bf16", "fp32"):
+                f, fl = dcn_fused_case(name, dtype_of(dt), cache)
+                m, _, _ = timer.run(f, max(10, steps // 2), 3)
+                tf = fl / (m * 1e-6) / 1e12
+                rows.append({"config": name + "_nhwc_fused", "dtype": dt, "us": round(m, 2),
+                             "TFLOP/s": round(tf, 2),
+                             "frac_mfma": round(tf / MFMA_PEAK_TFLOPS[dt], 4)})
+            f, fl = dcn_nchw_case(name, cache)
+            m, _, _ = timer.run(f, max(10, steps // 2), 3)
+            tf = fl / (m * 1e-6) / 1e12
+            rows.append({"config": name + "_nchw_module", "dtype": "fp32", "us": round(m, 2),
+                         "TFLOP/s": round(tf, 2),
+                         "frac_mfma": round(tf / MFMA_PEAK_TFLOPS["fp32"], 4)})
+        line["configs"] = rows
+
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(cache)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
