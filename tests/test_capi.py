@@ -1,0 +1,108 @@
+"""libbevk.so's C ABI on the CPU: the library loads without a GPU, exports every entry
+point include/bev_kernels.h declares, and rejects bad arguments (status code + message)
+before any device work. No call here reaches a HIP launch."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import _bevk
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "bev_kernels.h")
+INVALID, UNSUPPORTED = 1, 2
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(bevk_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_matches_binding_table():
+    assert declared_symbols() == sorted(_bevk.exported_symbols())
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(_bevk.library_path())
+    for name in declared_symbols():
+        assert hasattr(lib, name), f"{name} missing from {_bevk.library_path()}"
+
+
+def test_version():
+    assert _bevk.version().startswith("bevk ")
+
+
+def _err():
+    return _bevk.lib().bevk_last_error().decode()
+
+
+NULL = None
+
+
+def _nchw(entry, dtype=0, **kw):
+    a = dict(b=1, c=4, h=5, w=5, ho=5, wo=5, kh=3, kw=3, ph=1, pw=1, sh=1, sw=1, dh=1, dw=1, dg=1)
+    a.update(kw)
+    return getattr(_bevk.lib(), entry)(
+        dtype, NULL, NULL, NULL, a["b"], a["c"], a["h"], a["w"], a["ho"], a["wo"], a["kh"],
+        a["kw"], a["ph"], a["pw"], a["sh"], a["sw"], a["dh"], a["dw"], a["dg"], NULL, NULL)
+
+
+@pytest.mark.parametrize("entry", ["bevk_modulated_deformable_im2col",
+                                   "bevk_modulated_deformable_im2col_opt"])
+def test_nchw_validation(entry):
+    assert _nchw(entry, ho=4) == INVALID and "does not match" in _err()
+    assert _nchw(entry, dg=0) == INVALID and "deformable_group" in _err()
+    assert _nchw(entry, c=6, dg=4) == INVALID and "divisible" in _err()
+    assert _nchw(entry, sh=0) == INVALID
+    assert _nchw(entry, dtype=9) == INVALID and "dtype" in _err()
+    assert _nchw(entry) == INVALID and "null" in _err()   # valid sizes, no buffers
+    assert _nchw(entry, b=0) == 0                          # empty: nothing to do
+
+
+def _nhwc(dtype=0, last=18, dg=1, c=8, b=1):
+    return _bevk.lib().bevk_modulated_deformable_im2col_nhwc(
+        dtype, NULL, NULL, last, NULL, b, c, 5, 5, 5, 5, 3, 3, 1, 1, 1, 1, 1, 1, dg, NULL, NULL)
+
+
+def test_nhwc_validation():
+    assert _nhwc(dg=2) == INVALID and "deformable_group == 1" in _err()
+    assert _nhwc(last=20) == INVALID and "2T" in _err()
+    assert _nhwc() == INVALID and "null" in _err()
+    assert _nhwc(last=27) == INVALID and "null" in _err()
+    assert _nhwc(b=0) == 0
+
+
+def _fused(dtype=1, c=16, cout=8, last=18):
+    return _bevk.lib().bevk_dcn_fused_fwd_nhwc(
+        dtype, NULL, NULL, last, NULL, NULL, NULL, 1, c, 5, 5, 5, 5, cout, 3, 3, 1, 1, 1, 1, 1,
+        1, NULL, NULL)
+
+
+def test_fused_validation():
+    assert _fused(dtype=3) == UNSUPPORTED and "Double" in _err()
+    assert _fused(c=12) == UNSUPPORTED and "multiple of 8" in _err()     # fp16 needs C % 8
+    assert _fused(dtype=0, c=6) == UNSUPPORTED and "multiple of 4" in _err()
+    assert _fused(last=21) == INVALID
+    assert _fused() == INVALID and "null" in _err()
+    assert _fused(cout=0) == 0
+
+
+def _msda(step=64, b=2, nq=4, force=0):
+    return _bevk.lib().bevk_msda_forward(0, NULL, NULL, NULL, NULL, NULL, b, 10, 8, 32, 1, nq, 4,
+                                         step, force, NULL, NULL)
+
+
+def test_msda_validation():
+    assert _msda(step=0) == INVALID and "im2col_step" in _err()
+    assert _msda(b=6, step=4) == INVALID and "batch must divide im2col_step" in _err()
+    assert _msda() == INVALID and "null" in _err()
+    assert _msda(nq=0) == 0
+    assert _msda(b=0) == 0
+
+
+def test_call_raises_runtime_error_with_message():
+    with pytest.raises(RuntimeError, match="batch must divide im2col_step"):
+        _bevk.call("bevk_msda_forward", 0, NULL, NULL, NULL, NULL, NULL, 6, 10, 8, 32, 1, 4, 4,
+                   4, 0, NULL, NULL)
