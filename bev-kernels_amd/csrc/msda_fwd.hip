@@ -6,15 +6,22 @@
 //   -1 < h_im < H_l and -1 < w_im < W_l, and each of its four corners is zero outside
 //   the level. value[b, level_start[l] + y*W_l + x, h, c].
 //
-// Two kernels:
-//   * msda_wave_kernel: one wavefront owns UPW (b, q, head) units. Within a unit,
-//     G = D/VEC lanes cover the head_dim channels with VEC-wide (16 B) loads and the
-//     remaining lane groups take different (level, point) samples concurrently; the
-//     partial sums meet in a butterfly over the lane groups. Corner loads are buffer
-//     loads: an invalid corner gets an out-of-range offset and reads 0 without a
-//     memory request, so the zero padding is branch-free. Work is enumerated per
-//     (batch, head-group) slice and the slices are dealt to the 8 XCDs so each XCD's
-//     L2 holds one slice of `value` at a time.
+// Kernels:
+//   * msda_wave_kernel / msda_wave_lds_kernel: one wavefront owns UPW (b, q, head)
+//     units. G = D/VEC lanes cover the head_dim channels of one sample with 16-byte
+//     loads; the other lane groups take other (level, point) samples at the same time
+//     and the partial sums meet in a butterfly over the lane groups. All corner loads of
+//     a unit are issued before the first use. Corner loads are buffer loads: an invalid
+//     corner gets an out-of-range offset and reads 0 without a memory request, so the
+//     zero padding is branch-free.
+//     The _lds variant (many samples per unit) computes each sample's geometry once,
+//     in one lane, with the attention weight folded into the four corner weights, and
+//     shares it with the sample's lane group through LDS; the plain variant (few
+//     samples, or L/P known only at run time) lets every lane of the group compute it.
+//   * Work order: units are enumerated per (batch, head-group) slice, queries in order,
+//     slices one after the other. All 8 XCDs then work on the same slice at the same
+//     time: each XCD's L2 holds one slice (3.95 MB for fp32 SCA) and a line one XCD
+//     pulls from HBM is a MALL hit for the others.
 //   * msda_generic_kernel: one thread per output element, any shape and dtype.
 #include "bevk_common.h"
 #include "bevk_launch.h"
@@ -47,7 +54,6 @@ struct WaveParams {
   int heads_per_slice;    // heads sharing one slice (2 when two heads fill a 128 B line)
   int slices_per_batch;   // NH / heads_per_slice
   int blocks_per_slice;   // ceil(NQ * heads_per_slice / units_per_block)
-  int remap;              // deal slices round-robin over the 8 XCDs
   uint32_t batch_bytes;   // bytes of value per batch (buffer range; < 2^31)
 };
 
@@ -67,19 +73,9 @@ __global__ void __launch_bounds__(kBlock) msda_wave_kernel(const WaveParams p) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
 
-  // block -> (slice, chunk). With remap, consecutive blocks of one XCD (bid % 8) walk
-  // the same slice, so that XCD's L2 only ever holds that slice's value lines.
-  const int bid = blockIdx.x;
-  int slice, chunk;
-  if (p.remap) {
-    const int xcd = bid & 7;
-    const int j = bid >> 3;
-    slice = (j / p.blocks_per_slice) * 8 + xcd;
-    chunk = j - (j / p.blocks_per_slice) * p.blocks_per_slice;
-  } else {
-    slice = bid / p.blocks_per_slice;
-    chunk = bid - slice * p.blocks_per_slice;
-  }
+  // block -> (slice, chunk): slices one after the other, queries in order.
+  const int slice = blockIdx.x / p.blocks_per_slice;
+  const int chunk = blockIdx.x - slice * p.blocks_per_slice;
   const int b = slice / p.slices_per_batch;
   const int hg = slice - b * p.slices_per_batch;
   const int local = (chunk * kWavesPerBlock + wave) * UPW + lane / LPU;
@@ -224,6 +220,120 @@ __global__ void __launch_bounds__(kBlock) msda_wave_kernel(const WaveParams p) {
   }
 }
 
+// Geometry of one sample, shared through LDS: corner weights (bilinear x attention,
+// zero for invalid corners) and corner byte offsets (out-of-range sentinel if invalid).
+struct SampleGeo {
+  float w[4];
+  uint32_t o[4];
+};
+
+// Compile-time L/P with UPW * L * P <= 64: lane i of the wave computes sample i of the
+// wave's UPW units, then every lane group gathers its samples' corners.
+template <typename T, int D, int VEC, int NL, int NP, int UPW>
+__global__ void __launch_bounds__(kBlock) msda_wave_lds_kernel(const WaveParams p) {
+  using V = Vec<T, VEC>;
+  constexpr int G = D / VEC, LPU = kWave / UPW, SPU = LPU / G, NS = NL * NP;
+  constexpr int NITER = (NS + SPU - 1) / SPU;
+  static_assert(UPW * NS <= kWave && G >= 1 && (kWave % (G * UPW)) == 0, "bad lane split");
+  __shared__ SampleGeo geo[kWavesPerBlock][UPW * NS];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int slice = blockIdx.x / p.blocks_per_slice;
+  const int chunk = blockIdx.x - slice * p.blocks_per_slice;
+  const int b = slice / p.slices_per_batch;
+  const int hg = slice - b * p.slices_per_batch;
+  const int pos_stride = p.NH * D;
+  const uint32_t kOOB = p.batch_bytes;
+
+  // Phase 1: one lane per (unit, sample).
+  if (lane < UPW * NS) {
+    const int u = lane / NS, s = lane - (lane / NS) * NS;
+    const int local = (chunk * kWavesPerBlock + wave) * UPW + u;
+    const int q = local / p.heads_per_slice;
+    const int h = hg * p.heads_per_slice + (local - q * p.heads_per_slice);
+    const bool active = q < p.NQ;
+    const int qc = active ? q : p.NQ - 1;
+    const int64_t unit = ((int64_t)b * p.NQ + qc) * p.NH + h;
+    const int l = s / NP;
+    const int Hl = (int)p.shapes[2 * l], Wl = (int)p.shapes[2 * l + 1], Sl = (int)p.lsi[l];
+    float x, y;
+    load_loc<T>(static_cast<const T *>(p.loc) + (unit * NS + s) * 2, x, y);
+    const float a = static_cast<float>(load_nt(static_cast<const T *>(p.attn) + unit * NS + s));
+    const float him = y * (float)Hl - 0.5f, wim = x * (float)Wl - 0.5f;
+    SampleGeo sg;
+    sg.w[0] = sg.w[1] = sg.w[2] = sg.w[3] = 0.f;
+    sg.o[0] = sg.o[1] = sg.o[2] = sg.o[3] = kOOB;
+    if (active && him > -1.f && wim > -1.f && him < (float)Hl && wim < (float)Wl) {
+      const float fh = floorf(him), fw = floorf(wim);
+      const int hl = (int)fh, wl = (int)fw;
+      const float lh = him - fh, lw = wim - fw, hh = 1.f - lh, hw = 1.f - lw;
+      const uint32_t es = (uint32_t)sizeof(T);
+      const uint32_t base = (uint32_t)((Sl + hl * Wl + wl) * pos_stride + h * D) * es;
+      const uint32_t dx = (uint32_t)pos_stride * es, dy = (uint32_t)(Wl * pos_stride) * es;
+      const bool y0 = hl >= 0, y1 = hl + 1 <= Hl - 1, x0 = wl >= 0, x1 = wl + 1 <= Wl - 1;
+      if (y0 && x0) { sg.w[0] = hh * hw * a; sg.o[0] = base; }
+      if (y0 && x1) { sg.w[1] = hh * lw * a; sg.o[1] = base + dx; }
+      if (y1 && x0) { sg.w[2] = lh * hw * a; sg.o[2] = base + dy; }
+      if (y1 && x1) { sg.w[3] = lh * lw * a; sg.o[3] = base + dy + dx; }
+    }
+    geo[wave][lane] = sg;
+  }
+  // The wave reads what its own lanes wrote: order the LDS accesses within the wave.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // Phase 2: lane group gi of unit u gathers samples gi, gi + SPU, ...
+  const int u = lane / LPU, ul = lane & (LPU - 1), gi = ul / G, c0 = (ul - gi * G) * VEC;
+  const int local = (chunk * kWavesPerBlock + wave) * UPW + u;
+  const int q = local / p.heads_per_slice;
+  const int h = hg * p.heads_per_slice + (local - q * p.heads_per_slice);
+  const T *vbase = static_cast<const T *>(p.value) + (int64_t)b * p.S * p.NH * D;
+  const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(vbase, p.batch_bytes);
+  const uint32_t cb = (uint32_t)(c0 * sizeof(T));
+  V v[NITER][4];
+  float w[NITER][4];
+#pragma unroll
+  for (int it = 0; it < NITER; ++it) {
+    const int s = it * SPU + gi;
+    if (NS % SPU == 0 || s < NS) {
+      const SampleGeo sg = geo[wave][u * NS + s];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        w[it][c] = sg.w[c];
+        v[it][c] = buffer_load_vec<T, VEC>(rsrc, sg.o[c] == kOOB ? kOOB : sg.o[c] + cb);
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        w[it][c] = 0.f;
+        v[it][c] = buffer_load_vec<T, VEC>(rsrc, kOOB);
+      }
+    }
+  }
+  float acc[VEC];
+#pragma unroll
+  for (int k = 0; k < VEC; ++k) acc[k] = 0.f;
+#pragma unroll
+  for (int it = 0; it < NITER; ++it)
+#pragma unroll
+    for (int k = 0; k < VEC; ++k)
+      acc[k] += w[it][0] * (float)v[it][0].v[k] + w[it][1] * (float)v[it][1].v[k] +
+                w[it][2] * (float)v[it][2].v[k] + w[it][3] * (float)v[it][3].v[k];
+#pragma unroll
+  for (int m = G; m < LPU; m <<= 1)
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) acc[k] += __shfl_xor(acc[k], m);
+  if (q < p.NQ && gi == 0) {
+    V o;
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) o.v[k] = from_acc<T>(acc[k]);
+    const int64_t unit = ((int64_t)b * p.NQ + q) * p.NH + h;
+    store_vec_nt<T, VEC>(static_cast<T *>(p.out) + unit * D + c0, o);
+  }
+}
+
 // One thread per output element (b, q, h, c); any heads / channels / levels / points.
 template <typename T>
 __global__ void __launch_bounds__(kBlock) msda_generic_kernel(
@@ -302,7 +412,13 @@ template <typename T, int D, int NL, int NP>
 hipError_t launch_wave_t(const MsdaArgs &a, hipStream_t stream) {
   constexpr int VEC = 16 / sizeof(T) < D ? 16 / sizeof(T) : D;
   constexpr int G = D / VEC;
-  constexpr int UPW = (NL > 0 && NP > 0) ? upw_for(G, NL * NP) : 1;
+  constexpr bool kStatic = NL > 0 && NP > 0;
+  // Many samples per unit: shared geometry through LDS, two units per wave when their
+  // samples fit one geometry pass. Few samples: per-lane geometry, units packed so the
+  // wave's lanes are all busy.
+  constexpr bool kLds = kStatic && NL * NP >= 16 && NL * NP <= kWave;
+  constexpr int UPW = kLds ? (2 * NL * NP <= kWave && kWave % (2 * G) == 0 ? 2 : 1)
+                           : (kStatic ? upw_for(G, NL * NP) : 1);
   WaveParams p;
   p.value = a.value;
   p.shapes = a.spatial_shapes;
@@ -326,12 +442,15 @@ hipError_t launch_wave_t(const MsdaArgs &a, hipStream_t stream) {
   const int64_t units_per_slice = (int64_t)a.num_query * hps;
   p.blocks_per_slice = (int)((units_per_slice + units_per_block - 1) / units_per_block);
   const int64_t slices = (int64_t)a.batch * p.slices_per_batch;
-  p.remap = (slices % 8) == 0 ? 1 : 0;
   p.batch_bytes = (uint32_t)((int64_t)a.spatial_size * a.num_heads * D * sizeof(T));
   const int64_t blocks = slices * p.blocks_per_slice;
   if (blocks == 0) return hipSuccess;
-  hipLaunchKernelGGL((msda_wave_kernel<T, D, VEC, NL, NP, UPW>), dim3((unsigned)blocks),
-                     dim3(kBlock), 0, stream, p);
+  if constexpr (kLds)
+    hipLaunchKernelGGL((msda_wave_lds_kernel<T, D, VEC, NL, NP, UPW>), dim3((unsigned)blocks),
+                       dim3(kBlock), 0, stream, p);
+  else
+    hipLaunchKernelGGL((msda_wave_kernel<T, D, VEC, NL, NP, UPW>), dim3((unsigned)blocks),
+                       dim3(kBlock), 0, stream, p);
   return hipGetLastError();
 }
 
