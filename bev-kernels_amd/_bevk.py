@@ -34,9 +34,14 @@ _SIGNATURES = {
     "bevk_modulated_deformable_im2col": [_i, _vp, _vp, _vp] + [_i] * 15 + [_vp, _vp],
     "bevk_modulated_deformable_im2col_opt": [_i, _vp, _vp, _vp] + [_i] * 15 + [_vp, _vp],
     "bevk_modulated_deformable_im2col_nhwc": [_i, _vp, _vp, _i, _vp] + [_i] * 15 + [_vp, _vp],
+    "bevk_dcn_packed_weight_bytes": [_i] * 5,
+    "bevk_dcn_pack_weight": [_i, _vp] + [_i] * 4 + [_vp, _vp],
     "bevk_dcn_fused_fwd_nhwc": [_i, _vp, _vp, _i, _vp, _vp, _vp] + [_i] * 15 + [_vp, _vp],
     "bevk_msda_forward": [_i, _vp, _vp, _vp, _vp, _vp] + [_i] * 9 + [_vp, _vp],
 }
+
+# entry points that return a value instead of a bevk_status
+_RESTYPES = {"bevk_dcn_packed_weight_bytes": ctypes.c_int64}
 
 _lib = None
 _lock = threading.Lock()
@@ -79,7 +84,7 @@ def lib() -> ctypes.CDLL:
         handle.bevk_version.argtypes = []
         for name, args in _SIGNATURES.items():
             fn = getattr(handle, name)
-            fn.restype = ctypes.c_int
+            fn.restype = _RESTYPES.get(name, ctypes.c_int)
             fn.argtypes = args
         _lib = handle
         return _lib

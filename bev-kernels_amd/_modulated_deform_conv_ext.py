@@ -3,7 +3,7 @@
 Same module name, function names and argument order as the reference's pybind11
 module (naotic/bev-kernels csrc/binding.cpp:142-191), plus the MSDA ``forward`` /
 ``backward`` of its MUSA module (csrc_musa/msda/binding_musa.mu:545-557) and the fused
-NHWC entry point ``dcn_fused_fwd_nhwc``. Outputs are caller-allocated, as in the
+NHWC entry point ``dcn_fused_fwd_nhwc`` with its weight packer ``dcn_pack_weight``. Outputs are caller-allocated, as in the
 reference (MSDA forward allocates and returns its output).
 
 Unlike the reference launchers these wrappers check device, contiguity, dtype and
@@ -36,6 +36,8 @@ __all__ = [
     "modulated_deformable_col2im_fused_smem_nhwc_cuda",
     "modulated_deformable_col2im_perelem_nhwc_cuda",
     "modulated_deformable_col2im_perelem_smem_nhwc_cuda",
+    "dcn_packed_weight_numel",
+    "dcn_pack_weight",
     "dcn_fused_fwd_nhwc",
     "forward",
     "backward",
@@ -120,37 +122,75 @@ def modulated_deformable_im2col_nhwc_cuda(data_im, data_offset, data_mask, batch
             _b.stream_of(data_im))
 
 
-def dcn_fused_fwd_nhwc(data_im, data_offset, data_mask, weight_kc, bias, batch_size, channels,
-                       height_im, width_im, height_col, width_col, channels_out, kernel_h,
-                       kernel_w, pad_h, pad_w, stride_h, stride_w, dilation_h, dilation_w, out):
+def dcn_packed_weight_numel(dtype, channels_out, kernel_h, kernel_w, channels):
+    """Elements of the packed weight dcn_fused_fwd_nhwc takes for this shape and dtype."""
+    code = _b._DTYPE_CODES.get(dtype)
+    if code is None or code == _b.BEVK_F64:
+        raise RuntimeError(f"dcn_pack_weight: dtype {dtype} is not supported")
+    nbytes = _b.lib().bevk_dcn_packed_weight_bytes(code, channels_out, kernel_h, kernel_w,
+                                                    channels)
+    if nbytes < 0:
+        raise RuntimeError("dcn_pack_weight: invalid weight shape")
+    return nbytes // torch.empty((), dtype=dtype).element_size()
+
+
+def dcn_pack_weight(weight, packed=None):
+    """Module weight [Cout, C, kh, kw] -> the fused kernel's packed weight (1-D, same dtype).
+
+    fp32: [Cout, kh, kw, C]; fp16 / bf16: MFMA-fragment blocks of 32 output channels x 16
+    reduction elements (k = (i*kw + j)*C + c), zero padded. The reference permutes the
+    weight to [kh, kw, C, Cout] on every call (fused_tl.py:500-510); here it is packed
+    once per weight and reused."""
+    fn = "dcn_pack_weight"
+    if weight.dim() != 4:
+        raise RuntimeError(f"{fn}: weight must be [Cout, C, kh, kw], got {tuple(weight.shape)}")
+    cout, c, kh, kw = weight.shape
+    numel = dcn_packed_weight_numel(weight.dtype, cout, kh, kw, c)
+    if packed is None:
+        packed = weight.new_empty(numel)
+    _b.require_device(fn, weight, packed)
+    _b.require_contiguous(fn, weight=weight, packed=packed)
+    _b.require_dtype(fn, weight, packed=packed)
+    _b.require_numel(fn, "packed", packed, numel)
+    _b.call("bevk_dcn_pack_weight", _b.dtype_code(weight), _b.ptr(weight), cout, kh, kw, c,
+            _b.ptr(packed), _b.stream_of(weight))
+    return packed
+
+
+def dcn_fused_fwd_nhwc(data_im, data_offset, data_mask, weight_packed, bias, batch_size,
+                       channels, height_im, width_im, height_col, width_col, channels_out,
+                       kernel_h, kernel_w, pad_h, pad_w, stride_h, stride_w, dilation_h,
+                       dilation_w, out):
     """Fused NHWC DCNv2 forward into out [B, Ho, Wo, Cout] with no column buffer.
 
-    weight_kc is the main weight as [Cout, kh, kw, C] (weight.permute(0, 2, 3, 1));
-    bias is [Cout] in the input dtype or None; data_offset follows the 2T / 3T rule of
-    modulated_deformable_im2col_nhwc_cuda."""
+    weight_packed is dcn_pack_weight(weight) of the [Cout, C, kh, kw] weight in the input
+    dtype; bias is [Cout] in the input dtype or None; data_offset follows the 2T / 3T rule
+    of modulated_deformable_im2col_nhwc_cuda."""
     fn = "dcn_fused_fwd_nhwc"
-    _b.require_device(fn, data_im, data_offset, data_mask, weight_kc, bias, out)
+    _b.require_device(fn, data_im, data_offset, data_mask, weight_packed, bias, out)
     _b.require_contiguous(fn, data_im=data_im, data_offset=data_offset, data_mask=data_mask,
-                          weight_kc=weight_kc, bias=bias, out=out)
+                          weight_packed=weight_packed, bias=bias, out=out)
     taps = kernel_h * kernel_w
     last = data_offset.size(-1)
     fused_y = last == 3 * taps
-    _b.require_dtype(fn, data_im, data_offset=data_offset, weight_kc=weight_kc, bias=bias,
-                     out=out, data_mask=None if fused_y else data_mask)
+    _b.require_dtype(fn, data_im, data_offset=data_offset, weight_packed=weight_packed,
+                     bias=bias, out=out, data_mask=None if fused_y else data_mask)
     m = batch_size * height_col * width_col
     _b.require_numel(fn, "data_im", data_im, batch_size * height_im * width_im * channels)
     _b.require_numel(fn, "data_offset", data_offset, m * last)
     if not fused_y:
         _b.require_numel(fn, "data_mask", data_mask, m * taps)
-    _b.require_numel(fn, "weight_kc", weight_kc, channels_out * taps * channels)
+    _b.require_numel(fn, "weight_packed", weight_packed,
+                     dcn_packed_weight_numel(data_im.dtype, channels_out, kernel_h, kernel_w,
+                                             channels))
     if bias is not None:
         _b.require_numel(fn, "bias", bias, channels_out)
     _b.require_numel(fn, "out", out, m * channels_out)
     _b.call("bevk_dcn_fused_fwd_nhwc", _b.dtype_code(data_im), _b.ptr(data_im),
-            _b.ptr(data_offset), last, _b.ptr(data_mask), _b.ptr(weight_kc), _b.ptr(bias),
-            batch_size, channels, height_im, width_im, height_col, width_col, channels_out,
-            kernel_h, kernel_w, pad_h, pad_w, stride_h, stride_w, dilation_h, dilation_w,
-            _b.ptr(out), _b.stream_of(data_im))
+            _b.ptr(data_offset), last, _b.ptr(data_mask), _b.ptr(weight_packed),
+            _b.ptr(bias), batch_size, channels, height_im, width_im, height_col, width_col,
+            channels_out, kernel_h, kernel_w, pad_h, pad_w, stride_h, stride_w, dilation_h,
+            dilation_w, _b.ptr(out), _b.stream_of(data_im))
 
 
 def _backward_absent(name):

@@ -182,8 +182,37 @@ int bevk_modulated_deformable_im2col_nhwc(
                     fn);
 }
 
+int64_t bevk_dcn_packed_weight_bytes(int dtype, int channels_out, int kernel_h, int kernel_w,
+                                      int channels) {
+  if (dtype != BEVK_F32 && dtype != BEVK_F16 && dtype != BEVK_BF16) return -1;
+  if (channels_out < 0 || kernel_h <= 0 || kernel_w <= 0 || channels < 0) return -1;
+  return bevk::dcn_packed_weight_elems(dtype, channels_out, kernel_h * kernel_w * channels) *
+         dtype_size(dtype);
+}
+
+int bevk_dcn_pack_weight(int dtype, const void *weight, int channels_out, int kernel_h,
+                         int kernel_w, int channels, void *packed, void *stream) {
+  const char *fn = "dcn_pack_weight";
+  g_last_error.clear();
+  if (dtype != BEVK_F32 && dtype != BEVK_F16 && dtype != BEVK_BF16)
+    return fail(BEVK_ERR_UNSUPPORTED, "\"%s\" not implemented for '%s'", fn, dtype_name(dtype));
+  if (channels_out < 0 || kernel_h <= 0 || kernel_w <= 0 || channels < 0)
+    return fail(BEVK_ERR_INVALID, "%s: invalid weight shape", fn);
+  const long long bytes = bevk::dcn_packed_weight_elems(dtype, channels_out,
+                                                        kernel_h * kernel_w * channels) *
+                          dtype_size(dtype);
+  if (bytes == 0) return ok();
+  if (bytes > kMaxBufferBytes)
+    return fail(BEVK_ERR_INVALID, "%s: weight too large for 32-bit buffer offsets", fn);
+  if (!weight || !packed) return fail(BEVK_ERR_INVALID, "%s: null tensor pointer", fn);
+  return hip_status(bevk::launch_dcn_pack_weight(dtype, weight, channels_out, channels,
+                                                 kernel_h * kernel_w, packed,
+                                                 (hipStream_t)stream),
+                    fn);
+}
+
 int bevk_dcn_fused_fwd_nhwc(int dtype, const void *data_im, const void *data_offset,
-                            int offset_last_dim, const void *data_mask, const void *weight_kc,
+                            int offset_last_dim, const void *data_mask, const void *weight_packed,
                             const void *bias, int batch_size, int channels, int height_im,
                             int width_im, int height_col, int width_col, int channels_out,
                             int kernel_h, int kernel_w, int pad_h, int pad_w, int stride_h,
@@ -215,10 +244,13 @@ int bevk_dcn_fused_fwd_nhwc(int dtype, const void *data_im, const void *data_off
       (long long)taps * channels * channels_out * dtype_size(dtype) > kMaxBufferBytes ||
       m >= (1LL << 30))
     return fail(BEVK_ERR_INVALID, "%s: problem too large for 32-bit buffer offsets", fn);
-  if (!data_im || !data_offset || (!fused_y && !data_mask) || !weight_kc || !out)
+  if (bevk::dcn_packed_weight_elems(dtype, channels_out, taps * channels) * dtype_size(dtype) >
+      kMaxBufferBytes)
+    return fail(BEVK_ERR_INVALID, "%s: weight too large for 32-bit buffer offsets", fn);
+  if (!data_im || !data_offset || (!fused_y && !data_mask) || !weight_packed || !out)
     return fail(BEVK_ERR_INVALID, "%s: null tensor pointer", fn);
   return hip_status(bevk::launch_dcn_fused_nhwc(dtype, g, channels_out, data_im, data_offset,
-                                                fused_y, data_mask, weight_kc, bias, out,
+                                                fused_y, data_mask, weight_packed, bias, out,
                                                 (hipStream_t)stream),
                     fn);
 }

@@ -1,4 +1,7 @@
 // Fused NHWC DCNv2 forward for gfx950: deformable gather + GEMM with no column buffer.
+// This kernel serves fp32 (v_mfma_f32_32x32x2_f32) and half types with more than 9 taps;
+// fp16 / bf16 with up to 9 taps use dcn_fused_h.hip. Weights arrive in the layout of
+// bevk_dcn_pack_weight: [Cout][kh][kw][C] for fp32, MFMA-fragment blocks for half types.
 //
 //   out[m, n] = sum_k A[m, k] * Wkc[n, k] (+ bias[n]),  m = (b, oh, ow), k = t*C + c
 //   A[m, k]   = mask[m, t] * bilinear(x[b], h(m, t), w(m, t))[c]
@@ -204,7 +207,17 @@ __global__ void __launch_bounds__(kThreads) dcn_fused_nhwc_kernel(const FusedPar
       const int n = n0 + v / KV;
       const int k = ks * BK + (v - (v / KV) * KV) * VEC;
       const bool ok = n < p.Cout && k < p.K;
-      const uint32_t o = ok ? ((uint32_t)n * (uint32_t)p.K + (uint32_t)k) * (uint32_t)sizeof(T) : woob;
+      uint32_t o = woob;
+      if (ok) {
+        if constexpr (sizeof(T) == 4) {
+          o = ((uint32_t)n * (uint32_t)p.K + (uint32_t)k) * 4u;  // [Cout][K]
+        } else {
+          // fragment-packed: block (n/32, k/16), lane (n%32) + 32 * ((k%16)/8), 16 B each
+          const uint32_t kb_total = (uint32_t)(p.K + 15) / 16u;
+          o = (((uint32_t)(n >> 5) * kb_total + (uint32_t)(k >> 4)) * 64u + (uint32_t)(n & 31) +
+               32u * (uint32_t)((k & 15) >> 3)) * 16u;
+        }
+      }
       rb[i] = buffer_load_vec<T, VEC>(wr, o);
     }
   };
@@ -306,10 +319,13 @@ hipError_t launch_t(FusedParams p, bool fy, hipStream_t stream) {
 
 hipError_t launch_dcn_fused_nhwc(int dtype, const DcnGeom &g, int channels_out, const void *x,
                                  const void *off, bool fused_y, const void *msk,
-                                 const void *w_kc, const void *bias, void *out,
+                                 const void *w_packed, const void *bias, void *out,
                                  hipStream_t stream) {
+  if (dtype != 0 && dcn_fused_h_supported(g))
+    return launch_dcn_fused_h(dtype, g, channels_out, x, off, fused_y, msk, w_packed, bias, out,
+                              stream);
   FusedParams p;
-  p.x = x; p.off = off; p.msk = msk; p.w = w_kc; p.bias = bias; p.out = out;
+  p.x = x; p.off = off; p.msk = msk; p.w = w_packed; p.bias = bias; p.out = out;
   p.B = g.batch; p.C = g.channels; p.H = g.height; p.W = g.width;
   p.Ho = g.height_col; p.Wo = g.width_col; p.Cout = channels_out;
   p.kh = g.kernel_h; p.kw = g.kernel_w; p.ph = g.pad_h; p.pw = g.pad_w;
@@ -319,7 +335,8 @@ hipError_t launch_dcn_fused_nhwc(int dtype, const DcnGeom &g, int channels_out, 
   p.tiles_m = 0;
   const int es = dtype == 0 ? 4 : 2;
   p.x_bytes = (uint32_t)((int64_t)g.batch * g.height * g.width * g.channels * es);
-  p.w_bytes = (uint32_t)((int64_t)channels_out * p.K * es);
+  p.w_bytes = (uint32_t)(dtype == 0 ? (int64_t)channels_out * p.K * 4
+                                    : dcn_packed_weight_elems(dtype, channels_out, p.K) * 2);
   switch (dtype) {
     case 0: return launch_t<float>(p, fused_y, stream);
     case 1: return launch_t<f16>(p, fused_y, stream);

@@ -1,0 +1,356 @@
+// Fused NHWC DCNv2 forward for fp16 / bf16 on gfx950 (kernels with at most 9 taps).
+//
+//   out[m, n] = sum_k A[m, k] * W[n, k] (+ bias[n]),  m = (b, oh, ow), k = t*C + c
+//   A[m, k]   = mask[m, t] * bilinear(x[b], h(m, t), w(m, t))[c]
+//
+// Structure of one workgroup (4 waves, BM x BN output tile):
+//   * Geometry table: at start, each (tile row, tap) pair gets its four corner byte
+//     offsets (out-of-range sentinel if the corner is outside the image) and four
+//     bilinear x mask weights, once, in LDS.
+//   * A operand: per K step (BK = 64 channels of one tap) each thread gathers 16-byte
+//     vectors of the four corner rows of its (row, k-vector) slots with buffer loads
+//     (8 lanes cover 128 contiguous bytes of a pixel), blends them (packed fp16 FMA, or
+//     fp32 FMA for bf16) and writes the A tile to double-buffered LDS.
+//   * B operand: the weight is pre-packed in MFMA fragment order, so every B fragment is
+//     one coalesced 1 KB load straight into registers (double-buffered across K steps).
+//     LDS only carries the A tile.
+//   * MFMA v_mfma_f32_32x32x16_{f16,bf16}: each wave owns a 64 x 64 block of the tile.
+//   * Epilogue: fp32 accumulators + bias, one rounding to T.
+#include "bevk_common.h"
+#include "bevk_launch.h"
+
+namespace bevk {
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef int int4v __attribute__((ext_vector_type(4)));
+
+constexpr int kMaxTaps = 9;
+
+struct HParams {
+  const void *x, *off, *msk, *w, *bias;
+  void *out;
+  int C, H, W, Ho, Wo, Cout, kh, kw, ph, pw, sh, sw, dh, dw, M, K;
+  int taps, nb_total, kb_total;  // packed weight blocks: [nb_total][kb_total][64][16 B]
+  uint32_t x_bytes, w_bytes;
+};
+
+template <typename T> __device__ __forceinline__ floatx16 mfma16(const T *a, int4v b, floatx16 c);
+template <> __device__ __forceinline__ floatx16 mfma16<f16>(const f16 *a, int4v b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8 *>(a),
+                                                __builtin_bit_cast(half8, b), c, 0, 0, 0);
+}
+template <> __device__ __forceinline__ floatx16 mfma16<bf16>(const bf16 *a, int4v b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(*reinterpret_cast<const bf16x8 *>(a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+struct TapGeo {
+  float w[4];
+  uint32_t o[4];
+};
+
+template <typename T, int BM, int BN, int BK, int WM_, int WN_, bool FY>
+__global__ void __launch_bounds__(64 * WM_ * WN_) __attribute__((amdgpu_waves_per_eu(2, 8)))
+dcn_fused_h_kernel(const HParams p) {
+  constexpr int NT = 64 * WM_ * WN_, VEC = 8, KV = BK / VEC, KSUB = BK / 16;
+  constexpr int AV = BM * KV / NT, LDA = BK + VEC;
+  constexpr int WTM = BM / WM_, WTN = BN / WN_, TM = WTM / 32, TN = WTN / 32;
+  static_assert(AV >= 1 && (BM * KV) % NT == 0 && TM >= 1 && TN >= 1, "tile config");
+  using V = Vec<T, VEC>;
+  __shared__ __attribute__((aligned(16))) TapGeo geo[BM * kMaxTaps];
+  __shared__ __attribute__((aligned(16))) T As[2][BM * LDA];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN_, wn = wave - (wave / WN_) * WN_;
+  const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
+  const int HoWo = p.Ho * p.Wo, TT = p.taps;
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, p.x_bytes);
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, p.w_bytes);
+  const uint32_t xoob = p.x_bytes, woob = p.w_bytes;
+
+  // ---- geometry table -------------------------------------------------------------
+  for (int g = tid; g < BM * TT; g += NT) {
+    const int row = g / TT, t = g - row * TT, m = m0 + row;
+    TapGeo G;
+    G.w[0] = G.w[1] = G.w[2] = G.w[3] = 0.f;
+    G.o[0] = G.o[1] = G.o[2] = G.o[3] = xoob;
+    if (m < p.M) {
+      const int b = m / HoWo, r = m - b * HoWo, oh = r / p.Wo, ow = r - (r / p.Wo) * p.Wo;
+      float dy, dx, mk;
+      const T *op = static_cast<const T *>(p.off);
+      if constexpr (FY) {
+        const T *yp = op + (int64_t)m * 3 * TT;
+        dy = (float)yp[2 * t];
+        dx = (float)yp[2 * t + 1];
+        mk = sigmoid_f32((float)yp[2 * TT + t]);
+      } else {
+        dy = (float)op[(int64_t)m * 2 * TT + 2 * t];
+        dx = (float)op[(int64_t)m * 2 * TT + 2 * t + 1];
+        mk = (float)static_cast<const T *>(p.msk)[(int64_t)m * TT + t];
+      }
+      const int ki = t / p.kw, kj = t - (t / p.kw) * p.kw;
+      const float h = (float)(oh * p.sh - p.ph + ki * p.dh) + dy;
+      const float w = (float)(ow * p.sw - p.pw + kj * p.dw) + dx;
+      if (h > -1.f && w > -1.f && h < (float)p.H && w < (float)p.W) {
+        const float fh = floorf(h), fw = floorf(w);
+        const int hl = (int)fh, wl = (int)fw;
+        const float lh = h - fh, lw = w - fw, hh = 1.f - lh, hw = 1.f - lw;
+        const uint32_t rowb = (uint32_t)p.C * (uint32_t)sizeof(T);
+        const uint32_t base = (uint32_t)(b * p.H * p.W + hl * p.W + wl) * rowb;
+        const bool y0 = hl >= 0, y1 = hl + 1 <= p.H - 1, x0 = wl >= 0, x1 = wl + 1 <= p.W - 1;
+        if (y0 && x0) { G.w[0] = hh * hw * mk; G.o[0] = base; }
+        if (y0 && x1) { G.w[1] = hh * lw * mk; G.o[1] = base + rowb; }
+        if (y1 && x0) { G.w[2] = lh * hw * mk; G.o[2] = base + (uint32_t)p.W * rowb; }
+        if (y1 && x1) { G.w[3] = lh * lw * mk; G.o[3] = base + (uint32_t)(p.W + 1) * rowb; }
+      }
+    }
+    geo[g] = G;
+  }
+  __syncthreads();
+
+  // ---- A slots: (row, 16-byte k-vector); 8 consecutive lanes share a pixel ---------
+  int a_row[AV], a_kv[AV], a_t[AV], a_c[AV];
+#pragma unroll
+  for (int i = 0; i < AV; ++i) {
+    const int a = tid + i * NT;
+    a_row[i] = a / KV;
+    a_kv[i] = a - (a / KV) * KV;
+    const int k = a_kv[i] * VEC;
+    a_t[i] = k / p.C;
+    a_c[i] = k - a_t[i] * p.C;
+  }
+  V ra[AV][4];
+  float rw[AV][4];
+  auto issue_a = [&](int ks) {
+#pragma unroll
+    for (int i = 0; i < AV; ++i) {
+      if (ks > 0) {
+        a_c[i] += BK;
+        while (a_c[i] >= p.C) { a_c[i] -= p.C; ++a_t[i]; }
+      }
+      TapGeo G;
+      if (a_t[i] < TT) {
+        G = geo[a_row[i] * TT + a_t[i]];
+      } else {  // K tail
+        G.w[0] = G.w[1] = G.w[2] = G.w[3] = 0.f;
+        G.o[0] = G.o[1] = G.o[2] = G.o[3] = xoob;
+      }
+      const uint32_t cb = (uint32_t)a_c[i] * (uint32_t)sizeof(T);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        rw[i][q] = G.w[q];
+        ra[i][q] = buffer_load_vec<T, VEC>(xr, G.o[q] == xoob ? xoob : G.o[q] + cb);
+      }
+    }
+  };
+  int4v breg[2][KSUB][TN];
+  auto issue_b = [&](int ks, int4v (&br)[KSUB][TN]) {
+#pragma unroll
+    for (int kk = 0; kk < KSUB; ++kk)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int nb = (n0 >> 5) + wn * TN + j, kb = ks * KSUB + kk;
+        const uint32_t o = (nb < p.nb_total && kb < p.kb_total)
+                               ? ((uint32_t)(nb * p.kb_total + kb) * 64u + (uint32_t)lane) * 16u
+                               : woob;
+        br[kk][j] = __builtin_amdgcn_raw_buffer_load_b128(wr, o, 0, 0);
+      }
+  };
+  auto store_a = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < AV; ++i) {
+      V o;
+      if constexpr (__is_same(T, f16)) {
+        const half2v w1 = {(f16)rw[i][0], (f16)rw[i][0]}, w2 = {(f16)rw[i][1], (f16)rw[i][1]};
+        const half2v w3 = {(f16)rw[i][2], (f16)rw[i][2]}, w4 = {(f16)rw[i][3], (f16)rw[i][3]};
+#pragma unroll
+        for (int e = 0; e < VEC; e += 2) {
+          const half2v v1 = {ra[i][0].v[e], ra[i][0].v[e + 1]};
+          const half2v v2 = {ra[i][1].v[e], ra[i][1].v[e + 1]};
+          const half2v v3 = {ra[i][2].v[e], ra[i][2].v[e + 1]};
+          const half2v v4 = {ra[i][3].v[e], ra[i][3].v[e + 1]};
+          const half2v r = w1 * v1 + w2 * v2 + w3 * v3 + w4 * v4;
+          o.v[e] = r.x;
+          o.v[e + 1] = r.y;
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e)
+          o.v[e] = static_cast<T>(rw[i][0] * (float)ra[i][0].v[e] + rw[i][1] * (float)ra[i][1].v[e] +
+                                  rw[i][2] * (float)ra[i][2].v[e] + rw[i][3] * (float)ra[i][3].v[e]);
+      }
+      store_vec<T, VEC>(&As[buf][a_row[i] * LDA + a_kv[i] * VEC], o);
+    }
+  };
+
+  floatx16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+  const int lrow = lane & 31, lk = (lane >> 5) * 8;
+  auto compute = [&](int buf, const int4v (&br)[KSUB][TN]) {
+#pragma unroll
+    for (int kk = 0; kk < KSUB; ++kk)
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const T *a = &As[buf][(wm * WTM + i * 32 + lrow) * LDA + kk * 16 + lk];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma16<T>(a, br[kk][j], acc[i][j]);
+      }
+  };
+
+  // ---- K loop: A(k+1) is gathered and B(k+1) loaded while step k multiplies ---------
+  const int nk = (p.K + BK - 1) / BK;
+  issue_b(0, breg[0]);
+  issue_a(0);
+  store_a(0);
+  if (nk > 1) issue_a(1);
+  for (int ks = 0; ks < nk; ks += 2) {
+    __syncthreads();                       // A(ks) complete in buffer 0
+    if (ks + 1 < nk) issue_b(ks + 1, breg[1]);
+    compute(0, breg[0]);
+    if (ks + 1 >= nk) break;
+    store_a(1);                            // A(ks+1) -> buffer 1
+    if (ks + 2 < nk) issue_a(ks + 2);
+    __syncthreads();
+    if (ks + 2 < nk) issue_b(ks + 2, breg[0]);
+    compute(1, breg[1]);
+    if (ks + 2 < nk) {
+      store_a(0);                          // A(ks+2) -> buffer 0
+      if (ks + 3 < nk) issue_a(ks + 3);
+    }
+  }
+
+  // ---- epilogue: lane holds col = lane % 32, rows 8*(e/4) + 4*(lane/32) + e%4 --------
+  T *out = static_cast<T *>(p.out);
+  const T *bias = static_cast<const T *>(p.bias);
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int n = n0 + (wn * TN + j) * 32 + lrow;
+    const float bv = (bias != nullptr && n < p.Cout) ? (float)bias[n] : 0.f;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = m0 + wm * WTM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        if (m < p.M && n < p.Cout) out[(int64_t)m * p.Cout + n] = static_cast<T>(acc[i][j][e] + bv);
+      }
+  }
+}
+
+// Module weight [Cout][C][T] -> fragment blocks [NB][KB][64 lanes][8 elements]: lane l of
+// block (nb, kb) holds W[n = nb*32 + l%32][k = kb*16 + (l/32)*8 + e], k = t*C + c, zero
+// outside [0, Cout) x [0, K). One thread per 16-byte output chunk.
+__global__ void __launch_bounds__(256) pack_weight_frag_kernel(const uint16_t *__restrict__ w,
+                                                               uint16_t *__restrict__ packed,
+                                                               int cout, int C, int T, int KB,
+                                                               int64_t chunks) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= chunks) return;
+  const int64_t blk = i >> 6;
+  const int l = (int)(i & 63);
+  const int nb = (int)(blk / KB), kb = (int)(blk - (blk / KB) * KB);
+  const int n = nb * 32 + (l & 31), k0 = kb * 16 + (l >> 5) * 8;
+  const int K = C * T;
+  Vec<uint16_t, 8> v;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int k = k0 + e;
+    const int t = k / C, c = k - (k / C) * C;
+    v.v[e] = (n < cout && k < K) ? w[((int64_t)n * C + c) * T + t] : (uint16_t)0;
+  }
+  store_vec<uint16_t, 8>(packed + i * 8, v);
+}
+
+// Module weight [Cout][C][T] -> [Cout][T][C] (fp32), one thread per output element.
+__global__ void __launch_bounds__(256) pack_weight_kc_kernel(const float *__restrict__ w,
+                                                             float *__restrict__ packed, int C,
+                                                             int T, int64_t total) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int64_t n = i / ((int64_t)T * C);
+  const int r = (int)(i - n * T * C), t = r / C, c = r - (r / C) * C;
+  packed[i] = w[(n * C + c) * T + t];
+}
+
+template <typename T, int BM, int BN, int BK, int WM, int WN>
+hipError_t launch_cfg(const HParams &p, bool fy, hipStream_t stream) {
+  dim3 grid((p.M + BM - 1) / BM, (p.Cout + BN - 1) / BN);
+  if (fy)
+    hipLaunchKernelGGL((dcn_fused_h_kernel<T, BM, BN, BK, WM, WN, true>), grid, dim3(64 * WM * WN),
+                       0, stream, p);
+  else
+    hipLaunchKernelGGL((dcn_fused_h_kernel<T, BM, BN, BK, WM, WN, false>), grid,
+                       dim3(64 * WM * WN), 0, stream, p);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_t(const HParams &p, bool fy, hipStream_t stream) {
+  if (p.Cout > 128) return launch_cfg<T, 64, 256, 64, 1, 4>(p, fy, stream);
+  if (p.Cout > 64) return launch_cfg<T, 64, 128, 64, 2, 2>(p, fy, stream);
+  return launch_cfg<T, 64, 64, 64, 2, 2>(p, fy, stream);
+}
+
+}  // namespace
+
+int64_t dcn_packed_weight_elems(int dtype, int cout, int K) {
+  if (dtype == 0) return (int64_t)cout * K;
+  const int64_t nb = (cout + 31) / 32, kb = (K + 15) / 16;
+  return nb * kb * 64 * 8;
+}
+
+hipError_t launch_dcn_pack_weight(int dtype, const void *weight, int cout, int C, int T,
+                                  void *packed, hipStream_t stream) {
+  const int K = C * T;
+  if (dtype == 0) {
+    const int64_t total = (int64_t)cout * K;
+    if (total == 0) return hipSuccess;
+    hipLaunchKernelGGL(pack_weight_kc_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                       stream, static_cast<const float *>(weight), static_cast<float *>(packed),
+                       C, T, total);
+    return hipGetLastError();
+  }
+  const int KB = (K + 15) / 16;
+  const int64_t chunks = (int64_t)((cout + 31) / 32) * KB * 64;
+  if (chunks == 0) return hipSuccess;
+  hipLaunchKernelGGL(pack_weight_frag_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256),
+                     0, stream, static_cast<const uint16_t *>(weight),
+                     static_cast<uint16_t *>(packed), cout, C, T, KB, chunks);
+  return hipGetLastError();
+}
+
+bool dcn_fused_h_supported(const DcnGeom &g) { return g.kernel_h * g.kernel_w <= kMaxTaps; }
+
+hipError_t launch_dcn_fused_h(int dtype, const DcnGeom &g, int channels_out, const void *x,
+                              const void *off, bool fused_y, const void *msk,
+                              const void *w_packed, const void *bias, void *out,
+                              hipStream_t stream) {
+  HParams p;
+  p.x = x; p.off = off; p.msk = msk; p.w = w_packed; p.bias = bias; p.out = out;
+  p.C = g.channels; p.H = g.height; p.W = g.width; p.Ho = g.height_col; p.Wo = g.width_col;
+  p.Cout = channels_out; p.kh = g.kernel_h; p.kw = g.kernel_w;
+  p.ph = g.pad_h; p.pw = g.pad_w; p.sh = g.stride_h; p.sw = g.stride_w;
+  p.dh = g.dil_h; p.dw = g.dil_w;
+  p.M = g.batch * g.height_col * g.width_col;
+  p.taps = g.kernel_h * g.kernel_w;
+  p.K = p.taps * g.channels;
+  p.nb_total = (channels_out + 31) / 32;
+  p.kb_total = (p.K + 15) / 16;
+  p.x_bytes = (uint32_t)((int64_t)g.batch * g.height * g.width * g.channels * 2);
+  p.w_bytes = (uint32_t)(dcn_packed_weight_elems(dtype, channels_out, p.K) * 2);
+  switch (dtype) {
+    case 1: return launch_t<f16>(p, fused_y, stream);
+    case 2: return launch_t<bf16>(p, fused_y, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace bevk

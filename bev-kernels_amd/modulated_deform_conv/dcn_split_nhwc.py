@@ -15,6 +15,8 @@ from __future__ import annotations
 import torch
 import torch.nn.functional as F
 
+from ._packing import pack_weight, packed_weight
+
 
 def out_size(H, pad, dil, k, stride):
     return (H + 2 * pad - (dil * (k - 1) + 1)) // stride + 1
@@ -60,24 +62,25 @@ def _fused_forward(x_nhwc, offset, mask, weight, bias, stride, padding, dilation
     Ho = out_size(H, padding, dilation, kH, stride)
     Wo = out_size(W, padding, dilation, kW, stride)
     dt = x_nhwc.dtype
-    w_kc = weight.permute(0, 2, 3, 1)                        # [Cout, kH, kW, Cin]
+    w = weight
     b = bias
     if bn_scale is not None:
         # relu(scale * (conv + bias) + shift) == relu(conv_{w*scale} + shift + scale*bias)
-        w_kc = w_kc * bn_scale.to(w_kc.dtype).view(-1, 1, 1, 1)
+        w = weight * bn_scale.to(weight.dtype).view(-1, 1, 1, 1)
         b = bn_shift + (bias.to(bn_shift.dtype) * bn_scale if bias is not None else 0)
-    w_kc = w_kc.to(dt).contiguous()
     b = b.to(dt).contiguous() if b is not None else None
     out = torch.empty(B, Ho, Wo, Cout, device=x_nhwc.device, dtype=dt)
     vec = 16 // x_nhwc.element_size()
     if Cin % vec == 0 and dt != torch.float64:
+        # the BN-folded weight is a fresh tensor each call: pack it without caching
+        w_packed = pack_weight(w, dt) if bn_scale is not None else packed_weight(w, dt)
         _ext().dcn_fused_fwd_nhwc(
             x_nhwc.contiguous(), offset.contiguous(),
-            (mask if mask is not None else offset).contiguous(), w_kc, b, B, Cin, H, W, Ho, Wo,
-            Cout, kH, kW, padding, padding, stride, stride, dilation, dilation, out)
+            (mask if mask is not None else offset).contiguous(), w_packed, b, B, Cin, H, W,
+            Ho, Wo, Cout, kH, kW, padding, padding, stride, stride, dilation, dilation, out)
     else:
         col = gather_cols_nhwc(x_nhwc, offset, mask, kH, kW, stride, padding, dilation)
-        w_flat = w_kc.view(Cout, kH * kW * Cin).t()
+        w_flat = w.permute(0, 2, 3, 1).to(dt).contiguous().view(Cout, kH * kW * Cin).t()
         torch.mm(col, w_flat, out=out.view(-1, Cout))
         if b is not None:
             out += b.view(1, 1, 1, -1)

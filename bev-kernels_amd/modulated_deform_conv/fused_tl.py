@@ -20,6 +20,7 @@ import torch
 import torch.nn.functional as F
 
 from . import dcn_split_nhwc as _split
+from ._packing import packed_weight
 
 
 def out_size(H, pad, dil, k, stride):
@@ -134,15 +135,15 @@ def fused_dcn_forward_nhwc(data_im, offset, mask, weight, bias=None, stride=1, p
     Wo = out_size(W, pw, dw, kW, sw)
     dt = data_im.dtype
     out = torch.empty(B, Ho, Wo, Cout, device=data_im.device, dtype=dt)
-    w_kc = weight.permute(0, 2, 3, 1).to(dt).contiguous()
     b = bias.to(dt).contiguous() if bias is not None else None
     vec = 16 // data_im.element_size()
     if Cin % vec == 0 and dt != torch.float64:
         _ext().dcn_fused_fwd_nhwc(data_im.contiguous(), offset.contiguous(), mask.contiguous(),
-                                  w_kc, b, B, Cin, H, W, Ho, Wo, Cout, kH, kW, ph, pw, sh, sw,
+                                  packed_weight(weight, dt), b, B, Cin, H, W, Ho, Wo, Cout, kH, kW, ph, pw, sh, sw,
                                   dh, dw, out)
     else:
         cols = dcn_gather_cols_nhwc(data_im, offset, mask, kH, kW, (sh, sw), (ph, pw), (dh, dw))
+        w_kc = weight.permute(0, 2, 3, 1).to(dt).contiguous()
         torch.mm(cols, w_kc.view(Cout, -1).t(), out=out.view(-1, Cout))
         if b is not None:
             out += b.view(1, 1, 1, -1)

@@ -16,6 +16,7 @@ import torch.nn as nn
 from torch.autograd import Function
 from torch.autograd.function import once_differentiable
 from torch.nn.modules.utils import _pair, _single
+from ._packing import packed_weight
 
 _ext = None
 
@@ -292,10 +293,10 @@ def _modulated_deform_conv2d_forward(input, offset, mask, weight, bias, stride, 
         x_nhwc = input.permute(0, 2, 3, 1).contiguous()
         off_nhwc = offset.permute(0, 2, 3, 1).contiguous()
         msk_nhwc = mask.permute(0, 2, 3, 1).contiguous()
-        w_kc = weight.permute(0, 2, 3, 1).contiguous()
+        w_packed = packed_weight(weight, input.dtype)
         b = bias.to(input.dtype).contiguous() if bias is not None else None
         out = input.new_empty(batch, ho, wo, channels_out)
-        ext.dcn_fused_fwd_nhwc(x_nhwc, off_nhwc, msk_nhwc, w_kc, b, batch, channels, height,
+        ext.dcn_fused_fwd_nhwc(x_nhwc, off_nhwc, msk_nhwc, w_packed, b, batch, channels, height,
                                width, ho, wo, channels_out, kernel_h, kernel_w, pad_h, pad_w,
                                stride_h, stride_w, dil_h, dil_w, out)
         return out.permute(0, 3, 1, 2).contiguous()

@@ -97,20 +97,36 @@ int bevk_modulated_deformable_im2col_nhwc(
     int stride_h, int stride_w, int dilation_h, int dilation_w, int deformable_group,
     void *data_col, void *stream);
 
-/* Fused NHWC DCNv2 forward: bilinear x mask taps are produced straight into LDS
- * and multiplied on the matrix cores; no column buffer touches HBM.
- *   data_im     [B, H, W, C]
- *   data_offset [B, Ho, Wo, offset_last_dim] with the same 2T / 3T rule as above
- *   data_mask   [B, Ho, Wo, T] (ignored in the 3T form)
- *   weight_kc   [Cout, kh, kw, C]  (= torch weight.permute(0, 2, 3, 1)), K-contiguous
- *   bias        [Cout] in dtype, or NULL
- *   out         [B, Ho, Wo, Cout]; fully written. fp32 accumulation, one rounding.
+/* Bytes of the packed weight that bevk_dcn_fused_fwd_nhwc consumes for this shape
+ * (-1 for an unsupported dtype). */
+int64_t bevk_dcn_packed_weight_bytes(int dtype, int channels_out, int kernel_h, int kernel_w,
+                                     int channels);
+
+/* Repacks a module weight [Cout, C, kh, kw] (the layout of ModulatedDeformConv2d.weight)
+ * into the fused kernel's layout, into `packed` (bevk_dcn_packed_weight_bytes bytes):
+ *   F32:       [Cout, kh, kw, C]
+ *   F16, BF16: MFMA-fragment blocks: block (n/32, k/16) of 64 lanes x 8 elements, lane
+ *              (n%32) + 32*((k%16)/8), k = (i*kw + j)*C + c; zero padded to whole blocks.
+ * Done once per weight; the reference repacks per call (weight.permute(2,3,1,0), e.g.
+ * fused_tl.py:500-510, dcn_split_nhwc.py:143). */
+int bevk_dcn_pack_weight(int dtype, const void *weight, int channels_out, int kernel_h,
+                         int kernel_w, int channels, void *packed, void *stream);
+
+/* Fused NHWC DCNv2 forward: bilinear x mask taps are produced straight into LDS and
+ * multiplied on the matrix cores; no column buffer touches HBM.
+ *   data_im       [B, H, W, C]
+ *   data_offset   [B, Ho, Wo, offset_last_dim] with the same 2T / 3T rule as above
+ *   data_mask     [B, Ho, Wo, T] (ignored in the 3T form)
+ *   weight_packed the output of bevk_dcn_pack_weight
+ *   bias          [Cout] in dtype, or NULL
+ *   out           [B, Ho, Wo, Cout]; fully written. fp32 accumulation, one rounding.
+ * C must be a multiple of 16 bytes' worth of elements (8 for F16/BF16, 4 for F32).
  * Computes fused_tl.fused_dcn_forward_nhwc (fused_tl.py:513-556, algorithm of the
  * T.gemm kernel at :42-139) and the forward of DCNSplitNHWCFunction
  * (dcn_split_nhwc.py:158-228) after its offset conv. dtypes: F16, BF16, F32. */
 int bevk_dcn_fused_fwd_nhwc(
     int dtype, const void *data_im, const void *data_offset, int offset_last_dim,
-    const void *data_mask, const void *weight_kc, const void *bias, int batch_size,
+    const void *data_mask, const void *weight_packed, const void *bias, int batch_size,
     int channels, int height_im, int width_im, int height_col, int width_col,
     int channels_out, int kernel_h, int kernel_w, int pad_h, int pad_w, int stride_h,
     int stride_w, int dilation_h, int dilation_w, void *out, void *stream);

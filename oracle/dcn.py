@@ -91,16 +91,28 @@ def im2col_nchw(data_im, data_offset, data_mask, kernel_h, kernel_w, pad_h, pad_
     return cols.reshape(C * T, B, Ho, Wo)
 
 
+def _round_cols(cols, col_dtype):
+    """Columns rounded to the kernel's storage dtype, as the reference stores them: its
+    column buffer is allocated in the input dtype (modulated_deform_conv.py:370,
+    dcn_split_nhwc.py:40) and the fused kernel's A tile is `dtype` (fused_tl.py:68). The
+    GEMM after it stays in the oracle's precision."""
+    if col_dtype is None:
+        return cols
+    return cols.to(col_dtype).to(cols.dtype)
+
+
 def forward_nchw(x, offset, mask, weight, bias=None, stride=(1, 1), padding=(0, 0),
-                 dilation=(1, 1), groups=1, deform_groups=1):
+                 dilation=(1, 1), groups=1, deform_groups=1, col_dtype=None):
     """ModulatedDeformConv2dFunction.forward, modulated_deform_conv.py:331-403:
-    columns, one GEMM per group, [Cout, B, Ho, Wo] -> [B, Cout, Ho, Wo], + bias."""
+    columns, one GEMM per group, [Cout, B, Ho, Wo] -> [B, Cout, Ho, Wo], + bias.
+    col_dtype: round the columns to this dtype first (see _round_cols)."""
     B, C, H, W = x.shape
     Cout, _, kh, kw = weight.shape
     (sh, sw), (ph, pw), (dh, dw) = stride, padding, dilation
     Ho = out_size(H, ph, dh, kh, sh)
     Wo = out_size(W, pw, dw, kw, sw)
-    cols = im2col_nchw(x, offset, mask, kh, kw, ph, pw, sh, sw, dh, dw, deform_groups)
+    cols = _round_cols(im2col_nchw(x, offset, mask, kh, kw, ph, pw, sh, sw, dh, dw,
+                                   deform_groups), col_dtype)
     bhw = B * Ho * Wo
     cin_g_kk = (C // groups) * kh * kw
     col_g = cols.reshape(groups, cin_g_kk, bhw)
@@ -157,8 +169,10 @@ def columns_nhwc(x, offset, mask, kh, kw, sh, sw, ph, pw, dh, dw):
     return cols.reshape(B * Ho * Wo, T * C)
 
 
-def forward_nhwc(x, offset, mask, weight, bias=None, stride=1, padding=0, dilation=1):
-    """fused_tl.py:204-227: cols @ weight.permute(2,3,1,0).reshape(K, Cout) (+ bias)."""
+def forward_nhwc(x, offset, mask, weight, bias=None, stride=1, padding=0, dilation=1,
+                 col_dtype=None):
+    """fused_tl.py:204-227: cols @ weight.permute(2,3,1,0).reshape(K, Cout) (+ bias).
+    col_dtype: round the columns to this dtype first (see _round_cols)."""
     def two(v):
         return (v, v) if isinstance(v, int) else tuple(v)
     (sh, sw), (ph, pw), (dh, dw) = two(stride), two(padding), two(dilation)
@@ -166,7 +180,8 @@ def forward_nhwc(x, offset, mask, weight, bias=None, stride=1, padding=0, dilati
     Cout, _, kh, kw = weight.shape
     Ho = out_size(H, ph, dh, kh, sh)
     Wo = out_size(W, pw, dw, kw, sw)
-    cols = columns_nhwc(x, offset, mask, kh, kw, sh, sw, ph, pw, dh, dw)
+    cols = _round_cols(columns_nhwc(x, offset, mask, kh, kw, sh, sw, ph, pw, dh, dw),
+                       col_dtype)
     out = (cols @ weight.permute(2, 3, 1, 0).reshape(kh * kw * C, Cout)).view(B, Ho, Wo, Cout)
     if bias is not None:
         out = out + bias.view(1, 1, 1, -1)

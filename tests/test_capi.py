@@ -89,6 +89,25 @@ def test_fused_validation():
     assert _fused(cout=0) == 0
 
 
+def test_packed_weight_bytes():
+    f = _bevk.lib().bevk_dcn_packed_weight_bytes
+    assert f(0, 256, 3, 3, 256) == 256 * 9 * 256 * 4                # fp32: [Cout][kh][kw][C]
+    # half types: whole 32 x 16 fragment blocks of 2-byte elements
+    assert f(1, 256, 3, 3, 256) == 8 * 144 * 512 * 2
+    assert f(2, 40, 3, 3, 8) == 2 * 5 * 512 * 2                      # K = 72 -> 5 blocks
+    assert f(1, 0, 3, 3, 8) == 0
+    assert f(3, 8, 3, 3, 8) == -1                                    # no fp64 fused kernel
+    assert f(1, 8, 0, 3, 8) == -1
+
+
+def test_pack_weight_validation():
+    f = _bevk.lib().bevk_dcn_pack_weight
+    assert f(3, NULL, 8, 3, 3, 8, NULL, NULL) == UNSUPPORTED and "Double" in _err()
+    assert f(1, NULL, 8, 3, 3, 8, NULL, NULL) == INVALID and "null" in _err()
+    assert f(1, NULL, -1, 3, 3, 8, NULL, NULL) == INVALID
+    assert f(1, NULL, 0, 3, 3, 8, NULL, NULL) == 0                   # empty: nothing to do
+
+
 def _msda(step=64, b=2, nq=4, force=0):
     return _bevk.lib().bevk_msda_forward(0, NULL, NULL, NULL, NULL, NULL, b, 10, 8, 32, 1, nq, 4,
                                          step, force, NULL, NULL)

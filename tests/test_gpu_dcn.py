@@ -109,10 +109,16 @@ def test_im2col_nhwc(fused_y, dtype, geom):
 # Fused NHWC implicit GEMM (fused_tl.fused_dcn_forward_nhwc -> ext.dcn_fused_fwd_nhwc)
 # ---------------------------------------------------------------------------------------
 
+def _cols_dtype(dtype):
+    """The kernels round the deformable taps to the input dtype before the matrix cores,
+    as the reference's column buffer / A tile does; the oracle does the same."""
+    return None if dtype == torch.float32 else dtype
+
+
 def _fused_ref(d, dtype):
     return od.forward_nhwc(d["x"].double(), d["offset"].double(), d["mask"].double(),
                            d["weight"].double(), d["bias"].double(), d["stride"], d["padding"],
-                           d["dilation"])
+                           d["dilation"], col_dtype=_cols_dtype(dtype))
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16],
@@ -154,8 +160,94 @@ def test_fused_nhwc_full_size(cfg, dtype):
         sub = {k: (v[b:b + 1] if k in ("x", "offset", "mask") else v) for k, v in d.items()}
         sub["bias"] = None
         ref = od.forward_nhwc(sub["x"].double(), sub["offset"].double(), sub["mask"].double(),
-                              sub["weight"].double(), None, 1, 1, 1)
+                              sub["weight"].double(), None, 1, 1, 1,
+                              col_dtype=_cols_dtype(dtype))
         check(out[b:b + 1], ref, dtype, f"{cfg} image {b}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32],
+                         ids=["fp16", "bf16", "fp32"])
+@pytest.mark.parametrize("geom", [
+    # b, cin, cout, h, w, k, stride, pad, dil
+    (1, 16, 48, 12, 10, 5, 1, 2, 1),  # 25 taps: the general-K kernel
+    (2, 32, 64, 9, 9, 1, 1, 0, 1),    # 1x1: a single tap
+    (1, 8, 33, 7, 8, 2, 1, 0, 1),     # even kernel, K = 32, Cout tail of 1
+])
+def test_fused_nhwc_kernel_sizes(dtype, geom):
+    b, cin, cout, h, w, k, s, p, dl = geom
+    from modulated_deform_conv import fused_tl
+    d = inputs.nchw_to_nhwc(_rand_problem(b, cin, cout, h, w, k, s, p, dl, dtype=dtype,
+                                          seed=sum(geom)))
+    out = fused_tl.fused_dcn_forward_nhwc(d["x"].to(DEV), d["offset"].to(DEV),
+                                          d["mask"].to(DEV), d["weight"].to(DEV),
+                                          d["bias"].to(DEV), s, p, dl)
+    torch.cuda.synchronize()
+    check(out.cpu(), _fused_ref(d, dtype), dtype, f"fused k{k} {geom}")
+
+
+def _packed_layout_ref(weight, dtype):
+    """Packed weight layout of dcn_pack_weight, restated on the host (permutation + zeros)."""
+    cout, c, kh, kw = weight.shape
+    w_nk = weight.permute(0, 2, 3, 1).reshape(cout, kh * kw * c)     # [n][k], k = t*C + c
+    if dtype == torch.float32:
+        return w_nk.reshape(-1)
+    nb, kb = -(-cout // 32), -(-(kh * kw * c) // 16)
+    padded = torch.zeros(nb * 32, kb * 16, dtype=weight.dtype)
+    padded[:cout, :w_nk.shape[1]] = w_nk
+    # block (n/32, k/16); lane (n%32) + 32*((k%16)/8); 8 consecutive k per lane
+    blocks = padded.view(nb, 32, kb, 2, 8).permute(0, 2, 3, 1, 4)     # [nb][kb][half][n][8]
+    return blocks.reshape(-1)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32],
+                         ids=["fp16", "bf16", "fp32"])
+@pytest.mark.parametrize("shape", [(40, 24, 3, 3), (256, 256, 3, 3), (7, 8, 1, 1),
+                                   (33, 16, 5, 5)])
+def test_pack_weight_layout(dtype, shape):
+    g = torch.Generator().manual_seed(sum(shape))
+    w = torch.randn(*shape, generator=g).to(dtype)
+    packed = _ext().dcn_pack_weight(w.to(DEV))
+    torch.cuda.synchronize()
+    ref = _packed_layout_ref(w, dtype)
+    assert packed.shape == ref.shape
+    assert torch.equal(packed.cpu(), ref)                            # bit-exact permutation
+
+
+def test_packed_weight_cache_follows_updates():
+    """The module caches its packed weight; an in-place update must be seen next call."""
+    from modulated_deform_conv import ModulatedDeformConv2d
+    torch.manual_seed(1)
+    mod = ModulatedDeformConv2d(16, 32, 3, padding=1).half().to(DEV)
+    x = torch.randn(1, 16, 8, 9).half().to(DEV)
+    off = (0.5 * torch.randn(1, 18, 8, 9)).half().to(DEV)
+    msk = torch.rand(1, 9, 8, 9).half().to(DEV)
+    with torch.no_grad():
+        a = mod(x, off, msk)
+        mod.weight.mul_(-2.0)
+        b = mod(x, off, msk)
+    torch.cuda.synchronize()
+    bias = mod.bias.view(1, -1, 1, 1).float()
+    torch.testing.assert_close((b.float() - bias), -2.0 * (a.float() - bias), rtol=2e-3,
+                               atol=2e-3)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+def test_dcn_split_nhwc_half_3t(dtype):
+    """Raw 3T offset-conv output straight into the fused half-precision kernel."""
+    from modulated_deform_conv import dcn_split_nhwc as dsn
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(2, 11, 13, 64, generator=g).to(dtype)
+    w_off = (0.05 * torch.randn(27, 64, 3, 3, generator=g)).to(dtype)
+    b_off = (0.3 * torch.randn(27, generator=g)).to(dtype)
+    weight = (0.1 * torch.randn(96, 64, 3, 3, generator=g)).to(dtype)
+    bias = torch.randn(96, generator=g).to(dtype)
+    out = dsn.dcn_split_nhwc(*(t.to(DEV) for t in (x, w_off, b_off, weight, bias)), 1, 1, 1)
+    y = F.conv2d(x.to(DEV).permute(0, 3, 1, 2), w_off.to(DEV), b_off.to(DEV), 1, 1, 1)
+    torch.cuda.synchronize()
+    off, msk = od.split_y_nhwc(y.permute(0, 2, 3, 1).double().cpu(), 9)
+    ref = od.forward_nhwc(x.double(), off, msk, weight.double(), bias.double(), 1, 1, 1,
+                          col_dtype=dtype)
+    check(out.cpu(), ref, dtype, "split 3T half")
 
 
 def test_fused_matches_gather_plus_gemm():
@@ -237,7 +329,8 @@ def test_pack_module(backend, dtype):
     torch.cuda.synchronize()
     off, msk = od.split_y_nchw(y.double().cpu(), 9)
     ref = od.forward_nchw(x.double().cpu(), off, msk, mod.weight.double().cpu(),
-                          mod.bias.double().cpu(), (1, 1), (1, 1), (1, 1))
+                          mod.bias.double().cpu(), (1, 1), (1, 1), (1, 1),
+                          col_dtype=_cols_dtype(dtype))
     check(out.cpu(), ref, dtype, f"pack {backend}")
 
 

@@ -132,6 +132,32 @@ def test_linearity():
     torch.testing.assert_close(od.forward_nchw(x, off, 0.25 * m, w, None, s, p, d), 0.25 * base)
 
 
+@pytest.mark.parametrize("col_dtype", [torch.float16, torch.bfloat16])
+def test_column_rounding(col_dtype):
+    """col_dtype rounds each column once: exact columns are unchanged, and in general the
+    output moves by at most one half-ulp of every column times |weight|."""
+    g = torch.Generator().manual_seed(12)
+    x = torch.randint(-4, 5, (1, 4, 6, 7), generator=g).to(D64)
+    off = torch.randint(-2, 3, (1, 18, 6, 7), generator=g).to(D64)     # integer landings
+    m = torch.ones(1, 9, 6, 7, dtype=D64)
+    w = torch.randn(5, 4, 3, 3, generator=g, dtype=D64)
+    args = ((1, 1), (1, 1), (1, 1))
+    torch.testing.assert_close(od.forward_nchw(x, off, m, w, None, *args, col_dtype=col_dtype),
+                               od.forward_nchw(x, off, m, w, None, *args), rtol=0, atol=0)
+    x, off, m, w, b, s, p, d = _problem(1, 4, 7, 6, 3, seed=13)
+    exact = od.forward_nchw(x, off, m, w, None, s, p, d)
+    rounded = od.forward_nchw(x, off, m, w, None, s, p, d, col_dtype=col_dtype)
+    cols = od.im2col_nchw(x, off, m, 3, 3, 1, 1, 1, 1, 1, 1, 1)
+    half_ulp = 2.0 ** -(11 if col_dtype == torch.float16 else 8)
+    bound = half_ulp * (w.reshape(3, -1).abs() @ cols.abs().reshape(36, -1))
+    diff = (rounded - exact).permute(1, 0, 2, 3).reshape(3, -1)
+    assert (diff.abs() <= bound.reshape(3, -1) + 1e-12).all()
+    assert (diff != 0).any()                                            # rounding happened
+    nhwc = od.forward_nhwc(x.permute(0, 2, 3, 1), off.permute(0, 2, 3, 1),
+                           m.permute(0, 2, 3, 1), w, None, 1, 1, 1, col_dtype=col_dtype)
+    torch.testing.assert_close(nhwc.permute(0, 3, 1, 2), rounded, rtol=1e-12, atol=1e-12)
+
+
 @pytest.mark.parametrize("stride,pad,dil", [(1, 1, 1), (2, 1, 1), (1, 2, 2)])
 def test_nchw_and_nhwc_restatements_agree(stride, pad, dil):
     x, off, m, w, b, s, p, d = _problem(2, 6, 9, 8, 5, stride=stride, pad=pad, dil=dil, seed=11)
