@@ -37,6 +37,7 @@ HBM_PEAK_GBS = 8000.0
 MFMA_PEAK_TFLOPS = {"fp16": 2516.6, "bf16": 2516.6, "fp32": 157.3}
 METRIC = ("MSDA fwd µs + HBM GB/s (BEVFormer SCA); DCNv2 NHWC fwd µs + MFMA TFLOP/s")
 COUNTER_FILE = os.path.join(ROOT, "profiles", "msda_sca_fp32_counters.txt")
+DCN_COUNTER_FILE = os.path.join(ROOT, "profiles", "dcn_res4_fp16_counters.txt")
 
 
 def parse_args():
@@ -146,13 +147,14 @@ def dcn_nchw_case(name, cache):
     return (lambda: modulated_deform_conv2d(x, off, msk, w, None, 1, 1, 1, 1, 1)), flops
 
 
-def read_counters():
-    """FETCH_SIZE / WRITE_SIZE per dispatch of the SCA fp32 kernel and of a plain copy of
-    known size, from the committed rocprofv3 summary (None if absent)."""
-    if not os.path.exists(COUNTER_FILE):
+def read_counters(path=COUNTER_FILE):
+    """HBM-side bytes per launch from a committed rocprofv3 summary: the kernel's
+    FETCH_SIZE / WRITE_SIZE per dispatch, each scaled by what the same counter reads for a
+    plain copy of known size (None if the summary is absent)."""
+    if not os.path.exists(path):
         return None
     vals = {}
-    with open(COUNTER_FILE) as f:
+    with open(path) as f:
         for line in f:
             line = line.strip()
             if "=" in line and not line.startswith("#"):
@@ -251,6 +253,7 @@ def main():
     mean_us, med_us, wall_us = timer.run(fn, steps, warmup)
     gbs = nbytes / (mean_us * 1e-6) / 1e9
     traffic = read_counters()
+    dcn_traffic = read_counters(DCN_COUNTER_FILE)
     warm_us = Timer(cold=False).run(fn, steps, warmup)[0]
 
     # ---- secondary: DCN res4 fp16 fused -----------------------------------------------
@@ -286,7 +289,7 @@ def main():
             "roofline": {"bound": "mfma", "achieved": round(tflops, 2),
                          "peak": MFMA_PEAK_TFLOPS["fp16"], "unit": "TFLOP/s",
                          "frac": round(tflops / MFMA_PEAK_TFLOPS["fp16"], 4),
-                         "traffic": None}},
+                         "traffic": None if dcn_traffic is None else round(dcn_traffic)}},
     }
 
     if not args.no_configs:

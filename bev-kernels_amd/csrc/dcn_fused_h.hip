@@ -16,6 +16,8 @@
 //     LDS only carries the A tile.
 //   * MFMA v_mfma_f32_32x32x16_{f16,bf16}: each wave owns a 64 x 64 block of the tile.
 //   * Epilogue: fp32 accumulators + bias, one rounding to T.
+//   * Tile order: block b runs on XCD b % 8; each XCD takes a contiguous range of output
+//     tiles, so the image rows its tiles gather from stay in that XCD's L2.
 #include "bevk_common.h"
 #include "bevk_launch.h"
 
@@ -35,6 +37,7 @@ struct HParams {
   void *out;
   int C, H, W, Ho, Wo, Cout, kh, kw, ph, pw, sh, sw, dh, dw, M, K;
   int taps, nb_total, kb_total;  // packed weight blocks: [nb_total][kb_total][64][16 B]
+  int mt, nt, tiles_per_xcd;     // output tiles (M x N) and tiles per XCD
   uint32_t x_bytes, w_bytes;
 };
 
@@ -53,7 +56,9 @@ struct TapGeo {
   uint32_t o[4];
 };
 
-template <typename T, int BM, int BN, int BK, int WM_, int WN_, bool FY>
+// TAPSTEP: C % BK == 0, so every K step lies inside one tap and a thread keeps its corner
+// offsets and weights in registers from one tap to the next.
+template <typename T, int BM, int BN, int BK, int WM_, int WN_, bool FY, bool TAPSTEP>
 __global__ void __launch_bounds__(64 * WM_ * WN_) __attribute__((amdgpu_waves_per_eu(2, 8)))
 dcn_fused_h_kernel(const HParams p) {
   constexpr int NT = 64 * WM_ * WN_, VEC = 8, KV = BK / VEC, KSUB = BK / 16;
@@ -66,7 +71,11 @@ dcn_fused_h_kernel(const HParams p) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN_, wn = wave - (wave / WN_) * WN_;
-  const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
+  // XCD x (= blockIdx % 8) runs tiles [x * tiles_per_xcd, (x + 1) * tiles_per_xcd)
+  const int tile = (int)(blockIdx.x & 7) * p.tiles_per_xcd + (int)(blockIdx.x >> 3);
+  if ((int)(blockIdx.x >> 3) >= p.tiles_per_xcd || tile >= p.mt * p.nt) return;
+  const int mtile = tile / p.nt;
+  const int m0 = mtile * BM, n0 = (tile - mtile * p.nt) * BN;
   const int HoWo = p.Ho * p.Wo, TT = p.taps;
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, p.x_bytes);
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, p.w_bytes);
@@ -123,42 +132,90 @@ dcn_fused_h_kernel(const HParams p) {
     a_t[i] = k / p.C;
     a_c[i] = k - a_t[i] * p.C;
   }
+  const int spt = TAPSTEP ? p.C / BK : 1;   // K steps per tap
   V ra[AV][4];
   float rw[AV][4];
+  float gw[AV][4];      // TAPSTEP: weights and corner offsets of the current tap
+  uint32_t go[AV][4];
   auto issue_a = [&](int ks) {
+    if constexpr (TAPSTEP) {
+      const int t = ks / spt, cstep = ks - t * spt;
+      if (cstep == 0) {
 #pragma unroll
-    for (int i = 0; i < AV; ++i) {
-      if (ks > 0) {
-        a_c[i] += BK;
-        while (a_c[i] >= p.C) { a_c[i] -= p.C; ++a_t[i]; }
-      }
-      TapGeo G;
-      if (a_t[i] < TT) {
-        G = geo[a_row[i] * TT + a_t[i]];
-      } else {  // K tail
-        G.w[0] = G.w[1] = G.w[2] = G.w[3] = 0.f;
-        G.o[0] = G.o[1] = G.o[2] = G.o[3] = xoob;
-      }
-      const uint32_t cb = (uint32_t)a_c[i] * (uint32_t)sizeof(T);
+        for (int i = 0; i < AV; ++i) {
+          TapGeo G;
+          if (t < TT) {
+            G = geo[a_row[i] * TT + t];
+          } else {
+            G.w[0] = G.w[1] = G.w[2] = G.w[3] = 0.f;
+            G.o[0] = G.o[1] = G.o[2] = G.o[3] = xoob;
+          }
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        rw[i][q] = G.w[q];
-        ra[i][q] = buffer_load_vec<T, VEC>(xr, G.o[q] == xoob ? xoob : G.o[q] + cb);
+          for (int q = 0; q < 4; ++q) {
+            gw[i][q] = G.w[q];
+            go[i][q] = G.o[q] == xoob ? xoob : G.o[q] + (uint32_t)(a_kv[i] * VEC) * (uint32_t)sizeof(T);
+          }
+        }
+      }
+      // channel offset of this step is uniform: it goes into the scalar offset
+      const uint32_t so = (uint32_t)(cstep * BK) * (uint32_t)sizeof(T);
+#pragma unroll
+      for (int i = 0; i < AV; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          rw[i][q] = gw[i][q];
+          ra[i][q] = __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(xr, go[i][q], so, 0));
+        }
+    } else {
+#pragma unroll
+      for (int i = 0; i < AV; ++i) {
+        if (ks > 0) {
+          a_c[i] += BK;
+          while (a_c[i] >= p.C) { a_c[i] -= p.C; ++a_t[i]; }
+        }
+        TapGeo G;
+        if (a_t[i] < TT) {
+          G = geo[a_row[i] * TT + a_t[i]];
+        } else {  // K tail
+          G.w[0] = G.w[1] = G.w[2] = G.w[3] = 0.f;
+          G.o[0] = G.o[1] = G.o[2] = G.o[3] = xoob;
+        }
+        const uint32_t cb = (uint32_t)a_c[i] * (uint32_t)sizeof(T);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          rw[i][q] = G.w[q];
+          ra[i][q] = buffer_load_vec<T, VEC>(xr, G.o[q] == xoob ? xoob : G.o[q] + cb);
+        }
       }
     }
   };
+  // B: the block row of fragment column nb starts at bvo[j]; the K block goes into the
+  // scalar offset. An absent column (N tail) gets an offset past the buffer and reads 0.
   int4v breg[2][KSUB][TN];
+  uint32_t bvo[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int nb = (n0 >> 5) + wn * TN + j;
+    bvo[j] = nb < p.nb_total ? ((uint32_t)(nb * p.kb_total) * 64u + (uint32_t)lane) * 16u : woob;
+  }
   auto issue_b = [&](int ks, int4v (&br)[KSUB][TN]) {
+    if (ks * KSUB + KSUB <= p.kb_total) {
 #pragma unroll
-    for (int kk = 0; kk < KSUB; ++kk)
+      for (int kk = 0; kk < KSUB; ++kk)
 #pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int nb = (n0 >> 5) + wn * TN + j, kb = ks * KSUB + kk;
-        const uint32_t o = (nb < p.nb_total && kb < p.kb_total)
-                               ? ((uint32_t)(nb * p.kb_total + kb) * 64u + (uint32_t)lane) * 16u
-                               : woob;
-        br[kk][j] = __builtin_amdgcn_raw_buffer_load_b128(wr, o, 0, 0);
-      }
+        for (int j = 0; j < TN; ++j)
+          br[kk][j] = __builtin_amdgcn_raw_buffer_load_b128(
+              wr, bvo[j], (uint32_t)(ks * KSUB + kk) * 1024u, 0);
+    } else {  // K tail: blocks past kb_total read 0
+#pragma unroll
+      for (int kk = 0; kk < KSUB; ++kk)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int kb = ks * KSUB + kk;
+          br[kk][j] = __builtin_amdgcn_raw_buffer_load_b128(
+              wr, kb < p.kb_total ? bvo[j] : woob, kb < p.kb_total ? (uint32_t)kb * 1024u : 0u, 0);
+        }
+    }
   };
   auto store_a = [&](int buf) {
 #pragma unroll
@@ -207,16 +264,18 @@ dcn_fused_h_kernel(const HParams p) {
   };
 
   // ---- K loop: A(k+1) is gathered and B(k+1) loaded while step k multiplies ---------
+  // Pairs of steps with no exit in the middle of the body (an exit there makes the
+  // compiler keep two copies of the accumulators), then an odd last step.
   const int nk = (p.K + BK - 1) / BK;
   issue_b(0, breg[0]);
   issue_a(0);
   store_a(0);
   if (nk > 1) issue_a(1);
-  for (int ks = 0; ks < nk; ks += 2) {
+  int ks = 0;
+  for (; ks + 1 < nk; ks += 2) {
     __syncthreads();                       // A(ks) complete in buffer 0
-    if (ks + 1 < nk) issue_b(ks + 1, breg[1]);
+    issue_b(ks + 1, breg[1]);
     compute(0, breg[0]);
-    if (ks + 1 >= nk) break;
     store_a(1);                            // A(ks+1) -> buffer 1
     if (ks + 2 < nk) issue_a(ks + 2);
     __syncthreads();
@@ -226,6 +285,10 @@ dcn_fused_h_kernel(const HParams p) {
       store_a(0);                          // A(ks+2) -> buffer 0
       if (ks + 3 < nk) issue_a(ks + 3);
     }
+  }
+  if (ks < nk) {
+    __syncthreads();
+    compute(0, breg[0]);
   }
 
   // ---- epilogue: lane holds col = lane % 32, rows 8*(e/4) + 4*(lane/32) + e%4 --------
@@ -280,23 +343,31 @@ __global__ void __launch_bounds__(256) pack_weight_kc_kernel(const float *__rest
   packed[i] = w[(n * C + c) * T + t];
 }
 
-template <typename T, int BM, int BN, int BK, int WM, int WN>
-hipError_t launch_cfg(const HParams &p, bool fy, hipStream_t stream) {
-  dim3 grid((p.M + BM - 1) / BM, (p.Cout + BN - 1) / BN);
+template <typename T, int BM, int BN, int BK, int WM, int WN, bool TAPSTEP>
+hipError_t launch_cfg(HParams p, bool fy, hipStream_t stream) {
+  p.mt = (p.M + BM - 1) / BM;
+  p.nt = (p.Cout + BN - 1) / BN;
+  p.tiles_per_xcd = (p.mt * p.nt + 7) / 8;
+  const dim3 grid(8 * p.tiles_per_xcd);
   if (fy)
-    hipLaunchKernelGGL((dcn_fused_h_kernel<T, BM, BN, BK, WM, WN, true>), grid, dim3(64 * WM * WN),
-                       0, stream, p);
+    hipLaunchKernelGGL((dcn_fused_h_kernel<T, BM, BN, BK, WM, WN, true, TAPSTEP>), grid,
+                       dim3(64 * WM * WN), 0, stream, p);
   else
-    hipLaunchKernelGGL((dcn_fused_h_kernel<T, BM, BN, BK, WM, WN, false>), grid,
+    hipLaunchKernelGGL((dcn_fused_h_kernel<T, BM, BN, BK, WM, WN, false, TAPSTEP>), grid,
                        dim3(64 * WM * WN), 0, stream, p);
   return hipGetLastError();
 }
 
+template <typename T, bool TAPSTEP>
+hipError_t launch_tt(const HParams &p, bool fy, hipStream_t stream) {
+  if (p.Cout > 128) return launch_cfg<T, 64, 256, 64, 1, 4, TAPSTEP>(p, fy, stream);
+  if (p.Cout > 64) return launch_cfg<T, 64, 128, 64, 2, 2, TAPSTEP>(p, fy, stream);
+  return launch_cfg<T, 64, 64, 64, 2, 2, TAPSTEP>(p, fy, stream);
+}
+
 template <typename T>
 hipError_t launch_t(const HParams &p, bool fy, hipStream_t stream) {
-  if (p.Cout > 128) return launch_cfg<T, 64, 256, 64, 1, 4>(p, fy, stream);
-  if (p.Cout > 64) return launch_cfg<T, 64, 128, 64, 2, 2>(p, fy, stream);
-  return launch_cfg<T, 64, 64, 64, 2, 2>(p, fy, stream);
+  return p.C % 64 == 0 ? launch_tt<T, true>(p, fy, stream) : launch_tt<T, false>(p, fy, stream);
 }
 
 }  // namespace
