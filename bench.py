@@ -131,6 +131,28 @@ def dcn_fused_case(name, dtype, cache):
                                            1, 1, 1, 1, 1, 1, out)), flops
 
 
+def dcn_front_case(name, dtype, cache):
+    """Fused front end (offset conv + sigmoid + gather into the column buffer) of one DCN
+    configuration. Algorithmic bytes: x read once, columns written once, w_off and b_off."""
+    import torch
+    import _modulated_deform_conv_ext as ext
+    from oracle import inputs
+    if name not in cache:
+        cache[name] = inputs.nchw_to_nhwc(inputs.dcn_inputs(name))
+    d = cache[name]
+    dev = torch.device("cuda")
+    x = d["x"].to(dtype).to(dev)
+    B, H, W, C = x.shape
+    g = torch.Generator().manual_seed(11)
+    w_off = (2.0 / (9 * C) ** 0.5 * torch.randn(27, 9, C, generator=g)).to(dtype).to(dev)
+    b_off = torch.randn(27, generator=g).to(dev)
+    col = torch.empty(B * H * W, 9 * C, dtype=dtype, device=dev)
+    es = x.element_size()
+    nbytes = x.numel() * es + col.numel() * es + w_off.numel() * es + 27 * 4
+    return (lambda: ext.modulated_deformable_fused_im2col_nhwc_cuda(
+        x, w_off, b_off, B, C, H, W, H, W, 3, 3, 1, 1, 1, 1, 1, 1, 1, col)), nbytes
+
+
 def dcn_nchw_case(name, cache):
     """Module-level fp32 NCHW forward (modulated_deform_conv2d)."""
     import torch
@@ -235,6 +257,8 @@ def main():
             fn, _ = dcn_fused_case(name, dtype_of(dt), cache)
         elif kind == "dcn_nchw":
             fn, _ = dcn_nchw_case(name, cache)
+        elif kind == "dcn_front":
+            fn, _ = dcn_front_case(name, dtype_of(dt), cache)
         elif kind == "copy":
             # plain copy of known size: the counter calibration reference
             n = int(name) if name else 256 << 20
@@ -315,6 +339,11 @@ def main():
             rows.append({"config": name + "_nchw_module", "dtype": "fp32", "us": round(m, 2),
                          "TFLOP/s": round(tf, 2),
                          "frac_mfma": round(tf / MFMA_PEAK_TFLOPS["fp32"], 4)})
+            f, nb = dcn_front_case(name, dtype_of("fp16"), cache)
+            m, _, _ = timer.run(f, max(10, steps // 2), 3)
+            g = nb / (m * 1e-6) / 1e9
+            rows.append({"config": name + "_front_end", "dtype": "fp16", "us": round(m, 2),
+                         "GB/s": round(g, 1), "frac_hbm": round(g / HBM_PEAK_GBS, 4)})
         line["configs"] = rows
 
     if not args.no_cpu_baseline:

@@ -229,10 +229,35 @@ def modulated_deformable_fused_im2col_nhwc_cuda(data_im, w_off, b_off, batch_siz
                                                 kernel_h, kernel_w, pad_h, pad_w, stride_h,
                                                 stride_w, dilation_h, dilation_w,
                                                 deformable_group, data_col):
-    """Offset conv + gather in one kernel (binding.cpp:72-78). Not in this build yet."""
-    raise RuntimeError(
-        "modulated_deformable_fused_im2col_nhwc_cuda: the fused offset-conv front end is not "
-        "part of this build; use F.conv2d + modulated_deformable_im2col_nhwc_cuda")
+    """Offset conv + sigmoid + NHWC gather (binding.cpp:72-78, dcn_fused_nhwc_cuda.cu:92-126).
+
+    data_im [B, H, W, C]; w_off [3T, T, C] (the offset conv weight permuted (0, 2, 3, 1)) in
+    the input dtype; b_off [3T] float32; data_col [B*Ho*Wo, T*C]. The offset conv runs on
+    the matrix cores with fp32 accumulation and its output stays fp32."""
+    fn = "modulated_deformable_fused_im2col_nhwc_cuda"
+    if deformable_group != 1:
+        raise RuntimeError("NHWC fused path supports deformable_group == 1 only")
+    _b.require_device(fn, data_im, w_off, b_off, data_col)
+    _b.require_contiguous(fn, data_im=data_im, w_off=w_off, b_off=b_off, data_col=data_col)
+    _b.require_dtype(fn, data_im, w_off=w_off, data_col=data_col)
+    if b_off.dtype != torch.float32:
+        raise RuntimeError(f"{fn}: b_off must be float32, got {b_off.dtype}")
+    taps = kernel_h * kernel_w
+    m = batch_size * height_col * width_col
+    _b.require_numel(fn, "data_im", data_im, batch_size * height_im * width_im * channels)
+    _b.require_numel(fn, "w_off", w_off, 3 * taps * taps * channels)
+    _b.require_numel(fn, "b_off", b_off, 3 * taps)
+    _b.require_numel(fn, "data_col", data_col, m * taps * channels)
+    code = _b.dtype_code(data_im)
+    nbytes = _b.lib().bevk_dcn_fused_im2col_nhwc_workspace_bytes(
+        code, batch_size, channels, height_col, width_col, kernel_h, kernel_w)
+    if nbytes < 0:
+        raise RuntimeError(f"{fn}: dtype {data_im.dtype} is not supported")
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=data_im.device)
+    _b.call("bevk_modulated_deformable_fused_im2col_nhwc", code, _b.ptr(data_im), _b.ptr(w_off),
+            _b.ptr(b_off), batch_size, channels, height_im, width_im, height_col, width_col,
+            kernel_h, kernel_w, pad_h, pad_w, stride_h, stride_w, dilation_h, dilation_w,
+            deformable_group, _b.ptr(ws), nbytes, _b.ptr(data_col), _b.stream_of(data_im))
 
 
 # ---------------------------------------------------------------------------------------

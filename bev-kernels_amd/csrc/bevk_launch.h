@@ -37,25 +37,39 @@ hipError_t launch_im2col_nhwc(int dtype, const DcnGeom &g, const void *data_im,
                               const void *data_offset, bool fused_y, const void *data_mask,
                               void *data_col, hipStream_t stream);
 
+// Sample geometry of the fused kernels.
+enum DcnGeo {
+  kGeoMask = 0,     // offsets [M][2T] + mask [M][T]
+  kGeoY = 1,        // raw offset-conv output y [M][3T]; mask = sigmoid(y[2T + t])
+  kGeoRegular = 2,  // no offsets: a plain convolution (fp32 output; offset conv)
+};
+
 // Fused NHWC implicit-GEMM forward (dg == 1). w_packed: layout of launch_dcn_pack_weight.
+// kGeoRegular writes fp32 `out` and ignores data_offset / data_mask / bias.
 hipError_t launch_dcn_fused_nhwc(int dtype, const DcnGeom &g, int channels_out,
-                                 const void *data_im, const void *data_offset, bool fused_y,
+                                 const void *data_im, const void *data_offset, int geo,
                                  const void *data_mask, const void *w_packed,
                                  const void *bias, void *out, hipStream_t stream);
 
 // fp16 / bf16 implicit GEMM with the weight in MFMA-fragment blocks (<= 9 taps).
 bool dcn_fused_h_supported(const DcnGeom &g);
 hipError_t launch_dcn_fused_h(int dtype, const DcnGeom &g, int channels_out, const void *x,
-                              const void *off, bool fused_y, const void *msk,
+                              const void *off, int geo, const void *msk,
                               const void *w_packed, const void *bias, void *out,
                               hipStream_t stream);
 
 // Elements of the packed weight: fp32 Cout * K; half types ceil(Cout/32) * ceil(K/16) * 512.
 int64_t dcn_packed_weight_elems(int dtype, int cout, int K);
-// Module weight [Cout][C][kh*kw] -> packed: fp32 [Cout][kh*kw][C]; fp16 / bf16 MFMA-fragment
-// blocks (block (n/32, k/16), lane (n%32) + 32*((k%16)/8), 8 consecutive k), k = t*C + c,
-// zero outside [0, Cout) x [0, K).
+// Weight [Cout][C][kh*kw] (module layout; [Cout][kh*kw][C] with src_tc) -> packed: fp32
+// [Cout][kh*kw][C]; fp16 / bf16 MFMA-fragment blocks (block (n/32, k/16), lane
+// (n%32) + 32*((k%16)/8), 8 consecutive k), k = t*C + c, zero outside [0, Cout) x [0, K).
 hipError_t launch_dcn_pack_weight(int dtype, const void *weight, int cout, int C, int T,
-                                  void *packed, hipStream_t stream);
+                                  void *packed, hipStream_t stream, bool src_tc = false);
+
+// NHWC gather whose offsets / pre-sigmoid mask come from an fp32 y [M][3T] plus an fp32
+// bias [3T] (the fused front end: y is the offset conv without its bias).
+hipError_t launch_im2col_nhwc_yf32(int dtype, const DcnGeom &g, const void *data_im,
+                                   const float *y, const float *y_bias, void *data_col,
+                                   hipStream_t stream);
 
 }  // namespace bevk

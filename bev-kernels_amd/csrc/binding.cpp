@@ -182,6 +182,88 @@ int bevk_modulated_deformable_im2col_nhwc(
                     fn);
 }
 
+// Workspace of the fused front end: packed offset-conv weight, then y [M][3T] fp32.
+static long long fused_im2col_ws_parts(int dtype, long long m, int taps, int channels,
+                                       long long *y_offset) {
+  const long long packed = bevk::dcn_packed_weight_elems(dtype, 3 * taps, taps * channels) *
+                           dtype_size(dtype);
+  *y_offset = (packed + 255) / 256 * 256;
+  return *y_offset + m * 3 * taps * (long long)sizeof(float);
+}
+
+int64_t bevk_dcn_fused_im2col_nhwc_workspace_bytes(int dtype, int batch_size, int channels,
+                                                   int height_col, int width_col, int kernel_h,
+                                                   int kernel_w) {
+  if (dtype != BEVK_F32 && dtype != BEVK_F16 && dtype != BEVK_BF16) return -1;
+  if (batch_size < 0 || channels < 0 || height_col < 0 || width_col < 0 || kernel_h <= 0 ||
+      kernel_w <= 0)
+    return -1;
+  long long y_offset = 0;
+  return fused_im2col_ws_parts(dtype, (long long)batch_size * height_col * width_col,
+                               kernel_h * kernel_w, channels, &y_offset);
+}
+
+int bevk_modulated_deformable_fused_im2col_nhwc(
+    int dtype, const void *data_im, const void *w_off, const float *b_off, int batch_size,
+    int channels, int height_im, int width_im, int height_col, int width_col, int kernel_h,
+    int kernel_w, int pad_h, int pad_w, int stride_h, int stride_w, int dilation_h,
+    int dilation_w, int deformable_group, void *workspace, int64_t workspace_bytes,
+    void *data_col, void *stream) {
+  const char *fn = "modulated_deformable_fused_im2col_nhwc";
+  g_last_error.clear();
+  // dcn_fused_nhwc_cuda.cu:99-100
+  if (deformable_group != 1)
+    return fail(BEVK_ERR_INVALID, "NHWC fused path supports deformable_group == 1 only");
+  if (dtype != BEVK_F32 && dtype != BEVK_F16 && dtype != BEVK_BF16)
+    return fail(BEVK_ERR_UNSUPPORTED, "\"%s\" not implemented for '%s'", fn, dtype_name(dtype));
+  const bevk::DcnGeom g =
+      make_geom(batch_size, channels, height_im, width_im, height_col, width_col, kernel_h,
+                kernel_w, pad_h, pad_w, stride_h, stride_w, dilation_h, dilation_w, 1);
+  if (int rc = check_geom(fn, g)) return rc;
+  const int taps = kernel_h * kernel_w;
+  if (dtype != BEVK_F32 && taps > 9)
+    return fail(BEVK_ERR_UNSUPPORTED,
+                "%s: kernels of more than 9 taps are fp32-only (use the split path)", fn);
+  const long long m = (long long)batch_size * height_col * width_col;
+  // dcn_fused_nhwc_cuda.cu:101-103
+  if (m * taps * channels >= 2147483647LL)
+    return fail(BEVK_ERR_INVALID, "NHWC fused: Col element count exceeds int32 range");
+  if (m * taps * channels == 0) return ok();
+  const int vec = 16 / dtype_size(dtype);
+  if (channels % vec != 0)
+    return fail(BEVK_ERR_UNSUPPORTED,
+                "%s: channels (%d) must be a positive multiple of %d for '%s'", fn, channels,
+                vec, dtype_name(dtype));
+  if ((long long)batch_size * height_im * width_im * channels * dtype_size(dtype) >
+          kMaxBufferBytes ||
+      m >= (1LL << 30))
+    return fail(BEVK_ERR_INVALID, "%s: problem too large for 32-bit buffer offsets", fn);
+  long long y_offset = 0;
+  const long long need = fused_im2col_ws_parts(dtype, m, taps, channels, &y_offset);
+  if (workspace_bytes < need)
+    return fail(BEVK_ERR_INVALID, "%s: workspace of %lld bytes, %lld needed", fn,
+                (long long)workspace_bytes, need);
+  if (!data_im || !w_off || !b_off || !workspace || !data_col)
+    return fail(BEVK_ERR_INVALID, "%s: null tensor pointer", fn);
+  const hipStream_t st = (hipStream_t)stream;
+  void *packed = workspace;
+  float *y = reinterpret_cast<float *>(static_cast<char *>(workspace) + y_offset);
+  // 1. offset-conv weight [3T][T][C] -> the fused kernel's layout
+  if (int rc = hip_status(bevk::launch_dcn_pack_weight(dtype, w_off, 3 * taps, channels, taps,
+                                                       packed, st, /*src_tc=*/true),
+                          fn))
+    return rc;
+  // 2. y = offset conv without bias, fp32 accumulation, fp32 output (matrix cores)
+  if (int rc = hip_status(bevk::launch_dcn_fused_nhwc(dtype, g, 3 * taps, data_im, nullptr,
+                                                      bevk::kGeoRegular, nullptr, packed,
+                                                      nullptr, y, st),
+                          fn))
+    return rc;
+  // 3. sigmoid, bias and the deformable gather into the columns
+  return hip_status(bevk::launch_im2col_nhwc_yf32(dtype, g, data_im, y, b_off, data_col, st),
+                    fn);
+}
+
 int64_t bevk_dcn_packed_weight_bytes(int dtype, int channels_out, int kernel_h, int kernel_w,
                                       int channels) {
   if (dtype != BEVK_F32 && dtype != BEVK_F16 && dtype != BEVK_BF16) return -1;
@@ -250,7 +332,8 @@ int bevk_dcn_fused_fwd_nhwc(int dtype, const void *data_im, const void *data_off
   if (!data_im || !data_offset || (!fused_y && !data_mask) || !weight_packed || !out)
     return fail(BEVK_ERR_INVALID, "%s: null tensor pointer", fn);
   return hip_status(bevk::launch_dcn_fused_nhwc(dtype, g, channels_out, data_im, data_offset,
-                                                fused_y, data_mask, weight_packed, bias, out,
+                                                fused_y ? bevk::kGeoY : bevk::kGeoMask,
+                                                data_mask, weight_packed, bias, out,
                                                 (hipStream_t)stream),
                     fn);
 }

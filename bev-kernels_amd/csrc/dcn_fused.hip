@@ -72,7 +72,9 @@ template <> struct Mfma<float> {
 // chunk, lanes 32-63 the second).
 template <typename T> constexpr int lane_k() { return Mfma<T>::KSTEP / 2; }
 
-template <typename T, int BM, int BN, int BK, int WAVES_M, int WAVES_N, bool FY>
+// GEO: kGeoMask, kGeoY or kGeoRegular (see bevk_launch.h); kGeoRegular is used with
+// T = float only (the fp32 offset conv of the fused front end).
+template <typename T, int BM, int BN, int BK, int WAVES_M, int WAVES_N, int GEO>
 __global__ void __launch_bounds__(kThreads) dcn_fused_nhwc_kernel(const FusedParams p) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int KV = BK / VEC;                    // 16-byte vectors per tile row per step
@@ -144,10 +146,17 @@ __global__ void __launch_bounds__(kThreads) dcn_fused_nhwc_kernel(const FusedPar
     const int m = a_m[i];
     float w1 = 0.f, w2 = 0.f, w3 = 0.f, w4 = 0.f;
     uint32_t o1 = xoob, o2 = xoob, o3 = xoob, o4 = xoob;
-    if (m >= 0 && t < T_) {
+    if (GEO == kGeoRegular && m >= 0 && t < T_) {
+      const int ki = t / p.kw, kj = t - (t / p.kw) * p.kw;
+      const int h = a_hb[i] + ki * p.dh, w = a_wb[i] + kj * p.dw;
+      if (h >= 0 && h < p.H && w >= 0 && w < p.W) {
+        w1 = 1.f;
+        o1 = (uint32_t)(a_img[i] + h * p.W + w) * (uint32_t)p.C * (uint32_t)sizeof(T);
+      }
+    } else if (m >= 0 && t < T_) {
       float dy, dx, mk;
       const T *offp = static_cast<const T *>(p.off);
-      if constexpr (FY) {
+      if constexpr (GEO == kGeoY) {
         const T *yp = offp + (int64_t)m * 3 * T_;
         dy = (float)yp[2 * t];
         dx = (float)yp[2 * t + 1];
@@ -294,36 +303,42 @@ __global__ void __launch_bounds__(kThreads) dcn_fused_nhwc_kernel(const FusedPar
 }
 
 template <typename T, int BM, int BN, int BK, int WM, int WN>
-hipError_t launch_cfg(const FusedParams &p, bool fy, hipStream_t stream) {
+hipError_t launch_cfg(const FusedParams &p, int geo, hipStream_t stream) {
   dim3 grid(p.tiles_m, (p.Cout + BN - 1) / BN);
-  if (fy)
-    hipLaunchKernelGGL((dcn_fused_nhwc_kernel<T, BM, BN, BK, WM, WN, true>), grid,
+  if (geo == kGeoY)
+    hipLaunchKernelGGL((dcn_fused_nhwc_kernel<T, BM, BN, BK, WM, WN, kGeoY>), grid,
+                       dim3(kThreads), 0, stream, p);
+  else if (geo == kGeoRegular && sizeof(T) == 4)
+    hipLaunchKernelGGL((dcn_fused_nhwc_kernel<T, BM, BN, BK, WM, WN, kGeoRegular>), grid,
+                       dim3(kThreads), 0, stream, p);
+  else if (geo == kGeoMask)
+    hipLaunchKernelGGL((dcn_fused_nhwc_kernel<T, BM, BN, BK, WM, WN, kGeoMask>), grid,
                        dim3(kThreads), 0, stream, p);
   else
-    hipLaunchKernelGGL((dcn_fused_nhwc_kernel<T, BM, BN, BK, WM, WN, false>), grid,
-                       dim3(kThreads), 0, stream, p);
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 
 template <typename T>
-hipError_t launch_t(FusedParams p, bool fy, hipStream_t stream) {
+hipError_t launch_t(FusedParams p, int geo, hipStream_t stream) {
   constexpr int BK = sizeof(T) == 4 ? 16 : 32;
   constexpr int BM = 64;
   p.tiles_m = (p.M + BM - 1) / BM;
-  if (p.Cout > 128) return launch_cfg<T, BM, 256, BK, 1, 4>(p, fy, stream);
-  if (p.Cout > 64) return launch_cfg<T, BM, 128, BK, 1, 4>(p, fy, stream);
-  return launch_cfg<T, BM, 64, BK, 2, 2>(p, fy, stream);
+  if (p.Cout > 128) return launch_cfg<T, BM, 256, BK, 1, 4>(p, geo, stream);
+  if (p.Cout > 64) return launch_cfg<T, BM, 128, BK, 1, 4>(p, geo, stream);
+  return launch_cfg<T, BM, 64, BK, 2, 2>(p, geo, stream);
 }
 
 }  // namespace
 
 hipError_t launch_dcn_fused_nhwc(int dtype, const DcnGeom &g, int channels_out, const void *x,
-                                 const void *off, bool fused_y, const void *msk,
+                                 const void *off, int geo, const void *msk,
                                  const void *w_packed, const void *bias, void *out,
                                  hipStream_t stream) {
   if (dtype != 0 && dcn_fused_h_supported(g))
-    return launch_dcn_fused_h(dtype, g, channels_out, x, off, fused_y, msk, w_packed, bias, out,
+    return launch_dcn_fused_h(dtype, g, channels_out, x, off, geo, msk, w_packed, bias, out,
                               stream);
+  if (dtype != 0 && geo == kGeoRegular) return hipErrorInvalidValue;  // fp32 output only
   FusedParams p;
   p.x = x; p.off = off; p.msk = msk; p.w = w_packed; p.bias = bias; p.out = out;
   p.B = g.batch; p.C = g.channels; p.H = g.height; p.W = g.width;
@@ -338,9 +353,9 @@ hipError_t launch_dcn_fused_nhwc(int dtype, const DcnGeom &g, int channels_out, 
   p.w_bytes = (uint32_t)(dtype == 0 ? (int64_t)channels_out * p.K * 4
                                     : dcn_packed_weight_elems(dtype, channels_out, p.K) * 2);
   switch (dtype) {
-    case 0: return launch_t<float>(p, fused_y, stream);
-    case 1: return launch_t<f16>(p, fused_y, stream);
-    case 2: return launch_t<bf16>(p, fused_y, stream);
+    case 0: return launch_t<float>(p, geo, stream);
+    case 1: return launch_t<f16>(p, geo, stream);
+    case 2: return launch_t<bf16>(p, geo, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -56,9 +56,13 @@ struct TapGeo {
   uint32_t o[4];
 };
 
+// GEO: kGeoMask (offsets [M][2T] + mask [M][T]), kGeoY (raw offset-conv output [M][3T],
+// sigmoid of the mask part here) or kGeoRegular (no offsets: a plain convolution, used for
+// the offset conv of the fused front end). OutT: T, or float for the offset conv.
 // TAPSTEP: C % BK == 0, so every K step lies inside one tap and a thread keeps its corner
 // offsets and weights in registers from one tap to the next.
-template <typename T, int BM, int BN, int BK, int WM_, int WN_, bool FY, bool TAPSTEP>
+template <typename T, typename OutT, int BM, int BN, int BK, int WM_, int WN_, int GEO,
+          bool TAPSTEP>
 __global__ void __launch_bounds__(64 * WM_ * WN_) __attribute__((amdgpu_waves_per_eu(2, 8)))
 dcn_fused_h_kernel(const HParams p) {
   constexpr int NT = 64 * WM_ * WN_, VEC = 8, KV = BK / VEC, KSUB = BK / 16;
@@ -87,11 +91,19 @@ dcn_fused_h_kernel(const HParams p) {
     TapGeo G;
     G.w[0] = G.w[1] = G.w[2] = G.w[3] = 0.f;
     G.o[0] = G.o[1] = G.o[2] = G.o[3] = xoob;
-    if (m < p.M) {
+    if (GEO == kGeoRegular && m < p.M) {
+      const int b = m / HoWo, r = m - b * HoWo, oh = r / p.Wo, ow = r - (r / p.Wo) * p.Wo;
+      const int ki = t / p.kw, kj = t - (t / p.kw) * p.kw;
+      const int h = oh * p.sh - p.ph + ki * p.dh, w = ow * p.sw - p.pw + kj * p.dw;
+      if (h >= 0 && h < p.H && w >= 0 && w < p.W) {
+        G.w[0] = 1.f;
+        G.o[0] = (uint32_t)(b * p.H * p.W + h * p.W + w) * (uint32_t)p.C * (uint32_t)sizeof(T);
+      }
+    } else if (m < p.M) {
       const int b = m / HoWo, r = m - b * HoWo, oh = r / p.Wo, ow = r - (r / p.Wo) * p.Wo;
       float dy, dx, mk;
       const T *op = static_cast<const T *>(p.off);
-      if constexpr (FY) {
+      if constexpr (GEO == kGeoY) {
         const T *yp = op + (int64_t)m * 3 * TT;
         dy = (float)yp[2 * t];
         dx = (float)yp[2 * t + 1];
@@ -159,10 +171,11 @@ dcn_fused_h_kernel(const HParams p) {
       }
       // channel offset of this step is uniform: it goes into the scalar offset
       const uint32_t so = (uint32_t)(cstep * BK) * (uint32_t)sizeof(T);
+      constexpr int NQ = GEO == kGeoRegular ? 1 : 4;   // a plain conv reads one pixel
 #pragma unroll
       for (int i = 0; i < AV; ++i)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < NQ; ++q) {
           rw[i][q] = gw[i][q];
           ra[i][q] = __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(xr, go[i][q], so, 0));
         }
@@ -181,8 +194,9 @@ dcn_fused_h_kernel(const HParams p) {
           G.o[0] = G.o[1] = G.o[2] = G.o[3] = xoob;
         }
         const uint32_t cb = (uint32_t)a_c[i] * (uint32_t)sizeof(T);
+        constexpr int NQ = GEO == kGeoRegular ? 1 : 4;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < NQ; ++q) {
           rw[i][q] = G.w[q];
           ra[i][q] = buffer_load_vec<T, VEC>(xr, G.o[q] == xoob ? xoob : G.o[q] + cb);
         }
@@ -221,7 +235,9 @@ dcn_fused_h_kernel(const HParams p) {
 #pragma unroll
     for (int i = 0; i < AV; ++i) {
       V o;
-      if constexpr (__is_same(T, f16)) {
+      if constexpr (GEO == kGeoRegular) {
+        o = ra[i][0];  // weight 1 on the one in-range pixel; 0 (read as 0) outside
+      } else if constexpr (__is_same(T, f16)) {
         const half2v w1 = {(f16)rw[i][0], (f16)rw[i][0]}, w2 = {(f16)rw[i][1], (f16)rw[i][1]};
         const half2v w3 = {(f16)rw[i][2], (f16)rw[i][2]}, w4 = {(f16)rw[i][3], (f16)rw[i][3]};
 #pragma unroll
@@ -292,7 +308,7 @@ dcn_fused_h_kernel(const HParams p) {
   }
 
   // ---- epilogue: lane holds col = lane % 32, rows 8*(e/4) + 4*(lane/32) + e%4 --------
-  T *out = static_cast<T *>(p.out);
+  OutT *out = static_cast<OutT *>(p.out);
   const T *bias = static_cast<const T *>(p.bias);
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
@@ -303,18 +319,19 @@ dcn_fused_h_kernel(const HParams p) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int m = m0 + wm * WTM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-        if (m < p.M && n < p.Cout) out[(int64_t)m * p.Cout + n] = static_cast<T>(acc[i][j][e] + bv);
+        if (m < p.M && n < p.Cout) out[(int64_t)m * p.Cout + n] = static_cast<OutT>(acc[i][j][e] + bv);
       }
   }
 }
 
-// Module weight [Cout][C][T] -> fragment blocks [NB][KB][64 lanes][8 elements]: lane l of
-// block (nb, kb) holds W[n = nb*32 + l%32][k = kb*16 + (l/32)*8 + e], k = t*C + c, zero
-// outside [0, Cout) x [0, K). One thread per 16-byte output chunk.
+// Weight -> fragment blocks [NB][KB][64 lanes][8 elements]: lane l of block (nb, kb)
+// holds W[n = nb*32 + l%32][k = kb*16 + (l/32)*8 + e], k = t*C + c, zero outside
+// [0, Cout) x [0, K). Source layout [Cout][C][T] (module weight) or, with src_tc,
+// [Cout][T][C]. One thread per 16-byte output chunk.
 __global__ void __launch_bounds__(256) pack_weight_frag_kernel(const uint16_t *__restrict__ w,
                                                                uint16_t *__restrict__ packed,
                                                                int cout, int C, int T, int KB,
-                                                               int64_t chunks) {
+                                                               int64_t chunks, bool src_tc) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= chunks) return;
   const int64_t blk = i >> 6;
@@ -327,47 +344,54 @@ __global__ void __launch_bounds__(256) pack_weight_frag_kernel(const uint16_t *_
   for (int e = 0; e < 8; ++e) {
     const int k = k0 + e;
     const int t = k / C, c = k - (k / C) * C;
-    v.v[e] = (n < cout && k < K) ? w[((int64_t)n * C + c) * T + t] : (uint16_t)0;
+    const int64_t src = src_tc ? ((int64_t)n * T + t) * C + c : ((int64_t)n * C + c) * T + t;
+    v.v[e] = (n < cout && k < K) ? w[src] : (uint16_t)0;
   }
   store_vec<uint16_t, 8>(packed + i * 8, v);
 }
 
-// Module weight [Cout][C][T] -> [Cout][T][C] (fp32), one thread per output element.
+// Weight [Cout][C][T] (or [Cout][T][C] with src_tc) -> [Cout][T][C] (fp32), one thread
+// per output element.
 __global__ void __launch_bounds__(256) pack_weight_kc_kernel(const float *__restrict__ w,
                                                              float *__restrict__ packed, int C,
-                                                             int T, int64_t total) {
+                                                             int T, int64_t total, bool src_tc) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= total) return;
   const int64_t n = i / ((int64_t)T * C);
   const int r = (int)(i - n * T * C), t = r / C, c = r - (r / C) * C;
-  packed[i] = w[(n * C + c) * T + t];
+  packed[i] = src_tc ? w[i] : w[(n * C + c) * T + t];
 }
 
-template <typename T, int BM, int BN, int BK, int WM, int WN, bool TAPSTEP>
-hipError_t launch_cfg(HParams p, bool fy, hipStream_t stream) {
+template <typename T, typename OutT, int BM, int BN, int BK, int WM, int WN, bool TAPSTEP>
+hipError_t launch_cfg(HParams p, int geo, hipStream_t stream) {
   p.mt = (p.M + BM - 1) / BM;
   p.nt = (p.Cout + BN - 1) / BN;
   p.tiles_per_xcd = (p.mt * p.nt + 7) / 8;
-  const dim3 grid(8 * p.tiles_per_xcd);
-  if (fy)
-    hipLaunchKernelGGL((dcn_fused_h_kernel<T, BM, BN, BK, WM, WN, true, TAPSTEP>), grid,
-                       dim3(64 * WM * WN), 0, stream, p);
+  const dim3 grid(8 * p.tiles_per_xcd), block(64 * WM * WN);
+  if (geo == kGeoY)
+    hipLaunchKernelGGL((dcn_fused_h_kernel<T, OutT, BM, BN, BK, WM, WN, kGeoY, TAPSTEP>), grid,
+                       block, 0, stream, p);
+  else if (geo == kGeoRegular)
+    hipLaunchKernelGGL((dcn_fused_h_kernel<T, OutT, BM, BN, BK, WM, WN, kGeoRegular, TAPSTEP>),
+                       grid, block, 0, stream, p);
   else
-    hipLaunchKernelGGL((dcn_fused_h_kernel<T, BM, BN, BK, WM, WN, false, TAPSTEP>), grid,
-                       dim3(64 * WM * WN), 0, stream, p);
+    hipLaunchKernelGGL((dcn_fused_h_kernel<T, OutT, BM, BN, BK, WM, WN, kGeoMask, TAPSTEP>),
+                       grid, block, 0, stream, p);
   return hipGetLastError();
 }
 
 template <typename T, bool TAPSTEP>
-hipError_t launch_tt(const HParams &p, bool fy, hipStream_t stream) {
-  if (p.Cout > 128) return launch_cfg<T, 64, 256, 64, 1, 4, TAPSTEP>(p, fy, stream);
-  if (p.Cout > 64) return launch_cfg<T, 64, 128, 64, 2, 2, TAPSTEP>(p, fy, stream);
-  return launch_cfg<T, 64, 64, 64, 2, 2, TAPSTEP>(p, fy, stream);
+hipError_t launch_tt(const HParams &p, int geo, hipStream_t stream) {
+  if (geo == kGeoRegular)  // offset conv: Cout = 3T <= 27, fp32 output
+    return launch_cfg<T, float, 64, 64, 64, 2, 2, TAPSTEP>(p, geo, stream);
+  if (p.Cout > 128) return launch_cfg<T, T, 64, 256, 64, 1, 4, TAPSTEP>(p, geo, stream);
+  if (p.Cout > 64) return launch_cfg<T, T, 64, 128, 64, 2, 2, TAPSTEP>(p, geo, stream);
+  return launch_cfg<T, T, 64, 64, 64, 2, 2, TAPSTEP>(p, geo, stream);
 }
 
 template <typename T>
-hipError_t launch_t(const HParams &p, bool fy, hipStream_t stream) {
-  return p.C % 64 == 0 ? launch_tt<T, true>(p, fy, stream) : launch_tt<T, false>(p, fy, stream);
+hipError_t launch_t(const HParams &p, int geo, hipStream_t stream) {
+  return p.C % 64 == 0 ? launch_tt<T, true>(p, geo, stream) : launch_tt<T, false>(p, geo, stream);
 }
 
 }  // namespace
@@ -379,14 +403,14 @@ int64_t dcn_packed_weight_elems(int dtype, int cout, int K) {
 }
 
 hipError_t launch_dcn_pack_weight(int dtype, const void *weight, int cout, int C, int T,
-                                  void *packed, hipStream_t stream) {
+                                  void *packed, hipStream_t stream, bool src_tc) {
   const int K = C * T;
   if (dtype == 0) {
     const int64_t total = (int64_t)cout * K;
     if (total == 0) return hipSuccess;
     hipLaunchKernelGGL(pack_weight_kc_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                        stream, static_cast<const float *>(weight), static_cast<float *>(packed),
-                       C, T, total);
+                       C, T, total, src_tc);
     return hipGetLastError();
   }
   const int KB = (K + 15) / 16;
@@ -394,14 +418,14 @@ hipError_t launch_dcn_pack_weight(int dtype, const void *weight, int cout, int C
   if (chunks == 0) return hipSuccess;
   hipLaunchKernelGGL(pack_weight_frag_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256),
                      0, stream, static_cast<const uint16_t *>(weight),
-                     static_cast<uint16_t *>(packed), cout, C, T, KB, chunks);
+                     static_cast<uint16_t *>(packed), cout, C, T, KB, chunks, src_tc);
   return hipGetLastError();
 }
 
 bool dcn_fused_h_supported(const DcnGeom &g) { return g.kernel_h * g.kernel_w <= kMaxTaps; }
 
 hipError_t launch_dcn_fused_h(int dtype, const DcnGeom &g, int channels_out, const void *x,
-                              const void *off, bool fused_y, const void *msk,
+                              const void *off, int geo, const void *msk,
                               const void *w_packed, const void *bias, void *out,
                               hipStream_t stream) {
   HParams p;
@@ -418,8 +442,8 @@ hipError_t launch_dcn_fused_h(int dtype, const DcnGeom &g, int channels_out, con
   p.x_bytes = (uint32_t)((int64_t)g.batch * g.height * g.width * g.channels * 2);
   p.w_bytes = (uint32_t)(dcn_packed_weight_elems(dtype, channels_out, p.K) * 2);
   switch (dtype) {
-    case 1: return launch_t<f16>(p, fused_y, stream);
-    case 2: return launch_t<bf16>(p, fused_y, stream);
+    case 1: return launch_t<f16>(p, geo, stream);
+    case 2: return launch_t<bf16>(p, geo, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -106,10 +106,13 @@ __global__ void __launch_bounds__(kBlock) im2col_nchw_kernel(
 // Consecutive pairs are consecutive taps of one pixel, so one pixel's 9*C column
 // row is written contiguously.
 // ---------------------------------------------------------------------------
-template <typename T, int VEC, bool FUSED_Y>
+// FUSED_Y: offsets / pre-sigmoid mask from y [M][3T] of type Y (T, or float plus an fp32
+// bias [3T] for the fused front end); otherwise offsets [M][2T] and mask [M][T] of type T.
+template <typename T, int VEC, bool FUSED_Y, typename Y = T>
 __global__ void __launch_bounds__(kBlock) im2col_nhwc_kernel(
-    const T *__restrict__ im, const T *__restrict__ offset, const T *__restrict__ mask,
-    T *__restrict__ col, const DcnGeom g, int lpp_log2, uint32_t img_bytes) {
+    const T *__restrict__ im, const Y *__restrict__ offset, const T *__restrict__ mask,
+    T *__restrict__ col, const DcnGeom g, int lpp_log2, uint32_t img_bytes,
+    const float *__restrict__ y_bias = nullptr) {
   const int T_ = g.kernel_h * g.kernel_w;
   const int HoWo = g.height_col * g.width_col;
   const int b = blockIdx.y;
@@ -124,10 +127,16 @@ __global__ void __launch_bounds__(kBlock) im2col_nhwc_kernel(
 
   float dy, dx, mk;
   if constexpr (FUSED_Y) {  // y [B, Ho, Wo, 3T]: offsets then pre-sigmoid mask
-    const T *yp = offset + m * 3 * T_;
+    const Y *yp = offset + m * 3 * T_;
     dy = (float)yp[2 * t];
     dx = (float)yp[2 * t + 1];
-    mk = sigmoid_f32((float)yp[2 * T_ + t]);
+    float ym = (float)yp[2 * T_ + t];
+    if (y_bias != nullptr) {
+      dy += y_bias[2 * t];
+      dx += y_bias[2 * t + 1];
+      ym += y_bias[2 * T_ + t];
+    }
+    mk = sigmoid_f32(ym);
   } else {
     dy = (float)offset[m * 2 * T_ + 2 * t];
     dx = (float)offset[m * 2 * T_ + 2 * t + 1];
@@ -200,9 +209,9 @@ hipError_t launch_nchw_t(const DcnGeom &g, const void *im, const void *off, cons
   return hipGetLastError();
 }
 
-template <typename T, bool FY>
+template <typename T, bool FY, typename Y = T>
 hipError_t launch_nhwc_t(const DcnGeom &g, const void *im, const void *off, const void *msk,
-                         void *col, hipStream_t stream) {
+                         void *col, hipStream_t stream, const float *y_bias = nullptr) {
   constexpr int VEC = 16 / sizeof(T);
   const int C = g.channels;
   const bool vec = (C % VEC) == 0;
@@ -217,15 +226,15 @@ hipError_t launch_nhwc_t(const DcnGeom &g, const void *im, const void *off, cons
   dim3 grid((unsigned)((threads + kBlock - 1) / kBlock), g.batch);
   const uint32_t img_bytes = (uint32_t)((int64_t)g.height * g.width * C * sizeof(T));
   if (vec)
-    hipLaunchKernelGGL((im2col_nhwc_kernel<T, VEC, FY>), grid, dim3(kBlock), 0, stream,
-                       static_cast<const T *>(im), static_cast<const T *>(off),
+    hipLaunchKernelGGL((im2col_nhwc_kernel<T, VEC, FY, Y>), grid, dim3(kBlock), 0, stream,
+                       static_cast<const T *>(im), static_cast<const Y *>(off),
                        static_cast<const T *>(msk), static_cast<T *>(col), g, lpp_log2,
-                       img_bytes);
+                       img_bytes, y_bias);
   else
-    hipLaunchKernelGGL((im2col_nhwc_kernel<T, 1, FY>), grid, dim3(kBlock), 0, stream,
-                       static_cast<const T *>(im), static_cast<const T *>(off),
+    hipLaunchKernelGGL((im2col_nhwc_kernel<T, 1, FY, Y>), grid, dim3(kBlock), 0, stream,
+                       static_cast<const T *>(im), static_cast<const Y *>(off),
                        static_cast<const T *>(msk), static_cast<T *>(col), g, lpp_log2,
-                       img_bytes);
+                       img_bytes, y_bias);
   return hipGetLastError();
 }
 
@@ -253,6 +262,16 @@ hipError_t launch_im2col_nhwc(int dtype, const DcnGeom &g, const void *im, const
                            : launch_nhwc_t<bf16, false>(g, im, off, msk, col, stream);
     case 3: return fused_y ? launch_nhwc_t<double, true>(g, im, off, msk, col, stream)
                            : launch_nhwc_t<double, false>(g, im, off, msk, col, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_im2col_nhwc_yf32(int dtype, const DcnGeom &g, const void *im, const float *y,
+                                   const float *y_bias, void *col, hipStream_t stream) {
+  switch (dtype) {
+    case 0: return launch_nhwc_t<float, true, float>(g, im, y, nullptr, col, stream, y_bias);
+    case 1: return launch_nhwc_t<f16, true, float>(g, im, y, nullptr, col, stream, y_bias);
+    case 2: return launch_nhwc_t<bf16, true, float>(g, im, y, nullptr, col, stream, y_bias);
     default: return hipErrorInvalidValue;
   }
 }

@@ -97,6 +97,32 @@ int bevk_modulated_deformable_im2col_nhwc(
     int stride_h, int stride_w, int dilation_h, int dilation_w, int deformable_group,
     void *data_col, void *stream);
 
+/* Workspace bytes bevk_modulated_deformable_fused_im2col_nhwc needs (-1 on bad
+ * arguments): the packed offset-conv weight and the fp32 offset-conv output [M][3T]. */
+int64_t bevk_dcn_fused_im2col_nhwc_workspace_bytes(int dtype, int batch_size, int channels,
+                                                   int height_col, int width_col, int kernel_h,
+                                                   int kernel_w);
+
+/* Fused NHWC front end: offset conv + sigmoid + deformable gather.
+ *   data_im   [B, H, W, C]
+ *   w_off     [3T, T, C] (= torch weight [3T, C, kh, kw].permute(0, 2, 3, 1)), dtype
+ *   b_off     [3T] fp32
+ *   data_col  [B*Ho*Wo, T*C], fully written
+ * y = conv(x, w_off) + b_off is accumulated in fp32 and kept in fp32 (matrix cores, with the
+ * same stride / padding / dilation as the deformable taps); offsets = y[:, :2T] ((dy, dx) per
+ * tap), mask = sigmoid(y[:, 2T:3T]); then the NHWC gather. `workspace` (device memory of at
+ * least bevk_dcn_fused_im2col_nhwc_workspace_bytes) holds the packed w_off and y.
+ * Replaces binding.cpp:72-78 modulated_deformable_fused_im2col_nhwc_cuda
+ * (dcn_fused_nhwc_cuda.cu:92-126, kernel dcn_fused_nhwc_kernel.cuh:211-303). dg == 1.
+ * dtypes F32 (any kernel size), F16 / BF16 (at most 9 taps); C a multiple of 16 bytes'
+ * worth of elements. */
+int bevk_modulated_deformable_fused_im2col_nhwc(
+    int dtype, const void *data_im, const void *w_off, const float *b_off, int batch_size,
+    int channels, int height_im, int width_im, int height_col, int width_col, int kernel_h,
+    int kernel_w, int pad_h, int pad_w, int stride_h, int stride_w, int dilation_h,
+    int dilation_w, int deformable_group, void *workspace, int64_t workspace_bytes,
+    void *data_col, void *stream);
+
 /* Bytes of the packed weight that bevk_dcn_fused_fwd_nhwc consumes for this shape
  * (-1 for an unsupported dtype). */
 int64_t bevk_dcn_packed_weight_bytes(int dtype, int channels_out, int kernel_h, int kernel_w,

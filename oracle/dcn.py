@@ -18,6 +18,7 @@ from __future__ import annotations
 import math
 
 import torch
+import torch.nn.functional as F
 
 
 def out_size(size, pad, dil, k, stride):
@@ -186,6 +187,25 @@ def forward_nhwc(x, offset, mask, weight, bias=None, stride=1, padding=0, dilati
     if bias is not None:
         out = out + bias.view(1, 1, 1, -1)
     return out
+
+
+def fused_front_end_columns(x, w_off_tc, b_off, kh, kw, stride=1, padding=0, dilation=1,
+                            col_dtype=None):
+    """Fused NHWC front end (K12, dcn_fused_nhwc_kernel.cuh:211-303): y = conv(x, w_off) +
+    b_off with the deformable taps' stride / padding / dilation (:236-258), offsets =
+    y[..., :2T] ((dy, dx) per tap, :266-267), mask = sigmoid(y[..., 2T:3T]) (:268), then the
+    NHWC columns (:270-301). x [B, H, W, C]; w_off_tc [3T, T, C] (= [3T, C, kh, kw]
+    permuted (0, 2, 3, 1)); b_off [3T]."""
+    def two(v):
+        return (v, v) if isinstance(v, int) else tuple(v)
+    (sh, sw), (ph, pw), (dh, dw) = two(stride), two(padding), two(dilation)
+    T = kh * kw
+    C = x.shape[-1]
+    w_nchw = w_off_tc.reshape(3 * T, kh, kw, C).permute(0, 3, 1, 2)
+    y = F.conv2d(x.permute(0, 3, 1, 2), w_nchw, b_off, (sh, sw), (ph, pw), (dh, dw))
+    off, mask = split_y_nhwc(y.permute(0, 2, 3, 1), T)
+    cols = columns_nhwc(x, off, mask, kh, kw, sh, sw, ph, pw, dh, dw)
+    return _round_cols(cols, col_dtype)
 
 
 def split_y_nhwc(y, taps):

@@ -100,6 +100,33 @@ def test_packed_weight_bytes():
     assert f(1, 8, 0, 3, 8) == -1
 
 
+def test_fused_im2col_workspace_bytes():
+    f = _bevk.lib().bevk_dcn_fused_im2col_nhwc_workspace_bytes
+    packed = 1 * 144 * 512 * 2                                  # 27 -> one 32-column block
+    y_off = (packed + 255) // 256 * 256
+    assert f(1, 6, 256, 58, 100, 3, 3) == y_off + 6 * 58 * 100 * 27 * 4
+    assert f(0, 1, 8, 4, 4, 3, 3) == (27 * 72 * 4 + 255) // 256 * 256 + 16 * 27 * 4
+    assert f(3, 1, 8, 4, 4, 3, 3) == -1
+    assert f(1, 1, 8, 4, 4, 0, 3) == -1
+
+
+def _front(dtype=1, c=16, dg=1, kh=3, kw=3, ws=1 << 20, b=1):
+    ho = 5 + 2 - kh + 1                                          # pad 1, stride 1, dilation 1
+    return _bevk.lib().bevk_modulated_deformable_fused_im2col_nhwc(
+        dtype, NULL, NULL, NULL, b, c, 5, 5, ho, ho, kh, kw, 1, 1, 1, 1, 1, 1, dg, NULL, ws,
+        NULL, NULL)
+
+
+def test_fused_im2col_validation():
+    assert _front(dg=2) == INVALID and "deformable_group == 1" in _err()
+    assert _front(dtype=3) == UNSUPPORTED and "Double" in _err()
+    assert _front(kh=5, kw=5) == UNSUPPORTED and "9 taps" in _err()
+    assert _front(c=12) == UNSUPPORTED and "multiple of 8" in _err()
+    assert _front(ws=16) == INVALID and "workspace" in _err()
+    assert _front() == INVALID and "null" in _err()
+    assert _front(b=0) == 0
+
+
 def test_pack_weight_validation():
     f = _bevk.lib().bevk_dcn_pack_weight
     assert f(3, NULL, 8, 3, 3, 8, NULL, NULL) == UNSUPPORTED and "Double" in _err()

@@ -250,6 +250,69 @@ def test_dcn_split_nhwc_half_3t(dtype):
     check(out.cpu(), ref, dtype, "split 3T half")
 
 
+# ---------------------------------------------------------------------------------------
+# Fused front end: offset conv + sigmoid + gather (ext.modulated_deformable_fused_im2col_nhwc)
+# ---------------------------------------------------------------------------------------
+
+def _front_problem(b, cin, h, w, k, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    T = k * k
+    x = torch.randn(b, h, w, cin, generator=g).to(dtype)
+    # offset-conv outputs of a few pixels, as a trained offset conv gives
+    w_off = (2.0 / (T * cin) ** 0.5 * torch.randn(3 * T, T, cin, generator=g)).to(dtype)
+    b_off = torch.randn(3 * T, generator=g)
+    return x, w_off, b_off
+
+
+def _front_run(x, w_off, b_off, k, s, p, dl):
+    b, h, w, cin = x.shape
+    ho, wo = od.out_size(h, p, dl, k, s), od.out_size(w, p, dl, k, s)
+    col = torch.empty(b * ho * wo, k * k * cin, dtype=x.dtype, device=DEV)
+    _ext().modulated_deformable_fused_im2col_nhwc_cuda(
+        x.to(DEV), w_off.to(DEV), b_off.to(DEV), b, cin, h, w, ho, wo, k, k, p, p, s, s, dl, dl,
+        1, col)
+    torch.cuda.synchronize()
+    return col.cpu()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16],
+                         ids=["fp32", "fp16", "bf16"])
+@pytest.mark.parametrize("geom", [
+    # b, cin, h, w, k, stride, pad, dil
+    (2, 32, 11, 13, 3, 1, 1, 1),
+    (1, 64, 16, 12, 3, 2, 1, 1),
+    (1, 16, 9, 9, 3, 1, 2, 2),
+    (1, 8, 6, 7, 1, 1, 0, 1),
+])
+def test_fused_front_end(dtype, geom):
+    b, cin, h, w, k, s, p, dl = geom
+    x, w_off, b_off = _front_problem(b, cin, h, w, k, dtype, sum(geom))
+    col = _front_run(x, w_off, b_off, k, s, p, dl)
+    ref = od.fused_front_end_columns(x.double(), w_off.double(), b_off.double(), k, k, s, p, dl,
+                                     col_dtype=_cols_dtype(dtype))
+    check(col, ref, dtype, f"front end {geom}")
+
+
+def test_fused_front_end_fp32_large_kernel():
+    x, w_off, b_off = _front_problem(1, 8, 10, 9, 5, torch.float32, 7)
+    col = _front_run(x, w_off, b_off, 5, 1, 2, 1)
+    ref = od.fused_front_end_columns(x.double(), w_off.double(), b_off.double(), 5, 5, 1, 2, 1)
+    check(col, ref, torch.float32, "front end 5x5")
+
+
+def test_fused_front_end_res4_fp16():
+    """BASELINE res4 shape (B=6, 256 channels, 58x100), first and last image vs the oracle."""
+    d = inputs.nchw_to_nhwc(inputs.dcn_inputs("dcn_res4"))
+    x = d["x"].to(torch.float16)
+    _, w_off, b_off = _front_problem(1, 256, 1, 1, 3, torch.float16, 11)
+    col = _front_run(x, w_off, b_off, 3, 1, 1, 1).view(6, -1, 9 * 256)
+    assert torch.isfinite(col.float()).all()
+    for b in (0, 5):
+        ref = od.fused_front_end_columns(x[b:b + 1].double(), w_off.double(), b_off.double(), 3,
+                                         3, 1, 1, 1, col_dtype=torch.float16)
+        check(col[b], ref, torch.float16, f"front end res4 image {b}")
+
+
 def test_fused_matches_gather_plus_gemm():
     """Fused kernel == explicit columns (NHWC gather kernel) @ weight, same inputs."""
     d = inputs.nchw_to_nhwc(_rand_problem(2, 64, 128, 20, 24, seed=5, dtype=torch.float32))

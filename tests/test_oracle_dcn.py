@@ -132,6 +132,30 @@ def test_linearity():
     torch.testing.assert_close(od.forward_nchw(x, off, 0.25 * m, w, None, s, p, d), 0.25 * base)
 
 
+def test_fused_front_end_reduces_to_constant_offsets():
+    """w_off = 0: y is b_off everywhere, so the front end is the NHWC columns with one
+    constant (dy, dx) per tap and mask sigmoid(b); a weight on one input channel moves the
+    offsets by that channel's conv."""
+    g = torch.Generator().manual_seed(14)
+    x = torch.randn(2, 7, 6, 5, generator=g, dtype=D64)
+    T = 9
+    b_off = torch.randn(3 * T, generator=g, dtype=D64)
+    w0 = torch.zeros(3 * T, T, 5, dtype=D64)
+    cols = od.fused_front_end_columns(x, w0, b_off, 3, 3, 1, 1, 1)
+    off = b_off[:2 * T].expand(2, 7, 6, 2 * T)
+    msk = torch.sigmoid(b_off[2 * T:]).expand(2, 7, 6, T)
+    torch.testing.assert_close(cols, od.columns_nhwc(x, off, msk, 3, 3, 1, 1, 1, 1, 1, 1),
+                               rtol=0, atol=0)
+    # centre-tap weight 1 on channel 0 for the dy of tap 4: dy = x[..., 0] + b
+    w1 = w0.clone()
+    w1[8, 4, 0] = 1.0
+    cols = od.fused_front_end_columns(x, w1, b_off, 3, 3, 1, 1, 1)
+    off2 = off.clone()
+    off2[..., 8] = off2[..., 8] + x[..., 0]
+    torch.testing.assert_close(cols, od.columns_nhwc(x, off2, msk, 3, 3, 1, 1, 1, 1, 1, 1),
+                               rtol=1e-12, atol=1e-12)
+
+
 @pytest.mark.parametrize("col_dtype", [torch.float16, torch.bfloat16])
 def test_column_rounding(col_dtype):
     """col_dtype rounds each column once: exact columns are unchanged, and in general the
