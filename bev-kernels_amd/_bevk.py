@@ -34,6 +34,10 @@ _SIGNATURES = {
     "bevk_modulated_deformable_im2col": [_i, _vp, _vp, _vp] + [_i] * 15 + [_vp, _vp],
     "bevk_modulated_deformable_im2col_opt": [_i, _vp, _vp, _vp] + [_i] * 15 + [_vp, _vp],
     "bevk_modulated_deformable_im2col_nhwc": [_i, _vp, _vp, _i, _vp] + [_i] * 15 + [_vp, _vp],
+    "bevk_modulated_deformable_col2im_nchw": [_i, _vp, _vp, _vp, _vp] + [_i] * 15
+    + [_vp, _vp, _vp, _vp],
+    "bevk_modulated_deformable_col2im_nhwc": [_i, _vp, _vp, _vp, _i, _vp] + [_i] * 15
+    + [_vp, _vp, _vp, _vp],
     "bevk_dcn_fused_im2col_nhwc_workspace_bytes": [_i] * 7,
     "bevk_modulated_deformable_fused_im2col_nhwc": [_i, _vp, _vp, _vp] + [_i] * 15
     + [_vp, ctypes.c_int64, _vp, _vp],

@@ -193,35 +193,175 @@ def dcn_fused_fwd_nhwc(data_im, data_offset, data_mask, weight_packed, bias, bat
             dilation_w, _b.ptr(out), _b.stream_of(data_im))
 
 
-def _backward_absent(name):
-    def fn(*args, **kwargs):
-        raise RuntimeError(
-            f"{name}: the backward kernels are not part of this build (forward operators only)")
+def _col2im_nchw(fn, data_col, data_im, data_offset, data_mask, batch_size, channels,
+                 height_im, width_im, height_col, width_col, kernel_h, kernel_w, pad_h, pad_w,
+                 stride_h, stride_w, dilation_h, dilation_w, deformable_group, grad_im,
+                 grad_offset, grad_mask):
+    _b.require_device(fn, data_col, data_im, data_offset, data_mask, grad_im, grad_offset,
+                      grad_mask)
+    _b.require_contiguous(fn, data_col=data_col, data_im=data_im, data_offset=data_offset,
+                          data_mask=data_mask, grad_im=grad_im, grad_offset=grad_offset,
+                          grad_mask=grad_mask)
+    _b.require_dtype(fn, data_col, data_im=data_im, data_offset=data_offset,
+                     data_mask=data_mask, grad_im=grad_im, grad_offset=grad_offset,
+                     grad_mask=grad_mask)
+    if deformable_group <= 0:
+        raise RuntimeError(f"{fn}: deformable_group must be positive")
+    taps = kernel_h * kernel_w
+    plane = height_col * width_col
+    _b.require_numel(fn, "data_col", data_col, channels * taps * batch_size * plane)
+    if data_im is not None:
+        _b.require_numel(fn, "data_im", data_im, batch_size * channels * height_im * width_im)
+    _b.require_numel(fn, "data_offset", data_offset,
+                     batch_size * deformable_group * 2 * taps * plane)
+    _b.require_numel(fn, "data_mask", data_mask, batch_size * deformable_group * taps * plane)
+    if grad_im is not None:
+        _b.require_numel(fn, "grad_im", grad_im, batch_size * channels * height_im * width_im)
+    if grad_offset is not None:
+        _b.require_numel(fn, "grad_offset", grad_offset,
+                         batch_size * deformable_group * 2 * taps * plane)
+        _b.require_numel(fn, "grad_mask", grad_mask,
+                         batch_size * deformable_group * taps * plane)
+    _b.call("bevk_modulated_deformable_col2im_nchw", _b.dtype_code(data_col),
+            _b.ptr(data_col), _b.ptr(data_im), _b.ptr(data_offset), _b.ptr(data_mask),
+            batch_size, channels, height_im, width_im, height_col, width_col, kernel_h,
+            kernel_w, pad_h, pad_w, stride_h, stride_w, dilation_h, dilation_w,
+            deformable_group, _b.ptr(grad_im), _b.ptr(grad_offset), _b.ptr(grad_mask),
+            _b.stream_of(data_col))
+
+
+def _col2im_entry(name):
+    def fn(data_col, data_offset, data_mask, batch_size, channels, height_im, width_im,
+           height_col, width_col, kernel_h, kernel_w, pad_h, pad_w, stride_h, stride_w,
+           dilation_h, dilation_w, deformable_group, grad_im):
+        _col2im_nchw(name, data_col, None, data_offset, data_mask, batch_size, channels,
+                     height_im, width_im, height_col, width_col, kernel_h, kernel_w, pad_h,
+                     pad_w, stride_h, stride_w, dilation_h, dilation_w, deformable_group,
+                     grad_im, None, None)
     fn.__name__ = name
-    fn.__doc__ = "Backward entry point of the reference; not implemented in this build."
+    fn.__doc__ = ("NCHW backward column-to-image: grad_im [B,C,H,W] (input dtype) "
+                  "accumulated from data_col [C*kh*kw, B*Ho*Wo]; zero it first.")
     return fn
 
 
-modulated_deformable_col2im_cuda = _backward_absent("modulated_deformable_col2im_cuda")
-modulated_deformable_col2im_opt_cuda = _backward_absent("modulated_deformable_col2im_opt_cuda")
-modulated_deformable_col2im_smem_cuda = _backward_absent("modulated_deformable_col2im_smem_cuda")
-modulated_deformable_col2im_coord_cuda = _backward_absent(
+def _col2im_coord_entry(name):
+    def fn(data_col, data_im, data_offset, data_mask, batch_size, channels, height_im,
+           width_im, height_col, width_col, kernel_h, kernel_w, pad_h, pad_w, stride_h,
+           stride_w, dilation_h, dilation_w, deformable_group, grad_offset, grad_mask):
+        _col2im_nchw(name, data_col, data_im, data_offset, data_mask, batch_size, channels,
+                     height_im, width_im, height_col, width_col, kernel_h, kernel_w, pad_h,
+                     pad_w, stride_h, stride_w, dilation_h, dilation_w, deformable_group,
+                     None, grad_offset, grad_mask)
+    fn.__name__ = name
+    fn.__doc__ = ("NCHW backward: grad_offset [B,dg*2T,Ho,Wo] and grad_mask [B,dg*T,Ho,Wo] "
+                  "(input dtype), written.")
+    return fn
+
+
+# binding.cpp:13-19, :29-58. One kernel serves the reference's variants of each step.
+modulated_deformable_col2im_cuda = _col2im_entry("modulated_deformable_col2im_cuda")
+modulated_deformable_col2im_opt_cuda = _col2im_entry("modulated_deformable_col2im_opt_cuda")
+modulated_deformable_col2im_smem_cuda = _col2im_entry("modulated_deformable_col2im_smem_cuda")
+modulated_deformable_col2im_coord_cuda = _col2im_coord_entry(
     "modulated_deformable_col2im_coord_cuda")
-modulated_deformable_col2im_coord_opt_cuda = _backward_absent(
+modulated_deformable_col2im_coord_opt_cuda = _col2im_coord_entry(
     "modulated_deformable_col2im_coord_opt_cuda")
-modulated_deformable_col2im_nhwc_cuda = _backward_absent("modulated_deformable_col2im_nhwc_cuda")
-modulated_deformable_col2im_coord_nhwc_cuda = _backward_absent(
-    "modulated_deformable_col2im_coord_nhwc_cuda")
-modulated_deformable_gradx_smem_nhwc_cuda = _backward_absent(
-    "modulated_deformable_gradx_smem_nhwc_cuda")
-modulated_deformable_gradx_gather_nhwc_cuda = _backward_absent(
-    "modulated_deformable_gradx_gather_nhwc_cuda")
-modulated_deformable_col2im_fused_smem_nhwc_cuda = _backward_absent(
-    "modulated_deformable_col2im_fused_smem_nhwc_cuda")
-modulated_deformable_col2im_perelem_nhwc_cuda = _backward_absent(
-    "modulated_deformable_col2im_perelem_nhwc_cuda")
-modulated_deformable_col2im_perelem_smem_nhwc_cuda = _backward_absent(
-    "modulated_deformable_col2im_perelem_smem_nhwc_cuda")
+
+
+def _col2im_nhwc(fn, dcol, data_im, data_offset, data_mask, batch_size, channels, height_im,
+                 width_im, height_col, width_col, kernel_h, kernel_w, pad_h, pad_w, stride_h,
+                 stride_w, dilation_h, dilation_w, deformable_group, grad_im, grad_offset,
+                 grad_mask):
+    if deformable_group != 1:
+        raise RuntimeError("NHWC fused path supports deformable_group == 1 only")
+    _b.require_device(fn, dcol, data_im, data_offset, data_mask, grad_im, grad_offset,
+                      grad_mask)
+    _b.require_contiguous(fn, dcol=dcol, data_im=data_im, data_offset=data_offset,
+                          data_mask=data_mask, grad_im=grad_im, grad_offset=grad_offset,
+                          grad_mask=grad_mask)
+    taps = kernel_h * kernel_w
+    last = data_offset.size(-1)
+    fused_y = last == 3 * taps
+    _b.require_dtype(fn, dcol, data_im=data_im, data_offset=data_offset,
+                     data_mask=None if fused_y else data_mask)
+    for name, t in (("grad_im", grad_im), ("grad_offset", grad_offset),
+                    ("grad_mask", grad_mask)):
+        if t is not None and t.dtype != torch.float32:
+            raise RuntimeError(f"{fn}: {name} must be float32, got {t.dtype}")
+    m = batch_size * height_col * width_col
+    _b.require_numel(fn, "dcol", dcol, m * taps * channels)
+    if data_im is not None:
+        _b.require_numel(fn, "data_im", data_im, batch_size * height_im * width_im * channels)
+    _b.require_numel(fn, "data_offset", data_offset, m * last)
+    if not fused_y:
+        _b.require_numel(fn, "data_mask", data_mask, m * taps)
+    if grad_im is not None:
+        _b.require_numel(fn, "grad_im", grad_im, batch_size * height_im * width_im * channels)
+    if grad_offset is not None:
+        _b.require_numel(fn, "grad_offset", grad_offset, m * 2 * taps)
+        _b.require_numel(fn, "grad_mask", grad_mask, m * taps)
+    _b.call("bevk_modulated_deformable_col2im_nhwc", _b.dtype_code(dcol), _b.ptr(dcol),
+            _b.ptr(data_im), _b.ptr(data_offset), last, _b.ptr(data_mask), batch_size,
+            channels, height_im, width_im, height_col, width_col, kernel_h, kernel_w, pad_h,
+            pad_w, stride_h, stride_w, dilation_h, dilation_w, deformable_group,
+            _b.ptr(grad_im), _b.ptr(grad_offset), _b.ptr(grad_mask), _b.stream_of(dcol))
+
+
+def modulated_deformable_col2im_nhwc_cuda(dcol, data_im, data_offset, data_mask, batch_size,
+                                          channels, height_im, width_im, height_col, width_col,
+                                          kernel_h, kernel_w, pad_h, pad_w, stride_h, stride_w,
+                                          dilation_h, dilation_w, deformable_group, grad_im,
+                                          grad_offset, grad_mask):
+    """NHWC backward column-to-image (binding.cpp:80-86): grad_im [B,H,W,C] fp32 accumulated
+    (zero it first), grad_offset [M,2T] / grad_mask [M,T] fp32 written. data_offset may be
+    the raw offset-conv output y [..., 3T]; grad_mask is then the pre-sigmoid gradient."""
+    _col2im_nhwc("modulated_deformable_col2im_nhwc_cuda", dcol, data_im, data_offset,
+                 data_mask, batch_size, channels, height_im, width_im, height_col, width_col,
+                 kernel_h, kernel_w, pad_h, pad_w, stride_h, stride_w, dilation_h, dilation_w,
+                 deformable_group, grad_im, grad_offset, grad_mask)
+
+
+def modulated_deformable_col2im_coord_nhwc_cuda(dcol, data_im, data_offset, data_mask,
+                                                batch_size, channels, height_im, width_im,
+                                                height_col, width_col, kernel_h, kernel_w,
+                                                pad_h, pad_w, stride_h, stride_w, dilation_h,
+                                                dilation_w, deformable_group, grad_offset,
+                                                grad_mask):
+    """grad_offset / grad_mask only (binding.cpp:88-95)."""
+    _col2im_nhwc("modulated_deformable_col2im_coord_nhwc_cuda", dcol, data_im, data_offset,
+                 data_mask, batch_size, channels, height_im, width_im, height_col, width_col,
+                 kernel_h, kernel_w, pad_h, pad_w, stride_h, stride_w, dilation_h, dilation_w,
+                 deformable_group, None, grad_offset, grad_mask)
+
+
+def modulated_deformable_gradx_smem_nhwc_cuda(dcol, data_offset, data_mask, batch_size,
+                                              channels, height_im, width_im, height_col,
+                                              width_col, kernel_h, kernel_w, pad_h, pad_w,
+                                              stride_h, stride_w, dilation_h, dilation_w,
+                                              deformable_group, grad_im):
+    """grad_im only (binding.cpp:97-103), accumulated into grad_im."""
+    _col2im_nhwc("modulated_deformable_gradx_smem_nhwc_cuda", dcol, None, data_offset,
+                 data_mask, batch_size, channels, height_im, width_im, height_col, width_col,
+                 kernel_h, kernel_w, pad_h, pad_w, stride_h, stride_w, dilation_h, dilation_w,
+                 deformable_group, grad_im, None, None)
+
+
+def modulated_deformable_gradx_gather_nhwc_cuda(dcol, data_offset, data_mask, batch_size,
+                                                channels, height_im, width_im, height_col,
+                                                width_col, kernel_h, kernel_w, pad_h, pad_w,
+                                                stride_h, stride_w, dilation_h, dilation_w,
+                                                deformable_group, win, grad_im):
+    """grad_im only (binding.cpp:105-111). `win` (the reference's gather search window) has
+    no meaning here: every sample scatters its own corners."""
+    _col2im_nhwc("modulated_deformable_gradx_gather_nhwc_cuda", dcol, None, data_offset,
+                 data_mask, batch_size, channels, height_im, width_im, height_col, width_col,
+                 kernel_h, kernel_w, pad_h, pad_w, stride_h, stride_w, dilation_h, dilation_w,
+                 deformable_group, grad_im, None, None)
+
+
+modulated_deformable_col2im_fused_smem_nhwc_cuda = modulated_deformable_col2im_nhwc_cuda
+modulated_deformable_col2im_perelem_nhwc_cuda = modulated_deformable_col2im_nhwc_cuda
+modulated_deformable_col2im_perelem_smem_nhwc_cuda = modulated_deformable_col2im_nhwc_cuda
 
 
 def modulated_deformable_fused_im2col_nhwc_cuda(data_im, w_off, b_off, batch_size, channels,

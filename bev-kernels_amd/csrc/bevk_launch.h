@@ -72,4 +72,19 @@ hipError_t launch_im2col_nhwc_yf32(int dtype, const DcnGeom &g, const void *data
                                    const float *y, const float *y_bias, void *data_col,
                                    hipStream_t stream);
 
+// NCHW column-to-image backward (any dg), gradients in the input dtype: grad_im accumulated
+// with atomics (caller zeroes it; skipped when null), grad_offset / grad_mask written
+// (skipped when grad_offset is null).
+hipError_t launch_col2im_nchw(int dtype, const DcnGeom &g, const void *col, const void *im,
+                              const void *off, const void *msk, void *grad_im,
+                              void *grad_offset, void *grad_mask, hipStream_t stream);
+
+// NHWC column-to-image backward (dg == 1): grad_im [B,H,W,C] fp32 accumulated with atomics
+// (caller zeroes it; skipped when null), grad_offset [M][2T] and grad_mask [M][T] fp32
+// written (skipped when grad_offset is null). fused_y: offsets / pre-sigmoid mask from
+// y [M][3T] and grad_mask is the gradient of the pre-sigmoid value.
+hipError_t launch_col2im_nhwc(int dtype, const DcnGeom &g, const void *dcol, const void *im,
+                              const void *off, bool fused_y, const void *msk, float *grad_im,
+                              float *grad_offset, float *grad_mask, hipStream_t stream);
+
 }  // namespace bevk

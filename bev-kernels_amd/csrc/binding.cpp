@@ -182,6 +182,70 @@ int bevk_modulated_deformable_im2col_nhwc(
                     fn);
 }
 
+int bevk_modulated_deformable_col2im_nchw(
+    int dtype, const void *data_col, const void *data_im, const void *data_offset,
+    const void *data_mask, int batch_size, int channels, int height_im, int width_im,
+    int height_col, int width_col, int kernel_h, int kernel_w, int pad_h, int pad_w,
+    int stride_h, int stride_w, int dilation_h, int dilation_w, int deformable_group,
+    void *grad_im, void *grad_offset, void *grad_mask, void *stream) {
+  const char *fn = "modulated_deformable_col2im";
+  g_last_error.clear();
+  if (!valid_dtype(dtype)) return fail(BEVK_ERR_INVALID, "%s: unknown dtype code %d", fn, dtype);
+  const bevk::DcnGeom g =
+      make_geom(batch_size, channels, height_im, width_im, height_col, width_col, kernel_h,
+                kernel_w, pad_h, pad_w, stride_h, stride_w, dilation_h, dilation_w,
+                deformable_group);
+  if (int rc = check_geom(fn, g)) return rc;
+  const long long n = (long long)batch_size * deformable_group * kernel_h * kernel_w *
+                      height_col * width_col;
+  if (n == 0 || channels == 0) return ok();
+  if ((grad_offset == nullptr) != (grad_mask == nullptr))
+    return fail(BEVK_ERR_INVALID, "%s: grad_offset and grad_mask go together", fn);
+  if (!data_col || !data_offset || !data_mask || (!grad_im && !grad_offset) ||
+      (grad_offset && !data_im))
+    return fail(BEVK_ERR_INVALID, "%s: null tensor pointer", fn);
+  return hip_status(bevk::launch_col2im_nchw(dtype, g, data_col, data_im, data_offset, data_mask,
+                                             grad_im, grad_offset, grad_mask,
+                                             (hipStream_t)stream),
+                    fn);
+}
+
+int bevk_modulated_deformable_col2im_nhwc(
+    int dtype, const void *dcol, const void *data_im, const void *data_offset,
+    int offset_last_dim, const void *data_mask, int batch_size, int channels, int height_im,
+    int width_im, int height_col, int width_col, int kernel_h, int kernel_w, int pad_h, int pad_w,
+    int stride_h, int stride_w, int dilation_h, int dilation_w, int deformable_group,
+    float *grad_im, float *grad_offset, float *grad_mask, void *stream) {
+  const char *fn = "modulated_deformable_col2im_nhwc";
+  g_last_error.clear();
+  if (deformable_group != 1)
+    return fail(BEVK_ERR_INVALID, "NHWC fused path supports deformable_group == 1 only");
+  if (dtype != BEVK_F32 && dtype != BEVK_F16 && dtype != BEVK_BF16)
+    return fail(BEVK_ERR_UNSUPPORTED, "\"%s\" not implemented for '%s'", fn, dtype_name(dtype));
+  const bevk::DcnGeom g =
+      make_geom(batch_size, channels, height_im, width_im, height_col, width_col, kernel_h,
+                kernel_w, pad_h, pad_w, stride_h, stride_w, dilation_h, dilation_w, 1);
+  if (int rc = check_geom(fn, g)) return rc;
+  const int taps = kernel_h * kernel_w;
+  if (offset_last_dim != 2 * taps && offset_last_dim != 3 * taps)
+    return fail(BEVK_ERR_INVALID, "%s: offset last dim must be 2T (%d) or 3T (%d), got %d", fn,
+                2 * taps, 3 * taps, offset_last_dim);
+  const bool fused_y = offset_last_dim == 3 * taps;
+  const long long m = (long long)batch_size * height_col * width_col;
+  if (m * taps * channels >= 2147483647LL)
+    return fail(BEVK_ERR_INVALID, "NHWC col2im: Col element count exceeds int32 range");
+  if (m * taps == 0) return ok();
+  if ((grad_offset == nullptr) != (grad_mask == nullptr))
+    return fail(BEVK_ERR_INVALID, "%s: grad_offset and grad_mask go together", fn);
+  if (!dcol || !data_offset || (!fused_y && !data_mask) || (!grad_im && !grad_offset) ||
+      (grad_offset && !data_im))
+    return fail(BEVK_ERR_INVALID, "%s: null tensor pointer", fn);
+  return hip_status(bevk::launch_col2im_nhwc(dtype, g, dcol, data_im, data_offset, fused_y,
+                                             data_mask, grad_im, grad_offset, grad_mask,
+                                             (hipStream_t)stream),
+                    fn);
+}
+
 // Workspace of the fused front end: packed offset-conv weight, then y [M][3T] fp32.
 static long long fused_im2col_ws_parts(int dtype, long long m, int taps, int channels,
                                        long long *y_offset) {

@@ -22,7 +22,8 @@ ROOT = os.path.dirname(PKG)
 BUILD_DIR = os.path.join(PKG, "_build")
 LIB_PATH = os.path.join(PKG, "libbevk.so")
 
-SOURCES = ["binding.cpp", "msda_fwd.hip", "dcn_gather.hip", "dcn_fused.hip", "dcn_fused_h.hip"]
+SOURCES = ["binding.cpp", "msda_fwd.hip", "dcn_gather.hip", "dcn_fused.hip", "dcn_fused_h.hip",
+           "dcn_bwd.hip"]
 ARCH = "gfx950"
 
 

@@ -1,0 +1,294 @@
+// DCNv2 backward on gfx950: the column-to-image steps (NHWC and NCHW).
+//
+// Semantics (naotic/bev-kernels dcn_fused_nhwc_kernel.cuh:642-711, the per-element
+// kernel the reference's NHWC backward runs by default): for every column element
+// dcol[m, t*C + c] of output pixel m = (b, oh, ow) and tap t,
+//   (h, w)   = (oh*sh - ph + i*dh + dy, ow*sw - pw + j*dw + dx), corners clipped one by one
+//   dS       = dcol * mask
+//   gX[b, corner, c] += dS * bilinear weight of the corner        (fp32 atomics)
+//   gOff[m, 2t]     = sum_c dS * d(bilinear)/dh
+//   gOff[m, 2t + 1] = sum_c dS * d(bilinear)/dw
+//   gMask[m, t]     = sum_c dcol * bilinear, times s(1 - s) when the mask is the sigmoid s
+//                     of a raw offset-conv output y (3T form: the sigmoid backward is folded in)
+// A corner outside the image contributes nothing (the reference checks each corner; there
+// is no separate -1 / H gate in the backward).
+//
+// Mapping: LPP lanes own one (m, t) pair and sweep its C channels with 16-byte vectors, so
+// the dcol row and the four corner rows are read as contiguous runs; the three reductions
+// over channels meet in a shuffle butterfly and one lane writes them (no atomics, no
+// pre-zeroing for gOff / gMask). gX needs atomics: several pairs touch one input pixel.
+#include "bevk_common.h"
+#include "bevk_launch.h"
+
+#include <hip/amd_detail/amd_hip_unsafe_atomics.h>
+
+namespace bevk {
+namespace {
+
+constexpr int kBlock = 256;
+
+template <typename T, int VEC, bool FUSED_Y>
+__global__ void __launch_bounds__(kBlock) col2im_nhwc_kernel(
+    const T *__restrict__ dcol, const T *__restrict__ im, const T *__restrict__ offset,
+    const T *__restrict__ mask, const DcnGeom g, int lpp_log2, float *__restrict__ gx,
+    float *__restrict__ goff, float *__restrict__ gmask) {
+  const int T_ = g.kernel_h * g.kernel_w;
+  const int HoWo = g.height_col * g.width_col;
+  const int b = blockIdx.y;
+  const int pair = (blockIdx.x * kBlock + threadIdx.x) >> lpp_log2;
+  const int LPP = 1 << lpp_log2;
+  const int li = threadIdx.x & (LPP - 1);
+  // Lanes past the last pair still take part in the butterfly below; they do no work.
+  const bool live = pair < HoWo * T_;
+  const int pc = live ? pair : 0;
+  const int sp = pc / T_, t = pc - (pc / T_) * T_;
+  const int oh = sp / g.width_col, ow = sp - oh * g.width_col;
+  const int i = t / g.kernel_w, j = t - i * g.kernel_w;
+  const int64_t m = (int64_t)b * HoWo + sp;
+
+  float dy, dx, mk;
+  if constexpr (FUSED_Y) {
+    const T *yp = offset + m * 3 * T_;
+    dy = (float)yp[2 * t];
+    dx = (float)yp[2 * t + 1];
+    mk = sigmoid_f32((float)yp[2 * T_ + t]);
+  } else {
+    dy = (float)offset[m * 2 * T_ + 2 * t];
+    dx = (float)offset[m * 2 * T_ + 2 * t + 1];
+    mk = (float)mask[m * T_ + t];
+  }
+  const float h = (float)(oh * g.stride_h - g.pad_h + i * g.dil_h) + dy;
+  const float w = (float)(ow * g.stride_w - g.pad_w + j * g.dil_w) + dx;
+  const float fh = floorf(h), fw = floorf(w);
+  const float lh = h - fh, lw = w - fw, hh = 1.f - lh, hw = 1.f - lw;
+  // Corner validity, one by one. Clamp before converting so that far-away samples
+  // cannot overflow int.
+  const float fhc = fminf(fmaxf(fh, -2.f), (float)g.height);
+  const float fwc = fminf(fmaxf(fw, -2.f), (float)g.width);
+  const int hl = (int)fhc, wl = (int)fwc;
+  const bool in_h0 = hl >= 0 && hl < g.height, in_h1 = hl + 1 >= 0 && hl + 1 < g.height;
+  const bool in_w0 = wl >= 0 && wl < g.width, in_w1 = wl + 1 >= 0 && wl + 1 < g.width;
+  // finite coordinates only: NaN / inf offsets touch nothing
+  const bool fin = live && fh == fhc && fw == fwc;
+  const bool c1 = fin && in_h0 && in_w0, c2 = fin && in_h0 && in_w1;
+  const bool c3 = fin && in_h1 && in_w0, c4 = fin && in_h1 && in_w1;
+  const float w1 = hh * hw, w2 = hh * lw, w3 = lh * hw, w4 = lh * lw;
+
+  const int C = g.channels;
+  const int64_t img = (int64_t)b * g.height * g.width;
+  const int64_t p1 = (img + (int64_t)hl * g.width + wl) * C;
+  const int64_t p2 = p1 + C, p3 = p1 + (int64_t)g.width * C, p4 = p3 + C;
+  const T *drow = dcol + (m * T_ + t) * C;
+  const bool coord = goff != nullptr;  // gX alone needs no image reads
+  using V = Vec<T, VEC>;
+  float ah = 0.f, aw = 0.f, am = 0.f;
+  if (live) {
+    for (int c = li * VEC; c < C; c += LPP * VEC) {
+      V d, v1, v2, v3, v4;
+      if constexpr (VEC > 1) {
+        d = load_vec<T, VEC>(drow + c);
+      } else {
+        d.v[0] = drow[c];
+      }
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) v1.v[k] = v2.v[k] = v3.v[k] = v4.v[k] = (T)0.f;
+      if (coord && c1) v1 = load_vec<T, VEC>(im + p1 + c);
+      if (coord && c2) v2 = load_vec<T, VEC>(im + p2 + c);
+      if (coord && c3) v3 = load_vec<T, VEC>(im + p3 + c);
+      if (coord && c4) v4 = load_vec<T, VEC>(im + p4 + c);
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) {
+        const float dc = (float)d.v[k], ds = dc * mk;
+        const float x1 = (float)v1.v[k], x2 = (float)v2.v[k];
+        const float x3 = (float)v3.v[k], x4 = (float)v4.v[k];
+        ah += ds * (-hw * x1 - lw * x2 + hw * x3 + lw * x4);
+        aw += ds * (-hh * x1 + hh * x2 - lh * x3 + lh * x4);
+        am += dc * (w1 * x1 + w2 * x2 + w3 * x3 + w4 * x4);
+        if (gx != nullptr) {
+          if (c1) unsafeAtomicAdd(gx + p1 + c + k, ds * w1);
+          if (c2) unsafeAtomicAdd(gx + p2 + c + k, ds * w2);
+          if (c3) unsafeAtomicAdd(gx + p3 + c + k, ds * w3);
+          if (c4) unsafeAtomicAdd(gx + p4 + c + k, ds * w4);
+        }
+      }
+    }
+  }
+  for (int s = 1; s < LPP; s <<= 1) {
+    ah += __shfl_xor(ah, s);
+    aw += __shfl_xor(aw, s);
+    am += __shfl_xor(am, s);
+  }
+  if (live && li == 0 && goff != nullptr) {
+    goff[m * 2 * T_ + 2 * t] = ah;
+    goff[m * 2 * T_ + 2 * t + 1] = aw;
+    gmask[m * T_ + t] = FUSED_Y ? am * mk * (1.f - mk) : am;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// NCHW (any deformable_group): columns [C*T, B*Ho*Wo] (row c*T + t). Semantics of the
+// reference's NCHW backward (modulated_deform_conv_cuda_kernel.cuh:62-131, :257-339,
+// :509-620, :824-937): a sample with h <= -1, w <= -1, h >= H or w >= W contributes nothing
+// (to grad_im, grad_offset and grad_mask); inside, corners are checked one by one.
+//   grad_im[b, c, corner]          += col * mask * corner weight        (atomics, dtype T)
+//   grad_offset[b, g*2T + 2t(+1)]   = sum_c col * mask * d(bilinear)/dh (dw)   (written)
+//   grad_mask[b, g*T + t]           = sum_c col * bilinear                   (written)
+// One thread per (b, group, tap, output position); it walks the group's channels, so the
+// channel sums need no reduction and consecutive threads read consecutive column entries.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void atomic_add_elem(float *p, float v) { unsafeAtomicAdd(p, v); }
+__device__ __forceinline__ void atomic_add_elem(double *p, double v) { unsafeAtomicAdd(p, v); }
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef short short2v __attribute__((ext_vector_type(2)));
+// 16-bit types: a packed add on the aligned pair, zero into the neighbour.
+__device__ __forceinline__ void atomic_add_elem(f16 *p, float v) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  half2v *pair = reinterpret_cast<half2v *>(a & ~(uintptr_t)3);
+  const f16 h = (f16)v;
+  half2v d = (a & 2) ? half2v{(f16)0.f, h} : half2v{h, (f16)0.f};
+  __builtin_amdgcn_global_atomic_fadd_v2f16(pair, d);
+}
+__device__ __forceinline__ void atomic_add_elem(bf16 *p, float v) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  short2v *pair = reinterpret_cast<short2v *>(a & ~(uintptr_t)3);
+  const short b = __builtin_bit_cast(short, (bf16)v);
+  short2v d = (a & 2) ? short2v{0, b} : short2v{b, 0};
+  __builtin_amdgcn_global_atomic_fadd_v2bf16(pair, d);
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kBlock) col2im_nchw_kernel(
+    const T *__restrict__ col, const T *__restrict__ im, const T *__restrict__ offset,
+    const T *__restrict__ mask, const DcnGeom g, T *__restrict__ grad_im,
+    T *__restrict__ grad_offset, T *__restrict__ grad_mask) {
+  using A = typename Acc<T>::type;
+  const int T_ = g.kernel_h * g.kernel_w;
+  const int HoWo = g.height_col * g.width_col;
+  const int64_t n = (int64_t)g.batch * g.deformable_group * T_ * HoWo;
+  const int64_t idx = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (idx >= n) return;
+  const int sp = (int)(idx % HoWo);
+  int64_t r = idx / HoWo;
+  const int t = (int)(r % T_);
+  r /= T_;
+  const int grp = (int)(r % g.deformable_group);
+  const int b = (int)(r / g.deformable_group);
+  const int oh = sp / g.width_col, ow = sp - oh * g.width_col;
+  const int i = t / g.kernel_w, j = t - i * g.kernel_w;
+  const int cpg = g.channels / g.deformable_group;
+
+  const int64_t og = ((int64_t)b * g.deformable_group + grp) * T_;  // (b, group) tap base
+  const A dy = (A)offset[((og + t) * 2) * HoWo + sp];
+  const A dx = (A)offset[((og + t) * 2 + 1) * HoWo + sp];
+  const A mk = (A)mask[(og + t) * HoWo + sp];
+  const A h = (A)(oh * g.stride_h - g.pad_h + i * g.dil_h) + dy;
+  const A w = (A)(ow * g.stride_w - g.pad_w + j * g.dil_w) + dx;
+  A gh = 0, gw = 0, gm = 0;
+  if (h > (A)-1 && w > (A)-1 && h < (A)g.height && w < (A)g.width) {
+    const A fh = floor(h), fw = floor(w);
+    const int hl = (int)fh, wl = (int)fw;
+    const A lh = h - fh, lw = w - fw, hh = (A)1 - lh, hw = (A)1 - lw;
+    const bool c1 = hl >= 0 && wl >= 0, c2 = hl >= 0 && wl + 1 <= g.width - 1;
+    const bool c3 = hl + 1 <= g.height - 1 && wl >= 0;
+    const bool c4 = hl + 1 <= g.height - 1 && wl + 1 <= g.width - 1;
+    const A w1 = hh * hw, w2 = hh * lw, w3 = lh * hw, w4 = lh * lw;
+    const int64_t plane = (int64_t)g.height * g.width;
+    const int64_t q1 = (int64_t)hl * g.width + wl, q2 = q1 + 1, q3 = q1 + g.width, q4 = q3 + 1;
+    const int64_t bhw = (int64_t)g.batch * HoWo;
+    const int c0 = grp * cpg;
+    for (int c = c0; c < c0 + cpg; ++c) {
+      const A dc = (A)col[((int64_t)c * T_ + t) * bhw + (int64_t)b * HoWo + sp];
+      const A ds = dc * mk;
+      const int64_t pb = ((int64_t)b * g.channels + c) * plane;
+      if (grad_im != nullptr) {
+        if (c1) atomic_add_elem(grad_im + pb + q1, ds * w1);
+        if (c2) atomic_add_elem(grad_im + pb + q2, ds * w2);
+        if (c3) atomic_add_elem(grad_im + pb + q3, ds * w3);
+        if (c4) atomic_add_elem(grad_im + pb + q4, ds * w4);
+      }
+      if (grad_offset != nullptr) {
+        const A x1 = c1 ? (A)im[pb + q1] : (A)0, x2 = c2 ? (A)im[pb + q2] : (A)0;
+        const A x3 = c3 ? (A)im[pb + q3] : (A)0, x4 = c4 ? (A)im[pb + q4] : (A)0;
+        gh += ds * (-hw * x1 - lw * x2 + hw * x3 + lw * x4);
+        gw += ds * (-hh * x1 + hh * x2 - lh * x3 + lh * x4);
+        gm += dc * (w1 * x1 + w2 * x2 + w3 * x3 + w4 * x4);
+      }
+    }
+  }
+  if (grad_offset != nullptr) {
+    grad_offset[((og + t) * 2) * HoWo + sp] = (T)gh;
+    grad_offset[((og + t) * 2 + 1) * HoWo + sp] = (T)gw;
+    grad_mask[(og + t) * HoWo + sp] = (T)gm;
+  }
+}
+
+template <typename T>
+hipError_t launch_nchw_t(const DcnGeom &g, const void *col, const void *im, const void *off,
+                         const void *msk, void *grad_im, void *grad_offset, void *grad_mask,
+                         hipStream_t stream) {
+  const int64_t n = (int64_t)g.batch * g.deformable_group * g.kernel_h * g.kernel_w *
+                    g.height_col * g.width_col;
+  hipLaunchKernelGGL(col2im_nchw_kernel<T>, dim3((unsigned)((n + kBlock - 1) / kBlock)),
+                     dim3(kBlock), 0, stream, static_cast<const T *>(col),
+                     static_cast<const T *>(im), static_cast<const T *>(off),
+                     static_cast<const T *>(msk), g, static_cast<T *>(grad_im),
+                     static_cast<T *>(grad_offset), static_cast<T *>(grad_mask));
+  return hipGetLastError();
+}
+
+template <typename T, bool FY>
+hipError_t launch_t(const DcnGeom &g, const void *dcol, const void *im, const void *off,
+                    const void *msk, float *gx, float *goff, float *gmask, hipStream_t stream) {
+  constexpr int VEC = 16 / sizeof(T);
+  const int C = g.channels;
+  const bool vec = (C % VEC) == 0;
+  const int per_lane = vec ? VEC : 1;
+  int lpp = 1;
+  while (lpp < 64 && lpp * per_lane < C) lpp *= 2;
+  int lpp_log2 = 0;
+  while ((1 << lpp_log2) < lpp) ++lpp_log2;
+  const int64_t pairs = (int64_t)g.height_col * g.width_col * g.kernel_h * g.kernel_w;
+  const int64_t threads = pairs << lpp_log2;
+  const dim3 grid((unsigned)((threads + kBlock - 1) / kBlock), g.batch);
+  if (vec)
+    hipLaunchKernelGGL((col2im_nhwc_kernel<T, VEC, FY>), grid, dim3(kBlock), 0, stream,
+                       static_cast<const T *>(dcol), static_cast<const T *>(im),
+                       static_cast<const T *>(off), static_cast<const T *>(msk), g, lpp_log2,
+                       gx, goff, gmask);
+  else
+    hipLaunchKernelGGL((col2im_nhwc_kernel<T, 1, FY>), grid, dim3(kBlock), 0, stream,
+                       static_cast<const T *>(dcol), static_cast<const T *>(im),
+                       static_cast<const T *>(off), static_cast<const T *>(msk), g, lpp_log2,
+                       gx, goff, gmask);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_col2im_nchw(int dtype, const DcnGeom &g, const void *col, const void *im,
+                              const void *off, const void *msk, void *grad_im,
+                              void *grad_offset, void *grad_mask, hipStream_t stream) {
+  switch (dtype) {
+    case 0: return launch_nchw_t<float>(g, col, im, off, msk, grad_im, grad_offset, grad_mask, stream);
+    case 1: return launch_nchw_t<f16>(g, col, im, off, msk, grad_im, grad_offset, grad_mask, stream);
+    case 2: return launch_nchw_t<bf16>(g, col, im, off, msk, grad_im, grad_offset, grad_mask, stream);
+    case 3: return launch_nchw_t<double>(g, col, im, off, msk, grad_im, grad_offset, grad_mask, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_col2im_nhwc(int dtype, const DcnGeom &g, const void *dcol, const void *im,
+                              const void *off, bool fused_y, const void *msk, float *grad_im,
+                              float *grad_offset, float *grad_mask, hipStream_t stream) {
+  switch (dtype) {
+    case 0: return fused_y ? launch_t<float, true>(g, dcol, im, off, msk, grad_im, grad_offset, grad_mask, stream)
+                           : launch_t<float, false>(g, dcol, im, off, msk, grad_im, grad_offset, grad_mask, stream);
+    case 1: return fused_y ? launch_t<f16, true>(g, dcol, im, off, msk, grad_im, grad_offset, grad_mask, stream)
+                           : launch_t<f16, false>(g, dcol, im, off, msk, grad_im, grad_offset, grad_mask, stream);
+    case 2: return fused_y ? launch_t<bf16, true>(g, dcol, im, off, msk, grad_im, grad_offset, grad_mask, stream)
+                           : launch_t<bf16, false>(g, dcol, im, off, msk, grad_im, grad_offset, grad_mask, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace bevk

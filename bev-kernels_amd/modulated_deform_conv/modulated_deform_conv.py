@@ -3,8 +3,8 @@ implementation, with the public names of naotic/bev-kernels
 modulated_deform_conv/modulated_deform_conv.py.
 
 Forward runs on the gfx950 kernels of libbevk.so (through ``_modulated_deform_conv_ext``).
-The backward kernels are not part of this build: the autograd functions raise in
-backward.
+Backward: ModulatedDeformConv2dFunction.backward follows the reference's composition
+(modulated_deform_conv.py:405-500) on the NCHW column-to-image kernel.
 """
 from __future__ import annotations
 
@@ -263,6 +263,9 @@ class ModulatedDeformConv2dFunction(Function):
         ctx.with_bias = bias is not None
         input = input.type_as(offset)
         weight = weight.type_as(input)
+        if not ctx.with_bias:
+            bias = input.new_empty(0)
+        ctx.save_for_backward(input, offset, mask, weight, bias)
         return _modulated_deform_conv2d_forward(input, offset, mask, weight,
                                                 bias if ctx.with_bias else None, ctx.stride,
                                                 ctx.padding, ctx.dilation, groups,
@@ -271,8 +274,58 @@ class ModulatedDeformConv2dFunction(Function):
     @staticmethod
     @once_differentiable
     def backward(ctx, grad_output):
-        raise RuntimeError("ModulatedDeformConv2dFunction.backward: the backward kernels are "
-                           "not part of this build (forward operators only)")
+        """modulated_deform_conv.py:405-500: columns = W^T @ dO per group; grad_offset /
+        grad_mask and grad_input from the column-to-image kernel; the columns of the input
+        again for grad_weight = dO @ columns^T; grad_bias = sum of dO."""
+        input, offset, mask, weight, bias = ctx.saved_tensors
+        ext = _load_ext()
+        # 16-bit inputs: the gradients are accumulated in fp32 and rounded once (the
+        # reference has no 16-bit NCHW backward: its coordinate kernel is fp32/fp64 only)
+        out_dtype = input.dtype
+        if out_dtype in (torch.float16, torch.bfloat16):
+            input, offset, mask, weight = (t.float() for t in (input, offset, mask, weight))
+            grad_output = grad_output.float()
+        grad_input = torch.zeros_like(input)
+        grad_offset = torch.empty_like(offset)
+        grad_mask = torch.empty_like(mask)
+        grad_output = grad_output.contiguous()
+        batch, channels, height, width = input.shape
+        channels_out = weight.size(0)
+        groups, deform_groups = ctx.groups, ctx.deform_groups
+        c_out_g = channels_out // groups
+        kernel_h, kernel_w = weight.size(2), weight.size(3)
+        c_in_g_kkw = (channels // groups) * kernel_h * kernel_w
+        stride_h, stride_w = ctx.stride
+        pad_h, pad_w = ctx.padding
+        dil_h, dil_w = ctx.dilation
+        height_out = _out_size(height, pad_h, dil_h, kernel_h, stride_h)
+        width_out = _out_size(width, pad_w, dil_w, kernel_w, stride_w)
+        bhw = batch * height_out * width_out
+
+        grad_out_g = grad_output.permute(1, 0, 2, 3).contiguous().view(groups, c_out_g, bhw)
+        weight_g = weight.contiguous().view(groups, c_out_g, c_in_g_kkw)
+        columns = input.new_empty(groups, c_in_g_kkw, bhw)
+        for g in range(groups):
+            torch.mm(weight_g[g].t(), grad_out_g[g], out=columns[g])
+        columns = columns.view(channels * kernel_h * kernel_w, bhw)
+        args = (batch, channels, height, width, height_out, width_out, kernel_h, kernel_w,
+                pad_h, pad_w, stride_h, stride_w, dil_h, dil_w, deform_groups)
+        ext.modulated_deformable_col2im_coord_opt_cuda(columns, input, offset, mask, *args,
+                                                       grad_offset, grad_mask)
+        ext.modulated_deformable_col2im_smem_cuda(columns, offset, mask, *args, grad_input)
+        ext.modulated_deformable_im2col_opt_cuda(input, offset, mask, *args, columns)
+        col_g = columns.view(groups, c_in_g_kkw, bhw)
+        grad_weight = weight.new_empty(groups, c_out_g, c_in_g_kkw)
+        for g in range(groups):
+            torch.mm(grad_out_g[g], col_g[g].t(), out=grad_weight[g])
+        grad_weight = grad_weight.view_as(weight)
+        grad_bias = grad_output.sum(dim=(0, 2, 3)) if ctx.with_bias else None
+        if out_dtype != input.dtype:
+            grad_input, grad_offset, grad_mask, grad_weight = (
+                t.to(out_dtype) for t in (grad_input, grad_offset, grad_mask, grad_weight))
+            grad_bias = grad_bias.to(out_dtype) if grad_bias is not None else None
+        return (grad_input, grad_offset, grad_mask, grad_weight, grad_bias,
+                None, None, None, None, None)
 
 
 def _modulated_deform_conv2d_forward(input, offset, mask, weight, bias, stride, padding,

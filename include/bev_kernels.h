@@ -97,6 +97,44 @@ int bevk_modulated_deformable_im2col_nhwc(
     int stride_h, int stride_w, int dilation_h, int dilation_w, int deformable_group,
     void *data_col, void *stream);
 
+/* NCHW backward, column to image (any deformable_group):
+ *   data_col     [C*kh*kw, B*Ho*Wo] gradient of the columns (row c*T + t), dtype
+ *   data_im      [B, C, H, W] (may be NULL when grad_offset is NULL)
+ *   data_offset  [B, dg*2T, Ho, Wo], data_mask [B, dg*T, Ho, Wo]
+ *   grad_im      [B, C, H, W] dtype, ACCUMULATED with atomics (zero it first), or NULL. For
+ *                F16 / BF16 the adds are packed pairs with 0 added to the neighbour element,
+ *                so the buffer must be allocated to a multiple of 4 bytes.
+ *   grad_offset  [B, dg*2T, Ho, Wo] and grad_mask [B, dg*T, Ho, Wo] dtype, written, or NULL
+ * Replaces binding.cpp:13-19, :29-58 (modulated_deformable_col2im[_opt|_smem]_cuda and
+ * modulated_deformable_col2im_coord[_opt]_cuda; modulated_deform_conv_cuda_kernel.cuh:
+ * 62-131, :195-339, :509-937). A sample outside (-1, H) x (-1, W) contributes nothing.
+ * dtypes F32, F16, BF16, F64. */
+int bevk_modulated_deformable_col2im_nchw(
+    int dtype, const void *data_col, const void *data_im, const void *data_offset,
+    const void *data_mask, int batch_size, int channels, int height_im, int width_im,
+    int height_col, int width_col, int kernel_h, int kernel_w, int pad_h, int pad_w,
+    int stride_h, int stride_w, int dilation_h, int dilation_w, int deformable_group,
+    void *grad_im, void *grad_offset, void *grad_mask, void *stream);
+
+/* NHWC backward, column to image (dg == 1):
+ *   dcol         [B*Ho*Wo, T*C] gradient of the columns, dtype
+ *   data_im, data_offset, offset_last_dim, data_mask: as bevk_modulated_deformable_im2col_nhwc
+ *                (data_im may be NULL when grad_offset is NULL: grad_im needs no image)
+ *   grad_im      [B, H, W, C] fp32, ACCUMULATED with atomics (zero it first), or NULL
+ *   grad_offset  [B*Ho*Wo, 2T] fp32, written, or NULL (then grad_mask NULL too)
+ *   grad_mask    [B*Ho*Wo, T] fp32, written: the gradient of the mask, or of the
+ *                pre-sigmoid mask in the 3T form (sigmoid backward folded in)
+ * Replaces binding.cpp:80-86 modulated_deformable_col2im_nhwc_cuda and its variants
+ * (col2im_coord_nhwc, gradx_smem / gradx_gather, col2im_fused_smem, col2im_perelem[_smem],
+ * binding.cpp:88-140; per-element semantics of dcn_fused_nhwc_kernel.cuh:642-711).
+ * dtypes F32, F16, BF16. */
+int bevk_modulated_deformable_col2im_nhwc(
+    int dtype, const void *dcol, const void *data_im, const void *data_offset,
+    int offset_last_dim, const void *data_mask, int batch_size, int channels, int height_im,
+    int width_im, int height_col, int width_col, int kernel_h, int kernel_w, int pad_h, int pad_w,
+    int stride_h, int stride_w, int dilation_h, int dilation_w, int deformable_group,
+    float *grad_im, float *grad_offset, float *grad_mask, void *stream);
+
 /* Workspace bytes bevk_modulated_deformable_fused_im2col_nhwc needs (-1 on bad
  * arguments): the packed offset-conv weight and the fp32 offset-conv output [M][3T]. */
 int64_t bevk_dcn_fused_im2col_nhwc_workspace_bytes(int dtype, int batch_size, int channels,

@@ -124,9 +124,13 @@ def forward_nchw(x, offset, mask, weight, bias=None, stride=(1, 1), padding=(0, 
     return out.contiguous()
 
 
-def bilinear_nhwc(im_b, h, w):
+def bilinear_nhwc(im_b, h, w, gate=True):
     """fused_tl.py:146-174: im_b [H, W, C]; h, w [P] -> [P, C] with per-corner zeroing
-    and the outer gate -1 < h < H, -1 < w < W."""
+    and the outer gate -1 < h < H, -1 < w < W. gate=False drops the outer gate and keeps
+    only the per-corner checks, as the reference's NHWC kernels do
+    (dcn_fused_nhwc_kernel.cuh:270-301, :642-711): the same values for finite coordinates,
+    but at h = -1 (or w = -1) the derivative is the one-sided one of the cell [-1, 0]
+    instead of 0."""
     H, W, C = im_b.shape
     h_low = torch.floor(h)
     w_low = torch.floor(w)
@@ -146,12 +150,14 @@ def bilinear_nhwc(im_b, h, w):
            + (hh * lw).unsqueeze(-1) * corner(h_low, w_low + 1)
            + (lh * hw).unsqueeze(-1) * corner(h_low + 1, w_low)
            + (lh * lw).unsqueeze(-1) * corner(h_low + 1, w_low + 1))
+    if not gate:
+        return out
     outer = (h > -1) & (w > -1) & (h < H) & (w < W)
     return torch.where(outer.unsqueeze(-1), out, torch.zeros_like(out))
 
 
-def columns_nhwc(x, offset, mask, kh, kw, sh, sw, ph, pw, dh, dw):
-    """fused_tl.py:177-201: columns [B*Ho*Wo, T*C], k = t*C + c."""
+def columns_nhwc(x, offset, mask, kh, kw, sh, sw, ph, pw, dh, dw, gate=True):
+    """fused_tl.py:177-201: columns [B*Ho*Wo, T*C], k = t*C + c (gate: see bilinear_nhwc)."""
     B, H, W, C = x.shape
     T = kh * kw
     Ho = out_size(H, ph, dh, kh, sh)
@@ -165,15 +171,16 @@ def columns_nhwc(x, offset, mask, kh, kw, sh, sw, ph, pw, dh, dw):
             ki, kj = t // kw, t % kw
             h_im = oh * sh - ph + ki * dh + offset[b, :, :, 2 * t].reshape(-1)
             w_im = ow * sw - pw + kj * dw + offset[b, :, :, 2 * t + 1].reshape(-1)
-            samp = bilinear_nhwc(x[b], h_im, w_im)
+            samp = bilinear_nhwc(x[b], h_im, w_im, gate)
             cols[b, :, t, :] = samp * mask[b, :, :, t].reshape(-1, 1)
     return cols.reshape(B * Ho * Wo, T * C)
 
 
 def forward_nhwc(x, offset, mask, weight, bias=None, stride=1, padding=0, dilation=1,
-                 col_dtype=None):
+                 col_dtype=None, gate=True):
     """fused_tl.py:204-227: cols @ weight.permute(2,3,1,0).reshape(K, Cout) (+ bias).
-    col_dtype: round the columns to this dtype first (see _round_cols)."""
+    col_dtype: round the columns to this dtype first (see _round_cols); gate: see
+    bilinear_nhwc."""
     def two(v):
         return (v, v) if isinstance(v, int) else tuple(v)
     (sh, sw), (ph, pw), (dh, dw) = two(stride), two(padding), two(dilation)
@@ -181,7 +188,7 @@ def forward_nhwc(x, offset, mask, weight, bias=None, stride=1, padding=0, dilati
     Cout, _, kh, kw = weight.shape
     Ho = out_size(H, ph, dh, kh, sh)
     Wo = out_size(W, pw, dw, kw, sw)
-    cols = _round_cols(columns_nhwc(x, offset, mask, kh, kw, sh, sw, ph, pw, dh, dw),
+    cols = _round_cols(columns_nhwc(x, offset, mask, kh, kw, sh, sw, ph, pw, dh, dw, gate),
                        col_dtype)
     out = (cols @ weight.permute(2, 3, 1, 0).reshape(kh * kw * C, Cout)).view(B, Ho, Wo, Cout)
     if bias is not None:

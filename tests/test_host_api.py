@@ -1,6 +1,6 @@
 """Host-side behaviour of the Python operator layer on the CPU: device / contiguity /
-size checks raise RuntimeError before the library is asked to launch, the backward names
-raise, the Pack module's backend selection and mmcv checkpoint-key migration
+size checks raise RuntimeError before the library is asked to launch (forward and
+backward entry points), the Pack module's backend selection and mmcv checkpoint-key migration
 (modulated_deform_conv.py:584-643 of the reference), and BASELINE input generators."""
 import pytest
 import torch
@@ -46,15 +46,18 @@ def test_cpu_tensors_rejected():
                     d["sampling_loc"], d["attn_weight"])
 
 
-def test_backward_entry_points_raise():
-    with pytest.raises(RuntimeError, match="not part of this build"):
-        ext.modulated_deformable_col2im_coord_opt_cuda()
-    with pytest.raises(RuntimeError, match="not part of this build"):
-        ext.backward(*([None] * 9))
-    with pytest.raises(RuntimeError, match="not part of this build"):
+def test_backward_entry_points_check_their_inputs():
+    with pytest.raises(RuntimeError, match="HIP"):
         mdc.ext_modulated_deformable_col2im_smem(torch.zeros(36, 25), torch.zeros(1, 18, 5, 5),
                                                  torch.zeros(1, 9, 5, 5), 1, 4, 5, 5, 3, 3, 1,
                                                  1, 1, 1, 1, 1, 1)
+    with pytest.raises(RuntimeError, match="HIP"):
+        ext.modulated_deformable_col2im_nhwc_cuda(
+            torch.zeros(25, 36), torch.zeros(1, 5, 5, 4), torch.zeros(1, 5, 5, 18),
+            torch.zeros(1, 5, 5, 9), 1, 4, 5, 5, 5, 5, 3, 3, 1, 1, 1, 1, 1, 1, 1,
+            torch.zeros(1, 5, 5, 4), torch.zeros(1, 5, 5, 18), torch.zeros(1, 5, 5, 9))
+    with pytest.raises(RuntimeError, match="deformable_group == 1"):
+        ext.modulated_deformable_col2im_nhwc_cuda(*([None] * 18), 2, None, None, None)
 
 
 def test_pack_backend_selection(monkeypatch):

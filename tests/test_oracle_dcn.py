@@ -231,3 +231,67 @@ def test_package_pytorch_goldens_match_oracle():
     xn, on, mn = (t.permute(0, 2, 3, 1) for t in (x, off, m))
     torch.testing.assert_close(fused_tl.dcn_forward_golden_nhwc(xn, on, mn, w, b, 1, 1, 1),
                                od.forward_nhwc(xn, on, mn, w, b, 1, 1, 1))
+
+
+# ---------------------------------------------------------------------------------------
+# Gradients: the backward kernels are checked against autograd of these restatements, so
+# autograd of the restatements is pinned here against finite differences (gradcheck).
+# Offsets are continuous (no sample on a cell edge, where the derivative jumps).
+# ---------------------------------------------------------------------------------------
+
+def _smooth_problem(seed, b=1, c=3, h=5, w=6, cout=2, k=3, dg=1):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(b, c, h, w, generator=g, dtype=D64)
+    off = 1.3 * torch.randn(b, dg * 2 * k * k, h, w, generator=g, dtype=D64)
+    mask = torch.rand(b, dg * k * k, h, w, generator=g, dtype=D64)
+    weight = torch.randn(cout, c, k, k, generator=g, dtype=D64)
+    return x, off, mask, weight
+
+
+def test_gradcheck_forward_nchw():
+    x, off, mask, weight = _smooth_problem(21, dg=1)
+    f = lambda x, off, mask, weight: od.forward_nchw(x, off, mask, weight, None, (1, 1), (1, 1),
+                                                     (1, 1))
+    assert torch.autograd.gradcheck(f, (x.requires_grad_(), off.requires_grad_(),
+                                        mask.requires_grad_(), weight.requires_grad_()))
+
+
+def test_ungated_columns_equal_gated_values():
+    """gate=False changes no value (a sample outside (-1, H) x (-1, W) has no in-range
+    corner with a non-zero weight); only the derivative exactly at -1 differs."""
+    x, off, mask, w, b, s, p, d = _problem(2, 4, 7, 8, 3, seed=24)
+    args = (x.permute(0, 2, 3, 1), off.permute(0, 2, 3, 1), mask.permute(0, 2, 3, 1), 3, 3,
+            1, 1, 1, 1, 1, 1)
+    torch.testing.assert_close(od.columns_nhwc(*args, gate=False), od.columns_nhwc(*args),
+                               rtol=0, atol=0)
+    # one sample exactly on h = -1: value 0 both ways, derivative 0 (gated) vs one-sided
+    xx = torch.randn(1, 3, 3, 2, dtype=D64)
+    h = torch.tensor([-1.0], dtype=D64, requires_grad=True)
+    w = torch.tensor([0.5], dtype=D64)
+    g_on = torch.autograd.grad(od.bilinear_nhwc(xx[0], h, w).sum(), h)[0]
+    h2 = h.detach().clone().requires_grad_()
+    v = od.bilinear_nhwc(xx[0], h2, w, gate=False)
+    g_off = torch.autograd.grad(v.sum(), h2)[0]
+    assert g_on.item() == 0.0 and float(v.abs().sum()) == 0.0
+    # cell [-1, 0]: d/dh = (1 - lw) * x[0, 0] + lw * x[0, 1] summed over channels
+    expect = (0.5 * xx[0, 0, 0] + 0.5 * xx[0, 0, 1]).sum()
+    torch.testing.assert_close(g_off[0], expect)
+
+
+def test_gradcheck_columns_nhwc():
+    x, off, mask, _ = _smooth_problem(22)
+    f = lambda x, off, mask: od.columns_nhwc(x, off, mask, 3, 3, 1, 1, 1, 1, 1, 1)
+    args = (x.permute(0, 2, 3, 1).contiguous().requires_grad_(),
+            off.permute(0, 2, 3, 1).contiguous().requires_grad_(),
+            mask.permute(0, 2, 3, 1).contiguous().requires_grad_())
+    assert torch.autograd.gradcheck(f, args)
+
+
+def test_gradcheck_front_end_columns():
+    g = torch.Generator().manual_seed(23)
+    x = torch.randn(1, 4, 5, 3, generator=g, dtype=D64)
+    w_off = 0.3 * torch.randn(27, 9, 3, generator=g, dtype=D64)
+    b_off = torch.randn(27, generator=g, dtype=D64)
+    f = lambda x, w, b: od.fused_front_end_columns(x, w, b, 3, 3, 1, 1, 1)
+    assert torch.autograd.gradcheck(f, (x.requires_grad_(), w_off.requires_grad_(),
+                                        b_off.requires_grad_()))
