@@ -404,15 +404,11 @@ def modulated_deformable_fused_im2col_nhwc_cuda(data_im, w_off, b_off, batch_siz
 # Multi-scale deformable attention (binding_musa.mu:286-412, :545-557)
 # ---------------------------------------------------------------------------------------
 
-def forward(value, spatial_shapes, level_start_index, sampling_loc, attn_weight,
-            im2col_step=64, force_generic=False):
-    """MSDA forward. value [B, S, heads, D], spatial_shapes [L, 2] int64,
-    level_start_index [L] int64, sampling_loc [B, Lq, heads, L, P, 2],
-    attn_weight [B, Lq, heads, L, P] -> output [B, Lq, heads * D]."""
-    fn = "msda_forward"
+def _msda_check(fn, value, spatial_shapes, level_start_index, sampling_loc, attn_weight):
+    """Checks of binding_musa.mu:292-298 / :420-427 plus shape agreement; returns
+    (batch, spatial, heads, channels, num_levels, num_query, num_point)."""
     if value.device.type != "cuda":
         raise RuntimeError("value must be a HIP device tensor")
-    # binding_musa.mu:292-298
     if not value.is_contiguous():
         raise RuntimeError("value must be contiguous")
     if not spatial_shapes.is_contiguous():
@@ -444,6 +440,16 @@ def forward(value, spatial_shapes, level_start_index, sampling_loc, attn_weight,
     if tuple(attn_weight.shape) != (batch, num_query, heads, num_levels, num_point):
         raise RuntimeError(f"{fn}: attn_weight shape {tuple(attn_weight.shape)} does not match "
                            f"sampling_loc {tuple(sampling_loc.shape)}")
+    return batch, spatial, heads, channels, num_levels, num_query, num_point
+
+
+def forward(value, spatial_shapes, level_start_index, sampling_loc, attn_weight,
+            im2col_step=64, force_generic=False):
+    """MSDA forward. value [B, S, heads, D], spatial_shapes [L, 2] int64,
+    level_start_index [L] int64, sampling_loc [B, Lq, heads, L, P, 2],
+    attn_weight [B, Lq, heads, L, P] -> output [B, Lq, heads * D]."""
+    batch, spatial, heads, channels, num_levels, num_query, num_point = _msda_check(
+        "msda_forward", value, spatial_shapes, level_start_index, sampling_loc, attn_weight)
     output = torch.empty(batch, num_query, heads * channels, dtype=value.dtype,
                          device=value.device)
     _b.call("bevk_msda_forward", _b.dtype_code(value), _b.ptr(value), _b.ptr(spatial_shapes),
@@ -456,6 +462,36 @@ def forward(value, spatial_shapes, level_start_index, sampling_loc, attn_weight,
 def backward(value, spatial_shapes, level_start_index, sampling_loc, attn_weight, grad_output,
              grad_value, grad_sampling_loc, grad_attn_weight, im2col_step=64,
              force_generic_col2im=False):
-    """MSDA backward (binding_musa.mu:414-543). Not part of this build."""
-    raise RuntimeError("msda backward: the backward kernels are not part of this build "
-                       "(forward operators only)")
+    """MSDA backward (binding_musa.mu:414-543). Fills the caller's tensors:
+    grad_value [B, S, heads, D] is ADDED to for fp32/fp64 and overwritten for fp16/bf16
+    (accumulated in an fp32 buffer, then narrowed); grad_sampling_loc and
+    grad_attn_weight are written. grad_output [B, Lq, heads*D] may be strided."""
+    fn = "msda_backward"
+    batch, spatial, heads, channels, num_levels, num_query, num_point = _msda_check(
+        fn, value, spatial_shapes, level_start_index, sampling_loc, attn_weight)
+    if grad_output.device.type != "cuda":
+        raise RuntimeError("grad_output must be a HIP device tensor")
+    _b.require_device(fn, value, grad_output, grad_value, grad_sampling_loc, grad_attn_weight)
+    _b.require_dtype(fn, value, grad_output=grad_output, grad_value=grad_value,
+                     grad_sampling_loc=grad_sampling_loc, grad_attn_weight=grad_attn_weight)
+    _b.require_contiguous(fn, grad_value=grad_value, grad_sampling_loc=grad_sampling_loc,
+                          grad_attn_weight=grad_attn_weight)
+    if tuple(grad_value.shape) != tuple(value.shape) or \
+            tuple(grad_sampling_loc.shape) != tuple(sampling_loc.shape) or \
+            tuple(grad_attn_weight.shape) != tuple(attn_weight.shape):
+        raise RuntimeError(f"{fn}: gradient tensors must have the shapes of value, "
+                           "sampling_loc and attn_weight")
+    # binding_musa.mu:446-447 views grad_output per (batch, query, head, channel)
+    g4 = grad_output.view(batch, num_query, heads, channels)
+    sb, sq, sh, sc = g4.stride()
+    code = _b.dtype_code(value)
+    nbytes = _b.lib().bevk_msda_backward_workspace_bytes(code, batch, spatial, heads, channels)
+    if nbytes < 0:
+        raise RuntimeError(f"{fn}: invalid sizes")
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=value.device)
+    _b.call("bevk_msda_backward", code, _b.ptr(value), _b.ptr(spatial_shapes),
+            _b.ptr(level_start_index), _b.ptr(sampling_loc), _b.ptr(attn_weight), _b.ptr(g4),
+            sb, sq, sh, sc, batch, spatial, heads, channels, num_levels, num_query, num_point,
+            int(im2col_step), 1 if force_generic_col2im else 0, _b.ptr(grad_value),
+            _b.ptr(grad_sampling_loc), _b.ptr(grad_attn_weight), _b.ptr(ws), nbytes,
+            _b.stream_of(value))

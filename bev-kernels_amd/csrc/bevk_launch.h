@@ -21,6 +21,19 @@ struct MsdaArgs {
 hipError_t launch_msda_forward(int dtype, const MsdaArgs &a, bool force_generic,
                                hipStream_t stream);
 
+// MSDA backward: f holds the forward inputs (f.output unused).
+struct MsdaBwdArgs {
+  MsdaArgs f;
+  const void *grad_output;
+  int64_t go_stride[4];  // grad_output strides over (batch, query, head, channel), elements
+  void *grad_value, *grad_loc, *grad_attn;
+  void *workspace;       // fp32 accumulator for 16-bit dtypes
+};
+
+// Bytes of fp32 accumulator the 16-bit backward needs (0 for f32 / f64).
+int64_t msda_backward_workspace_bytes(int dtype, int64_t value_elems);
+hipError_t launch_msda_backward(int dtype, const MsdaBwdArgs &a, hipStream_t stream);
+
 struct DcnGeom {
   int batch, channels, height, width, height_col, width_col;
   int kernel_h, kernel_w, pad_h, pad_w, stride_h, stride_w, dil_h, dil_w;

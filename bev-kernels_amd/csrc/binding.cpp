@@ -433,4 +433,65 @@ int bevk_msda_forward(int dtype, const void *value, const int64_t *spatial_shape
       bevk::launch_msda_forward(dtype, a, force_generic != 0, (hipStream_t)stream), fn);
 }
 
+int64_t bevk_msda_backward_workspace_bytes(int dtype, int batch, int spatial_size,
+                                           int num_heads, int channels) {
+  if (!valid_dtype(dtype) || batch < 0 || spatial_size < 0 || num_heads < 0 || channels < 0)
+    return -1;
+  return bevk::msda_backward_workspace_bytes(
+      dtype, (int64_t)batch * spatial_size * num_heads * channels);
+}
+
+int bevk_msda_backward(int dtype, const void *value, const int64_t *spatial_shapes,
+                       const int64_t *level_start_index, const void *sampling_loc,
+                       const void *attn_weight, const void *grad_output, int64_t go_stride_b,
+                       int64_t go_stride_q, int64_t go_stride_h, int64_t go_stride_c,
+                       int batch, int spatial_size, int num_heads, int channels,
+                       int num_levels, int num_query, int num_point, int im2col_step,
+                       int force_generic_col2im, void *grad_value, void *grad_sampling_loc,
+                       void *grad_attn_weight, void *workspace, int64_t workspace_bytes,
+                       void *stream) {
+  const char *fn = "msda_backward";
+  g_last_error.clear();
+  (void)force_generic_col2im;
+  if (!valid_dtype(dtype)) return fail(BEVK_ERR_INVALID, "%s: unknown dtype code %d", fn, dtype);
+  if (batch < 0 || spatial_size < 0 || num_heads < 0 || channels < 0 || num_levels < 0 ||
+      num_query < 0 || num_point < 0)
+    return fail(BEVK_ERR_INVALID, "%s: negative size", fn);
+  if (im2col_step <= 0) return fail(BEVK_ERR_INVALID, "%s: im2col_step must be positive", fn);
+  // binding_musa.mu:438-439
+  const int step = batch < im2col_step ? batch : im2col_step;
+  if (step > 0 && batch % step != 0)
+    return fail(BEVK_ERR_INVALID, "batch must divide im2col_step");
+  const int64_t value_elems = (int64_t)batch * spatial_size * num_heads * channels;
+  const int64_t need = bevk::msda_backward_workspace_bytes(dtype, value_elems);
+  if (workspace_bytes < need)
+    return fail(BEVK_ERR_INVALID, "%s: workspace of %lld bytes, %lld needed", fn,
+                (long long)workspace_bytes, (long long)need);
+  const long long units = (long long)batch * num_query * num_heads;
+  // 16-bit grad_value is fully written (narrowed from the cleared accumulator) even when
+  // there are no queries; with no values there is nothing to write at all
+  if (value_elems == 0 || (units == 0 && need == 0)) return ok();
+  if (channels == 0) return ok();
+  if (!value || !spatial_shapes || !level_start_index || !grad_value ||
+      (units > 0 && (!sampling_loc || !attn_weight || !grad_output || !grad_sampling_loc ||
+                     !grad_attn_weight)) ||
+      (need > 0 && !workspace))
+    return fail(BEVK_ERR_INVALID, "%s: null tensor pointer", fn);
+  if (units * 64 >= (1LL << 42))
+    return fail(BEVK_ERR_INVALID, "%s: problem too large", fn);
+  bevk::MsdaBwdArgs a;
+  a.f.value = value; a.f.spatial_shapes = spatial_shapes;
+  a.f.level_start_index = level_start_index; a.f.sampling_loc = sampling_loc;
+  a.f.attn_weight = attn_weight; a.f.output = nullptr;
+  a.f.batch = batch; a.f.spatial_size = spatial_size; a.f.num_heads = num_heads;
+  a.f.channels = channels; a.f.num_levels = num_levels; a.f.num_query = num_query;
+  a.f.num_point = num_point;
+  a.grad_output = grad_output;
+  a.go_stride[0] = go_stride_b; a.go_stride[1] = go_stride_q;
+  a.go_stride[2] = go_stride_h; a.go_stride[3] = go_stride_c;
+  a.grad_value = grad_value; a.grad_loc = grad_sampling_loc; a.grad_attn = grad_attn_weight;
+  a.workspace = workspace;
+  return hip_status(bevk::launch_msda_backward(dtype, a, (hipStream_t)stream), fn);
+}
+
 }  // extern "C"

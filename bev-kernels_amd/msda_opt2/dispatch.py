@@ -43,8 +43,9 @@ def ms_deform_attn_backward(
     im2col_step: int = 64,
     force_generic_col2im: bool = False,
 ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """Gradients (value, sampling_loc, attn_weight); the backward kernels are not part of
-    this build and this raises RuntimeError."""
+    """Gradients (value, sampling_loc, attn_weight) of ms_deform_attn_forward for
+    grad_output [B, Lq, heads * D]. fp32 / fp64, and fp16 / bf16 with fp32 arithmetic and
+    an fp32 grad_value accumulator."""
     if not torch.cuda.is_available():
         raise RuntimeError("ms_deform_attn_backward requires a HIP device (torch.cuda)")
     grad_value = torch.zeros_like(value)

@@ -219,6 +219,39 @@ int bevk_msda_forward(
     int num_query, int num_point, int im2col_step, int force_generic, void *output,
     void *stream);
 
+/* Bytes of workspace bevk_msda_backward needs: an fp32 accumulator of
+ * batch*spatial_size*num_heads*channels elements for F16/BF16, 0 for F32/F64, -1 for an
+ * unknown dtype or a negative size. The reference allocates this buffer inside its
+ * fp16 backward (binding_musa.mu:456-463); here the caller owns it. */
+int64_t bevk_msda_backward_workspace_bytes(int dtype, int batch, int spatial_size,
+                                           int num_heads, int channels);
+
+/* MSDA backward.
+ *   value, spatial_shapes, level_start_index, sampling_loc, attn_weight: as the forward.
+ *   grad_output        [B, num_query, num_heads*channels]; go_stride_{b,q,h,c} are its
+ *                      element strides over (batch, query, head, channel) (the
+ *                      reference reads a strided grad_output too).
+ *   grad_value         [B, spatial_size, num_heads, channels]. F32/F64: gradients are
+ *                      ADDED to what it holds (the caller zeroes it, as
+ *                      ms_deform_attn_backward in dispatch.py:36-69 does). F16/BF16: the
+ *                      gradient is accumulated in the fp32 workspace, which is cleared
+ *                      here, and then written over grad_value.
+ *   grad_sampling_loc  [B, num_query, num_heads, num_levels, num_point, 2]; written.
+ *   grad_attn_weight   [B, num_query, num_heads, num_levels, num_point]; written.
+ *   workspace          bevk_msda_backward_workspace_bytes(...) bytes, device memory.
+ * im2col_step keeps the reference's contract; force_generic_col2im is accepted for
+ * compatibility (one kernel serves every geometry).
+ * Replaces _msda_opt2_musa.backward (binding_musa.mu:414-543, :550-556).
+ * dtypes: F32, F16, BF16 (fp32 arithmetic and accumulation), F64. */
+int bevk_msda_backward(
+    int dtype, const void *value, const int64_t *spatial_shapes,
+    const int64_t *level_start_index, const void *sampling_loc, const void *attn_weight,
+    const void *grad_output, int64_t go_stride_b, int64_t go_stride_q, int64_t go_stride_h,
+    int64_t go_stride_c, int batch, int spatial_size, int num_heads, int channels,
+    int num_levels, int num_query, int num_point, int im2col_step, int force_generic_col2im,
+    void *grad_value, void *grad_sampling_loc, void *grad_attn_weight, void *workspace,
+    int64_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

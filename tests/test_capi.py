@@ -148,6 +148,33 @@ def test_msda_validation():
     assert _msda(b=0) == 0
 
 
+def _msda_bwd(dtype=0, step=64, b=2, nq=4, ws=0):
+    return _bevk.lib().bevk_msda_backward(dtype, NULL, NULL, NULL, NULL, NULL, NULL,
+                                          nq * 256, 256, 32, 1, b, 10, 8, 32, 1, nq, 4, step,
+                                          0, NULL, NULL, NULL, NULL, ws, NULL)
+
+
+def test_msda_backward_workspace_bytes():
+    f = _bevk.lib().bevk_msda_backward_workspace_bytes
+    assert f(0, 2, 10, 8, 32) == 0
+    assert f(3, 2, 10, 8, 32) == 0
+    assert f(1, 2, 10, 8, 32) == 2 * 10 * 8 * 32 * 4
+    assert f(2, 6, 30825, 8, 32) == 6 * 30825 * 8 * 32 * 4
+    assert f(4, 2, 10, 8, 32) == -1
+    assert f(1, -1, 10, 8, 32) == -1
+
+
+def test_msda_backward_validation():
+    assert _msda_bwd(step=0) == INVALID and "im2col_step" in _err()
+    assert _msda_bwd(b=6, step=4) == INVALID and "batch must divide im2col_step" in _err()
+    assert _msda_bwd() == INVALID and "null" in _err()
+    assert _msda_bwd(dtype=1) == INVALID and "workspace" in _err()
+    assert _msda_bwd(dtype=1, ws=2 * 10 * 8 * 32 * 4) == INVALID and "null" in _err()
+    assert _msda_bwd(dtype=7) == INVALID and "dtype" in _err()
+    assert _msda_bwd(nq=0) == 0                     # f32: nothing to add
+    assert _msda_bwd(b=0) == 0
+
+
 def test_call_raises_runtime_error_with_message():
     with pytest.raises(RuntimeError, match="batch must divide im2col_step"):
         _bevk.call("bevk_msda_forward", 0, NULL, NULL, NULL, NULL, NULL, 6, 10, 8, 32, 1, 4, 4,

@@ -1,0 +1,190 @@
+"""MSDA backward on the GPU vs the float64 CPU oracle (oracle/msda.py backward, pinned
+against autograd and finite differences), through the reference-shaped API
+(msda_opt2.ms_deform_attn_backward -> _modulated_deform_conv_ext.backward -> libbevk.so
+bevk_msda_backward).
+
+Reduced BASELINE configurations are compared whole. At full size, grad_sampling_loc and
+grad_attn_weight of a random query subset are compared with the oracle run on that
+subset (they depend only on the query's own data), and the whole of grad_value and
+grad_attn_weight through the identities of a function linear in value and in attn:
+  sum(grad_value * value) = sum(grad_output * out) = sum(grad_attn * attn)."""
+import pytest
+import torch
+
+from _tol import check
+from oracle import inputs
+from oracle import msda as om
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+IDS = ["fp32", "fp16", "bf16"]
+DEV = torch.device("cuda")
+
+
+def _api():
+    import msda_opt2
+    return msda_opt2
+
+
+def _grad_output(d, seed=11, dtype=torch.float32):
+    B, Lq, NH = d["sampling_loc"].shape[:3]
+    D = d["value"].shape[-1]
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(B, Lq, NH * D, generator=g).to(dtype)
+
+
+def _dev(d, dtype):
+    return dict(value=d["value"].to(dtype).to(DEV), spatial_shapes=d["spatial_shapes"].to(DEV),
+                level_start_index=d["level_start_index"].to(DEV),
+                sampling_loc=d["sampling_loc"].to(dtype).to(DEV),
+                attn_weight=d["attn_weight"].to(dtype).to(DEV))
+
+
+def _run(d, go, dtype, **kw):
+    dd = _dev(d, dtype)
+    gv, gl, ga = _api().ms_deform_attn_backward(**dd, grad_output=go.to(dtype).to(DEV), **kw)
+    torch.cuda.synchronize()
+    return gv.cpu(), gl.cpu(), ga.cpu()
+
+
+def _ref(d, go, dtype, q_idx=None):
+    """Oracle backward in float64 on the dtype-rounded inputs, at the sampling coordinates
+    the fp32 algorithm defines (h_im = loc*H - 0.5 rounded to fp32, as the reference's
+    `float h_im` and the kernel's fused multiply-add compute it: grad_sampling_loc scales
+    the coordinate's rounding error by W, above the 1e-4 bound); optionally a query subset
+    (its grad_value then covers only that subset's samples)."""
+    v = d["value"].to(dtype).double()
+    loc = d["sampling_loc"].to(dtype).double()
+    att = d["attn_weight"].to(dtype).double()
+    g = go.to(dtype).double()
+    if q_idx is not None:
+        loc, att, g = loc[:, q_idx], att[:, q_idx], g[:, q_idx]
+    coord = None if dtype == torch.float64 else torch.float32
+    return om.backward(v, d["spatial_shapes"], d["level_start_index"], loc, att, g,
+                       coord_dtype=coord)
+
+
+def _check3(got, ref, dtype, what):
+    for name, x, r in zip(("grad_value", "grad_sampling_loc", "grad_attn_weight"), got, ref):
+        assert x.dtype == dtype, f"{what} {name}: dtype {x.dtype}"
+        check(x, r, dtype, f"{what} {name}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
+@pytest.mark.parametrize("cfg", ["msda_detr", "msda_tsa", "msda_sca"])
+def test_configs_reduced(cfg, dtype):
+    d = inputs.msda_inputs(cfg, scale_q=0.02)
+    go = _grad_output(d)
+    _check3(_run(d, go, dtype), _ref(d, go, dtype), dtype, f"{cfg} {dtype}")
+
+
+def test_fp64():
+    d = inputs.msda_inputs("msda_sca", scale_q=0.01, batch=2)
+    go = _grad_output(d)
+    got = _run(d, go, torch.float64)
+    for x, r in zip(got, _ref(d, go, torch.float64)):
+        torch.testing.assert_close(x, r, rtol=1e-10, atol=1e-10)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
+@pytest.mark.parametrize("cfg", ["msda_detr", "msda_tsa", "msda_sca"])
+def test_configs_full_size(cfg, dtype):
+    d = inputs.msda_inputs(cfg)
+    go = _grad_output(d)
+    gv, gl, ga = _run(d, go, dtype)
+    nq = d["sampling_loc"].shape[1]
+    g = torch.Generator().manual_seed(321)
+    q_idx = torch.randperm(nq, generator=g)[:300].sort().values
+    q_idx = torch.cat([q_idx, torch.tensor([0, nq - 1])]).unique()
+    _, rl, ra = _ref(d, go, dtype, q_idx)
+    check(gl[:, q_idx], rl, dtype, f"{cfg} full {dtype} grad_sampling_loc")
+    check(ga[:, q_idx], ra, dtype, f"{cfg} full {dtype} grad_attn_weight")
+    # whole-tensor identities, float64 sums of the kernel's own outputs
+    v = d["value"].to(dtype).double()
+    a = d["attn_weight"].to(dtype).double()
+    out = _api().ms_deform_attn_forward(**_dev(d, dtype)).cpu().double()
+    lhs = (go.to(dtype).double() * out).sum().item()
+    rel = 1e-4 if dtype == torch.float32 else 2e-2
+    scale = (go.to(dtype).double() * out).abs().sum().item()
+    assert abs((gv.double() * v).sum().item() - lhs) <= rel * scale, cfg
+    assert abs((ga.double() * a).sum().item() - lhs) <= rel * scale, cfg
+    for t in (gv, gl, ga):
+        assert torch.isfinite(t).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["fp32", "fp16"])
+def test_strided_grad_output(dtype):
+    """grad_output read through its strides (binding_musa.mu:446-447 views it)."""
+    d = inputs.msda_inputs("msda_detr", scale_q=0.01, batch=2)
+    go = _grad_output(d)
+    wide = torch.zeros(go.shape[0], go.shape[1], 2 * go.shape[2])
+    wide[..., ::2] = go
+    strided = wide.to(dtype).to(DEV)[..., ::2]
+    assert not strided.is_contiguous()
+    dd = _dev(d, dtype)
+    got = _api().ms_deform_attn_backward(**dd, grad_output=strided)
+    ref = _api().ms_deform_attn_backward(**dd, grad_output=go.to(dtype).to(DEV))
+    torch.cuda.synchronize()
+    for x, r in zip(got, ref):
+        check(x.cpu(), r.cpu().double(), dtype, "strided grad_output")
+
+
+def test_grad_value_accumulates_fp32_and_is_written_fp16():
+    """fp32: the kernels add into the caller's grad_value; fp16: the fp32 accumulator is
+    narrowed over it (binding_musa.mu:508-510)."""
+    import _modulated_deform_conv_ext as ext
+    d = inputs.msda_inputs("msda_sca", scale_q=0.005, batch=1)
+    go = _grad_output(d)
+    for dtype in (torch.float32, torch.float16):
+        dd = _dev(d, dtype)
+        gv = torch.full_like(dd["value"], 3.0)
+        gl = torch.full_like(dd["sampling_loc"], 7.0)
+        ga = torch.full_like(dd["attn_weight"], 7.0)
+        ext.backward(dd["value"], dd["spatial_shapes"], dd["level_start_index"],
+                     dd["sampling_loc"], dd["attn_weight"], go.to(dtype).to(DEV), gv, gl, ga)
+        torch.cuda.synchronize()
+        rv, rl, ra = _ref(d, go, dtype)
+        base = 3.0 if dtype == torch.float32 else 0.0
+        check(gv.cpu(), rv + base, dtype, f"{dtype} grad_value")
+        check(gl.cpu(), rl, dtype, f"{dtype} grad_sampling_loc written")
+        check(ga.cpu(), ra, dtype, f"{dtype} grad_attn_weight written")
+
+
+@pytest.mark.parametrize("geom", [
+    (2, [(5, 6), (3, 4)], 7, 2, 48, 3),        # D not a power of two
+    (1, [(4, 7)], 5, 3, 96, 2),                # D > 64: two channel passes
+    (2, [(1, 1), (2, 3), (6, 2)], 9, 4, 8, 5),
+    (1, [(9, 11)], 13, 1, 1, 1),
+    (3, [(3, 3), (2, 2)], 6, 2, 64, 4),
+])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16,
+                                   torch.float64], ids=IDS + ["fp64"])
+def test_generic_shapes(geom, dtype):
+    d = inputs.msda_random(*geom, seed=13, loc_lo=-0.3, loc_hi=1.3)
+    go = _grad_output(d, seed=3)
+    got = _run(d, go, dtype)
+    ref = _ref(d, go, dtype)
+    if dtype == torch.float64:
+        for x, r in zip(got, ref):
+            torch.testing.assert_close(x, r, rtol=1e-10, atol=1e-10)
+    else:
+        _check3(got, ref, dtype, f"{geom} {dtype}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["fp32", "fp16"])
+def test_empty_queries(dtype):
+    d = inputs.msda_random(2, [(3, 4)], 0, 2, 32, 2)
+    go = torch.zeros(2, 0, 64)
+    gv, gl, ga = _run(d, go, dtype)
+    assert gl.numel() == 0 and ga.numel() == 0
+    assert gv.abs().max().item() == 0.0
+
+
+def test_im2col_step_contract():
+    d = inputs.msda_random(6, [(3, 4)], 2, 2, 32, 2)
+    go = _grad_output(d)
+    with pytest.raises(RuntimeError, match="batch must divide im2col_step"):
+        _run(d, go, torch.float32, im2col_step=4)
+    got = _run(d, go, torch.float32, im2col_step=3)
+    _check3(got, _ref(d, go, torch.float32), torch.float32, "im2col_step=3")

@@ -58,6 +58,12 @@ def test_backward_entry_points_check_their_inputs():
             torch.zeros(1, 5, 5, 4), torch.zeros(1, 5, 5, 18), torch.zeros(1, 5, 5, 9))
     with pytest.raises(RuntimeError, match="deformable_group == 1"):
         ext.modulated_deformable_col2im_nhwc_cuda(*([None] * 18), 2, None, None, None)
+    d = inputs.msda_random(1, [(3, 3)], 2, 8, 32, 4)
+    go = torch.zeros(1, 2, 256)
+    with pytest.raises(RuntimeError, match="HIP device tensor"):
+        ext.backward(d["value"], d["spatial_shapes"], d["level_start_index"],
+                     d["sampling_loc"], d["attn_weight"], go, torch.zeros_like(d["value"]),
+                     torch.zeros_like(d["sampling_loc"]), torch.zeros_like(d["attn_weight"]))
 
 
 def test_pack_backend_selection(monkeypatch):

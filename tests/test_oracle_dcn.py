@@ -272,7 +272,7 @@ def test_ungated_columns_equal_gated_values():
     h2 = h.detach().clone().requires_grad_()
     v = od.bilinear_nhwc(xx[0], h2, w, gate=False)
     g_off = torch.autograd.grad(v.sum(), h2)[0]
-    assert g_on.item() == 0.0 and float(v.abs().sum()) == 0.0
+    assert g_on.item() == 0.0 and float(v.detach().abs().sum()) == 0.0
     # cell [-1, 0]: d/dh = (1 - lw) * x[0, 0] + lw * x[0, 1] summed over channels
     expect = (0.5 * xx[0, 0, 0] + 0.5 * xx[0, 0, 1]).sum()
     torch.testing.assert_close(g_off[0], expect)

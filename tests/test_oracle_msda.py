@@ -111,3 +111,104 @@ def test_fixture():
     out = om.forward(fx["value"], fx["spatial_shapes"], fx["level_start_index"],
                      fx["sampling_loc"], fx["attn_weight"])
     torch.testing.assert_close(out, fx["out"], rtol=0, atol=0)
+
+
+# ---------------------------------------------------------------------------------------
+# backward: the explicit per-sample restatement against autograd of both forward
+# restatements (the direct loop and torch's grid_sample backward) and finite differences.
+# A swapped W/H factor, a sign error in one corner term or a missing attention factor
+# fails the autograd comparisons.
+
+def _autograd(fwd, d, grad_output):
+    v = d["value"].clone().requires_grad_(True)
+    loc = d["sampling_loc"].clone().requires_grad_(True)
+    a = d["attn_weight"].clone().requires_grad_(True)
+    out = fwd(v, d["spatial_shapes"], d["level_start_index"], loc, a)
+    gv, gl, ga = torch.autograd.grad(out, (v, loc, a), grad_output, allow_unused=True)
+    return gv, gl, ga
+
+
+@pytest.mark.parametrize("geom", [
+    (2, [(5, 6), (3, 4)], 7, 2, 4, 3),
+    (1, [(4, 7)], 5, 3, 2, 4),
+    (2, [(1, 1), (2, 3), (6, 2)], 4, 1, 3, 2),
+])
+@pytest.mark.parametrize("fwd", ["loop", "grid_sample"])
+def test_backward_vs_autograd(geom, fwd):
+    d = _d64(inputs.msda_random(*geom, seed=5, loc_lo=-0.4, loc_hi=1.4))
+    B, Lq, NH, L, P, _ = d["sampling_loc"].shape
+    D = d["value"].shape[-1]
+    g = torch.Generator().manual_seed(9)
+    go = torch.randn(B, Lq, NH * D, generator=g, dtype=D64)
+    ref = _autograd(om.forward if fwd == "loop" else om.forward_grid_sample, d, go)
+    got = om.backward(**d, grad_output=go)
+    for r, x in zip(ref, got):
+        torch.testing.assert_close(x, r, rtol=1e-11, atol=1e-12)
+
+
+def test_backward_gradcheck():
+    """Finite differences on a tiny pyramid, locations kept off the integer grid lines
+    (where the bilinear form has kinks)."""
+    d = _d64(inputs.msda_random(1, [(3, 4), (2, 2)], 3, 2, 3, 2, seed=7, loc_lo=-0.3,
+                                loc_hi=1.3))
+    ss, lsi = d["spatial_shapes"], d["level_start_index"]
+    torch.autograd.gradcheck(
+        lambda v, loc, a: om.forward(v, ss, lsi, loc, a),
+        (d["value"].requires_grad_(True), d["sampling_loc"].requires_grad_(True),
+         d["attn_weight"].requires_grad_(True)), eps=1e-6, atol=1e-6)
+
+
+def test_backward_outside_gate_is_zero():
+    """Samples past the -1 / H gates: every gradient is zero."""
+    ss, lsi, s = inputs.msda_meta([(4, 5)])
+    value = torch.randn(1, s, 1, 3, dtype=D64)
+    loc = torch.tensor([[-0.2, 0.5], [0.5, -0.2], [1.2, 0.5], [0.5, 1.3]], dtype=D64)
+    loc = loc.view(1, 4, 1, 1, 1, 2)
+    attn = torch.ones(1, 4, 1, 1, 1, dtype=D64)
+    go = torch.randn(1, 4, 3, dtype=D64)
+    gv, gl, ga = om.backward(value, ss, lsi, loc, attn, go)
+    assert gv.abs().max() == 0 and gl.abs().max() == 0 and ga.abs().max() == 0
+
+
+def test_backward_pixel_centre():
+    """At a pixel centre all weight is on one corner: grad_value is top*a there, grad_attn
+    is top . v(pixel), and grad_loc is W (H) times the one-sided difference toward the
+    next column (row)."""
+    ss, lsi, s = inputs.msda_meta([(3, 5)])
+    g = torch.Generator().manual_seed(1)
+    value = torch.randn(1, s, 1, 4, generator=g, dtype=D64)
+    y, x = 1, 2
+    loc = torch.tensor([(x + 0.5) / 5, (y + 0.5) / 3], dtype=D64).view(1, 1, 1, 1, 1, 2)
+    attn = torch.full((1, 1, 1, 1, 1), 0.7, dtype=D64)
+    go = torch.randn(1, 1, 4, generator=g, dtype=D64)
+    gv, gl, ga = om.backward(value, ss, lsi, loc, attn, go)
+    vmap = value[0, :, 0].view(3, 5, 4)
+    expect_gv = torch.zeros(3, 5, 4, dtype=D64)
+    expect_gv[y, x] = 0.7 * go[0, 0]
+    torch.testing.assert_close(gv[0, :, 0].view(3, 5, 4), expect_gv, rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(ga.flatten()[0], (go[0, 0] * vmap[y, x]).sum(), rtol=1e-12,
+                               atol=1e-12)
+    gx = 5 * 0.7 * (go[0, 0] * (vmap[y, x + 1] - vmap[y, x])).sum()
+    gy = 3 * 0.7 * (go[0, 0] * (vmap[y + 1, x] - vmap[y, x])).sum()
+    torch.testing.assert_close(gl.flatten(), torch.stack([gx, gy]), rtol=1e-12, atol=1e-12)
+
+
+def test_fp32_coordinates():
+    """coord_dtype=float32 is the identity where loc*H - 0.5 is exact in fp32 (loc a
+    multiple of 2^-10, H <= 256), and otherwise moves h_im by at most half an fp32 ulp."""
+    ss, lsi, s = inputs.msda_meta([(37, 200), (19, 100)])
+    g = torch.Generator().manual_seed(4)
+    value = torch.randn(1, s, 2, 5, generator=g, dtype=D64)
+    loc = (torch.randint(-100, 1124, (1, 6, 2, 2, 3, 2), generator=g) / 1024.0).to(D64)
+    attn = torch.rand(1, 6, 2, 2, 3, generator=g, dtype=D64)
+    go = torch.randn(1, 6, 10, generator=g, dtype=D64)
+    for a, b in zip(om.backward(value, ss, lsi, loc, attn, go, coord_dtype=torch.float32),
+                    om.backward(value, ss, lsi, loc, attn, go)):
+        torch.testing.assert_close(a, b, rtol=0, atol=0)
+    torch.testing.assert_close(om.forward(value, ss, lsi, loc, attn, coord_dtype=torch.float32),
+                               om.forward(value, ss, lsi, loc, attn), rtol=0, atol=0)
+    loc_h = torch.rand(1000, generator=g, dtype=D64) * 1.4 - 0.2
+    h, _ = om._coords(loc_h, loc_h, 200, 200, torch.float32)
+    exact = loc_h * 200 - 0.5
+    assert ((h - exact).abs() <= torch.abs(exact) * 2.0 ** -24 + 1e-300).all()
+    assert (h != exact).any()
