@@ -11,7 +11,9 @@ Len_q 10000, 8 heads x 32, 8 points), fp32, with inputs resident in HBM:
   roofline   the same figure against 8 TB/s, kernel time from HIP events on the stream
              the kernel runs on; `traffic` from the committed rocprofv3 counter summary
   secondary  the fused NHWC DCNv2 res4 fp16 forward in MFMA TFLOP/s (2*M*K*Cout flops)
-  configs    every BASELINE configuration x dtype: us, GB/s or TFLOP/s, roofline fraction
+  configs    every BASELINE configuration x dtype: us, GB/s or TFLOP/s, roofline fraction;
+             the backward kernels (MSDA backward, DCN NHWC column-to-image) in GB/s of
+             compulsory bytes
   cpu_baseline  the CPU oracle (grid_sample form) on the same SCA workload, timed on the
              host cores of this machine
 Cold-cache protocol (default): a 1 GiB buffer is overwritten before every timed launch so
@@ -153,6 +155,60 @@ def dcn_front_case(name, dtype, cache):
         x, w_off, b_off, B, C, H, W, H, W, 3, 3, 1, 1, 1, 1, 1, 1, 1, col)), nbytes
 
 
+def msda_bwd_case(name, dtype, cache):
+    """MSDA backward (ext.backward) of one configuration. Algorithmic bytes: value,
+    sampling_loc, attn_weight and grad_output read once; grad_value, grad_sampling_loc and
+    grad_attn_weight written once (in the input dtype)."""
+    import torch
+    import _modulated_deform_conv_ext as ext
+    from oracle import inputs
+    if name not in cache:
+        cache[name] = inputs.msda_inputs(name)
+    d = cache[name]
+    dev = torch.device("cuda")
+    v = d["value"].to(dtype).to(dev)
+    ss = d["spatial_shapes"].to(dev)
+    lsi = d["level_start_index"].to(dev)
+    loc = d["sampling_loc"].to(dtype).to(dev)
+    att = d["attn_weight"].to(dtype).to(dev)
+    B, S, NH, D = v.shape
+    g = torch.Generator().manual_seed(17)
+    go = torch.randn(B, loc.shape[1], NH * D, generator=g).to(dtype).to(dev)
+    gv = torch.zeros_like(v)
+    gl = torch.empty_like(loc)
+    ga = torch.empty_like(att)
+    es = v.element_size()
+    nbytes = (2 * (v.numel() + loc.numel() + att.numel()) + go.numel()) * es
+    return (lambda: ext.backward(v, ss, lsi, loc, att, go, gv, gl, ga, 64, False)), nbytes
+
+
+def dcn_bwd_case(name, dtype, cache):
+    """NHWC column-to-image backward (col2im_nhwc: grad_x, grad_offset, grad_mask) of one
+    DCN configuration. Algorithmic bytes: column gradient, x, offset and mask read once;
+    fp32 grad_x, grad_offset and grad_mask written once."""
+    import torch
+    import _modulated_deform_conv_ext as ext
+    from oracle import inputs
+    if name not in cache:
+        cache[name] = inputs.nchw_to_nhwc(inputs.dcn_inputs(name))
+    d = cache[name]
+    dev = torch.device("cuda")
+    x = d["x"].to(dtype).to(dev)
+    off = d["offset"].to(dtype).to(dev)
+    msk = d["mask"].to(dtype).to(dev)
+    B, H, W, C = x.shape
+    g = torch.Generator().manual_seed(19)
+    dcol = torch.randn(B * H * W, 9 * C, generator=g).to(dtype).to(dev)
+    gx = torch.zeros(B, H, W, C, dtype=torch.float32, device=dev)
+    goff = torch.empty(B, H, W, 18, dtype=torch.float32, device=dev)
+    gmask = torch.empty(B, H, W, 9, dtype=torch.float32, device=dev)
+    es = x.element_size()
+    nbytes = ((dcol.numel() + x.numel() + off.numel() + msk.numel()) * es
+              + (gx.numel() + goff.numel() + gmask.numel()) * 4)
+    return (lambda: ext.modulated_deformable_col2im_nhwc_cuda(
+        dcol, x, off, msk, B, C, H, W, H, W, 3, 3, 1, 1, 1, 1, 1, 1, 1, gx, goff, gmask)), nbytes
+
+
 def dcn_nchw_case(name, cache):
     """Module-level fp32 NCHW forward (modulated_deform_conv2d)."""
     import torch
@@ -259,6 +315,10 @@ def main():
             fn, _ = dcn_nchw_case(name, cache)
         elif kind == "dcn_front":
             fn, _ = dcn_front_case(name, dtype_of(dt), cache)
+        elif kind == "msda_bwd":
+            fn, _ = msda_bwd_case(name, dtype_of(dt), cache)
+        elif kind == "dcn_bwd":
+            fn, _ = dcn_bwd_case(name, dtype_of(dt), cache)
         elif kind == "copy":
             # plain copy of known size: the counter calibration reference
             n = int(name) if name else 256 << 20
@@ -344,6 +404,20 @@ def main():
             g = nb / (m * 1e-6) / 1e9
             rows.append({"config": name + "_front_end", "dtype": "fp16", "us": round(m, 2),
                          "GB/s": round(g, 1), "frac_hbm": round(g / HBM_PEAK_GBS, 4)})
+            for dt in ("fp16", "fp32"):
+                f, nb = dcn_bwd_case(name, dtype_of(dt), cache)
+                m, _, _ = timer.run(f, max(10, steps // 2), 3)
+                g = nb / (m * 1e-6) / 1e9
+                rows.append({"config": name + "_col2im_nhwc_backward", "dtype": dt,
+                             "us": round(m, 2), "GB/s": round(g, 1),
+                             "frac_hbm": round(g / HBM_PEAK_GBS, 4)})
+        for name in ("msda_sca", "msda_tsa", "msda_detr"):
+            for dt in ("fp32", "fp16", "bf16"):
+                f, nb = msda_bwd_case(name, dtype_of(dt), cache)
+                m, _, _ = timer.run(f, max(10, steps // 2), 3)
+                g = nb / (m * 1e-6) / 1e9
+                rows.append({"config": name + "_backward", "dtype": dt, "us": round(m, 2),
+                             "GB/s": round(g, 1), "frac_hbm": round(g / HBM_PEAK_GBS, 4)})
         line["configs"] = rows
 
     if not args.no_cpu_baseline:

@@ -13,10 +13,12 @@
 // A corner outside the image contributes nothing (the reference checks each corner; there
 // is no separate -1 / H gate in the backward).
 //
-// Mapping: LPP lanes own one (m, t) pair and sweep its C channels with 16-byte vectors, so
-// the dcol row and the four corner rows are read as contiguous runs; the three reductions
-// over channels meet in a shuffle butterfly and one lane writes them (no atomics, no
-// pre-zeroing for gOff / gMask). gX needs atomics: several pairs touch one input pixel.
+// Mapping: LPP = min(64, next power of two >= C) lanes own one (m, t) pair; lane li takes
+// channels li, li + LPP, ..., so each gX atomic instruction adds LPP consecutive floats
+// (fp32 atomics are issued per cache line: one lane holding 4 or 8 consecutive channels
+// made them 4-9x slower). The three reductions over channels meet in a shuffle butterfly
+// and one lane writes them (no atomics, no pre-zeroing for gOff / gMask). gX needs
+// atomics: several pairs touch one input pixel.
 #include "bevk_common.h"
 #include "bevk_launch.h"
 
@@ -27,7 +29,7 @@ namespace {
 
 constexpr int kBlock = 256;
 
-template <typename T, int VEC, bool FUSED_Y>
+template <typename T, bool FUSED_Y>
 __global__ void __launch_bounds__(kBlock) col2im_nhwc_kernel(
     const T *__restrict__ dcol, const T *__restrict__ im, const T *__restrict__ offset,
     const T *__restrict__ mask, const DcnGeom g, int lpp_log2, float *__restrict__ gx,
@@ -80,36 +82,29 @@ __global__ void __launch_bounds__(kBlock) col2im_nhwc_kernel(
   const int64_t p2 = p1 + C, p3 = p1 + (int64_t)g.width * C, p4 = p3 + C;
   const T *drow = dcol + (m * T_ + t) * C;
   const bool coord = goff != nullptr;  // gX alone needs no image reads
-  using V = Vec<T, VEC>;
   float ah = 0.f, aw = 0.f, am = 0.f;
   if (live) {
-    for (int c = li * VEC; c < C; c += LPP * VEC) {
-      V d, v1, v2, v3, v4;
-      if constexpr (VEC > 1) {
-        d = load_vec<T, VEC>(drow + c);
-      } else {
-        d.v[0] = drow[c];
-      }
-#pragma unroll
-      for (int k = 0; k < VEC; ++k) v1.v[k] = v2.v[k] = v3.v[k] = v4.v[k] = (T)0.f;
-      if (coord && c1) v1 = load_vec<T, VEC>(im + p1 + c);
-      if (coord && c2) v2 = load_vec<T, VEC>(im + p2 + c);
-      if (coord && c3) v3 = load_vec<T, VEC>(im + p3 + c);
-      if (coord && c4) v4 = load_vec<T, VEC>(im + p4 + c);
-#pragma unroll
-      for (int k = 0; k < VEC; ++k) {
-        const float dc = (float)d.v[k], ds = dc * mk;
-        const float x1 = (float)v1.v[k], x2 = (float)v2.v[k];
-        const float x3 = (float)v3.v[k], x4 = (float)v4.v[k];
+    // lane li takes channels li, li + LPP, ...: every load and every atomic below covers
+    // LPP consecutive elements (fp32 atomics run several times slower when the lanes of
+    // one instruction are spread over more cache lines)
+#pragma unroll 4
+    for (int c = li; c < C; c += LPP) {
+      const float dc = (float)drow[c], ds = dc * mk;
+      float x1 = 0.f, x2 = 0.f, x3 = 0.f, x4 = 0.f;
+      if (coord) {
+        if (c1) x1 = (float)im[p1 + c];
+        if (c2) x2 = (float)im[p2 + c];
+        if (c3) x3 = (float)im[p3 + c];
+        if (c4) x4 = (float)im[p4 + c];
         ah += ds * (-hw * x1 - lw * x2 + hw * x3 + lw * x4);
         aw += ds * (-hh * x1 + hh * x2 - lh * x3 + lh * x4);
         am += dc * (w1 * x1 + w2 * x2 + w3 * x3 + w4 * x4);
-        if (gx != nullptr) {
-          if (c1) unsafeAtomicAdd(gx + p1 + c + k, ds * w1);
-          if (c2) unsafeAtomicAdd(gx + p2 + c + k, ds * w2);
-          if (c3) unsafeAtomicAdd(gx + p3 + c + k, ds * w3);
-          if (c4) unsafeAtomicAdd(gx + p4 + c + k, ds * w4);
-        }
+      }
+      if (gx != nullptr) {
+        if (c1) unsafeAtomicAdd(gx + p1 + c, ds * w1);
+        if (c2) unsafeAtomicAdd(gx + p2 + c, ds * w2);
+        if (c3) unsafeAtomicAdd(gx + p3 + c, ds * w3);
+        if (c4) unsafeAtomicAdd(gx + p4 + c, ds * w4);
       }
     }
   }
@@ -239,27 +234,15 @@ hipError_t launch_nchw_t(const DcnGeom &g, const void *col, const void *im, cons
 template <typename T, bool FY>
 hipError_t launch_t(const DcnGeom &g, const void *dcol, const void *im, const void *off,
                     const void *msk, float *gx, float *goff, float *gmask, hipStream_t stream) {
-  constexpr int VEC = 16 / sizeof(T);
-  const int C = g.channels;
-  const bool vec = (C % VEC) == 0;
-  const int per_lane = vec ? VEC : 1;
-  int lpp = 1;
-  while (lpp < 64 && lpp * per_lane < C) lpp *= 2;
   int lpp_log2 = 0;
-  while ((1 << lpp_log2) < lpp) ++lpp_log2;
+  while (lpp_log2 < 6 && (1 << lpp_log2) < g.channels) ++lpp_log2;
   const int64_t pairs = (int64_t)g.height_col * g.width_col * g.kernel_h * g.kernel_w;
   const int64_t threads = pairs << lpp_log2;
   const dim3 grid((unsigned)((threads + kBlock - 1) / kBlock), g.batch);
-  if (vec)
-    hipLaunchKernelGGL((col2im_nhwc_kernel<T, VEC, FY>), grid, dim3(kBlock), 0, stream,
-                       static_cast<const T *>(dcol), static_cast<const T *>(im),
-                       static_cast<const T *>(off), static_cast<const T *>(msk), g, lpp_log2,
-                       gx, goff, gmask);
-  else
-    hipLaunchKernelGGL((col2im_nhwc_kernel<T, 1, FY>), grid, dim3(kBlock), 0, stream,
-                       static_cast<const T *>(dcol), static_cast<const T *>(im),
-                       static_cast<const T *>(off), static_cast<const T *>(msk), g, lpp_log2,
-                       gx, goff, gmask);
+  hipLaunchKernelGGL((col2im_nhwc_kernel<T, FY>), grid, dim3(kBlock), 0, stream,
+                     static_cast<const T *>(dcol), static_cast<const T *>(im),
+                     static_cast<const T *>(off), static_cast<const T *>(msk), g, lpp_log2,
+                     gx, goff, gmask);
   return hipGetLastError();
 }
 
