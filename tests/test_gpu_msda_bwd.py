@@ -188,3 +188,48 @@ def test_im2col_step_contract():
         _run(d, go, torch.float32, im2col_step=4)
     got = _run(d, go, torch.float32, im2col_step=3)
     _check3(got, _ref(d, go, torch.float32), torch.float32, "im2col_step=3")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["fp32", "fp16"])
+def test_autograd_function(dtype):
+    """MultiScaleDeformableAttnFunction: autograd gradients equal the oracle's; the
+    integer inputs get none."""
+    d = inputs.msda_inputs("msda_sca", scale_q=0.005, batch=2)
+    go = _grad_output(d)
+    dd = _dev(d, dtype)
+    v = dd["value"].requires_grad_(True)
+    loc = dd["sampling_loc"].requires_grad_(True)
+    a = dd["attn_weight"].requires_grad_(True)
+    out = _api().multi_scale_deformable_attn(v, dd["spatial_shapes"], dd["level_start_index"],
+                                             loc, a)
+    (out * go.to(dtype).to(DEV)).sum().backward()
+    torch.cuda.synchronize()
+    _check3((v.grad.cpu(), loc.grad.cpu(), a.grad.cpu()), _ref(d, go, dtype), dtype,
+            f"Function {dtype}")
+
+
+def test_autograd_expanded_grad_output():
+    """A gradient that cannot be viewed per (b, q, head, c) (an expanded one) is made dense."""
+    d = inputs.msda_random(1, [(4, 5)], 3, 2, 8, 2, seed=2)
+    dd = _dev(d, torch.float32)
+    v = dd["value"].requires_grad_(True)
+    out = _api().multi_scale_deformable_attn(v, dd["spatial_shapes"], dd["level_start_index"],
+                                             dd["sampling_loc"], dd["attn_weight"])
+    out.sum().backward()                       # grad_output = ones expanded from a scalar
+    torch.cuda.synchronize()
+    go = torch.ones(1, 3, 16)
+    rv, _, _ = _ref(d, go, torch.float32)
+    check(v.grad.cpu(), rv, torch.float32, "expanded grad_output")
+
+
+def test_gradcheck_fp64():
+    """Finite differences of the GPU forward against the GPU backward, float64, locations
+    away from the integer grid lines."""
+    d = inputs.msda_random(1, [(3, 4), (2, 3)], 3, 2, 4, 2, seed=21, loc_lo=-0.2,
+                           loc_hi=1.2)
+    dd = _dev(d, torch.float64)
+    fn = _api().MultiScaleDeformableAttnFunction.apply
+    torch.autograd.gradcheck(
+        lambda v, loc, a: fn(v, dd["spatial_shapes"], dd["level_start_index"], loc, a, 64),
+        (dd["value"].requires_grad_(True), dd["sampling_loc"].requires_grad_(True),
+         dd["attn_weight"].requires_grad_(True)), eps=1e-6, atol=1e-6)
