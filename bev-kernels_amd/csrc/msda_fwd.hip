@@ -334,6 +334,285 @@ __global__ void __launch_bounds__(kBlock) msda_wave_lds_kernel(const WaveParams 
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// LDS-cached kernel. One block of kCachedBlock threads per CU, persistent. Work item = one
+// (batch, head) slice (or a query range of it); item i runs on XCD i % 8 and the XCD's
+// blocks split its queries, so each XCD's L2 holds one slice at a time. At the start of an
+// item the block copies the slice's coarsest levels (whole image rows, coarsest level
+// first, as many as fit) into LDS; corners in cached rows are then read from LDS, the rest
+// from the value buffer. LDS gathers do not use the vector-memory path (whose throughput
+// is set by the number of 128 B lines it serves, not by the bytes used), and the coarse
+// levels are exactly the ones each line of which is read by hundreds of samples.
+// Within a wave round, iteration `it` covers one level for UPI units, so fully cached
+// levels never diverge; invalid corners of a cached level read a zero row of the cache.
+constexpr int kLdsBytes = 160 * 1024;               // gfx950 LDS per CU
+constexpr uint32_t kLdsFlag = 0x80000000u;          // corner offset names an LDS address
+
+struct CachedParams {
+  const void *value;
+  const int64_t *shapes;
+  const int64_t *lsi;
+  const void *loc;
+  const void *attn;
+  void *out;
+  int S, NH, NQ;
+  int nitems;            // slices * parts
+  int parts;             // query ranges per slice
+  int blocks_per_xcd;    // gridDim.x / 8
+  int xcd_group;         // XCDs sharing one item (1, 2, 4 or 8)
+  uint32_t batch_bytes;  // bytes of value per batch (buffer range; < 2^31)
+};
+
+// WPB waves per block, UPW (b, q, head) units per wave round, MIXL the one level that may
+// be cached in part (-1: none).
+template <typename T, int D, int NL, int NP, int WPB, int UPW, int MIXL>
+__global__ void __launch_bounds__(WPB * kWave) msda_cached_kernel(const CachedParams p) {
+  using V = Vec<T, 16 / sizeof(T)>;
+  constexpr int VEC = 16 / sizeof(T);
+  constexpr int G = D / VEC;           // lanes per sample
+  constexpr int NS = NL * NP;          // samples per unit
+  constexpr int kBlockThreads = WPB * kWave;
+  constexpr int kCacheBytes = kLdsBytes - WPB * UPW * NS * (int)sizeof(SampleGeo);
+  constexpr int LPL = NP * G;          // lanes per (unit, level)
+  constexpr int UPI = kWave / LPL;     // units per iteration
+  constexpr int NACC = UPW / UPI;      // accumulator sets per lane
+  constexpr int NIT = NL * NACC;       // iterations per round
+  constexpr uint32_t ROW = D * sizeof(T);
+  static_assert(G >= 1 && UPW * NS <= kWave && LPL <= kWave && kWave % LPL == 0 &&
+                    UPW % UPI == 0, "unsupported MSDA geometry");
+
+  __shared__ __attribute__((aligned(16))) unsigned char cache[kCacheBytes];
+  __shared__ SampleGeo geo[WPB][UPW * NS];
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  // Block -> (group of xcd_group XCDs, rank in the group). Items of group gi are
+  // gi, gi + ngroups, ...; the group's blocks split each item's queries.
+  const int xcd = blockIdx.x & 7;
+  const int ngroups = 8 / p.xcd_group;
+  const int gi = xcd / p.xcd_group;
+  const int kb = (xcd - gi * p.xcd_group) * p.blocks_per_xcd + (blockIdx.x >> 3);
+  const int nkb = p.xcd_group * p.blocks_per_xcd;
+  const int pos_stride = p.NH * D;
+  const uint32_t kOOB = p.batch_bytes;
+
+  // Level table and cache layout: row 0 of the cache is zeros, then levels from the
+  // coarsest. Level MIXL keeps as many whole rows as still fit; every other level is
+  // cached whole or not at all, so its reads take one path for the whole wave.
+  int lvH[NL], lvW[NL], lvS[NL], lvR[NL];
+  uint32_t lvOff[NL];
+  {
+    uint32_t used = ROW;
+#pragma unroll
+    for (int l = NL - 1; l >= 0; --l) {
+      lvH[l] = (int)p.shapes[2 * l];
+      lvW[l] = (int)p.shapes[2 * l + 1];
+      lvS[l] = (int)p.lsi[l];
+      const int64_t rowb = (int64_t)lvW[l] * ROW;
+      int64_t r = (lvH[l] > 0 && rowb > 0) ? ((int64_t)kCacheBytes - used) / rowb : 0;
+      if (r > lvH[l]) r = lvH[l];
+      if (r < 0) r = 0;
+      if (l != MIXL && r < lvH[l]) r = 0;
+      lvR[l] = (int)r;
+      lvOff[l] = used;
+      used += (uint32_t)(r * rowb);
+    }
+  }
+  if (threadIdx.x < (int)(ROW / 16)) {
+    typedef int i4 __attribute__((ext_vector_type(4)));
+    *reinterpret_cast<i4 *>(cache + threadIdx.x * 16) = i4{0, 0, 0, 0};
+  }
+
+  const int ul = lane & (LPL - 1);
+  const int ui = lane / LPL;
+  const int pt = ul / G;
+  const uint32_t cb = (uint32_t)((ul - pt * G) * VEC * sizeof(T));
+
+  for (int item = gi; item < p.nitems; item += ngroups) {
+    const int slice = item / p.parts;
+    const int part = item - slice * p.parts;
+    const int b = slice / p.NH;
+    const int h = slice - b * p.NH;
+    const int qa = (int)((int64_t)p.NQ * part / p.parts);
+    const int nqp = (int)((int64_t)p.NQ * (part + 1) / p.parts) - qa;
+    const int q0 = qa + (int)((int64_t)nqp * kb / nkb);
+    const int q1 = qa + (int)((int64_t)nqp * (kb + 1) / nkb);
+    if (q0 >= q1) continue;  // uniform over the block
+
+    const T *vbase = static_cast<const T *>(p.value) + (int64_t)b * p.S * pos_stride;
+    const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(vbase, p.batch_bytes);
+
+    // Fill the cache (the previous item's readers are done after this barrier).
+    __syncthreads();
+#pragma unroll
+    for (int l = NL - 1; l >= 0; --l) {
+      const int n16 = lvR[l] * lvW[l] * G;  // 16-byte pieces of this level's cached rows
+      const uint32_t src0 = (uint32_t)((lvS[l] * pos_stride + h * D) * sizeof(T));
+      for (int i0 = threadIdx.x; i0 < n16; i0 += 4 * kBlockThreads) {
+        typedef int i4 __attribute__((ext_vector_type(4)));
+        i4 v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int i = i0 + k * kBlockThreads;
+          const int pos = i / G, piece = i - (i / G) * G;
+          v[k] = __builtin_amdgcn_raw_buffer_load_b128(
+              rsrc, i < n16 ? src0 + (uint32_t)(pos * pos_stride) * sizeof(T) + piece * 16 : kOOB,
+              0, 0);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int i = i0 + k * kBlockThreads;
+          if (i < n16) *reinterpret_cast<i4 *>(cache + lvOff[l] + (uint32_t)i * 16) = v[k];
+        }
+      }
+    }
+    __syncthreads();
+
+    const int nunits = q1 - q0;
+    const int64_t unit_base = ((int64_t)b * p.NQ + q0) * p.NH + h;  // unit of query q0
+    // Phase-1 inputs of this lane's sample (lanes past UPW * NS repeat lower lanes).
+    const int s1 = lane % NS;
+    const int u1 = (lane % (UPW * NS)) / NS;
+    const int l1 = s1 / NP;
+    auto load_in = [&](int u0, float &x, float &y, float &a) {
+      const int u = u0 + u1;
+      const int uc = u < nunits ? u : nunits - 1;
+      const int64_t unit = unit_base + (int64_t)uc * p.NH;
+      load_loc<T>(static_cast<const T *>(p.loc) + (unit * NS + s1) * 2, x, y);
+      a = static_cast<float>(load_nt(static_cast<const T *>(p.attn) + unit * NS + s1));
+    };
+    // Loads of the next round are issued before this round's gathers (indices clamped,
+    // so the loads are unconditional and their registers carry over without a copy).
+    float nx, ny, na;
+    const bool geo_lane = lane < UPW * NS;
+    load_in(wave * UPW, nx, ny, na);
+
+    for (int u0 = wave * UPW; u0 < nunits; u0 += WPB * UPW) {
+      const float x = nx, y = ny, a = na;
+      load_in(u0 + WPB * UPW, nx, ny, na);
+      // Phase 1: lane i computes sample i % NS of unit u0 + i / NS.
+      if (geo_lane) {
+        int Hl = lvH[0], Wl = lvW[0], Sl = lvS[0], Rl = lvR[0];
+        uint32_t Ol = lvOff[0];
+#pragma unroll
+        for (int i = 1; i < NL; ++i)
+          if (l1 == i) { Hl = lvH[i]; Wl = lvW[i]; Sl = lvS[i]; Rl = lvR[i]; Ol = lvOff[i]; }
+        const float him = y * (float)Hl - 0.5f, wim = x * (float)Wl - 0.5f;
+        // Invalid corners: the zero row when the level is cached, else out of range.
+        const uint32_t zero = Rl > 0 ? kLdsFlag : kOOB;
+        SampleGeo sg;
+        sg.w[0] = sg.w[1] = sg.w[2] = sg.w[3] = 0.f;
+        sg.o[0] = sg.o[1] = sg.o[2] = sg.o[3] = zero;
+        if (u0 + u1 < nunits && him > -1.f && wim > -1.f && him < (float)Hl && wim < (float)Wl) {
+          const float fh = floorf(him), fw = floorf(wim);
+          const int hl = (int)fh, wl = (int)fw;
+          const float lh = him - fh, lw = wim - fw, hh = 1.f - lh, hw = 1.f - lw;
+          const bool y0 = hl >= 0, y1 = hl + 1 <= Hl - 1, x0 = wl >= 0, x1 = wl + 1 <= Wl - 1;
+          auto corner = [&](int yy, int xx) -> uint32_t {
+            if (yy < Rl) return kLdsFlag | (Ol + (uint32_t)(yy * Wl + xx) * ROW);
+            return (uint32_t)(((Sl + yy * Wl + xx) * pos_stride + h * D) * sizeof(T));
+          };
+          if (y0 && x0) { sg.w[0] = hh * hw * a; sg.o[0] = corner(hl, wl); }
+          if (y0 && x1) { sg.w[1] = hh * lw * a; sg.o[1] = corner(hl, wl + 1); }
+          if (y1 && x0) { sg.w[2] = lh * hw * a; sg.o[2] = corner(hl + 1, wl); }
+          if (y1 && x1) { sg.w[3] = lh * lw * a; sg.o[3] = corner(hl + 1, wl + 1); }
+        }
+        geo[wave][lane] = sg;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+      // Phase 2: iteration it gathers level it % NL of units (it / NL) * UPI + ui. All
+      // geometry reads first, then every corner load, then the arithmetic.
+      SampleGeo sg[NIT];
+#pragma unroll
+      for (int it = 0; it < NIT; ++it)
+        sg[it] = geo[wave][((it / NL) * UPI + ui) * NS + (it % NL) * NP + pt];
+      V v[NIT][4];
+      V vx[NACC][4];  // level MIXL: the value-buffer half of a cached-in-part level
+#pragma unroll
+      for (int it = 0; it < NIT; ++it) {
+        const int l = it % NL;
+        if (l == MIXL && lvR[l] > 0 && lvR[l] < lvH[l]) {
+          // Each corner is in the cache or in the value buffer; the other read returns 0.
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            const uint32_t o = sg[it].o[c];
+            const bool in_lds = (o & kLdsFlag) != 0;
+            v[it][c] = *reinterpret_cast<const V *>(cache + (in_lds ? (o & ~kLdsFlag) + cb : cb));
+            vx[it / NL][c] = buffer_load_vec<T, VEC>(rsrc, in_lds ? kOOB : o + cb);
+          }
+        } else if (lvR[l] > 0) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            v[it][c] = *reinterpret_cast<const V *>(cache + ((sg[it].o[c] & ~kLdsFlag) + cb));
+            if (l == MIXL) vx[it / NL][c] = V{};
+          }
+        } else {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            v[it][c] = buffer_load_vec<T, VEC>(rsrc, sg[it].o[c] + cb);
+            if (l == MIXL) vx[it / NL][c] = V{};
+          }
+        }
+      }
+      if constexpr (MIXL >= 0) {
+        // One of each pair is all-zero bits: OR keeps the other exactly.
+#pragma unroll
+        for (int it = MIXL; it < NIT; it += NL)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            typedef int i4 __attribute__((ext_vector_type(4)));
+            v[it][c] = __builtin_bit_cast(V, __builtin_bit_cast(i4, v[it][c]) |
+                                                 __builtin_bit_cast(i4, vx[it / NL][c]));
+          }
+      }
+      float acc[NACC][VEC];
+#pragma unroll
+      for (int a = 0; a < NACC; ++a)
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) acc[a][k] = 0.f;
+#pragma unroll
+      for (int it = 0; it < NIT; ++it)
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) {
+          float t = acc[it / NL][k];
+          t += sg[it].w[0] * (float)v[it][0].v[k];
+          t += sg[it].w[1] * (float)v[it][1].v[k];
+          t += sg[it].w[2] * (float)v[it][2].v[k];
+          t += sg[it].w[3] * (float)v[it][3].v[k];
+          acc[it / NL][k] = t;
+        }
+      // Sum over the points of each (unit, level) lane block.
+#pragma unroll
+      for (int m = G; m < LPL; m <<= 1)
+#pragma unroll
+        for (int a = 0; a < NACC; ++a)
+#pragma unroll
+          for (int k = 0; k < VEC; ++k) acc[a][k] += __shfl_xor(acc[a][k], m);
+      if (pt == 0) {
+#pragma unroll
+        for (int a = 0; a < NACC; ++a) {
+          const int u = u0 + a * UPI + ui;
+          if (u < nunits) {
+            V o;
+#pragma unroll
+            for (int k = 0; k < VEC; ++k) o.v[k] = from_acc<T>(acc[a][k]);
+            store_vec_nt<T, VEC>(static_cast<T *>(p.out) + (unit_base + (int64_t)u * p.NH) * D +
+                                     cb / sizeof(T),
+                                 o);
+          }
+        }
+      }
+      // The next round rewrites this wave's geometry slots.
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+  }
+}
+
 // One thread per output element (b, q, h, c); any heads / channels / levels / points.
 template <typename T>
 __global__ void __launch_bounds__(kBlock) msda_generic_kernel(
@@ -454,14 +733,81 @@ hipError_t launch_wave_t(const MsdaArgs &a, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// Compute units of the current device (cached per device).
+int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return 0;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+int gcd_int(int x, int y) {
+  while (y) { const int t = x % y; x = y; y = t; }
+  return x;
+}
+
+// The cached kernel pays one LDS fill per (item, block); it is used when every block
+// has a few hundred units per item and there is more than one level to cache.
+template <typename T, int D, int NL, int NP>
+bool cached_worthwhile(const MsdaArgs &a) {
+  const int cus = device_cus();
+  if (NL < 2 || cus < 8) return false;
+  const int64_t units = (int64_t)a.batch * a.num_heads * a.num_query;
+  return units >= (int64_t)cus * 256;
+}
+
+// UPW_MIN: wanted units per wave round, raised to a whole iteration's units.
+template <typename T, int D, int NL, int NP, int WPB, int UPW_MIN, int MIXL = NL - 2>
+hipError_t launch_cached_t(const MsdaArgs &a, hipStream_t stream, int xcd_group = 1) {
+  constexpr int UPI = kWave / (NP * (D / (16 / (int)sizeof(T))));
+  constexpr int UPW = UPW_MIN > UPI ? UPW_MIN : UPI;
+  CachedParams p;
+  p.value = a.value;
+  p.shapes = a.spatial_shapes;
+  p.lsi = a.level_start_index;
+  p.loc = a.sampling_loc;
+  p.attn = a.attn_weight;
+  p.out = a.output;
+  p.S = a.spatial_size;
+  p.NH = a.num_heads;
+  p.NQ = a.num_query;
+  const int slices = a.batch * a.num_heads;
+  p.parts = 8 / gcd_int(slices, 8);  // items = a multiple of the 8 XCDs
+  p.nitems = slices * p.parts;
+  const int blocks = (device_cus() / 8) * 8;
+  p.blocks_per_xcd = blocks / 8;
+  p.xcd_group = xcd_group;
+  p.batch_bytes = (uint32_t)((int64_t)a.spatial_size * a.num_heads * D * sizeof(T));
+  if (blocks == 0 || p.nitems == 0) return hipSuccess;
+  hipLaunchKernelGGL((msda_cached_kernel<T, D, NL, NP, WPB, UPW, MIXL>), dim3(blocks),
+                     dim3(WPB * kWave), 0, stream, p);
+  return hipGetLastError();
+}
+
 template <typename T>
 hipError_t launch_wave(const MsdaArgs &a, hipStream_t stream) {
   const int L = a.num_levels, P = a.num_point;
   switch (a.channels) {
     case 32:
-      if (L == 4 && P == 8) return launch_wave_t<T, 32, 4, 8>(a, stream);  // BEVFormer SCA
+      if (L == 4 && P == 8) {  // BEVFormer SCA
+        // fp32: the per-sample gather kernel at high occupancy measured faster than the
+        // cached kernel (whose partly cached level still costs a load per corner).
+        if (sizeof(T) == 2 && cached_worthwhile<T, 32, 4, 8>(a))
+          return launch_cached_t<T, 32, 4, 8, 12, 2>(a, stream);
+        return launch_wave_t<T, 32, 4, 8>(a, stream);
+      }
       if (L == 1 && P == 4) return launch_wave_t<T, 32, 1, 4>(a, stream);  // BEVFormer TSA
-      if (L == 4 && P == 4) return launch_wave_t<T, 32, 4, 4>(a, stream);  // Deformable DETR
+      if (L == 4 && P == 4) {  // Deformable DETR
+        if (cached_worthwhile<T, 32, 4, 4>(a))
+          return launch_cached_t<T, 32, 4, 4, 12, 2>(a, stream);
+        return launch_wave_t<T, 32, 4, 4>(a, stream);
+      }
       return launch_wave_t<T, 32, 0, 0>(a, stream);
     case 16: return launch_wave_t<T, 16, 0, 0>(a, stream);
     case 64: return launch_wave_t<T, 64, 0, 0>(a, stream);

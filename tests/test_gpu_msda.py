@@ -64,6 +64,37 @@ def test_configs_full_size(cfg, dtype):
     check(out[:, q_idx], _ref(d, dtype, q_idx), dtype, f"{cfg} full {dtype}")
 
 
+@pytest.mark.parametrize("dtype", DTYPES, ids=["fp32", "fp16", "bf16"])
+@pytest.mark.parametrize("geom", [
+    # batch, heads, num_query, shapes, points: large enough for the LDS-cached kernel
+    (3, 2, 11001, [(64, 90), (32, 45), (16, 23), (8, 12)], 8),   # level 1 partly cached,
+    #   6 slices -> each slice split into query ranges over the 8 XCDs
+    (1, 8, 8193, [(40, 70), (20, 35), (10, 18), (5, 9)], 4),      # 8 slices, DETR points
+])
+def test_cached_kernel_whole_output(geom, dtype):
+    """Every query against the one-thread-per-element kernel (an independent code path),
+    a subset against the float64 oracle; 40% of the samples lie outside the image."""
+    b, nh, nq, shapes, npnt = geom
+    d = inputs.msda_random(b, shapes, nq, nh, 32, npnt, seed=11, loc_lo=-0.25, loc_hi=1.25)
+    # Exact pixel centres, edges and gates on a few queries.
+    loc = d["sampling_loc"]
+    loc[0, 0] = 0.0
+    loc[0, 1] = 1.0
+    H0, W0 = shapes[0]
+    loc[0, 2, :, :, :, 0] = (W0 - 0.5) / W0
+    loc[0, 2, :, :, :, 1] = 0.5 / H0
+    out = _run(d, dtype)
+    gen = _run(d, dtype, force_generic=True)
+    if dtype == torch.float32:
+        torch.testing.assert_close(out, gen, rtol=1e-5, atol=1e-5)
+    else:
+        check(out.double(), gen.double(), dtype, f"cached vs generic {geom}")
+    g = torch.Generator().manual_seed(5)
+    q_idx = torch.randperm(nq, generator=g)[:300].sort().values
+    q_idx = torch.cat([q_idx, torch.tensor([0, 1, 2, nq - 1])]).unique()
+    check(out[:, q_idx], _ref(d, dtype, q_idx), dtype, f"cached {geom}")
+
+
 def test_sca_full_linearity():
     """Whole-output properties at the full SCA size: out is linear in value and in attn."""
     d = inputs.msda_inputs("msda_sca")
