@@ -389,8 +389,310 @@ hipError_t launch_tt(const HParams &p, int geo, hipStream_t stream) {
   return launch_cfg<T, T, 64, 64, 64, 2, 2, TAPSTEP>(p, geo, stream);
 }
 
+// ---------------------------------------------------------------------------------------
+// Persistent, row-balanced variant (Cout <= 256, C % 64 == 0). One block of 4 waves per
+// CU owns a contiguous range of 8-9 blocks of 16 output rows (all of M split evenly over
+// the CUs, so no CU runs a second round) and all BN = 256 output channels for the whole K
+// loop; wave w computes columns [64 w, 64 w + 64) of every row block with
+// v_mfma_f32_16x16x32. Per K step (BK = 64 channels of one tap): the next step's corner
+// gathers and B fragments (from the fragment-packed weight) are issued before this step's
+// MFMAs, and the gathered corners are blended after them into the other half of a
+// double-buffered LDS A tile. The block's row range is XCD-contiguous (XCD x owns the x-th
+// eighth of M), so the image rows its gathers touch stay in that XCD's L2.
+constexpr int kPRowBlocks = 9;                  // max 16-row blocks per workgroup
+constexpr int kPRows = kPRowBlocks * 16;
+constexpr int kPBK = 32, kPLDA = kPBK + 8;      // K step, A tile row pitch (elements)
+constexpr int kPDepth = 3;                      // gather register sets
+constexpr int kPThreads = 256;
+constexpr int kPSlots = kPRows * (kPBK / 8);    // (row, 16-byte k-vector) slots
+constexpr int kPSPT = (kPSlots + kPThreads - 1) / kPThreads;  // slots per thread
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+template <typename T> __device__ __forceinline__ floatx4 mfma16x16(int4v a, int4v b, floatx4 c);
+template <> __device__ __forceinline__ floatx4 mfma16x16<f16>(int4v a, int4v b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a),
+                                                __builtin_bit_cast(half8, b), c, 0, 0, 0);
+}
+template <> __device__ __forceinline__ floatx4 mfma16x16<bf16>(int4v a, int4v b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+struct PParams {
+  HParams h;
+  int rb_total;  // 16-row blocks of M
+  int nblocks;   // workgroups (a multiple of 8)
+};
+
+// K loop and epilogue of one workgroup: always 9 row blocks (compile-time, so the MFMA loop
+// and the accumulator registers carry no run-time conditions); nrb row blocks are stored.
+// K steps of kPBK channels; the corner gathers of step k + PD - 1 are issued at step k
+// (PD register sets, rotated by unrolling the step loop PD times).
+template <typename T, int PD, int NS>
+__device__ __forceinline__ void dcn_p_main(const HParams &p, const TapGeo *geo,
+                                           T (*As)[kPRows * kPLDA], int m0, int nrb, int tid,
+                                           int lane, int wave) {
+  using V = Vec<T, 8>;
+  constexpr int NRB = kPRowBlocks;
+  constexpr int KV = kPBK / 8;         // 16-byte k-vectors per row per step
+  const int TT = p.taps;
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, p.x_bytes);
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, p.w_bytes);
+  const uint32_t xoob = p.x_bytes, woob = p.w_bytes;
+  // Gather slot i of a thread is (row, k-vector) = (s / KV, s % KV), s = tid + 256 i; NS
+  // slots per thread (wave 0 takes the last, partial set). Every load of the K loop is
+  // issued unconditionally (steps past the end read out of range), so the wait counts the
+  // compiler derives stay exact and the gathers of the next steps stay in flight.
+  const int kv = tid % KV;
+  const int spt = p.C / kPBK;  // K steps per tap
+  const int nk = TT * spt;
+  uint32_t go[NS][4];          // corner offsets of the tap being issued (+ k-vector)
+  auto load_geo = [&](int t) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      if (t < TT) {
+        const TapGeo &G = geo[((tid + i * kPThreads) / KV) * TT + t];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          go[i][q] = G.o[q] == xoob ? xoob : G.o[q] + (uint32_t)(kv * 8 * sizeof(T));
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) go[i][q] = xoob;
+      }
+    }
+  };
+  auto issue_gather = [&](int ks, V (&ra)[NS][4]) __attribute__((always_inline)) {
+    const int t = ks / spt, cs = ks - t * spt;
+    if (cs == 0) load_geo(t);
+    const uint32_t so = (uint32_t)(cs * kPBK * sizeof(T));
+#pragma unroll
+    for (int i = 0; i < NS; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        ra[i][q] = __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(xr, go[i][q], so, 0));
+  };
+  auto blend = [&](int ks, const V (&ra)[NS][4], int buf) __attribute__((always_inline)) {
+    const int t = ks / spt;
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      {
+        const int row = (tid + i * kPThreads) / KV;
+        const float4 w = *reinterpret_cast<const float4 *>(geo[row * TT + t].w);
+        V o;
+        if constexpr (__is_same(T, f16)) {
+          const half2v w1 = {(f16)w.x, (f16)w.x}, w2 = {(f16)w.y, (f16)w.y};
+          const half2v w3 = {(f16)w.z, (f16)w.z}, w4 = {(f16)w.w, (f16)w.w};
+#pragma unroll
+          for (int e = 0; e < 8; e += 2) {
+            const half2v v1 = {ra[i][0].v[e], ra[i][0].v[e + 1]};
+            const half2v v2 = {ra[i][1].v[e], ra[i][1].v[e + 1]};
+            const half2v v3 = {ra[i][2].v[e], ra[i][2].v[e + 1]};
+            const half2v v4 = {ra[i][3].v[e], ra[i][3].v[e + 1]};
+            const half2v rr = w1 * v1 + w2 * v2 + w3 * v3 + w4 * v4;
+            o.v[e] = rr.x;
+            o.v[e + 1] = rr.y;
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            o.v[e] = static_cast<T>(w.x * (float)ra[i][0].v[e] + w.y * (float)ra[i][1].v[e] +
+                                    w.z * (float)ra[i][2].v[e] + w.w * (float)ra[i][3].v[e]);
+        }
+        store_vec<T, 8>(&As[buf][row * kPLDA + kv * 8], o);
+      }
+    }
+  };
+
+  // B fragments (16x16x32, read from the 32x32x16 fragment packing): lane l takes column
+  // n = 64 wave + 16 cb + (l & 15) and k = 32 kh + 8 (l >> 4) .. + 8 of the step.
+  constexpr int KH = kPBK / 32;
+  uint32_t bo[KH][4];
+#pragma unroll
+  for (int kh = 0; kh < KH; ++kh)
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) {
+      const int n = wave * 64 + cb * 16 + (lane & 15);
+      const int nb = n >> 5;
+      bo[kh][cb] = nb < p.nb_total
+                       ? ((uint32_t)(nb * p.kb_total + kh * 2 + (lane >> 5)) * 64u +
+                          (uint32_t)((n & 31) + 32 * ((lane >> 4) & 1))) * 16u
+                       : woob;
+    }
+  auto issue_b = [&](int ks, int4v (&br)[KH][4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int kh = 0; kh < KH; ++kh)
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb)
+        br[kh][cb] = __builtin_amdgcn_raw_buffer_load_b128(
+            wr, bo[kh][cb], (uint32_t)ks * (uint32_t)(kPBK / 16) * 1024u, 0);
+  };
+
+  floatx4 acc[NRB][4];
+#pragma unroll
+  for (int i = 0; i < NRB; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  auto mfma_step = [&](int buf, const int4v (&br)[KH][4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int rbi = 0; rbi < NRB; ++rbi)
+#pragma unroll
+      for (int kh = 0; kh < KH; ++kh) {
+        const int4v a = *reinterpret_cast<const int4v *>(
+            &As[buf][(rbi * 16 + (lane & 15)) * kPLDA + kh * 32 + 8 * (lane >> 4)]);
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) acc[rbi][cb] = mfma16x16<T>(a, br[kh][cb], acc[rbi][cb]);
+      }
+  };
+
+  // Step k: issue B(k+1) and gather(k+2), MFMA(k) from A buffer k % 2, blend A(k+1) into
+  // the other buffer, barrier. Three register sets, named by literal indices (unrolled by
+  // hand) so they stay in registers.
+  static_assert(PD == 3 && kPSlots == (kPSPT - 1) * kPThreads + kWave,
+                "the step loop below is written for three register sets, one partial slot wave");
+  V ra0[NS][4], ra1[NS][4], ra2[NS][4];
+  int4v br0[KH][4], br1[KH][4], br2[KH][4];
+  auto step = [&](int ks, V (&ra_issue)[NS][4], const V (&ra_blend)[NS][4],
+                  int4v (&b_next)[KH][4], const int4v (&b_cur)[KH][4]) __attribute__((always_inline)) {
+    issue_b(ks + 1, b_next);
+    issue_gather(ks + 2, ra_issue);
+    mfma_step(ks & 1, b_cur);
+    if (ks + 1 < nk) blend(ks + 1, ra_blend, (ks + 1) & 1);
+    __syncthreads();
+  };
+  issue_gather(0, ra0);
+  issue_gather(1, ra1);
+  issue_b(0, br0);
+  blend(0, ra0, 0);
+  __syncthreads();
+  int k0 = 0;
+  for (; k0 + 3 <= nk; k0 += 3) {
+    step(k0, ra2, ra1, br1, br0);
+    step(k0 + 1, ra0, ra2, br2, br1);
+    step(k0 + 2, ra1, ra0, br0, br2);
+  }
+  if (k0 < nk) step(k0, ra2, ra1, br1, br0);
+  if (k0 + 1 < nk) step(k0 + 1, ra0, ra2, br2, br1);
+
+  // Epilogue: lane holds column 64 wave + 16 cb + (lane & 15), rows 4 (lane >> 4) + e.
+  T *out = static_cast<T *>(p.out);
+  const T *bias = static_cast<const T *>(p.bias);
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb) {
+    const int n = wave * 64 + cb * 16 + (lane & 15);
+    const float bv = (bias != nullptr && n < p.Cout) ? (float)bias[n] : 0.f;
+#pragma unroll
+    for (int rbi = 0; rbi < NRB; ++rbi)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = m0 + rbi * 16 + 4 * (lane >> 4) + e;
+        if (rbi < nrb && m < p.M && n < p.Cout)
+          out[(int64_t)m * p.Cout + n] = static_cast<T>(acc[rbi][cb][e] + bv);
+      }
+  }
+}
+
+template <typename T, int GEO>
+__global__ void __launch_bounds__(kPThreads) dcn_fused_p_kernel(const PParams pp) {
+  const HParams &p = pp.h;
+  __shared__ __attribute__((aligned(16))) TapGeo geo[kPRows * kMaxTaps];
+  __shared__ __attribute__((aligned(16))) T As[2][kPRows * kPLDA];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // XCD-contiguous row ranges: block b runs on XCD b % 8.
+  const int bpx = pp.nblocks >> 3;
+  const int r = (int)(blockIdx.x & 7) * bpx + (int)(blockIdx.x >> 3);
+  const int rb0 = (int)((int64_t)pp.rb_total * r / pp.nblocks);
+  const int nrb = (int)((int64_t)pp.rb_total * (r + 1) / pp.nblocks) - rb0;  // 8 or 9
+  if (nrb < kPRowBlocks - 1 || nrb > kPRowBlocks) return;
+  const int m0 = rb0 * 16;
+  const int nrows = nrb * 16;
+  const int HoWo = p.Ho * p.Wo, TT = p.taps;
+  const uint32_t xoob = p.x_bytes;
+
+  // Geometry table for all 144 rows (rows outside the range or past M: zero weights,
+  // out-of-range offsets).
+  for (int g = tid; g < kPRows * TT; g += kPThreads) {
+    const int row = g / TT, t = g - row * TT, m = m0 + row;
+    TapGeo G;
+    G.w[0] = G.w[1] = G.w[2] = G.w[3] = 0.f;
+    G.o[0] = G.o[1] = G.o[2] = G.o[3] = xoob;
+    if (row < nrows && m < p.M) {
+      const int b = m / HoWo, rr = m - b * HoWo, oh = rr / p.Wo, ow = rr - (rr / p.Wo) * p.Wo;
+      float dy, dx, mk;
+      const T *op = static_cast<const T *>(p.off);
+      if constexpr (GEO == kGeoY) {
+        const T *yp = op + (int64_t)m * 3 * TT;
+        dy = (float)yp[2 * t];
+        dx = (float)yp[2 * t + 1];
+        mk = sigmoid_f32((float)yp[2 * TT + t]);
+      } else {
+        dy = (float)op[(int64_t)m * 2 * TT + 2 * t];
+        dx = (float)op[(int64_t)m * 2 * TT + 2 * t + 1];
+        mk = (float)static_cast<const T *>(p.msk)[(int64_t)m * TT + t];
+      }
+      const int ki = t / p.kw, kj = t - (t / p.kw) * p.kw;
+      const float h = (float)(oh * p.sh - p.ph + ki * p.dh) + dy;
+      const float w = (float)(ow * p.sw - p.pw + kj * p.dw) + dx;
+      if (h > -1.f && w > -1.f && h < (float)p.H && w < (float)p.W) {
+        const float fh = floorf(h), fw = floorf(w);
+        const int hl = (int)fh, wl = (int)fw;
+        const float lh = h - fh, lw = w - fw, hh = 1.f - lh, hw = 1.f - lw;
+        const uint32_t rowb = (uint32_t)p.C * (uint32_t)sizeof(T);
+        const uint32_t base = (uint32_t)(b * p.H * p.W + hl * p.W + wl) * rowb;
+        const bool y0 = hl >= 0, y1 = hl + 1 <= p.H - 1, x0 = wl >= 0, x1 = wl + 1 <= p.W - 1;
+        if (y0 && x0) { G.w[0] = hh * hw * mk; G.o[0] = base; }
+        if (y0 && x1) { G.w[1] = hh * lw * mk; G.o[1] = base + rowb; }
+        if (y1 && x0) { G.w[2] = lh * hw * mk; G.o[2] = base + (uint32_t)p.W * rowb; }
+        if (y1 && x1) { G.w[3] = lh * lw * mk; G.o[3] = base + (uint32_t)(p.W + 1) * rowb; }
+      }
+    }
+    geo[g] = G;
+  }
+  __syncthreads();
+  // Always the 9-block body: a range of 8 blocks has zero geometry in its 9th block (see
+  // above) and does not store it; the kernel's time is set by the 9-block ranges anyway.
+  // Wave 0 takes the partial last set of gather slots (a separate copy of the K loop, so
+  // neither copy has conditional loads).
+  if (wave == 0)
+    dcn_p_main<T, kPDepth, kPSPT>(p, geo, As, m0, nrb, tid, lane, wave);
+  else
+    dcn_p_main<T, kPDepth, kPSPT - 1>(p, geo, As, m0, nrb, tid, lane, wave);
+}
+
+// The persistent kernel runs one workgroup per CU with 8 or 9 row blocks each (gather
+// slots 0-3 then always fall on rows of the workgroup's range).
+int p_blocks_for(const HParams &p, int geo) {
+  if (geo == kGeoRegular || p.C % 64 != 0 || p.Cout <= 128 || p.Cout > 256) return 0;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 0;
+  const int nb = (cus / 8) * 8;
+  const int rb = (p.M + 15) / 16;
+  if (nb < 8 || rb < nb * (kPRowBlocks - 1) || rb > nb * kPRowBlocks) return 0;
+  return nb;
+}
+
+template <typename T>
+hipError_t launch_p(const HParams &h, int geo, int nblocks, hipStream_t stream) {
+  PParams pp;
+  pp.h = h;
+  pp.rb_total = (h.M + 15) / 16;
+  pp.nblocks = nblocks;
+  if (geo == kGeoY)
+    hipLaunchKernelGGL((dcn_fused_p_kernel<T, kGeoY>), dim3(nblocks), dim3(kPThreads), 0,
+                       stream, pp);
+  else
+    hipLaunchKernelGGL((dcn_fused_p_kernel<T, kGeoMask>), dim3(nblocks), dim3(kPThreads), 0,
+                       stream, pp);
+  return hipGetLastError();
+}
+
 template <typename T>
 hipError_t launch_t(const HParams &p, int geo, hipStream_t stream) {
+  if (const int nb = p_blocks_for(p, geo)) return launch_p<T>(p, geo, nb, stream);
   return p.C % 64 == 0 ? launch_tt<T, true>(p, geo, stream) : launch_tt<T, false>(p, geo, stream);
 }
 

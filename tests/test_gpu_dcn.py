@@ -313,6 +313,50 @@ def test_fused_front_end_res4_fp16():
         check(col[b], ref, torch.float16, f"front end res4 image {b}")
 
 
+@pytest.mark.parametrize("dtype", HALF, ids=["fp16", "bf16"])
+@pytest.mark.parametrize("form", ["mask", "y3t"])
+def test_fused_half_row_balanced(dtype, form):
+    """Shapes that take the row-balanced persistent kernel (M = 33280 rows: 8- and 9-block
+    row ranges per workgroup and a partial last row block; Cout = 200, a column tail inside
+    the 256-wide tile). Every output against explicit columns (the NHWC gather kernel, in
+    the input dtype as the reference's column buffer) times the weight in fp32 on the GPU;
+    the first and last 1500 rows against the float64 oracle."""
+    from modulated_deform_conv import fused_tl
+    b, cin, cout, h, w = 2, 64, 200, 130, 128  # M = b * h * w (stride 1, pad 1)
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(b, h, w, cin, generator=g).to(dtype)
+    off = 2.0 * torch.randn(b, h, w, 18, generator=g)
+    off.view(-1)[::13] = 40.0
+    weight = (0.1 * torch.randn(cout, cin, 3, 3, generator=g)).to(dtype)
+    bias = torch.randn(cout, generator=g).to(dtype)
+    if form == "y3t":
+        y = torch.cat([off, torch.randn(b, h, w, 9, generator=g)], -1).to(dtype)
+        offset, mask = y, None
+        off_r, msk_r = od.split_y_nhwc(y.double(), 9)
+    else:
+        offset = off.to(dtype)
+        mask = torch.rand(b, h, w, 9, generator=g).to(dtype)
+        off_r, msk_r = offset.double(), mask.double()
+    from modulated_deform_conv import dcn_split_nhwc as dsn
+    dv = lambda t: None if t is None else t.to(DEV)
+    if form == "y3t":
+        out = dsn._fused_forward(dv(x), dv(offset), None, dv(weight), dv(bias), 1, 1, 1)
+        cols = dsn.gather_cols_nhwc(dv(x), dv(offset), None, 3, 3, 1, 1, 1)
+    else:
+        out = fused_tl.fused_dcn_forward_nhwc(dv(x), dv(offset), dv(mask), dv(weight),
+                                              dv(bias), 1, 1, 1)
+        cols = fused_tl.dcn_gather_cols_nhwc(dv(x), dv(offset), dv(mask), 3, 3, 1, 1, 1)
+    w_flat = weight.to(DEV).permute(2, 3, 1, 0).reshape(-1, cout).float()
+    split = (cols.float() @ w_flat + bias.to(DEV).float()).view(out.shape)
+    torch.cuda.synchronize()
+    check(out.float().cpu(), split.cpu(), dtype, f"row-balanced {form} vs columns x weight")
+    ref = od.forward_nhwc(x.double(), off_r, msk_r, weight.double(), bias.double(), 1, 1, 1,
+                          col_dtype=dtype)
+    flat_out, flat_ref = out.cpu().reshape(-1, cout), ref.reshape(-1, cout)
+    for sl in (slice(0, 1500), slice(-1500, None)):
+        check(flat_out[sl], flat_ref[sl], dtype, f"row-balanced {form} vs oracle")
+
+
 def test_fused_matches_gather_plus_gemm():
     """Fused kernel == explicit columns (NHWC gather kernel) @ weight, same inputs."""
     d = inputs.nchw_to_nhwc(_rand_problem(2, 64, 128, 20, 24, seed=5, dtype=torch.float32))
