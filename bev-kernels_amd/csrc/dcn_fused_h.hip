@@ -390,22 +390,31 @@ hipError_t launch_tt(const HParams &p, int geo, hipStream_t stream) {
 }
 
 // ---------------------------------------------------------------------------------------
-// Persistent, row-balanced variant (Cout <= 256, C % 64 == 0). One block of 4 waves per
-// CU owns a contiguous range of 8-9 blocks of 16 output rows (all of M split evenly over
-// the CUs, so no CU runs a second round) and all BN = 256 output channels for the whole K
-// loop; wave w computes columns [64 w, 64 w + 64) of every row block with
-// v_mfma_f32_16x16x32. Per K step (BK = 64 channels of one tap): the next step's corner
-// gathers and B fragments (from the fragment-packed weight) are issued before this step's
-// MFMAs, and the gathered corners are blended after them into the other half of a
-// double-buffered LDS A tile. The block's row range is XCD-contiguous (XCD x owns the x-th
-// eighth of M), so the image rows its gathers touch stay in that XCD's L2.
+// Persistent, row-balanced variant (128 < Cout <= 256, C % 64 == 0). One workgroup of 8
+// waves per CU owns a contiguous range of 8-9 blocks of 16 output rows (all of M split
+// evenly over the CUs, so no CU runs a second round) and all BN = 256 output channels for
+// the whole K loop. The waves specialise: waves 0-3 ("consumers") run the MFMAs, wave c
+// computing columns [64 c, 64 c + 64) of every row block with v_mfma_f32_16x16x32 and
+// loading its B fragments from the fragment-packed weight one step ahead; waves 4-7
+// ("producers") gather the four corners of every (row, 16-byte k-vector) slot two steps
+// ahead into two register sets, blend them (bilinear x mask weights) and write the A
+// tile of the next step into a double-buffered LDS tile. A workgroup's waves are spread
+// round-robin over the CU's four SIMDs, so every SIMD runs one consumer and one producer:
+// the matrix core works while the other wave's gathers and blend math proceed. One
+// barrier per K step (64 channels of one tap) hands the A tile over. The row range is
+// XCD-contiguous (XCD x owns the x-th eighth of M), so the image rows its gathers touch
+// stay in that XCD's L2.
 constexpr int kPRowBlocks = 9;                  // max 16-row blocks per workgroup
 constexpr int kPRows = kPRowBlocks * 16;
-constexpr int kPBK = 32, kPLDA = kPBK + 8;      // K step, A tile row pitch (elements)
-constexpr int kPDepth = 3;                      // gather register sets
-constexpr int kPThreads = 256;
-constexpr int kPSlots = kPRows * (kPBK / 8);    // (row, 16-byte k-vector) slots
-constexpr int kPSPT = (kPSlots + kPThreads - 1) / kPThreads;  // slots per thread
+constexpr int kPBK = 64, kPLDA = kPBK + 8;      // K step, A tile row pitch (elements)
+constexpr int kPKH = kPBK / 32;                 // 16x16x32 MFMA k-blocks per step
+constexpr int kPThreads = 512;                  // 4 consumer + 4 producer waves
+constexpr int kPProd = 256;                     // producer threads
+constexpr int kPSlots = kPRows * (kPBK / 8);    // (row, 16-byte k-vector) slots per step
+constexpr int kPSPT = (kPSlots + kPProd - 1) / kPProd;  // slots per producer thread
+constexpr int kPLastWaves = (kPSlots - (kPSPT - 1) * kPProd) / kWave;
+static_assert(kPLastWaves * kWave == kPSlots - (kPSPT - 1) * kPProd && kPLastWaves >= 1,
+              "the last slot set must cover whole producer waves");
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
@@ -425,34 +434,106 @@ struct PParams {
   int nblocks;   // workgroups (a multiple of 8)
 };
 
-// K loop and epilogue of one workgroup: always 9 row blocks (compile-time, so the MFMA loop
-// and the accumulator registers carry no run-time conditions); nrb row blocks are stored.
-// K steps of kPBK channels; the corner gathers of step k + PD - 1 are issued at step k
-// (PD register sets, rotated by unrolling the step loop PD times).
-template <typename T, int PD, int NS>
-__device__ __forceinline__ void dcn_p_main(const HParams &p, const TapGeo *geo,
-                                           T (*As)[kPRows * kPLDA], int m0, int nrb, int tid,
-                                           int lane, int wave) {
-  using V = Vec<T, 8>;
+// Consumer wave c: B(k+1) issued at step k, MFMA(k) from A buffer k % 2, one barrier per
+// step; then the epilogue. Always 9 row blocks (compile-time, so the MFMA loop and the
+// accumulators carry no run-time conditions); nrb row blocks are stored.
+template <typename T>
+__device__ __forceinline__ void dcn_p_consumer(const HParams &p, T (*As)[kPRows * kPLDA],
+                                               int m0, int nrb, int nk, int lane, int wave) {
   constexpr int NRB = kPRowBlocks;
-  constexpr int KV = kPBK / 8;         // 16-byte k-vectors per row per step
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, p.w_bytes);
+  const uint32_t woob = p.w_bytes;
+  // B fragments (16x16x32, read from the 32x32x16 fragment packing): lane l takes column
+  // n = 64 wave + 16 cb + (l & 15) and k = k0 + 8 (l >> 4) .. + 8 of the step.
+  uint32_t bo[kPKH][4];
+#pragma unroll
+  for (int kh = 0; kh < kPKH; ++kh)
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) {
+      const int n = wave * 64 + cb * 16 + (lane & 15);
+      const int nb = n >> 5;
+      bo[kh][cb] = nb < p.nb_total ? ((uint32_t)(nb * p.kb_total + 2 * kh + (lane >> 5)) * 64u +
+                                      (uint32_t)((n & 31) + 32 * ((lane >> 4) & 1))) * 16u
+                                   : woob;
+    }
+  auto issue_b = [&](int ks, int4v (&br)[kPKH][4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int kh = 0; kh < kPKH; ++kh)
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb)
+        br[kh][cb] = __builtin_amdgcn_raw_buffer_load_b128(
+            wr, bo[kh][cb], (uint32_t)ks * (uint32_t)(kPBK / 16) * 1024u, 0);
+  };
+  floatx4 acc[NRB][4];
+#pragma unroll
+  for (int i = 0; i < NRB; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  // One B register set: B(k+1) is loaded right after step k's MFMAs (it has the barrier
+  // and the next step's A-fragment reads to arrive).
+  int4v br[kPKH][4];
+  auto step = [&](int ks) __attribute__((always_inline)) {
+    const int buf = ks & 1;
+#pragma unroll
+    for (int kh = 0; kh < kPKH; ++kh) {
+      int4v af[NRB];
+#pragma unroll
+      for (int rbi = 0; rbi < NRB; ++rbi)
+        af[rbi] = *reinterpret_cast<const int4v *>(
+            &As[buf][(rbi * 16 + (lane & 15)) * kPLDA + kh * 32 + 8 * (lane >> 4)]);
+#pragma unroll
+      for (int rbi = 0; rbi < NRB; ++rbi)
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+          acc[rbi][cb] = mfma16x16<T>(af[rbi], br[kh][cb], acc[rbi][cb]);
+    }
+    issue_b(ks + 1, br);
+    __syncthreads();
+  };
+  issue_b(0, br);
+  __syncthreads();  // A(0) written by the producers
+  for (int ks = 0; ks < nk; ++ks) step(ks);
+
+  // Epilogue: lane holds column 64 wave + 16 cb + (lane & 15), rows 4 (lane >> 4) + e.
+  T *out = static_cast<T *>(p.out);
+  const T *bias = static_cast<const T *>(p.bias);
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb) {
+    const int n = wave * 64 + cb * 16 + (lane & 15);
+    const float bv = (bias != nullptr && n < p.Cout) ? (float)bias[n] : 0.f;
+#pragma unroll
+    for (int rbi = 0; rbi < NRB; ++rbi)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = m0 + rbi * 16 + 4 * (lane >> 4) + e;
+        if (rbi < nrb && m < p.M && n < p.Cout)
+          out[(int64_t)m * p.Cout + n] = static_cast<T>(acc[rbi][cb][e] + bv);
+      }
+  }
+}
+
+// Producer thread ptid (0..255) with NS gather slots: slot i is (row, k-vector) =
+// (s / KV, s % KV), s = ptid + 256 i. The gathers of step k + 2 are issued at step k into
+// register set k % 2 (blended at step k - 1); A(k+1) is blended at step k from set
+// (k+1) % 2 into buffer (k+1) % 2. Every
+// load is issued unconditionally (steps past the end read out of range), so the compiler's
+// wait counts stay exact and the gathers of the next steps stay in flight.
+template <typename T, int NS>
+__device__ __forceinline__ void dcn_p_producer(const HParams &p, const TapGeo *geo,
+                                               T (*As)[kPRows * kPLDA], int nk, int ptid) {
+  using V = Vec<T, 8>;
+  constexpr int KV = kPBK / 8;
   const int TT = p.taps;
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, p.x_bytes);
-  const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, p.w_bytes);
-  const uint32_t xoob = p.x_bytes, woob = p.w_bytes;
-  // Gather slot i of a thread is (row, k-vector) = (s / KV, s % KV), s = tid + 256 i; NS
-  // slots per thread (wave 0 takes the last, partial set). Every load of the K loop is
-  // issued unconditionally (steps past the end read out of range), so the wait counts the
-  // compiler derives stay exact and the gathers of the next steps stay in flight.
-  const int kv = tid % KV;
+  const uint32_t xoob = p.x_bytes;
+  const int kv = ptid % KV;
   const int spt = p.C / kPBK;  // K steps per tap
-  const int nk = TT * spt;
   uint32_t go[NS][4];          // corner offsets of the tap being issued (+ k-vector)
   auto load_geo = [&](int t) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
       if (t < TT) {
-        const TapGeo &G = geo[((tid + i * kPThreads) / KV) * TT + t];
+        const TapGeo &G = geo[((ptid + i * kPProd) / KV) * TT + t];
 #pragma unroll
         for (int q = 0; q < 4; ++q)
           go[i][q] = G.o[q] == xoob ? xoob : G.o[q] + (uint32_t)(kv * 8 * sizeof(T));
@@ -473,123 +554,53 @@ __device__ __forceinline__ void dcn_p_main(const HParams &p, const TapGeo *geo,
         ra[i][q] = __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(xr, go[i][q], so, 0));
   };
   auto blend = [&](int ks, const V (&ra)[NS][4], int buf) __attribute__((always_inline)) {
-    const int t = ks / spt;
+    // Past the last step the gathered corners are zero (out-of-range offsets); the tap is
+    // clamped so the weight read stays inside the table.
+    const int t = min(ks / spt, TT - 1);
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
-      {
-        const int row = (tid + i * kPThreads) / KV;
-        const float4 w = *reinterpret_cast<const float4 *>(geo[row * TT + t].w);
-        V o;
-        if constexpr (__is_same(T, f16)) {
-          const half2v w1 = {(f16)w.x, (f16)w.x}, w2 = {(f16)w.y, (f16)w.y};
-          const half2v w3 = {(f16)w.z, (f16)w.z}, w4 = {(f16)w.w, (f16)w.w};
+      const int row = (ptid + i * kPProd) / KV;
+      const float4 w = *reinterpret_cast<const float4 *>(geo[row * TT + t].w);
+      V o;
+      if constexpr (__is_same(T, f16)) {
+        const half2v w1 = {(f16)w.x, (f16)w.x}, w2 = {(f16)w.y, (f16)w.y};
+        const half2v w3 = {(f16)w.z, (f16)w.z}, w4 = {(f16)w.w, (f16)w.w};
 #pragma unroll
-          for (int e = 0; e < 8; e += 2) {
-            const half2v v1 = {ra[i][0].v[e], ra[i][0].v[e + 1]};
-            const half2v v2 = {ra[i][1].v[e], ra[i][1].v[e + 1]};
-            const half2v v3 = {ra[i][2].v[e], ra[i][2].v[e + 1]};
-            const half2v v4 = {ra[i][3].v[e], ra[i][3].v[e + 1]};
-            const half2v rr = w1 * v1 + w2 * v2 + w3 * v3 + w4 * v4;
-            o.v[e] = rr.x;
-            o.v[e + 1] = rr.y;
-          }
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            o.v[e] = static_cast<T>(w.x * (float)ra[i][0].v[e] + w.y * (float)ra[i][1].v[e] +
-                                    w.z * (float)ra[i][2].v[e] + w.w * (float)ra[i][3].v[e]);
+        for (int e = 0; e < 8; e += 2) {
+          const half2v v1 = {ra[i][0].v[e], ra[i][0].v[e + 1]};
+          const half2v v2 = {ra[i][1].v[e], ra[i][1].v[e + 1]};
+          const half2v v3 = {ra[i][2].v[e], ra[i][2].v[e + 1]};
+          const half2v v4 = {ra[i][3].v[e], ra[i][3].v[e + 1]};
+          const half2v rr = w1 * v1 + w2 * v2 + w3 * v3 + w4 * v4;
+          o.v[e] = rr.x;
+          o.v[e + 1] = rr.y;
         }
-        store_vec<T, 8>(&As[buf][row * kPLDA + kv * 8], o);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          o.v[e] = static_cast<T>(w.x * (float)ra[i][0].v[e] + w.y * (float)ra[i][1].v[e] +
+                                  w.z * (float)ra[i][2].v[e] + w.w * (float)ra[i][3].v[e]);
       }
+      store_vec<T, 8>(&As[buf][row * kPLDA + kv * 8], o);
     }
   };
-
-  // B fragments (16x16x32, read from the 32x32x16 fragment packing): lane l takes column
-  // n = 64 wave + 16 cb + (l & 15) and k = 32 kh + 8 (l >> 4) .. + 8 of the step.
-  constexpr int KH = kPBK / 32;
-  uint32_t bo[KH][4];
-#pragma unroll
-  for (int kh = 0; kh < KH; ++kh)
-#pragma unroll
-    for (int cb = 0; cb < 4; ++cb) {
-      const int n = wave * 64 + cb * 16 + (lane & 15);
-      const int nb = n >> 5;
-      bo[kh][cb] = nb < p.nb_total
-                       ? ((uint32_t)(nb * p.kb_total + kh * 2 + (lane >> 5)) * 64u +
-                          (uint32_t)((n & 31) + 32 * ((lane >> 4) & 1))) * 16u
-                       : woob;
-    }
-  auto issue_b = [&](int ks, int4v (&br)[KH][4]) __attribute__((always_inline)) {
-#pragma unroll
-    for (int kh = 0; kh < KH; ++kh)
-#pragma unroll
-      for (int cb = 0; cb < 4; ++cb)
-        br[kh][cb] = __builtin_amdgcn_raw_buffer_load_b128(
-            wr, bo[kh][cb], (uint32_t)ks * (uint32_t)(kPBK / 16) * 1024u, 0);
-  };
-
-  floatx4 acc[NRB][4];
-#pragma unroll
-  for (int i = 0; i < NRB; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-  auto mfma_step = [&](int buf, const int4v (&br)[KH][4]) __attribute__((always_inline)) {
-#pragma unroll
-    for (int rbi = 0; rbi < NRB; ++rbi)
-#pragma unroll
-      for (int kh = 0; kh < KH; ++kh) {
-        const int4v a = *reinterpret_cast<const int4v *>(
-            &As[buf][(rbi * 16 + (lane & 15)) * kPLDA + kh * 32 + 8 * (lane >> 4)]);
-#pragma unroll
-        for (int cb = 0; cb < 4; ++cb) acc[rbi][cb] = mfma16x16<T>(a, br[kh][cb], acc[rbi][cb]);
-      }
-  };
-
-  // Step k: issue B(k+1) and gather(k+2), MFMA(k) from A buffer k % 2, blend A(k+1) into
-  // the other buffer, barrier. Three register sets, named by literal indices (unrolled by
-  // hand) so they stay in registers.
-  static_assert(PD == 3 && kPSlots == (kPSPT - 1) * kPThreads + kWave,
-                "the step loop below is written for three register sets, one partial slot wave");
-  V ra0[NS][4], ra1[NS][4], ra2[NS][4];
-  int4v br0[KH][4], br1[KH][4], br2[KH][4];
-  auto step = [&](int ks, V (&ra_issue)[NS][4], const V (&ra_blend)[NS][4],
-                  int4v (&b_next)[KH][4], const int4v (&b_cur)[KH][4]) __attribute__((always_inline)) {
-    issue_b(ks + 1, b_next);
+  V ra0[NS][4], ra1[NS][4];
+  auto step = [&](int ks, V (&ra_issue)[NS][4], const V (&ra_blend)[NS][4])
+      __attribute__((always_inline)) {
     issue_gather(ks + 2, ra_issue);
-    mfma_step(ks & 1, b_cur);
-    if (ks + 1 < nk) blend(ks + 1, ra_blend, (ks + 1) & 1);
+    blend(ks + 1, ra_blend, (ks + 1) & 1);
     __syncthreads();
   };
   issue_gather(0, ra0);
   issue_gather(1, ra1);
-  issue_b(0, br0);
   blend(0, ra0, 0);
   __syncthreads();
   int k0 = 0;
-  for (; k0 + 3 <= nk; k0 += 3) {
-    step(k0, ra2, ra1, br1, br0);
-    step(k0 + 1, ra0, ra2, br2, br1);
-    step(k0 + 2, ra1, ra0, br0, br2);
+  for (; k0 + 2 <= nk; k0 += 2) {
+    step(k0, ra0, ra1);
+    step(k0 + 1, ra1, ra0);
   }
-  if (k0 < nk) step(k0, ra2, ra1, br1, br0);
-  if (k0 + 1 < nk) step(k0 + 1, ra0, ra2, br2, br1);
-
-  // Epilogue: lane holds column 64 wave + 16 cb + (lane & 15), rows 4 (lane >> 4) + e.
-  T *out = static_cast<T *>(p.out);
-  const T *bias = static_cast<const T *>(p.bias);
-#pragma unroll
-  for (int cb = 0; cb < 4; ++cb) {
-    const int n = wave * 64 + cb * 16 + (lane & 15);
-    const float bv = (bias != nullptr && n < p.Cout) ? (float)bias[n] : 0.f;
-#pragma unroll
-    for (int rbi = 0; rbi < NRB; ++rbi)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int m = m0 + rbi * 16 + 4 * (lane >> 4) + e;
-        if (rbi < nrb && m < p.M && n < p.Cout)
-          out[(int64_t)m * p.Cout + n] = static_cast<T>(acc[rbi][cb][e] + bv);
-      }
-  }
+  if (k0 < nk) step(k0, ra0, ra1);
 }
 
 template <typename T, int GEO>
@@ -651,14 +662,16 @@ __global__ void __launch_bounds__(kPThreads) dcn_fused_p_kernel(const PParams pp
     geo[g] = G;
   }
   __syncthreads();
+  const int nk = TT * (p.C / kPBK);
   // Always the 9-block body: a range of 8 blocks has zero geometry in its 9th block (see
   // above) and does not store it; the kernel's time is set by the 9-block ranges anyway.
-  // Wave 0 takes the partial last set of gather slots (a separate copy of the K loop, so
-  // neither copy has conditional loads).
-  if (wave == 0)
-    dcn_p_main<T, kPDepth, kPSPT>(p, geo, As, m0, nrb, tid, lane, wave);
+  // Consumers and producers run the same number of barriers (one per step + prologue).
+  if (wave < 4)
+    dcn_p_consumer<T>(p, As, m0, nrb, nk, lane, wave);
+  else if (wave - 4 < kPLastWaves)
+    dcn_p_producer<T, kPSPT>(p, geo, As, nk, tid - kPProd);
   else
-    dcn_p_main<T, kPDepth, kPSPT - 1>(p, geo, As, m0, nrb, tid, lane, wave);
+    dcn_p_producer<T, kPSPT - 1>(p, geo, As, nk, tid - kPProd);
 }
 
 // The persistent kernel runs one workgroup per CU with 8 or 9 row blocks each (gather
