@@ -53,9 +53,16 @@ struct WaveParams {
   int S, NH, NQ, nl, np;
   int heads_per_slice;    // heads sharing one slice (2 when two heads fill a 128 B line)
   int slices_per_batch;   // NH / heads_per_slice
-  int blocks_per_slice;   // ceil(NQ * heads_per_slice / units_per_block)
+  int blocks_per_slice;   // ceil(NQ * heads_per_slice / units_per_block), a multiple of 8
   uint32_t batch_bytes;   // bytes of value per batch (buffer range; < 2^31)
 };
+
+// Block r of a slice (blocks_per_slice a multiple of 8, the slice's first block index a
+// multiple of 8) runs on XCD r % 8; it takes chunk (r % 8) * (bps / 8) + r / 8, so each
+// XCD works through one contiguous eighth of the slice's queries. Where sampling
+// locations follow the queries (temporal self-attention over a BEV grid), the value rows
+// an XCD needs then stay in its own L2 instead of every XCD fetching every row.
+__device__ __forceinline__ int xcd_chunk(int r, int bps) { return (r & 7) * (bps >> 3) + (r >> 3); }
 
 // NL/NP > 0: compile-time level/point counts; 0: read from params.
 template <typename T, int D, int VEC, int NL, int NP, int UPW>
@@ -73,9 +80,10 @@ __global__ void __launch_bounds__(kBlock) msda_wave_kernel(const WaveParams p) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
 
-  // block -> (slice, chunk): slices one after the other, queries in order.
+  // block -> (slice, chunk): slices one after the other; within a slice, the blocks of
+  // XCD x (block index = x mod 8) take the x-th contiguous eighth of the queries.
   const int slice = blockIdx.x / p.blocks_per_slice;
-  const int chunk = blockIdx.x - slice * p.blocks_per_slice;
+  const int chunk = xcd_chunk(blockIdx.x - slice * p.blocks_per_slice, p.blocks_per_slice);
   const int b = slice / p.slices_per_batch;
   const int hg = slice - b * p.slices_per_batch;
   const int local = (chunk * kWavesPerBlock + wave) * UPW + lane / LPU;
@@ -240,7 +248,7 @@ __global__ void __launch_bounds__(kBlock) msda_wave_lds_kernel(const WaveParams 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int slice = blockIdx.x / p.blocks_per_slice;
-  const int chunk = blockIdx.x - slice * p.blocks_per_slice;
+  const int chunk = xcd_chunk(blockIdx.x - slice * p.blocks_per_slice, p.blocks_per_slice);
   const int b = slice / p.slices_per_batch;
   const int hg = slice - b * p.slices_per_batch;
   const int pos_stride = p.NH * D;
@@ -719,7 +727,8 @@ hipError_t launch_wave_t(const MsdaArgs &a, hipStream_t stream) {
   p.slices_per_batch = a.num_heads / hps;
   const int units_per_block = kWavesPerBlock * UPW;
   const int64_t units_per_slice = (int64_t)a.num_query * hps;
-  p.blocks_per_slice = (int)((units_per_slice + units_per_block - 1) / units_per_block);
+  p.blocks_per_slice =
+      (int)((units_per_slice + units_per_block - 1) / units_per_block + 7) & ~7;
   const int64_t slices = (int64_t)a.batch * p.slices_per_batch;
   p.batch_bytes = (uint32_t)((int64_t)a.spatial_size * a.num_heads * D * sizeof(T));
   const int64_t blocks = slices * p.blocks_per_slice;
