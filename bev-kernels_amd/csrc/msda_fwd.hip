@@ -799,6 +799,255 @@ hipError_t launch_cached_t(const MsdaArgs &a, hipStream_t stream, int xcd_group 
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------------------
+// Tiled single-level kernel for self-attention over one grid (BEVFormer temporal
+// self-attention): one level, num_query == H * W, query q being cell (q / W, q % W), and
+// each query samples near its own cell. Work item = (batch, head, TS x TS tile of query
+// cells). The block copies the tile's neighbourhood (the tile grown by MG cells on every
+// side) of the head's value rows into LDS once, and every corner inside it is read from
+// there; a corner outside it is read from the value buffer in a branch taken only when
+// some lane of the wave needs it. When the shapes do not describe the queries
+// (H * W != num_query) the kernel takes the queries in index order and reads every corner
+// from the value buffer. Persistent blocks; each XCD takes a contiguous range of items, so
+// neighbouring tiles (which share neighbourhood rows) meet in its L2.
+struct TileParams {
+  const void *value;
+  const int64_t *shapes;
+  const int64_t *lsi;
+  const void *loc;
+  const void *attn;
+  void *out;
+  int B, S, NH, NQ;
+  int blocks_per_xcd;    // gridDim.x / 8
+  uint32_t batch_bytes;  // bytes of value per batch (< 2^31)
+};
+
+// BPC workgroups of WPB waves per CU: the second bound is waves per SIMD.
+template <typename T, int NP, int TS, int MG, int WPB, int BPC>
+__global__ void __launch_bounds__(WPB * kWave, (WPB * BPC + 3) / 4) msda_tile_kernel(const TileParams p) {
+  constexpr int D = 32;
+  constexpr int VEC = 16 / (int)sizeof(T);
+  using V = Vec<T, VEC>;
+  constexpr int G = D / VEC;             // lanes per corner
+  constexpr int NG = kWave / G;          // lane groups per wave
+  constexpr int RS = TS + 2 * MG;        // neighbourhood side
+  constexpr uint32_t ROW = D * sizeof(T);
+  constexpr uint32_t kRegion = RS * RS * ROW;
+  constexpr int UPP = kWave / NP;        // units per geometry pass (one sample per lane)
+  constexpr int UPG = UPP / NG;          // units per lane group and pass
+  constexpr int NPASS = (TS * TS + WPB * UPP - 1) / (WPB * UPP);  // geometry passes per wave
+  static_assert(kWave % NP == 0 && UPP % NG == 0 && UPG >= 1, "unsupported tile geometry");
+  __shared__ __attribute__((aligned(16))) unsigned char region[kRegion + ROW];  // + zero row
+  __shared__ SampleGeo geo[WPB][kWave];   // weights, LDS byte address of every corner
+  __shared__ uint4 far_off[WPB][kWave];    // value-buffer offsets of corners outside it
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int H = (int)p.shapes[0], W = (int)p.shapes[1], S0 = (int)p.lsi[0];
+  const bool grid = (int64_t)H * W == p.NQ && H > 0 && W > 0;
+  const int tiles_x = grid ? (W + TS - 1) / TS : 1;
+  const int ntile = grid ? tiles_x * ((H + TS - 1) / TS) : (p.NQ + TS * TS - 1) / (TS * TS);
+  const int nitems = p.B * p.NH * ntile;
+  const int xcd = blockIdx.x & 7;
+  const int per = (nitems + 7) / 8;
+  const int i_end = min(nitems, (xcd + 1) * per);
+  const int pos_stride = p.NH * D;
+  const uint32_t kOOB = p.batch_bytes;
+  const float Hf = (float)H, Wf = (float)W;
+  if (threadIdx.x < (int)(ROW / 16)) {
+    typedef int i4 __attribute__((ext_vector_type(4)));
+    *reinterpret_cast<i4 *>(region + kRegion + threadIdx.x * 16) = i4{0, 0, 0, 0};
+  }
+  const int g = lane / G;
+  const uint32_t cb = (uint32_t)(lane % G) * 16u;
+
+  for (int item = xcd * per + (blockIdx.x >> 3); item < i_end; item += p.blocks_per_xcd) {
+    const int tile = item % ntile;
+    const int bh = item / ntile;
+    const int h = bh % p.NH, b = bh / p.NH;
+    const int ty = tile / tiles_x, tx = tile - ty * tiles_x;
+    // Neighbourhood origin; a huge origin when there is no grid keeps every corner out.
+    const int ry0 = grid ? ty * TS - MG : -(1 << 28), rx0 = grid ? tx * TS - MG : -(1 << 28);
+    const T *vbase = static_cast<const T *>(p.value) + (int64_t)b * p.S * pos_stride;
+    const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(vbase, p.batch_bytes);
+    const uint32_t hoff = (uint32_t)(h * D * sizeof(T));
+
+    // Query of unit ul of the tile (valid flag in qv).
+    auto query = [&](int ul, bool &qv) __attribute__((always_inline)) -> int {
+      if (grid) {
+        const int qy = ty * TS + ul / TS, qx = tx * TS + ul % TS;
+        qv = ul < TS * TS && qy < H && qx < W;
+        return qy * W + qx;
+      }
+      const int q = tile * TS * TS + ul;
+      qv = ul < TS * TS && q < p.NQ;
+      return q;
+    };
+    // Locations and weights of all this wave's samples of the tile, loaded before the
+    // neighbourhood so that both are in flight together.
+    float lx[NPASS], ly[NPASS], la[NPASS];
+#pragma unroll
+    for (int ps = 0; ps < NPASS; ++ps) {
+      bool qv;
+      const int q = query((wave + ps * WPB) * UPP + lane / NP, qv);
+      const int64_t unit = ((int64_t)b * p.NQ + (qv ? q : 0)) * p.NH + h;
+      load_loc<T>(static_cast<const T *>(p.loc) + (unit * NP + lane % NP) * 2, lx[ps], ly[ps]);
+      la[ps] = static_cast<float>(load_nt(static_cast<const T *>(p.attn) + unit * NP + lane % NP));
+    }
+
+    __syncthreads();  // the previous item's readers are done
+    if (grid) {
+      // All of a thread's loads are in flight before the first LDS write.
+      constexpr int P16 = ROW / 16;
+      constexpr int NPC = RS * RS * P16;
+      constexpr int NT = WPB * kWave;
+      constexpr int NLD = (NPC + NT - 1) / NT;
+      typedef int i4 __attribute__((ext_vector_type(4)));
+      i4 v[NLD];
+#pragma unroll
+      for (int k = 0; k < NLD; ++k) {
+        const int i = (int)threadIdx.x + k * NT;
+        const int pos = i / P16, piece = i - pos * P16;
+        const int y = ry0 + pos / RS, x = rx0 + pos % RS;
+        const bool in = i < NPC && (unsigned)y < (unsigned)H && (unsigned)x < (unsigned)W;
+        v[k] = __builtin_amdgcn_raw_buffer_load_b128(
+            rsrc, in ? (uint32_t)((S0 + y * W + x) * pos_stride) * sizeof(T) + hoff + piece * 16
+                     : kOOB,
+            0, 0);
+      }
+#pragma unroll
+      for (int k = 0; k < NLD; ++k) {
+        const int i = (int)threadIdx.x + k * NT;
+        if (i < NPC) *reinterpret_cast<i4 *>(region + (uint32_t)i * 16) = v[k];
+      }
+    }
+    __syncthreads();
+
+#pragma unroll
+    for (int ps = 0; ps < NPASS; ++ps) {
+      const int u0 = (wave + ps * WPB) * UPP;
+      if (u0 >= TS * TS) break;  // uniform over the wave
+      // Phase 1: lane = (unit u0 + lane / NP, point lane % NP).
+      bool far;  // some corner of the pass lies outside the neighbourhood
+      {
+        bool qv;
+        query(u0 + lane / NP, qv);
+        const float x = lx[ps], y = ly[ps], a = la[ps];
+        const float him = y * Hf - 0.5f, wim = x * Wf - 0.5f;
+        // Corners inside the neighbourhood: their LDS address; outside it (or invalid):
+        // the zero row, and for a valid one its value-buffer offset in far_off. Written
+        // with selects (no per-corner branches), so every array index stays constant.
+        SampleGeo sg;
+        uint32_t fo[4];
+        const bool in = qv && him > -1.f && wim > -1.f && him < Hf && wim < Wf;
+        const float fh = floorf(him), fw = floorf(wim);
+        const int hl = (int)fh, wl = (int)fw;
+        const float lh = him - fh, lw = wim - fw, hh = 1.f - lh, hw = 1.f - lw;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int yy = hl + (c >> 1), xx = wl + (c & 1);
+          const bool ok = in && (unsigned)yy < (unsigned)H && (unsigned)xx < (unsigned)W;
+          const int ry = yy - ry0, rx = xx - rx0;
+          const bool near = (unsigned)ry < (unsigned)RS && (unsigned)rx < (unsigned)RS;
+          const float wy = (c >> 1) ? lh : hh, wx = (c & 1) ? lw : hw;
+          sg.w[c] = ok ? wy * wx * a : 0.f;
+          sg.o[c] = ok && near ? (uint32_t)(ry * RS + rx) * ROW : kRegion;
+          fo[c] = ok && !near ? (uint32_t)((S0 + yy * W + xx) * pos_stride) * sizeof(T) + hoff
+                              : kOOB;
+        }
+        far_off[wave][lane] = uint4{fo[0], fo[1], fo[2], fo[3]};
+        far = __builtin_amdgcn_ballot_w64(fo[0] != kOOB || fo[1] != kOOB || fo[2] != kOOB ||
+                                          fo[3] != kOOB) != 0;
+        geo[wave][lane] = sg;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+      // Phase 2: lane group g sums the NP samples of units g, g + NG, ... in registers.
+#pragma unroll
+      for (int k = 0; k < UPG; ++k) {
+        const int uu = g + NG * k;
+        SampleGeo sg[NP];
+#pragma unroll
+        for (int s = 0; s < NP; ++s) sg[s] = geo[wave][uu * NP + s];
+        V v[NP][4];
+#pragma unroll
+        for (int s = 0; s < NP; ++s)
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            v[s][c] = *reinterpret_cast<const V *>(region + (sg[s].o[c] + cb));
+        if (far) {
+          // Corners outside the neighbourhood: the LDS read above returned zero bits.
+#pragma unroll
+          for (int s = 0; s < NP; ++s) {
+            const uint4 fo = far_off[wave][uu * NP + s];
+            const uint32_t fa[4] = {fo.x, fo.y, fo.z, fo.w};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              const V f = buffer_load_vec<T, VEC>(rsrc, fa[c] + cb);
+              typedef int i4 __attribute__((ext_vector_type(4)));
+              v[s][c] = __builtin_bit_cast(V, __builtin_bit_cast(i4, v[s][c]) |
+                                                  __builtin_bit_cast(i4, f));
+            }
+          }
+        }
+        float acc[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+#pragma unroll
+        for (int s = 0; s < NP; ++s)
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            float t = acc[e];
+            t += sg[s].w[0] * (float)v[s][0].v[e];
+            t += sg[s].w[1] * (float)v[s][1].v[e];
+            t += sg[s].w[2] * (float)v[s][2].v[e];
+            t += sg[s].w[3] * (float)v[s][3].v[e];
+            acc[e] = t;
+          }
+        bool qv;
+        const int q = query(u0 + uu, qv);
+        if (qv) {
+          V o;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) o.v[e] = from_acc<T>(acc[e]);
+          store_vec_nt<T, VEC>(static_cast<T *>(p.out) +
+                                   (((int64_t)b * p.NQ + q) * p.NH + h) * D + (lane % G) * VEC,
+                               o);
+        }
+      }
+      // The next pass rewrites this wave's geometry.
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+  }
+}
+
+// BPC: workgroups per CU (the LDS use must allow it).
+template <typename T, int NP, int TS, int MG, int WPB, int BPC>
+hipError_t launch_tile_t(const MsdaArgs &a, hipStream_t stream) {
+  TileParams p;
+  p.value = a.value;
+  p.shapes = a.spatial_shapes;
+  p.lsi = a.level_start_index;
+  p.loc = a.sampling_loc;
+  p.attn = a.attn_weight;
+  p.out = a.output;
+  p.B = a.batch;
+  p.S = a.spatial_size;
+  p.NH = a.num_heads;
+  p.NQ = a.num_query;
+  const int blocks = (device_cus() / 8) * 8 * BPC;
+  p.blocks_per_xcd = blocks / 8;
+  p.batch_bytes = (uint32_t)((int64_t)a.spatial_size * a.num_heads * 32 * sizeof(T));
+  if (blocks == 0 || a.batch == 0 || a.num_query == 0) return hipSuccess;
+  hipLaunchKernelGGL((msda_tile_kernel<T, NP, TS, MG, WPB, BPC>), dim3(blocks), dim3(WPB * kWave), 0,
+                     stream, p);
+  return hipGetLastError();
+}
+
 template <typename T>
 hipError_t launch_wave(const MsdaArgs &a, hipStream_t stream) {
   const int L = a.num_levels, P = a.num_point;
@@ -811,7 +1060,14 @@ hipError_t launch_wave(const MsdaArgs &a, hipStream_t stream) {
           return launch_cached_t<T, 32, 4, 8, 12, 2>(a, stream);
         return launch_wave_t<T, 32, 4, 8>(a, stream);
       }
-      if (L == 1 && P == 4) return launch_wave_t<T, 32, 1, 4>(a, stream);  // BEVFormer TSA
+      if (L == 1 && P == 4) {  // BEVFormer TSA
+        // fp32: the tiled kernel (neighbourhood in LDS) measured 25% faster than the
+        // per-sample gather kernel; for 16-bit types the two are even.
+        if constexpr (sizeof(T) == 4)
+          if (a.num_query == a.spatial_size && device_cus() >= 8)
+            return launch_tile_t<T, 4, 16, 6, 8, 1>(a, stream);
+        return launch_wave_t<T, 32, 1, 4>(a, stream);
+      }
       if (L == 4 && P == 4) {  // Deformable DETR
         if (cached_worthwhile<T, 32, 4, 4>(a))
           return launch_cached_t<T, 32, 4, 4, 12, 2>(a, stream);

@@ -95,6 +95,49 @@ def test_cached_kernel_whole_output(geom, dtype):
     check(out[:, q_idx], _ref(d, dtype, q_idx), dtype, f"cached {geom}")
 
 
+def _tsa_like(b, H, W, sigma, seed, heads=8, points=4, extra=0):
+    """Queries = the cells of one H x W grid (row-major), locations = cell centre + N(0, sigma)
+    in normalised units, as BEVFormer temporal self-attention. extra > 0 appends unused value
+    positions (spatial_size != H * W), which the tiled kernel must take in index order."""
+    g = torch.Generator().manual_seed(seed)
+    S = H * W + extra
+    nq = S
+    value = torch.randn(b, S, heads, 32, generator=g)
+    q = torch.arange(nq)
+    ref = torch.stack([((q % W).double() + 0.5) / W, ((q // W).double() + 0.5) / H], -1).float()
+    loc = ref.view(1, nq, 1, 1, 1, 2).expand(b, nq, heads, 1, points, 2).clone()
+    loc += sigma * torch.randn(b, nq, heads, 1, points, 2, generator=g)
+    attn = torch.softmax(torch.randn(b, nq, heads, points, generator=g), -1)
+    return dict(value=value, spatial_shapes=torch.tensor([[H, W]], dtype=torch.int64),
+                level_start_index=torch.tensor([0], dtype=torch.int64),
+                sampling_loc=loc.contiguous(), attn_weight=attn.view(b, nq, heads, 1, points))
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=["fp32", "fp16", "bf16"])
+@pytest.mark.parametrize("geom", [
+    # batch, H, W, sigma, extra positions
+    (2, 40, 37, 0.01, 0),    # partial tiles on both edges, samples near their cell
+    (1, 33, 50, 0.15, 0),    # wide offsets: many corners outside the staged neighbourhood
+    (2, 16, 16, 0.01, 0),    # a single tile
+    (1, 10, 12, 0.05, 10),   # spatial_size != H * W: queries taken in index order
+])
+def test_tsa_tiled(geom, dtype):
+    """Single-level self-attention over a grid (the tiled kernel): every query against the
+    float64 oracle and, in fp32, against the one-thread-per-element kernel."""
+    b, H, W, sigma, extra = geom
+    d = _tsa_like(b, H, W, sigma, seed=21, extra=extra)
+    # Exact cell centres, image corners and far-outside samples on a few queries.
+    loc = d["sampling_loc"]
+    loc[0, 0] = 0.0
+    loc[0, 1] = 1.0
+    loc[0, 2, :, :, :, 0] = 5.0
+    out = _run(d, dtype)
+    check(out, _ref(d, dtype), dtype, f"tsa tiled {geom}")
+    if dtype == torch.float32:
+        gen = _run(d, dtype, force_generic=True)
+        torch.testing.assert_close(out, gen, rtol=1e-5, atol=1e-5)
+
+
 def test_sca_full_linearity():
     """Whole-output properties at the full SCA size: out is linear in value and in attn."""
     d = inputs.msda_inputs("msda_sca")
