@@ -404,17 +404,22 @@ hipError_t launch_tt(const HParams &p, int geo, hipStream_t stream) {
 // barrier per K step (64 channels of one tap) hands the A tile over. The row range is
 // XCD-contiguous (XCD x owns the x-th eighth of M), so the image rows its gathers touch
 // stay in that XCD's L2.
-constexpr int kPRowBlocks = 9;                  // max 16-row blocks per workgroup
-constexpr int kPRows = kPRowBlocks * 16;
 constexpr int kPBK = 64, kPLDA = kPBK + 8;      // K step, A tile row pitch (elements)
 constexpr int kPKH = kPBK / 32;                 // 16x16x32 MFMA k-blocks per step
 constexpr int kPThreads = 512;                  // 4 consumer + 4 producer waves
 constexpr int kPProd = 256;                     // producer threads
-constexpr int kPSlots = kPRows * (kPBK / 8);    // (row, 16-byte k-vector) slots per step
-constexpr int kPSPT = (kPSlots + kPProd - 1) / kPProd;  // slots per producer thread
-constexpr int kPLastWaves = (kPSlots - (kPSPT - 1) * kPProd) / kWave;
-static_assert(kPLastWaves * kWave == kPSlots - (kPSPT - 1) * kPProd && kPLastWaves >= 1,
-              "the last slot set must cover whole producer waves");
+constexpr int kPCols = 256;                     // output columns per workgroup
+
+// Workgroup shape for NRB 16-row blocks (at most; a workgroup stores NRB - 1 or NRB).
+template <int NRB>
+struct PShape {
+  static constexpr int kRows = NRB * 16;
+  static constexpr int kSlots = kRows * (kPBK / 8);  // (row, 16-byte k-vector) slots per step
+  static constexpr int kSPT = (kSlots + kPProd - 1) / kPProd;  // slots per producer thread
+  static constexpr int kLastWaves = (kSlots - (kSPT - 1) * kPProd) / kWave;
+  static_assert(kLastWaves * kWave == kSlots - (kSPT - 1) * kPProd && kLastWaves >= 1,
+                "the last slot set must cover whole producer waves");
+};
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
@@ -432,15 +437,16 @@ struct PParams {
   HParams h;
   int rb_total;  // 16-row blocks of M
   int nblocks;   // workgroups (a multiple of 8)
+  int halves;    // 256-column halves of Cout (1 or 2): XCDs 0-3 take half 0, 4-7 half 1
 };
 
 // Consumer wave c: B(k+1) issued at step k, MFMA(k) from A buffer k % 2, one barrier per
 // step; then the epilogue. Always 9 row blocks (compile-time, so the MFMA loop and the
 // accumulators carry no run-time conditions); nrb row blocks are stored.
-template <typename T>
-__device__ __forceinline__ void dcn_p_consumer(const HParams &p, T (*As)[kPRows * kPLDA],
-                                               int m0, int nrb, int nk, int lane, int wave) {
-  constexpr int NRB = kPRowBlocks;
+template <typename T, int NRB>
+__device__ __forceinline__ void dcn_p_consumer(const HParams &p, T (*As)[NRB * 16 * kPLDA],
+                                               int m0, int nrb, int n0, int nk, int lane,
+                                               int wave) {
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, p.w_bytes);
   const uint32_t woob = p.w_bytes;
   // B fragments (16x16x32, read from the 32x32x16 fragment packing): lane l takes column
@@ -450,7 +456,7 @@ __device__ __forceinline__ void dcn_p_consumer(const HParams &p, T (*As)[kPRows 
   for (int kh = 0; kh < kPKH; ++kh)
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb) {
-      const int n = wave * 64 + cb * 16 + (lane & 15);
+      const int n = n0 + wave * 64 + cb * 16 + (lane & 15);
       const int nb = n >> 5;
       bo[kh][cb] = nb < p.nb_total ? ((uint32_t)(nb * p.kb_total + 2 * kh + (lane >> 5)) * 64u +
                                       (uint32_t)((n & 31) + 32 * ((lane >> 4) & 1))) * 16u
@@ -499,7 +505,7 @@ __device__ __forceinline__ void dcn_p_consumer(const HParams &p, T (*As)[kPRows 
   const T *bias = static_cast<const T *>(p.bias);
 #pragma unroll
   for (int cb = 0; cb < 4; ++cb) {
-    const int n = wave * 64 + cb * 16 + (lane & 15);
+    const int n = n0 + wave * 64 + cb * 16 + (lane & 15);
     const float bv = (bias != nullptr && n < p.Cout) ? (float)bias[n] : 0.f;
 #pragma unroll
     for (int rbi = 0; rbi < NRB; ++rbi)
@@ -518,9 +524,9 @@ __device__ __forceinline__ void dcn_p_consumer(const HParams &p, T (*As)[kPRows 
 // (k+1) % 2 into buffer (k+1) % 2. Every
 // load is issued unconditionally (steps past the end read out of range), so the compiler's
 // wait counts stay exact and the gathers of the next steps stay in flight.
-template <typename T, int NS>
+template <typename T, int NS, int NRB>
 __device__ __forceinline__ void dcn_p_producer(const HParams &p, const TapGeo *geo,
-                                               T (*As)[kPRows * kPLDA], int nk, int ptid) {
+                                               T (*As)[NRB * 16 * kPLDA], int nk, int ptid) {
   using V = Vec<T, 8>;
   constexpr int KV = kPBK / 8;
   const int TT = p.taps;
@@ -603,26 +609,34 @@ __device__ __forceinline__ void dcn_p_producer(const HParams &p, const TapGeo *g
   if (k0 < nk) step(k0, ra0, ra1);
 }
 
-template <typename T, int GEO>
+template <typename T, int GEO, int NRB>
 __global__ void __launch_bounds__(kPThreads) dcn_fused_p_kernel(const PParams pp) {
+  using SH = PShape<NRB>;
+  constexpr int kPRows = SH::kRows;
   const HParams &p = pp.h;
   __shared__ __attribute__((aligned(16))) TapGeo geo[kPRows * kMaxTaps];
   __shared__ __attribute__((aligned(16))) T As[2][kPRows * kPLDA];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  // XCD-contiguous row ranges: block b runs on XCD b % 8.
+  // XCD-contiguous row ranges: block b runs on XCD b % 8. With two column halves, XCDs
+  // 0-3 take half 0 and 4-7 half 1, so each XCD's L2 holds one half of the weight.
   const int bpx = pp.nblocks >> 3;
-  const int r = (int)(blockIdx.x & 7) * bpx + (int)(blockIdx.x >> 3);
-  const int rb0 = (int)((int64_t)pp.rb_total * r / pp.nblocks);
-  const int nrb = (int)((int64_t)pp.rb_total * (r + 1) / pp.nblocks) - rb0;  // 8 or 9
-  if (nrb < kPRowBlocks - 1 || nrb > kPRowBlocks) return;
+  const int xcd = (int)(blockIdx.x & 7);
+  const int xph = 8 / pp.halves;                       // XCDs per half
+  const int half = xcd / xph;
+  const int nbh = pp.nblocks / pp.halves;              // workgroups per half
+  const int r = (xcd - half * xph) * bpx + (int)(blockIdx.x >> 3);
+  const int rb0 = (int)((int64_t)pp.rb_total * r / nbh);
+  const int nrb = (int)((int64_t)pp.rb_total * (r + 1) / nbh) - rb0;  // NRB - 1 or NRB
+  if (nrb < NRB - 1 || nrb > NRB) return;
+  const int n0 = half * kPCols;
   const int m0 = rb0 * 16;
   const int nrows = nrb * 16;
   const int HoWo = p.Ho * p.Wo, TT = p.taps;
   const uint32_t xoob = p.x_bytes;
 
-  // Geometry table for all 144 rows (rows outside the range or past M: zero weights,
+  // Geometry table for all NRB * 16 rows (rows outside the range or past M: zero weights,
   // out-of-range offsets).
   for (int g = tid; g < kPRows * TT; g += kPThreads) {
     const int row = g / TT, t = g - row * TT, m = m0 + row;
@@ -663,49 +677,71 @@ __global__ void __launch_bounds__(kPThreads) dcn_fused_p_kernel(const PParams pp
   }
   __syncthreads();
   const int nk = TT * (p.C / kPBK);
-  // Always the 9-block body: a range of 8 blocks has zero geometry in its 9th block (see
-  // above) and does not store it; the kernel's time is set by the 9-block ranges anyway.
+  // Always the NRB-block body: a range of NRB - 1 blocks has zero geometry in its last
+  // block (see above) and does not store it; the kernel's time is set by the full ranges.
   // Consumers and producers run the same number of barriers (one per step + prologue).
   if (wave < 4)
-    dcn_p_consumer<T>(p, As, m0, nrb, nk, lane, wave);
-  else if (wave - 4 < kPLastWaves)
-    dcn_p_producer<T, kPSPT>(p, geo, As, nk, tid - kPProd);
+    dcn_p_consumer<T, NRB>(p, As, m0, nrb, n0, nk, lane, wave);
+  else if (wave - 4 < SH::kLastWaves)
+    dcn_p_producer<T, SH::kSPT, NRB>(p, geo, As, nk, tid - kPProd);
   else
-    dcn_p_producer<T, kPSPT - 1>(p, geo, As, nk, tid - kPProd);
+    dcn_p_producer<T, SH::kSPT - 1, NRB>(p, geo, As, nk, tid - kPProd);
 }
 
-// The persistent kernel runs one workgroup per CU with 8 or 9 row blocks each (gather
-// slots 0-3 then always fall on rows of the workgroup's range).
-int p_blocks_for(const HParams &p, int geo) {
-  if (geo == kGeoRegular || p.C % 64 != 0 || p.Cout <= 128 || p.Cout > 256) return 0;
+// The persistent kernel runs one workgroup per CU over one 256-column half of Cout and
+// NRB - 1 or NRB row blocks (NRB = 9: res4-like shapes; NRB = 5: res5-like, Cout 512).
+struct PConfig {
+  int nblocks = 0, nrb = 0, halves = 0;
+};
+PConfig p_config_for(const HParams &p, int geo) {
+  PConfig c;
+  if (geo == kGeoRegular || p.C % 64 != 0 || p.Cout <= 128 || p.Cout > 2 * kPCols) return c;
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    return 0;
+    return c;
   const int nb = (cus / 8) * 8;
-  const int rb = (p.M + 15) / 16;
-  if (nb < 8 || rb < nb * (kPRowBlocks - 1) || rb > nb * kPRowBlocks) return 0;
-  return nb;
+  const int halves = p.Cout > kPCols ? 2 : 1;
+  const int64_t rb = (int64_t)((p.M + 15) / 16);
+  const int64_t nbh = nb / halves;
+  if (nb < 8) return c;
+  for (int nrb : {9, 5}) {
+    if (rb >= nbh * (nrb - 1) && rb <= nbh * nrb) {
+      c.nblocks = nb;
+      c.nrb = nrb;
+      c.halves = halves;
+      return c;
+    }
+  }
+  return c;
 }
 
-template <typename T>
-hipError_t launch_p(const HParams &h, int geo, int nblocks, hipStream_t stream) {
-  PParams pp;
-  pp.h = h;
-  pp.rb_total = (h.M + 15) / 16;
-  pp.nblocks = nblocks;
-  if (geo == kGeoY)
-    hipLaunchKernelGGL((dcn_fused_p_kernel<T, kGeoY>), dim3(nblocks), dim3(kPThreads), 0,
+template <typename T, int GEO>
+hipError_t launch_p_geo(const PParams &pp, int nrb, hipStream_t stream) {
+  if (nrb == 9)
+    hipLaunchKernelGGL((dcn_fused_p_kernel<T, GEO, 9>), dim3(pp.nblocks), dim3(kPThreads), 0,
                        stream, pp);
   else
-    hipLaunchKernelGGL((dcn_fused_p_kernel<T, kGeoMask>), dim3(nblocks), dim3(kPThreads), 0,
+    hipLaunchKernelGGL((dcn_fused_p_kernel<T, GEO, 5>), dim3(pp.nblocks), dim3(kPThreads), 0,
                        stream, pp);
   return hipGetLastError();
 }
 
 template <typename T>
+hipError_t launch_p(const HParams &h, int geo, const PConfig &c, hipStream_t stream) {
+  PParams pp;
+  pp.h = h;
+  pp.rb_total = (h.M + 15) / 16;
+  pp.nblocks = c.nblocks;
+  pp.halves = c.halves;
+  if (geo == kGeoY) return launch_p_geo<T, kGeoY>(pp, c.nrb, stream);
+  return launch_p_geo<T, kGeoMask>(pp, c.nrb, stream);
+}
+
+template <typename T>
 hipError_t launch_t(const HParams &p, int geo, hipStream_t stream) {
-  if (const int nb = p_blocks_for(p, geo)) return launch_p<T>(p, geo, nb, stream);
+  const PConfig c = p_config_for(p, geo);
+  if (c.nblocks) return launch_p<T>(p, geo, c, stream);
   return p.C % 64 == 0 ? launch_tt<T, true>(p, geo, stream) : launch_tt<T, false>(p, geo, stream);
 }
 

@@ -315,14 +315,20 @@ def test_fused_front_end_res4_fp16():
 
 @pytest.mark.parametrize("dtype", HALF, ids=["fp16", "bf16"])
 @pytest.mark.parametrize("form", ["mask", "y3t"])
-def test_fused_half_row_balanced(dtype, form):
-    """Shapes that take the row-balanced persistent kernel (M = 33280 rows: 8- and 9-block
-    row ranges per workgroup and a partial last row block; Cout = 200, a column tail inside
-    the 256-wide tile). Every output against explicit columns (the NHWC gather kernel, in
-    the input dtype as the reference's column buffer) times the weight in fp32 on the GPU;
-    the first and last 1500 rows against the float64 oracle."""
+@pytest.mark.parametrize("shape", [
+    # batch, cin, cout, h, w (M = b * h * w, stride 1, pad 1)
+    (2, 64, 200, 130, 128),   # one column half, 8- and 9-block row ranges, column tail
+    (1, 64, 320, 90, 100),    # two column halves (the second 64 wide), 4- and 5-block ranges
+    (1, 128, 512, 80, 110),   # two full halves, 4- and 5-block ranges
+], ids=["half1", "half2-tail", "half2"])
+def test_fused_half_row_balanced(dtype, form, shape):
+    """Shapes that take the row-balanced persistent kernel (on a 256-CU device: NRB - 1 or
+    NRB row blocks per workgroup, a partial last row block, one or two 256-column halves
+    of Cout). Every output against explicit columns (the NHWC gather kernel, in the input
+    dtype as the reference's column buffer) times the weight in fp32 on the GPU; the first
+    and last 1500 rows against the float64 oracle."""
     from modulated_deform_conv import fused_tl
-    b, cin, cout, h, w = 2, 64, 200, 130, 128  # M = b * h * w (stride 1, pad 1)
+    b, cin, cout, h, w = shape
     g = torch.Generator().manual_seed(21)
     x = torch.randn(b, h, w, cin, generator=g).to(dtype)
     off = 2.0 * torch.randn(b, h, w, 18, generator=g)
