@@ -101,83 +101,131 @@ __global__ void __launch_bounds__(kBlock) im2col_nchw_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// NHWC (dg == 1): col[m, t*C + c], m = (b, oh, ow). A group of LPP lanes owns one
-// (m, t) pair and sweeps the channels with 16-byte loads of the four corner rows.
-// Consecutive pairs are consecutive taps of one pixel, so one pixel's 9*C column
-// row is written contiguously.
+// NHWC (dg == 1): col[m, t*C + c], m = (b, oh, ow). A wave owns kPPW consecutive (m, t)
+// pairs of one image. Lane i < kPPW first computes the geometry of pair i (offsets and
+// mask read once, bilinear weights, corner byte offsets) into LDS; then groups of LPP
+// lanes take the wave's pairs in turn and sweep the channels with 16-byte loads of the
+// four corner rows, so each pair costs four gathers and one store per channel chunk and
+// no per-lane geometry loads; kPPW = 16 keeps enough waves and loads in flight. Consecutive pairs are consecutive taps of one pixel, so one
+// pixel's 9*C column row is written contiguously.
 // ---------------------------------------------------------------------------
-// FUSED_Y: offsets / pre-sigmoid mask from y [M][3T] of type Y (T, or float plus an fp32
-// bias [3T] for the fused front end); otherwise offsets [M][2T] and mask [M][T] of type T.
-template <typename T, int VEC, bool FUSED_Y, typename Y = T>
+constexpr int kPPW = 16;  // pairs per wave
+
+struct PairGeo {
+  float w[4];   // corner weights (zero for invalid corners)
+  float mk;     // mask (applied after the blend, as the column is defined)
+  uint32_t o[4];  // corner byte offsets in the image, out of range when invalid
+};
+
+template <typename T, int VEC, bool FUSED_Y, typename Y>
 __global__ void __launch_bounds__(kBlock) im2col_nhwc_kernel(
     const T *__restrict__ im, const Y *__restrict__ offset, const T *__restrict__ mask,
     T *__restrict__ col, const DcnGeom g, int lpp_log2, uint32_t img_bytes,
-    const float *__restrict__ y_bias = nullptr) {
+    const float *__restrict__ y_bias, int chunks) {
+  __shared__ PairGeo geo[kBlock / kWave * kPPW];
   const int T_ = g.kernel_h * g.kernel_w;
   const int HoWo = g.height_col * g.width_col;
-  const int b = blockIdx.y;
-  const int pair = (blockIdx.x * kBlock + threadIdx.x) >> lpp_log2;
-  if (pair >= HoWo * T_) return;
-  const int LPP = 1 << lpp_log2;
-  const int li = threadIdx.x & (LPP - 1);
-  const int sp = pair / T_, t = pair - (pair / T_) * T_;
-  const int oh = sp / g.width_col, ow = sp - oh * g.width_col;
-  const int i = t / g.kernel_w, j = t - i * g.kernel_w;
-  const int64_t m = (int64_t)b * HoWo + sp;
-
-  float dy, dx, mk;
-  if constexpr (FUSED_Y) {  // y [B, Ho, Wo, 3T]: offsets then pre-sigmoid mask
-    const Y *yp = offset + m * 3 * T_;
-    dy = (float)yp[2 * t];
-    dx = (float)yp[2 * t + 1];
-    float ym = (float)yp[2 * T_ + t];
-    if (y_bias != nullptr) {
-      dy += y_bias[2 * t];
-      dx += y_bias[2 * t + 1];
-      ym += y_bias[2 * T_ + t];
-    }
-    mk = sigmoid_f32(ym);
-  } else {
-    dy = (float)offset[m * 2 * T_ + 2 * t];
-    dx = (float)offset[m * 2 * T_ + 2 * t + 1];
-    mk = (float)mask[m * T_ + t];
-  }
-  const float h = (float)(oh * g.stride_h - g.pad_h + i * g.dil_h) + dy;
-  const float w = (float)(ow * g.stride_w - g.pad_w + j * g.dil_w) + dx;
-  const Tap<float> tp = make_tap<float>(h, w, g.height, g.width);
-
+  // Block l runs on XCD l % 8 and takes chunk (l % 8) * (n / 8) + l / 8 of the n =
+  // batch * chunks chunks (n a multiple of 8), so each XCD gathers from one contiguous
+  // range of pixels and the input rows stay in its L2.
+  const int n8 = (int)(gridDim.x >> 3);
+  const int cid = (int)(blockIdx.x & 7) * n8 + (int)(blockIdx.x >> 3);
+  const int b = cid / chunks;
+  if (b >= g.batch) return;  // padding chunks
+  const int chunk = cid - b * chunks;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int npairs = HoWo * T_;
+  const int pbase = (chunk * (kBlock / kWave) + wave) * kPPW;  // first pair of the wave
+  if (pbase >= npairs) return;                           // uniform over the wave
   const int C = g.channels;
-  const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(im + (int64_t)b * g.height * g.width * C, img_bytes);
   const uint32_t oob = img_bytes;
   const uint32_t row = (uint32_t)C * (uint32_t)sizeof(T);
-  const uint32_t o1 = tp.i1 < 0 ? oob : (uint32_t)tp.i1 * row;
-  const uint32_t o2 = tp.i2 < 0 ? oob : (uint32_t)tp.i2 * row;
-  const uint32_t o3 = tp.i3 < 0 ? oob : (uint32_t)tp.i3 * row;
-  const uint32_t o4 = tp.i4 < 0 ? oob : (uint32_t)tp.i4 * row;
-  T *out = col + m * T_ * C + (int64_t)t * C;
+
+  // Phase 1: geometry of pair pbase + lane.
+  if (lane < kPPW) {
+    const int pair = pbase + lane;
+    PairGeo G;
+    G.w[0] = G.w[1] = G.w[2] = G.w[3] = 0.f;
+    G.mk = 0.f;
+    G.o[0] = G.o[1] = G.o[2] = G.o[3] = oob;
+    if (pair < npairs) {
+      const int sp = pair / T_, t = pair - (pair / T_) * T_;
+      const int oh = sp / g.width_col, ow = sp - oh * g.width_col;
+      const int i = t / g.kernel_w, j = t - i * g.kernel_w;
+      const int64_t m = (int64_t)b * HoWo + sp;
+      float dy, dx, mk;
+      if constexpr (FUSED_Y) {  // y [B, Ho, Wo, 3T]: offsets then pre-sigmoid mask
+        const Y *yp = offset + m * 3 * T_;
+        dy = (float)yp[2 * t];
+        dx = (float)yp[2 * t + 1];
+        float ym = (float)yp[2 * T_ + t];
+        if (y_bias != nullptr) {
+          dy += y_bias[2 * t];
+          dx += y_bias[2 * t + 1];
+          ym += y_bias[2 * T_ + t];
+        }
+        mk = sigmoid_f32(ym);
+      } else {
+        dy = (float)offset[m * 2 * T_ + 2 * t];
+        dx = (float)offset[m * 2 * T_ + 2 * t + 1];
+        mk = (float)mask[m * T_ + t];
+      }
+      const float h = (float)(oh * g.stride_h - g.pad_h + i * g.dil_h) + dy;
+      const float w = (float)(ow * g.stride_w - g.pad_w + j * g.dil_w) + dx;
+      const Tap<float> tp = make_tap<float>(h, w, g.height, g.width);
+      G.w[0] = tp.w1; G.w[1] = tp.w2; G.w[2] = tp.w3; G.w[3] = tp.w4;
+      G.mk = mk;
+      G.o[0] = tp.i1 < 0 ? oob : (uint32_t)tp.i1 * row;
+      G.o[1] = tp.i2 < 0 ? oob : (uint32_t)tp.i2 * row;
+      G.o[2] = tp.i3 < 0 ? oob : (uint32_t)tp.i3 * row;
+      G.o[3] = tp.i4 < 0 ? oob : (uint32_t)tp.i4 * row;
+    }
+    geo[wave * kPPW + lane] = G;
+  }
+  // The wave reads what its own lanes wrote: order the LDS accesses within the wave.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // Phase 2: lane group gi (LPP lanes) takes pairs gi, gi + PPI, ... of the wave. An
+  // out-of-range corner offset stays out of range with the channel offset added
+  // (img_bytes < 2^31), so every load is issued unconditionally.
+  const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(im + (int64_t)b * g.height * g.width * C, img_bytes);
+  const int LPP = 1 << lpp_log2;
+  const int PPI = kWave >> lpp_log2;  // pairs per iteration
+  const int li = lane & (LPP - 1), gi = lane >> lpp_log2;
+  const int nk = min(kPPW, npairs - pbase);
   using V = Vec<T, VEC>;
-  for (int c = li * VEC; c < C; c += LPP * VEC) {
-    const uint32_t cb = (uint32_t)c * (uint32_t)sizeof(T);
-    V v1, v2, v3, v4;
-    if constexpr (VEC > 1) {
-      v1 = buffer_load_vec<T, VEC>(rsrc, o1 == oob ? oob : o1 + cb);
-      v2 = buffer_load_vec<T, VEC>(rsrc, o2 == oob ? oob : o2 + cb);
-      v3 = buffer_load_vec<T, VEC>(rsrc, o3 == oob ? oob : o3 + cb);
-      v4 = buffer_load_vec<T, VEC>(rsrc, o4 == oob ? oob : o4 + cb);
-    } else {
-      v1.v[0] = buffer_load_one<T>(rsrc, o1 == oob ? oob : o1 + cb);
-      v2.v[0] = buffer_load_one<T>(rsrc, o2 == oob ? oob : o2 + cb);
-      v3.v[0] = buffer_load_one<T>(rsrc, o3 == oob ? oob : o3 + cb);
-      v4.v[0] = buffer_load_one<T>(rsrc, o4 == oob ? oob : o4 + cb);
-    }
-    V o;
+#pragma unroll 4
+  for (int k = gi; k < nk; k += PPI) {
+    const PairGeo G = geo[wave * kPPW + k];
+    const int pair = pbase + k;
+    const int sp = pair / T_, t = pair - (pair / T_) * T_;
+    T *out = col + ((int64_t)b * HoWo + sp) * T_ * C + (int64_t)t * C;
+    for (int c = li * VEC; c < C; c += LPP * VEC) {
+      const uint32_t cb = (uint32_t)c * (uint32_t)sizeof(T);
+      V v1, v2, v3, v4;
+      if constexpr (VEC > 1) {
+        v1 = buffer_load_vec<T, VEC>(rsrc, G.o[0] + cb);
+        v2 = buffer_load_vec<T, VEC>(rsrc, G.o[1] + cb);
+        v3 = buffer_load_vec<T, VEC>(rsrc, G.o[2] + cb);
+        v4 = buffer_load_vec<T, VEC>(rsrc, G.o[3] + cb);
+      } else {
+        v1.v[0] = buffer_load_one<T>(rsrc, G.o[0] + cb);
+        v2.v[0] = buffer_load_one<T>(rsrc, G.o[1] + cb);
+        v3.v[0] = buffer_load_one<T>(rsrc, G.o[2] + cb);
+        v4.v[0] = buffer_load_one<T>(rsrc, G.o[3] + cb);
+      }
+      V o;
 #pragma unroll
-    for (int k = 0; k < VEC; ++k) {
-      const float val = tp.w1 * (float)v1.v[k] + tp.w2 * (float)v2.v[k] +
-                        tp.w3 * (float)v3.v[k] + tp.w4 * (float)v4.v[k];
-      o.v[k] = static_cast<T>(val * mk);
+      for (int e = 0; e < VEC; ++e) {
+        const float val = G.w[0] * (float)v1.v[e] + G.w[1] * (float)v2.v[e] +
+                          G.w[2] * (float)v3.v[e] + G.w[3] * (float)v4.v[e];
+        o.v[e] = static_cast<T>(val * G.mk);
+      }
+      store_vec<T, VEC>(out + c, o);
     }
-    store_vec<T, VEC>(out + c, o);
   }
 }
 
@@ -222,19 +270,21 @@ hipError_t launch_nhwc_t(const DcnGeom &g, const void *im, const void *off, cons
   while ((1 << lpp_log2) < lpp) ++lpp_log2;
   const int T_ = g.kernel_h * g.kernel_w;
   const int64_t pairs = (int64_t)g.height_col * g.width_col * T_;
-  const int64_t threads = pairs << lpp_log2;
-  dim3 grid((unsigned)((threads + kBlock - 1) / kBlock), g.batch);
+  constexpr int kPairsPerBlock = kBlock / kWave * kPPW;
+  const int chunks = (int)((pairs + kPairsPerBlock - 1) / kPairsPerBlock);
+  const int64_t nblk = ((int64_t)chunks * g.batch + 7) / 8 * 8;
+  dim3 grid((unsigned)nblk);
   const uint32_t img_bytes = (uint32_t)((int64_t)g.height * g.width * C * sizeof(T));
   if (vec)
     hipLaunchKernelGGL((im2col_nhwc_kernel<T, VEC, FY, Y>), grid, dim3(kBlock), 0, stream,
                        static_cast<const T *>(im), static_cast<const Y *>(off),
                        static_cast<const T *>(msk), static_cast<T *>(col), g, lpp_log2,
-                       img_bytes, y_bias);
+                       img_bytes, y_bias, chunks);
   else
     hipLaunchKernelGGL((im2col_nhwc_kernel<T, 1, FY, Y>), grid, dim3(kBlock), 0, stream,
                        static_cast<const T *>(im), static_cast<const Y *>(off),
                        static_cast<const T *>(msk), static_cast<T *>(col), g, lpp_log2,
-                       img_bytes, y_bias);
+                       img_bytes, y_bias, chunks);
   return hipGetLastError();
 }
 
