@@ -39,6 +39,9 @@ __all__ = [
     "dcn_packed_weight_numel",
     "dcn_pack_weight",
     "dcn_fused_fwd_nhwc",
+    "transpose",
+    "nchw_to_nhwc",
+    "nhwc_to_nchw",
     "forward",
     "backward",
 ]
@@ -155,6 +158,34 @@ def dcn_pack_weight(weight, packed=None):
     _b.call("bevk_dcn_pack_weight", _b.dtype_code(weight), _b.ptr(weight), cout, kh, kw, c,
             _b.ptr(packed), _b.stream_of(weight))
     return packed
+
+
+def transpose(src, dst, batch, rows, cols):
+    """dst[b][c][r] = src[b][r][c] over a contiguous [batch, rows, cols] source (fp32, fp16,
+    bf16; a bit-exact copy)."""
+    fn = "transpose"
+    _b.require_device(fn, src, dst)
+    _b.require_contiguous(fn, src=src, dst=dst)
+    _b.require_dtype(fn, src, dst=dst)
+    _b.require_numel(fn, "src", src, batch * rows * cols)
+    _b.require_numel(fn, "dst", dst, batch * rows * cols)
+    _b.call("bevk_transpose", _b.dtype_code(src), _b.ptr(src), _b.ptr(dst), batch, rows, cols,
+            _b.stream_of(src))
+    return dst
+
+
+def nchw_to_nhwc(x):
+    """[B, C, H, W] (contiguous) -> a new contiguous [B, H, W, C] tensor."""
+    b, c, h, w = x.shape
+    out = x.new_empty(b, h, w, c)
+    return transpose(x.contiguous(), out, b, c, h * w)
+
+
+def nhwc_to_nchw(x):
+    """[B, H, W, C] (contiguous) -> a new contiguous [B, C, H, W] tensor."""
+    b, h, w, c = x.shape
+    out = x.new_empty(b, c, h, w)
+    return transpose(x.contiguous(), out, b, h * w, c)
 
 
 def dcn_fused_fwd_nhwc(data_im, data_offset, data_mask, weight_packed, bias, batch_size,

@@ -79,6 +79,10 @@ int64_t dcn_packed_weight_elems(int dtype, int cout, int K);
 hipError_t launch_dcn_pack_weight(int dtype, const void *weight, int cout, int C, int T,
                                   void *packed, hipStream_t stream, bool src_tc = false);
 
+// dst[b][c][r] = src[b][r][c] for 2- or 4-byte elements (NCHW <-> NHWC).
+hipError_t launch_transpose(int elem_bytes, const void *src, void *dst, int batch, int rows,
+                            int cols, hipStream_t stream);
+
 // NHWC gather whose offsets / pre-sigmoid mask come from an fp32 y [M][3T] plus an fp32
 // bias [3T] (the fused front end: y is the offset conv without its bias).
 hipError_t launch_im2col_nhwc_yf32(int dtype, const DcnGeom &g, const void *data_im,

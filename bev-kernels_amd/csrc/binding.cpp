@@ -357,6 +357,23 @@ int bevk_dcn_pack_weight(int dtype, const void *weight, int channels_out, int ke
                     fn);
 }
 
+int bevk_transpose(int dtype, const void *src, void *dst, int batch, int rows, int cols,
+                   void *stream) {
+  const char *fn = "transpose";
+  g_last_error.clear();
+  if (dtype != BEVK_F32 && dtype != BEVK_F16 && dtype != BEVK_BF16)
+    return fail(BEVK_ERR_UNSUPPORTED, "\"%s\" not implemented for '%s'", fn, dtype_name(dtype));
+  if (batch < 0 || rows < 0 || cols < 0)
+    return fail(BEVK_ERR_INVALID, "%s: negative size", fn);
+  if (batch == 0 || rows == 0 || cols == 0) return ok();
+  if (batch > 65535 || (rows + 63) / 64 > 65535 || (cols + 63) / 64 > (1 << 30))
+    return fail(BEVK_ERR_INVALID, "%s: shape exceeds the launch grid", fn);
+  if (!src || !dst) return fail(BEVK_ERR_INVALID, "%s: null tensor pointer", fn);
+  return hip_status(bevk::launch_transpose(dtype_size(dtype), src, dst, batch, rows, cols,
+                                           (hipStream_t)stream),
+                    fn);
+}
+
 int bevk_dcn_fused_fwd_nhwc(int dtype, const void *data_im, const void *data_offset,
                             int offset_last_dim, const void *data_mask, const void *weight_packed,
                             const void *bias, int batch_size, int channels, int height_im,

@@ -23,7 +23,7 @@ BUILD_DIR = os.path.join(PKG, "_build")
 LIB_PATH = os.path.join(PKG, "libbevk.so")
 
 SOURCES = ["binding.cpp", "msda_fwd.hip", "dcn_gather.hip", "dcn_fused.hip", "dcn_fused_h.hip",
-           "dcn_bwd.hip", "msda_bwd.hip"]
+           "dcn_bwd.hip", "msda_bwd.hip", "layout.hip"]
 ARCH = "gfx950"
 
 

@@ -343,16 +343,16 @@ def _modulated_deform_conv2d_forward(input, offset, mask, weight, bias, stride, 
     if (groups == 1 and deform_groups == 1 and input.dtype != torch.float64
             and channels % vec == 0):
         # Implicit GEMM: NHWC views of the inputs, output produced as [B, Ho, Wo, Cout].
-        x_nhwc = input.permute(0, 2, 3, 1).contiguous()
-        off_nhwc = offset.permute(0, 2, 3, 1).contiguous()
-        msk_nhwc = mask.permute(0, 2, 3, 1).contiguous()
+        x_nhwc = ext.nchw_to_nhwc(input)
+        off_nhwc = ext.nchw_to_nhwc(offset)
+        msk_nhwc = ext.nchw_to_nhwc(mask)
         w_packed = packed_weight(weight, input.dtype)
         b = bias.to(input.dtype).contiguous() if bias is not None else None
         out = input.new_empty(batch, ho, wo, channels_out)
         ext.dcn_fused_fwd_nhwc(x_nhwc, off_nhwc, msk_nhwc, w_packed, b, batch, channels, height,
                                width, ho, wo, channels_out, kernel_h, kernel_w, pad_h, pad_w,
                                stride_h, stride_w, dil_h, dil_w, out)
-        return out.permute(0, 3, 1, 2).contiguous()
+        return ext.nhwc_to_nchw(out)
     # Columns [C*kh*kw, B*Ho*Wo] then one GEMM per group (modulated_deform_conv.py:369-401).
     bhw = batch * ho * wo
     columns = input.new_empty(channels * kernel_h * kernel_w, bhw)

@@ -176,6 +176,14 @@ int64_t bevk_dcn_packed_weight_bytes(int dtype, int channels_out, int kernel_h, 
 int bevk_dcn_pack_weight(int dtype, const void *weight, int channels_out, int kernel_h,
                          int kernel_w, int channels, void *packed, void *stream);
 
+/* Layout change: dst[b][c][r] = src[b][r][c] over a [batch, rows, cols] source, i.e.
+ * NCHW -> NHWC with rows = C, cols = H*W, and back with rows = H*W, cols = C. No
+ * counterpart in the reference, whose NCHW module path feeds NCHW kernels; here the NCHW
+ * module (modulated_deform_conv.py:331-403 interface) runs the NHWC fused kernel and
+ * changes layout on the way in and out. dtypes: F16, BF16, F32; bit-exact copy. */
+int bevk_transpose(int dtype, const void *src, void *dst, int batch, int rows, int cols,
+                   void *stream);
+
 /* Fused NHWC DCNv2 forward: bilinear x mask taps are produced straight into LDS and
  * multiplied on the matrix cores; no column buffer touches HBM.
  *   data_im       [B, H, W, C]

@@ -465,3 +465,20 @@ def test_dcn_split_nhwc_bn_relu_epilogue():
     conv = od.forward_nhwc(x.double(), off, msk, weight.double(), bias.double(), 1, 1, 1)
     ref = torch.relu(conv * scale.double() + shift.double())
     check(out.cpu(), ref, torch.float32, "bn relu")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16],
+                         ids=["fp32", "fp16", "bf16"])
+@pytest.mark.parametrize("shape", [(2, 256, 58, 100), (1, 3, 5, 7), (3, 18, 29, 50),
+                                   (1, 130, 1, 67)])
+def test_transpose_layouts(dtype, shape):
+    """The NCHW <-> NHWC layout kernel is a bit-exact copy: tile-aligned, ragged and
+    odd-sized shapes (the vector and the scalar path), both directions."""
+    import _modulated_deform_conv_ext as ext
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(*shape, generator=g).to(dtype).to(DEV)
+    y = ext.nchw_to_nhwc(x)
+    assert y.shape == (shape[0], shape[2], shape[3], shape[1])
+    assert torch.equal(y, x.permute(0, 2, 3, 1).contiguous())
+    z = ext.nhwc_to_nchw(y)
+    assert torch.equal(z, x)
