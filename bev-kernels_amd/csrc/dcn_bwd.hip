@@ -231,6 +231,228 @@ hipError_t launch_nchw_t(const DcnGeom &g, const void *col, const void *im, cons
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// NHWC grad_x by output tile (dg == 1), without float atomics in LDS. A workgroup takes a
+// TH x TW tile of output pixels of one image and 64*CPL channels:
+//   1. every (pixel, tap) sample's valid bilinear corners become (dcol row, weight * mask)
+//      pairs, binned by target input position: one bin per position of the tile's input
+//      footprint (the rows / columns its taps reach, grown by kGbMargin pixels for the
+//      offsets) plus one bin for corners beyond it. An integer LDS atomic per pair gives
+//      its rank inside its bin;
+//   2. an exclusive scan of the bin counts gives the bin starts, and every pair is stored
+//      at start + rank (a counting sort);
+//   3. each wave takes whole bins: lane l holds channels l, l+64, ... and sums the bin's
+//      pairs in registers (weight times the dcol element), then adds the sum to grad_x
+//      with one fp32 atomic per channel. Pairs of the far bin are added one by one.
+// Each input element receives ~36 contributions from a tile (9 taps x 4 corners); they
+// collapse to one global atomic, and LDS only ever sees integer atomics (one per pair,
+// not per channel). Same per-corner semantics as col2im_nhwc_kernel: finite coordinates
+// only, each corner checked against the image.
+// ---------------------------------------------------------------------------
+constexpr int kGbThreads = 256;
+constexpr int kGbMargin = 8;
+constexpr int kGbMaxPos = 1024;                               // footprint bins
+constexpr int kGbMaxPairs = 2304;                             // pairs per tile (4 per sample)
+constexpr int kGbSPT = (kGbMaxPairs / 4 + kGbThreads - 1) / kGbThreads;  // samples / thread
+
+struct GbPair {
+  uint32_t row;  // dcol row (m * T + t)
+  float w;       // bilinear weight times the modulation
+  int tgt;       // target pixel y * W + x in the image (used by the far bin)
+};
+
+struct GxBin {
+  int th, tw;        // output tile
+  int rh, rw;        // footprint rows / columns
+  int tiles_x, ntile, chunks;
+  int per_xcd;       // items per XCD (XCD-contiguous item ranges)
+};
+
+template <typename T, bool FUSED_Y, int CPL>
+__global__ void __launch_bounds__(kGbThreads) col2im_nhwc_gx_bin_kernel(
+    const T *__restrict__ dcol, const T *__restrict__ offset, const T *__restrict__ mask,
+    const DcnGeom g, const GxBin tl, float *__restrict__ gx) {
+  __shared__ int bin_at[kGbMaxPos + 2];  // counts, then exclusive bin starts
+  __shared__ int wsum[kGbThreads / kWave];
+  __shared__ GbPair list[kGbMaxPairs];
+  const int T_ = g.kernel_h * g.kernel_w;
+  const int HoWo = g.height_col * g.width_col;
+  const int C = g.channels;
+  const int nitems = g.batch * tl.ntile * tl.chunks;
+  const int item = (int)(blockIdx.x & 7) * tl.per_xcd + (int)(blockIdx.x >> 3);
+  if (item >= nitems || (int)(blockIdx.x >> 3) >= tl.per_xcd) return;  // uniform
+  const int chunk = item % tl.chunks;
+  const int tile = (item / tl.chunks) % tl.ntile;
+  const int b = item / (tl.chunks * tl.ntile);
+  const int ty = tile / tl.tiles_x, tx = tile - ty * tl.tiles_x;
+  const int oh0 = ty * tl.th, ow0 = tx * tl.tw;
+  const int fy0 = oh0 * g.stride_h - g.pad_h - kGbMargin;
+  const int fx0 = ow0 * g.stride_w - g.pad_w - kGbMargin;
+  const int npos = tl.rh * tl.rw;
+  const int nbins = npos + 1;  // bin npos: corners beyond the footprint
+  const int tid = threadIdx.x;
+  for (int i = tid; i < nbins + 1; i += kGbThreads) bin_at[i] = 0;
+  __syncthreads();
+
+  // 1. Pairs and their ranks (registers: kGbSPT samples x 4 corners per thread).
+  const int nsamp = tl.th * tl.tw * T_;
+  int pbin[kGbSPT][4], prank[kGbSPT][4], ptgt[kGbSPT][4];
+  float pw[kGbSPT][4];
+  uint32_t prow[kGbSPT];
+#pragma unroll
+  for (int k = 0; k < kGbSPT; ++k) {
+    const int s = tid + k * kGbThreads;
+    const int pix = s / T_, t = s - (s / T_) * T_;
+    const int oh = oh0 + pix / tl.tw, ow = ow0 + pix % tl.tw;
+    const bool live = s < nsamp && oh < g.height_col && ow < g.width_col;
+    const int m = b * HoWo + (live ? oh * g.width_col + ow : 0);
+    const int tt = live ? t : 0;
+    float dy = 0.f, dx = 0.f, mk = 0.f;
+    if (live) {
+      if constexpr (FUSED_Y) {
+        const T *o = offset + (int64_t)m * 3 * T_;
+        dy = (float)o[2 * tt];
+        dx = (float)o[2 * tt + 1];
+        mk = sigmoid_f32((float)o[2 * T_ + tt]);
+      } else {
+        dy = (float)offset[(int64_t)m * 2 * T_ + 2 * tt];
+        dx = (float)offset[(int64_t)m * 2 * T_ + 2 * tt + 1];
+        mk = (float)mask[(int64_t)m * T_ + tt];
+      }
+    }
+    prow[k] = (uint32_t)m * (uint32_t)T_ + (uint32_t)tt;
+    const int i = tt / g.kernel_w, j = tt - i * g.kernel_w;
+    const float h = (float)(oh * g.stride_h - g.pad_h + i * g.dil_h) + dy;
+    const float w = (float)(ow * g.stride_w - g.pad_w + j * g.dil_w) + dx;
+    const float fh = floorf(h), fw = floorf(w);
+    const float lh = h - fh, lw = w - fw, hh = 1.f - lh, hw = 1.f - lw;
+    const float fhc = fminf(fmaxf(fh, -2.f), (float)g.height);
+    const float fwc = fminf(fmaxf(fw, -2.f), (float)g.width);
+    const int hl = (int)fhc, wl = (int)fwc;
+    const bool fin = live && fh == fhc && fw == fwc;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int yy = hl + (q >> 1), xx = wl + (q & 1);
+      const bool ok = fin && yy >= 0 && yy < g.height && xx >= 0 && xx < g.width;
+      const int ry = yy - fy0, rx = xx - fx0;
+      const bool in = (unsigned)ry < (unsigned)tl.rh && (unsigned)rx < (unsigned)tl.rw;
+      pbin[k][q] = ok ? (in ? ry * tl.rw + rx : npos) : -1;
+      pw[k][q] = ((q >> 1) ? lh : hh) * ((q & 1) ? lw : hw) * mk;
+      ptgt[k][q] = yy * g.width + xx;
+      prank[k][q] = ok ? atomicAdd(&bin_at[pbin[k][q]], 1) : 0;
+    }
+  }
+  __syncthreads();
+
+  // 2. Exclusive scan of the nbins counts: thread tid owns entries [tid*E, tid*E + E).
+  {
+    const int E = (nbins + kGbThreads - 1) / kGbThreads;
+    const int e0 = min(tid * E, nbins), e1 = min(e0 + E, nbins);
+    int local = 0;
+    for (int e = e0; e < e1; ++e) local += bin_at[e];
+    const int lane = tid & (kWave - 1), wave = tid / kWave;
+    int incl = local;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const int v = __shfl_up(incl, d, kWave);
+      if (lane >= d) incl += v;
+    }
+    if (lane == kWave - 1) wsum[wave] = incl;
+    __syncthreads();
+    int run = incl - local;
+    for (int w2 = 0; w2 < wave; ++w2) run += wsum[w2];
+    for (int e = e0; e < e1; ++e) {
+      const int c = bin_at[e];
+      bin_at[e] = run;
+      run += c;
+    }
+    if (tid == kGbThreads - 1) {
+      int tot = 0;
+      for (int w2 = 0; w2 < kGbThreads / kWave; ++w2) tot += wsum[w2];
+      bin_at[nbins] = tot;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < kGbSPT; ++k)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (pbin[k][q] >= 0) list[bin_at[pbin[k][q]] + prank[k][q]] = GbPair{prow[k], pw[k][q], ptgt[k][q]};
+  __syncthreads();
+
+  // 3. Per-bin sums, one wave per bin.
+  const int lane = tid & (kWave - 1), wave = tid / kWave;
+  const int64_t img = (int64_t)b * g.height * g.width;
+  const T *dc = dcol + chunk * (kWave * CPL) + lane;
+  float *gxc = gx + chunk * (kWave * CPL) + lane;
+  for (int p = wave; p < npos; p += kGbThreads / kWave) {
+    const int beg = bin_at[p], end = bin_at[p + 1];
+    if (beg == end) continue;
+    float acc[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) acc[c] = 0.f;
+    for (int k = beg; k < end; k += 4) {
+      GbPair e[4];
+      float v[4][CPL];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) e[u] = list[min(k + u, end - 1)];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) v[u][c] = (float)dc[(int64_t)e[u].row * C + c * kWave];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) acc[c] += (k + u < end) ? e[u].w * v[u][c] : 0.f;
+    }
+    const int y = fy0 + p / tl.rw, x = fx0 + p % tl.rw;
+    float *dst = gxc + (img + (int64_t)y * g.width + x) * C;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) unsafeAtomicAdd(dst + c * kWave, acc[c]);
+  }
+  // Far bin: pairs spread over the waves, one pair at a time.
+  for (int k = bin_at[npos] + wave; k < bin_at[nbins]; k += kGbThreads / kWave) {
+    const GbPair e = list[k];
+    float *dst = gxc + (img + e.tgt) * C;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c)
+      unsafeAtomicAdd(dst + c * kWave, e.w * (float)dc[(int64_t)e.row * C + c * kWave]);
+  }
+}
+
+// Tile plan for the binned grad_x kernel; false when C is not a multiple of 64 or a tile
+// of the smallest size does not fit the LDS bins / pair list.
+bool gx_bin_plan(const DcnGeom &g, int cpl, GxBin &tl) {
+  const int T_ = g.kernel_h * g.kernel_w;
+  if (g.deformable_group != 1 || g.channels <= 0 || g.channels % (kWave * cpl) != 0) return false;
+  if ((int64_t)g.batch * g.height_col * g.width_col * T_ >= (int64_t)1 << 31) return false;
+  int th = 8, tw = 8;
+  auto extent = [&](int t, int s, int k, int d) {
+    return (t - 1) * s + (k - 1) * d + 2 + 2 * kGbMargin;
+  };
+  auto fits = [&]() {
+    return th * tw * T_ * 4 <= kGbMaxPairs &&
+           extent(th, g.stride_h, g.kernel_h, g.dil_h) * extent(tw, g.stride_w, g.kernel_w, g.dil_w) <=
+               kGbMaxPos;
+  };
+  while (!fits()) {
+    if (th >= tw && th > 1) th /= 2;
+    else if (tw > 1) tw /= 2;
+    else return false;
+  }
+  tl.th = th;
+  tl.tw = tw;
+  tl.rh = extent(th, g.stride_h, g.kernel_h, g.dil_h);
+  tl.rw = extent(tw, g.stride_w, g.kernel_w, g.dil_w);
+  tl.tiles_x = (g.width_col + tw - 1) / tw;
+  tl.ntile = tl.tiles_x * ((g.height_col + th - 1) / th);
+  tl.chunks = g.channels / (kWave * cpl);
+  const int64_t nitems = (int64_t)g.batch * tl.ntile * tl.chunks;
+  if (nitems > (1 << 28)) return false;
+  tl.per_xcd = (int)((nitems + 7) / 8);
+  return true;
+}
+
 template <typename T, bool FY>
 hipError_t launch_t(const DcnGeom &g, const void *dcol, const void *im, const void *off,
                     const void *msk, float *gx, float *goff, float *gmask, hipStream_t stream) {
@@ -239,6 +461,27 @@ hipError_t launch_t(const DcnGeom &g, const void *dcol, const void *im, const vo
   const int64_t pairs = (int64_t)g.height_col * g.width_col * g.kernel_h * g.kernel_w;
   const int64_t threads = pairs << lpp_log2;
   const dim3 grid((unsigned)((threads + kBlock - 1) / kBlock), g.batch);
+  // grad_x through the binned kernel where it applies; the per-sample kernel then computes
+  // only grad_offset / grad_mask.
+  GxBin tl;
+  if (gx != nullptr && g.channels % kWave == 0) {
+    const int cpl = g.channels % (4 * kWave) == 0 ? 4 : (g.channels % (2 * kWave) == 0 ? 2 : 1);
+    if (gx_bin_plan(g, cpl, tl)) {
+      const dim3 bgrid((unsigned)(tl.per_xcd * 8));
+      const T *dc = static_cast<const T *>(dcol), *of = static_cast<const T *>(off);
+      const T *mk = static_cast<const T *>(msk);
+      if (cpl == 4)
+        hipLaunchKernelGGL((col2im_nhwc_gx_bin_kernel<T, FY, 4>), bgrid, dim3(kGbThreads), 0, stream, dc, of, mk, g, tl, gx);
+      else if (cpl == 2)
+        hipLaunchKernelGGL((col2im_nhwc_gx_bin_kernel<T, FY, 2>), bgrid, dim3(kGbThreads), 0, stream, dc, of, mk, g, tl, gx);
+      else
+        hipLaunchKernelGGL((col2im_nhwc_gx_bin_kernel<T, FY, 1>), bgrid, dim3(kGbThreads), 0, stream, dc, of, mk, g, tl, gx);
+      const hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return e;
+      gx = nullptr;
+      if (goff == nullptr) return hipSuccess;
+    }
+  }
   hipLaunchKernelGGL((col2im_nhwc_kernel<T, FY>), grid, dim3(kBlock), 0, stream,
                      static_cast<const T *>(dcol), static_cast<const T *>(im),
                      static_cast<const T *>(off), static_cast<const T *>(msk), g, lpp_log2,

@@ -53,6 +53,12 @@ def _nhwc(t):
     (1, 16, 12, 10, 3, 2, 1, 1),
     (1, 64, 8, 9, 3, 1, 2, 2),
     (1, 12, 6, 7, 1, 1, 0, 1),
+    # C a multiple of 64: the binned grad_x kernel, with 1, 2 and 4 channels per lane,
+    # several output tiles per image, stride 2 and a 5x5 kernel (smaller tiles)
+    (1, 128, 21, 30, 3, 1, 1, 1),
+    (2, 256, 17, 19, 3, 1, 1, 1),
+    (1, 64, 20, 23, 3, 2, 1, 1),
+    (1, 64, 13, 14, 5, 1, 2, 1),
 ])
 def test_col2im_nhwc(dtype, form, geom):
     b, cin, h, w, k, s, p, dl = geom
