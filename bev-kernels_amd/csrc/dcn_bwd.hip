@@ -232,6 +232,99 @@ hipError_t launch_nchw_t(const DcnGeom &g, const void *col, const void *im, cons
 }
 
 // ---------------------------------------------------------------------------
+// NHWC grad_offset / grad_mask alone, 16-byte vectors: lane li of a pair's LPP lanes takes
+// the VEC = 16 / sizeof(T) consecutive channels at li*VEC (then + LPP*VEC), so one dcol
+// load and four corner loads move 16 bytes per lane; LPP = min(64, next power of two >=
+// C / VEC), two pairs share a wave when C*sizeof(T) is 512 bytes. Corners outside the
+// image read zeros through the buffer path (their offset is set past the end of the
+// image), so there are no branches around the loads. Same arithmetic per channel as
+// col2im_nhwc_kernel; the channel sums meet in a shuffle butterfly.
+// ---------------------------------------------------------------------------
+template <typename T, bool FUSED_Y>
+__global__ void __launch_bounds__(kBlock) col2im_coord_nhwc_vec_kernel(
+    const T *__restrict__ dcol, const T *__restrict__ im, const T *__restrict__ offset,
+    const T *__restrict__ mask, const DcnGeom g, int lpp_log2, uint32_t im_bytes,
+    float *__restrict__ goff, float *__restrict__ gmask) {
+  constexpr int VEC = 16 / sizeof(T);
+  constexpr uint32_t kPast = 0x80000000u;  // >= im_bytes: loads there return zeros
+  const int T_ = g.kernel_h * g.kernel_w;
+  const int HoWo = g.height_col * g.width_col;
+  const int b = blockIdx.y;
+  const int pair = (blockIdx.x * kBlock + threadIdx.x) >> lpp_log2;
+  const int LPP = 1 << lpp_log2;
+  const int li = threadIdx.x & (LPP - 1);
+  const bool live = pair < HoWo * T_;
+  const int pc = live ? pair : 0;
+  const int sp = pc / T_, t = pc - (pc / T_) * T_;
+  const int oh = sp / g.width_col, ow = sp - oh * g.width_col;
+  const int i = t / g.kernel_w, j = t - i * g.kernel_w;
+  const int64_t m = (int64_t)b * HoWo + sp;
+
+  float dy, dx, mk;
+  if constexpr (FUSED_Y) {
+    const T *yp = offset + m * 3 * T_;
+    dy = (float)yp[2 * t];
+    dx = (float)yp[2 * t + 1];
+    mk = sigmoid_f32((float)yp[2 * T_ + t]);
+  } else {
+    dy = (float)offset[m * 2 * T_ + 2 * t];
+    dx = (float)offset[m * 2 * T_ + 2 * t + 1];
+    mk = (float)mask[m * T_ + t];
+  }
+  const float h = (float)(oh * g.stride_h - g.pad_h + i * g.dil_h) + dy;
+  const float w = (float)(ow * g.stride_w - g.pad_w + j * g.dil_w) + dx;
+  const float fh = floorf(h), fw = floorf(w);
+  const float lh = h - fh, lw = w - fw, hh = 1.f - lh, hw = 1.f - lw;
+  const float fhc = fminf(fmaxf(fh, -2.f), (float)g.height);
+  const float fwc = fminf(fmaxf(fw, -2.f), (float)g.width);
+  const int hl = (int)fhc, wl = (int)fwc;
+  const bool in_h0 = hl >= 0 && hl < g.height, in_h1 = hl + 1 >= 0 && hl + 1 < g.height;
+  const bool in_w0 = wl >= 0 && wl < g.width, in_w1 = wl + 1 >= 0 && wl + 1 < g.width;
+  const bool fin = live && fh == fhc && fw == fwc;
+  const int C = g.channels;
+  const int64_t img = (int64_t)b * g.height * g.width;
+  const int64_t e1 = (img + (int64_t)hl * g.width + wl) * C;  // element index of corner 1
+  const uint32_t eb = (uint32_t)sizeof(T);
+  const uint32_t o1 = (fin && in_h0 && in_w0) ? (uint32_t)(e1 * eb) : kPast;
+  const uint32_t o2 = (fin && in_h0 && in_w1) ? (uint32_t)((e1 + C) * eb) : kPast;
+  const uint32_t o3 = (fin && in_h1 && in_w0) ? (uint32_t)((e1 + (int64_t)g.width * C) * eb) : kPast;
+  const uint32_t o4 = (fin && in_h1 && in_w1) ? (uint32_t)((e1 + (int64_t)(g.width + 1) * C) * eb) : kPast;
+  const float w1 = hh * hw, w2 = hh * lw, w3 = lh * hw, w4 = lh * lw;
+  const __amdgpu_buffer_rsrc_t rim = make_rsrc(im, im_bytes);
+  const T *drow = dcol + (m * T_ + t) * C;
+  float ah = 0.f, aw = 0.f, am = 0.f;
+  if (live) {
+    for (int c = li * VEC; c < C; c += LPP * VEC) {
+      const Vec<T, VEC> dv = load_vec<T, VEC>(drow + c);
+      const uint32_t cb = (uint32_t)c * eb;
+      const Vec<T, VEC> v1 = buffer_load_vec<T, VEC>(rim, o1 + cb);
+      const Vec<T, VEC> v2 = buffer_load_vec<T, VEC>(rim, o2 + cb);
+      const Vec<T, VEC> v3 = buffer_load_vec<T, VEC>(rim, o3 + cb);
+      const Vec<T, VEC> v4 = buffer_load_vec<T, VEC>(rim, o4 + cb);
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float dc = (float)dv.v[e], ds = dc * mk;
+        const float x1 = (float)v1.v[e], x2 = (float)v2.v[e];
+        const float x3 = (float)v3.v[e], x4 = (float)v4.v[e];
+        ah += ds * (-hw * x1 - lw * x2 + hw * x3 + lw * x4);
+        aw += ds * (-hh * x1 + hh * x2 - lh * x3 + lh * x4);
+        am += dc * (w1 * x1 + w2 * x2 + w3 * x3 + w4 * x4);
+      }
+    }
+  }
+  for (int s = 1; s < LPP; s <<= 1) {
+    ah += __shfl_xor(ah, s);
+    aw += __shfl_xor(aw, s);
+    am += __shfl_xor(am, s);
+  }
+  if (live && li == 0) {
+    goff[m * 2 * T_ + 2 * t] = ah;
+    goff[m * 2 * T_ + 2 * t + 1] = aw;
+    gmask[m * T_ + t] = FUSED_Y ? am * mk * (1.f - mk) : am;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // NHWC grad_x by output tile (dg == 1), without float atomics in LDS. A workgroup takes a
 // TH x TW tile of output pixels of one image and 64*CPL channels:
 //   1. every (pixel, tap) sample's valid bilinear corners become (dcol row, weight * mask)
@@ -461,31 +554,47 @@ hipError_t launch_t(const DcnGeom &g, const void *dcol, const void *im, const vo
   const int64_t pairs = (int64_t)g.height_col * g.width_col * g.kernel_h * g.kernel_w;
   const int64_t threads = pairs << lpp_log2;
   const dim3 grid((unsigned)((threads + kBlock - 1) / kBlock), g.batch);
-  // grad_x through the binned kernel where it applies; the per-sample kernel then computes
-  // only grad_offset / grad_mask.
-  GxBin tl;
-  if (gx != nullptr && g.channels % kWave == 0) {
+  const T *dc = static_cast<const T *>(dcol), *of = static_cast<const T *>(off);
+  const T *mk = static_cast<const T *>(msk), *xim = static_cast<const T *>(im);
+  // grad_offset / grad_mask through the 16-byte kernel where rows are 16-byte aligned and
+  // the image fits the 31-bit buffer offsets; grad_x then goes separately.
+  constexpr int VEC = 16 / sizeof(T);
+  const int64_t im_bytes = (int64_t)g.batch * g.height * g.width * g.channels * sizeof(T);
+  const bool vec = goff != nullptr && (sizeof(T) == 2 || sizeof(T) == 4) && g.channels % VEC == 0 &&
+                   im_bytes < ((int64_t)1 << 31) && reinterpret_cast<uintptr_t>(dcol) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(im) % 16 == 0;
+  if (gx != nullptr) {
+    // grad_x through the binned kernel where it applies, else through the per-sample
+    // kernel (alone when the 16-byte kernel takes the coordinates).
+    GxBin tl;
     const int cpl = g.channels % (4 * kWave) == 0 ? 4 : (g.channels % (2 * kWave) == 0 ? 2 : 1);
-    if (gx_bin_plan(g, cpl, tl)) {
+    if (g.channels % kWave == 0 && gx_bin_plan(g, cpl, tl)) {
       const dim3 bgrid((unsigned)(tl.per_xcd * 8));
-      const T *dc = static_cast<const T *>(dcol), *of = static_cast<const T *>(off);
-      const T *mk = static_cast<const T *>(msk);
       if (cpl == 4)
         hipLaunchKernelGGL((col2im_nhwc_gx_bin_kernel<T, FY, 4>), bgrid, dim3(kGbThreads), 0, stream, dc, of, mk, g, tl, gx);
       else if (cpl == 2)
         hipLaunchKernelGGL((col2im_nhwc_gx_bin_kernel<T, FY, 2>), bgrid, dim3(kGbThreads), 0, stream, dc, of, mk, g, tl, gx);
       else
         hipLaunchKernelGGL((col2im_nhwc_gx_bin_kernel<T, FY, 1>), bgrid, dim3(kGbThreads), 0, stream, dc, of, mk, g, tl, gx);
-      const hipError_t e = hipGetLastError();
-      if (e != hipSuccess) return e;
       gx = nullptr;
-      if (goff == nullptr) return hipSuccess;
+    } else if (vec || goff == nullptr) {
+      hipLaunchKernelGGL((col2im_nhwc_kernel<T, FY>), grid, dim3(kBlock), 0, stream, dc, xim,
+                         of, mk, g, lpp_log2, gx, (float *)nullptr, (float *)nullptr);
+      gx = nullptr;
     }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess || goff == nullptr) return e;
   }
-  hipLaunchKernelGGL((col2im_nhwc_kernel<T, FY>), grid, dim3(kBlock), 0, stream,
-                     static_cast<const T *>(dcol), static_cast<const T *>(im),
-                     static_cast<const T *>(off), static_cast<const T *>(msk), g, lpp_log2,
-                     gx, goff, gmask);
+  if (vec) {
+    int vl2 = 0;
+    while (vl2 < 6 && (1 << vl2) * VEC < g.channels) ++vl2;
+    const dim3 vgrid((unsigned)(((pairs << vl2) + kBlock - 1) / kBlock), g.batch);
+    hipLaunchKernelGGL((col2im_coord_nhwc_vec_kernel<T, FY>), vgrid, dim3(kBlock), 0, stream, dc,
+                       xim, of, mk, g, vl2, (uint32_t)im_bytes, goff, gmask);
+  } else {
+    hipLaunchKernelGGL((col2im_nhwc_kernel<T, FY>), grid, dim3(kBlock), 0, stream, dc, xim, of,
+                       mk, g, lpp_log2, gx, goff, gmask);
+  }
   return hipGetLastError();
 }
 
