@@ -342,7 +342,7 @@ __global__ void __launch_bounds__(kBlock) col2im_coord_nhwc_vec_kernel(
 // not per channel). Same per-corner semantics as col2im_nhwc_kernel: finite coordinates
 // only, each corner checked against the image.
 // ---------------------------------------------------------------------------
-constexpr int kGbThreads = 256;
+constexpr int kGbThreads = 512;
 constexpr int kGbMargin = 8;
 constexpr int kGbMaxPos = 1024;                               // footprint bins
 constexpr int kGbMaxPairs = 2304;                             // pairs per tile (4 per sample)
@@ -351,7 +351,7 @@ constexpr int kGbSPT = (kGbMaxPairs / 4 + kGbThreads - 1) / kGbThreads;  // samp
 struct GbPair {
   uint32_t row;  // dcol row (m * T + t)
   float w;       // bilinear weight times the modulation
-  int tgt;       // target pixel y * W + x in the image (used by the far bin)
+  int tgt;       // near pairs: bin; far pairs: target pixel y * W + x
 };
 
 struct GxBin {
@@ -359,15 +359,37 @@ struct GxBin {
   int rh, rw;        // footprint rows / columns
   int tiles_x, ntile, chunks;
   int per_xcd;       // items per XCD (XCD-contiguous item ranges)
+  uint32_t dcol_bytes;  // bytes of dcol (the buffer range of the pair loads)
 };
+
+// One pair's CPL channels through the buffer path: lane offset in a VGPR, the pair's
+// byte offset in an SGPR.
+template <typename T, int N>
+__device__ __forceinline__ Vec<T, N> buffer_load_vec_s(__amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                                       uint32_t soff) {
+  constexpr int bytes = sizeof(T) * N;
+  if constexpr (bytes == 16) {
+    typedef int i4 __attribute__((ext_vector_type(4)));
+    return __builtin_bit_cast(Vec<T, N>, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+  } else if constexpr (bytes == 8) {
+    typedef int i2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(Vec<T, N>, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+  } else if constexpr (bytes == 4) {
+    return __builtin_bit_cast(Vec<T, N>, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+  } else {
+    static_assert(bytes == 2, "unsupported vector width");
+    return __builtin_bit_cast(Vec<T, N>, __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0));
+  }
+}
 
 template <typename T, bool FUSED_Y, int CPL>
 __global__ void __launch_bounds__(kGbThreads) col2im_nhwc_gx_bin_kernel(
     const T *__restrict__ dcol, const T *__restrict__ offset, const T *__restrict__ mask,
     const DcnGeom g, const GxBin tl, float *__restrict__ gx) {
-  __shared__ int bin_at[kGbMaxPos + 2];  // counts, then exclusive bin starts
+  __shared__ int bin_at[kGbMaxPos + kGbThreads / kWave + 2];  // counts, then bin starts
   __shared__ int wsum[kGbThreads / kWave];
   __shared__ GbPair list[kGbMaxPairs];
+  __shared__ float xpose[kGbThreads / kWave][kWave * CPL];
   const int T_ = g.kernel_h * g.kernel_w;
   const int HoWo = g.height_col * g.width_col;
   const int C = g.channels;
@@ -381,8 +403,14 @@ __global__ void __launch_bounds__(kGbThreads) col2im_nhwc_gx_bin_kernel(
   const int oh0 = ty * tl.th, ow0 = tx * tl.tw;
   const int fy0 = oh0 * g.stride_h - g.pad_h - kGbMargin;
   const int fx0 = ow0 * g.stride_w - g.pad_w - kGbMargin;
+  // Footprint position p goes to bin (p % 8) * P8 + p / 8, so that wave w's bins (the
+  // positions p = w mod 8) are contiguous in the sorted list; bin nnb takes the corners
+  // beyond the footprint.
+  constexpr int kNW = kGbThreads / kWave;
   const int npos = tl.rh * tl.rw;
-  const int nbins = npos + 1;  // bin npos: corners beyond the footprint
+  const int P8 = (npos + kNW - 1) / kNW;
+  const int nnb = P8 * kNW;
+  const int nbins = nnb + 1;
   const int tid = threadIdx.x;
   for (int i = tid; i < nbins + 1; i += kGbThreads) bin_at[i] = 0;
   __syncthreads();
@@ -429,9 +457,11 @@ __global__ void __launch_bounds__(kGbThreads) col2im_nhwc_gx_bin_kernel(
       const bool ok = fin && yy >= 0 && yy < g.height && xx >= 0 && xx < g.width;
       const int ry = yy - fy0, rx = xx - fx0;
       const bool in = (unsigned)ry < (unsigned)tl.rh && (unsigned)rx < (unsigned)tl.rw;
-      pbin[k][q] = ok ? (in ? ry * tl.rw + rx : npos) : -1;
+      const int pos = ry * tl.rw + rx;
+      const int nb = (pos % kNW) * P8 + pos / kNW;
+      pbin[k][q] = ok ? (in ? nb : nnb) : -1;
       pw[k][q] = ((q >> 1) ? lh : hh) * ((q & 1) ? lw : hw) * mk;
-      ptgt[k][q] = yy * g.width + xx;
+      ptgt[k][q] = in ? nb : yy * g.width + xx;
       prank[k][q] = ok ? atomicAdd(&bin_at[pbin[k][q]], 1) : 0;
     }
   }
@@ -473,52 +503,105 @@ __global__ void __launch_bounds__(kGbThreads) col2im_nhwc_gx_bin_kernel(
       if (pbin[k][q] >= 0) list[bin_at[pbin[k][q]] + prank[k][q]] = GbPair{prow[k], pw[k][q], ptgt[k][q]};
   __syncthreads();
 
-  // 3. Per-bin sums, one wave per bin.
+  // 3. Sums per bin. Wave w streams through the pairs of its bins (positions p = w mod 8
+  // in row order: the waves sweep the footprint together, so the four corner reads of a
+  // sample's dcol row, a footprint row apart, stay close in time and hit L2) in groups of
+  // kG pairs, one list entry per lane; each pair's dcol offset, weight and bin are then
+  // taken into scalar registers (readlane), so a pair costs one buffer load (scalar
+  // offset) and CPL FMAs. Lane l holds the CPL consecutive channels at l*CPL of the
+  // workgroup's 64*CPL. When the bin changes, the finished sum goes through the wave's
+  // LDS slot so that each grad_x atomic instruction adds 64 consecutive floats (fp32
+  // atomics are issued per cache line).
   const int lane = tid & (kWave - 1), wave = tid / kWave;
   const int64_t img = (int64_t)b * g.height * g.width;
-  const T *dc = dcol + chunk * (kWave * CPL) + lane;
-  float *gxc = gx + chunk * (kWave * CPL) + lane;
-  for (int p = wave; p < npos; p += kGbThreads / kWave) {
-    const int beg = bin_at[p], end = bin_at[p + 1];
-    if (beg == end) continue;
+  const int cbase = chunk * (kWave * CPL);
+  float *gxc = gx + cbase + lane;
+  float *xp = xpose[wave];
+  const int lo = bin_at[wave * P8], hi = bin_at[(wave + 1) * P8];
+  if (lo < hi) {
+    auto flush = [&](int bin, const float *acc) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) xp[lane * CPL + c] = acc[c];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const int pos = (bin % P8) * kNW + bin / P8;
+      const int y = fy0 + pos / tl.rw, x = fx0 + pos % tl.rw;
+      float *dst = gxc + (img + (int64_t)y * g.width + x) * C;
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) unsafeAtomicAdd(dst + c * kWave, xp[c * kWave + lane]);
+    };
+    const __amdgpu_buffer_rsrc_t rdc = make_rsrc(dcol + cbase, tl.dcol_bytes - (uint32_t)(cbase * sizeof(T)));
+    const uint32_t vlane = (uint32_t)(lane * CPL * sizeof(T));
+    const uint32_t row_bytes = (uint32_t)(C * sizeof(T));
+    constexpr int kG = sizeof(T) * CPL <= 8 ? 16 : 8;  // pairs per group
+    // Lanes u < kG (and their copies every kG lanes) hold the entries of the group at k0.
+    auto entries = [&](int k0) { return list[min(k0 + (lane & (kG - 1)), hi - 1)]; };
+    auto issue = [&](const GbPair &e, Vec<T, CPL> *v) {
+      const uint32_t off = e.row * row_bytes;
+#pragma unroll
+      for (int u = 0; u < kG; ++u)
+        v[u] = buffer_load_vec_s<T, CPL>(rdc, vlane, (uint32_t)__builtin_amdgcn_readlane((int)off, u));
+    };
+    int cur = __builtin_amdgcn_readfirstlane(list[lo].tgt);
     float acc[CPL];
 #pragma unroll
     for (int c = 0; c < CPL; ++c) acc[c] = 0.f;
-    for (int k = beg; k < end; k += 4) {
-      GbPair e[4];
-      float v[4][CPL];
+    auto consume = [&](int k0, const GbPair &e, const Vec<T, CPL> *v) {
+      const int ew = __builtin_bit_cast(int, e.w);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) e[u] = list[min(k + u, end - 1)];
+      for (int u = 0; u < kG; ++u) {
+        if (k0 + u < hi) {
+          const int t = __builtin_amdgcn_readlane(e.tgt, u);
+          if (t != cur) {
+            flush(cur, acc);
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
+            for (int c = 0; c < CPL; ++c) acc[c] = 0.f;
+            cur = t;
+          }
+          const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(ew, u));
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) v[u][c] = (float)dc[(int64_t)e[u].row * C + c * kWave];
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-#pragma unroll
-        for (int c = 0; c < CPL; ++c) acc[c] += (k + u < end) ? e[u].w * v[u][c] : 0.f;
+          for (int c = 0; c < CPL; ++c) acc[c] += w * (float)v[u].v[c];
+        }
+      }
+    };
+    // Two value buffers in turn (no register copies of loaded values, which would wait
+    // for the loads): the group after next is in flight while a group is summed.
+    Vec<T, CPL> va[kG], vb[kG];
+    GbPair ea = entries(lo);
+    issue(ea, va);
+    for (int k0 = lo; k0 < hi; k0 += 2 * kG) {
+      const GbPair eb = entries(k0 + kG);
+      issue(eb, vb);
+      consume(k0, ea, va);
+      ea = entries(k0 + 2 * kG);
+      issue(ea, va);
+      consume(k0 + kG, eb, vb);
     }
-    const int y = fy0 + p / tl.rw, x = fx0 + p % tl.rw;
-    float *dst = gxc + (img + (int64_t)y * g.width + x) * C;
-#pragma unroll
-    for (int c = 0; c < CPL; ++c) unsafeAtomicAdd(dst + c * kWave, acc[c]);
+    flush(cur, acc);
   }
-  // Far bin: pairs spread over the waves, one pair at a time.
-  for (int k = bin_at[npos] + wave; k < bin_at[nbins]; k += kGbThreads / kWave) {
+  // Far bin: pairs spread over the waves, one pair at a time (lane l: channels l + 64c).
+  const T *dcs = dcol + cbase + lane;
+  for (int k = bin_at[nnb] + wave; k < bin_at[nbins]; k += kNW) {
     const GbPair e = list[k];
     float *dst = gxc + (img + e.tgt) * C;
 #pragma unroll
     for (int c = 0; c < CPL; ++c)
-      unsafeAtomicAdd(dst + c * kWave, e.w * (float)dc[(int64_t)e.row * C + c * kWave]);
+      unsafeAtomicAdd(dst + c * kWave, e.w * (float)dcs[(int64_t)e.row * C + c * kWave]);
   }
 }
 
 // Tile plan for the binned grad_x kernel; false when C is not a multiple of 64 or a tile
 // of the smallest size does not fit the LDS bins / pair list.
-bool gx_bin_plan(const DcnGeom &g, int cpl, GxBin &tl) {
+bool gx_bin_plan(const DcnGeom &g, int cpl, int elem_bytes, GxBin &tl) {
   const int T_ = g.kernel_h * g.kernel_w;
   if (g.deformable_group != 1 || g.channels <= 0 || g.channels % (kWave * cpl) != 0) return false;
-  if ((int64_t)g.batch * g.height_col * g.width_col * T_ >= (int64_t)1 << 31) return false;
+  const int64_t dcol_bytes = (int64_t)g.batch * g.height_col * g.width_col * T_ * g.channels * elem_bytes;
+  if (dcol_bytes >= ((int64_t)1 << 32)) return false;  // 32-bit buffer offsets
+  tl.dcol_bytes = (uint32_t)dcol_bytes;
   int th = 8, tw = 8;
   auto extent = [&](int t, int s, int k, int d) {
     return (t - 1) * s + (k - 1) * d + 2 + 2 * kGbMargin;
@@ -568,7 +651,8 @@ hipError_t launch_t(const DcnGeom &g, const void *dcol, const void *im, const vo
     // kernel (alone when the 16-byte kernel takes the coordinates).
     GxBin tl;
     const int cpl = g.channels % (4 * kWave) == 0 ? 4 : (g.channels % (2 * kWave) == 0 ? 2 : 1);
-    if (g.channels % kWave == 0 && gx_bin_plan(g, cpl, tl)) {
+    if (g.channels % kWave == 0 && reinterpret_cast<uintptr_t>(dcol) % 16 == 0 &&
+        gx_bin_plan(g, cpl, (int)sizeof(T), tl)) {
       const dim3 bgrid((unsigned)(tl.per_xcd * 8));
       if (cpl == 4)
         hipLaunchKernelGGL((col2im_nhwc_gx_bin_kernel<T, FY, 4>), bgrid, dim3(kGbThreads), 0, stream, dc, of, mk, g, tl, gx);
