@@ -23,6 +23,7 @@
 #include "bevk_launch.h"
 
 #include <hip/amd_detail/amd_hip_unsafe_atomics.h>
+#include <type_traits>
 
 namespace bevk {
 namespace {
@@ -237,8 +238,8 @@ hipError_t launch_nchw_t(const DcnGeom &g, const void *col, const void *im, cons
 // load and four corner loads move 16 bytes per lane; LPP = min(64, next power of two >=
 // C / VEC), two pairs share a wave when C*sizeof(T) is 512 bytes. Corners outside the
 // image read zeros through the buffer path (their offset is set past the end of the
-// image), so there are no branches around the loads. Same arithmetic per channel as
-// col2im_nhwc_kernel; the channel sums meet in a shuffle butterfly.
+// image), so there are no branches around the loads. The gradients are formed from the
+// four corner dot products once per (pixel, tap) after a shuffle butterfly.
 // ---------------------------------------------------------------------------
 template <typename T, bool FUSED_Y>
 __global__ void __launch_bounds__(kBlock) col2im_coord_nhwc_vec_kernel(
@@ -292,7 +293,10 @@ __global__ void __launch_bounds__(kBlock) col2im_coord_nhwc_vec_kernel(
   const float w1 = hh * hw, w2 = hh * lw, w3 = lh * hw, w4 = lh * lw;
   const __amdgpu_buffer_rsrc_t rim = make_rsrc(im, im_bytes);
   const T *drow = dcol + (m * T_ + t) * C;
-  float ah = 0.f, aw = 0.f, am = 0.f;
+  // The three gradients are fixed combinations of the corner dot products
+  // S_k = sum_c dcol[c] * x_k[c]; the lanes accumulate S_1..S_4 (two channels per
+  // v_dot2 for the 16-bit types: exact products, fp32 sums) and lane 0 combines them.
+  float s1 = 0.f, s2 = 0.f, s3 = 0.f, s4 = 0.f;
   if (live) {
     for (int c = li * VEC; c < C; c += LPP * VEC) {
       const Vec<T, VEC> dv = load_vec<T, VEC>(drow + c);
@@ -301,25 +305,68 @@ __global__ void __launch_bounds__(kBlock) col2im_coord_nhwc_vec_kernel(
       const Vec<T, VEC> v2 = buffer_load_vec<T, VEC>(rim, o2 + cb);
       const Vec<T, VEC> v3 = buffer_load_vec<T, VEC>(rim, o3 + cb);
       const Vec<T, VEC> v4 = buffer_load_vec<T, VEC>(rim, o4 + cb);
+      if constexpr (sizeof(T) == 2) {
+        using P2 = T __attribute__((ext_vector_type(2)));
+        struct Pairs { P2 p[VEC / 2]; };
+        const Pairs d = __builtin_bit_cast(Pairs, dv), p1 = __builtin_bit_cast(Pairs, v1);
+        const Pairs p2 = __builtin_bit_cast(Pairs, v2), p3 = __builtin_bit_cast(Pairs, v3);
+        const Pairs p4 = __builtin_bit_cast(Pairs, v4);
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        const float dc = (float)dv.v[e], ds = dc * mk;
-        const float x1 = (float)v1.v[e], x2 = (float)v2.v[e];
-        const float x3 = (float)v3.v[e], x4 = (float)v4.v[e];
-        ah += ds * (-hw * x1 - lw * x2 + hw * x3 + lw * x4);
-        aw += ds * (-hh * x1 + hh * x2 - lh * x3 + lh * x4);
-        am += dc * (w1 * x1 + w2 * x2 + w3 * x3 + w4 * x4);
+        for (int e = 0; e < VEC / 2; ++e) {
+          if constexpr (std::is_same_v<T, f16>) {
+            s1 = __builtin_amdgcn_fdot2(d.p[e], p1.p[e], s1, false);
+            s2 = __builtin_amdgcn_fdot2(d.p[e], p2.p[e], s2, false);
+            s3 = __builtin_amdgcn_fdot2(d.p[e], p3.p[e], s3, false);
+            s4 = __builtin_amdgcn_fdot2(d.p[e], p4.p[e], s4, false);
+          } else {
+            s1 = __builtin_amdgcn_fdot2_f32_bf16(d.p[e], p1.p[e], s1, false);
+            s2 = __builtin_amdgcn_fdot2_f32_bf16(d.p[e], p2.p[e], s2, false);
+            s3 = __builtin_amdgcn_fdot2_f32_bf16(d.p[e], p3.p[e], s3, false);
+            s4 = __builtin_amdgcn_fdot2_f32_bf16(d.p[e], p4.p[e], s4, false);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const float dc = (float)dv.v[e];
+          s1 = fmaf(dc, (float)v1.v[e], s1);
+          s2 = fmaf(dc, (float)v2.v[e], s2);
+          s3 = fmaf(dc, (float)v3.v[e], s3);
+          s4 = fmaf(dc, (float)v4.v[e], s4);
+        }
       }
     }
   }
-  for (int s = 1; s < LPP; s <<= 1) {
-    ah += __shfl_xor(ah, s);
-    aw += __shfl_xor(aw, s);
-    am += __shfl_xor(am, s);
+  if (LPP >= 4) {
+    // Packed reduction over the LPP lanes: the lower half keeps (S1, S2) and the upper
+    // half (S3, S4), then each quarter keeps one of them and sums it over its lanes; lane
+    // 0 reads the other three totals (log2(LPP) + 4 shuffles instead of 4 log2(LPP)).
+    const int hf = LPP >> 1, qt = LPP >> 2;
+    const bool up = li & hf;
+    float a = up ? s3 : s1, c = up ? s4 : s2;
+    a += __shfl_xor(up ? s1 : s3, hf, kWave);
+    c += __shfl_xor(up ? s2 : s4, hf, kWave);
+    const bool up2 = li & qt;
+    float v = up2 ? c : a;
+    v += __shfl_xor(up2 ? a : c, qt, kWave);
+    for (int st = qt >> 1; st >= 1; st >>= 1) v += __shfl_xor(v, st, kWave);
+    const int base = (threadIdx.x & (kWave - 1)) & ~(LPP - 1);
+    s1 = v;
+    s2 = __shfl(v, base + qt, kWave);
+    s3 = __shfl(v, base + hf, kWave);
+    s4 = __shfl(v, base + hf + qt, kWave);
+  } else {
+    for (int st = 1; st < LPP; st <<= 1) {
+      s1 += __shfl_xor(s1, st, kWave);
+      s2 += __shfl_xor(s2, st, kWave);
+      s3 += __shfl_xor(s3, st, kWave);
+      s4 += __shfl_xor(s4, st, kWave);
+    }
   }
   if (live && li == 0) {
-    goff[m * 2 * T_ + 2 * t] = ah;
-    goff[m * 2 * T_ + 2 * t + 1] = aw;
+    goff[m * 2 * T_ + 2 * t] = mk * (hw * (s3 - s1) + lw * (s4 - s2));
+    goff[m * 2 * T_ + 2 * t + 1] = mk * (hh * (s2 - s1) + lh * (s4 - s3));
+    const float am = w1 * s1 + w2 * s2 + w3 * s3 + w4 * s4;
     gmask[m * T_ + t] = FUSED_Y ? am * mk * (1.f - mk) : am;
   }
 }
