@@ -8,6 +8,9 @@
 
 namespace bevk {
 
+// Compute units of the current device (cached per device; 0 when the query fails).
+int device_cus();
+
 struct MsdaArgs {
   const void *value;
   const int64_t *spatial_shapes;

@@ -38,7 +38,32 @@ struct BwdParams {
   int64_t go_sb, go_sq, go_sh, go_sc;  // grad_output strides, elements
   int64_t units;                       // batch * num_query * num_heads
   int S, NH, D, NL, NQ, NP, log2_g;
+  int gv_mode;                         // grad_value adds: kGvAll, or kGvFar after the owner pass
 };
+
+constexpr int kGvAll = 0;  // every sample adds to grad_value
+constexpr int kGvFar = 1;  // only samples the owner pass leaves out (not near their query)
+
+// Sampling coordinates of a sample, as fused multiply-adds so that every kernel that
+// classifies samples gets the same bits.
+template <typename A>
+__device__ __forceinline__ void sample_coords(A lx, A ly, int Hl, int Wl, A &him, A &wim) {
+  him = fma(ly, (A)Hl, (A)-0.5);
+  wim = fma(lx, (A)Wl, (A)-0.5);
+}
+
+// One-level grids whose queries are the grid cells (q = y * W + x): a sample is "near"
+// when all four of its corners lie within kOwnMargin cells of its query's cell. The
+// owner pass adds near samples to grad_value without atomics; the others are added by
+// msda_col2im_kernel in kGvFar mode.
+constexpr int kOwnMargin = 6;
+__device__ __forceinline__ bool near_cell(int hl, int wl, int qy, int qx) {
+  return hl >= qy - kOwnMargin && hl + 1 <= qy + kOwnMargin && wl >= qx - kOwnMargin &&
+         wl + 1 <= qx + kOwnMargin;
+}
+__device__ __forceinline__ bool near_query(int hl, int wl, int q, int Wl) {
+  return near_cell(hl, wl, q / Wl, q - (q / Wl) * Wl);
+}
 
 // T: input dtype; A: arithmetic / grad_value type.
 template <typename T, typename A>
@@ -78,11 +103,13 @@ __global__ void __launch_bounds__(kBlock) msda_col2im_kernel(
     for (int pt = 0; pt < p.NP; ++pt) {
       const int s = l * p.NP + pt;
       const A lx = (A)lp[2 * s], ly = (A)lp[2 * s + 1], a = (A)ap[s];
-      const A him = ly * (A)Hl - (A)0.5, wim = lx * (A)Wl - (A)0.5;
+      A him, wim;
+      sample_coords<A>(lx, ly, Hl, Wl, him, wim);
       A gh = 0, gw = 0, ga = 0;
       if (him > (A)-1 && wim > (A)-1 && him < (A)Hl && wim < (A)Wl) {
         const A fh = floor(him), fw = floor(wim);
         const int hl = (int)fh, wl = (int)fw;
+        const bool add = p.gv_mode == kGvAll || !near_query(hl, wl, q, Wl);
         const A lh = him - fh, lw = wim - fw, hh = (A)1 - lh, hw = (A)1 - lw;
         const A w1 = hh * hw, w2 = hh * lw, w3 = lh * hw, w4 = lh * lw;
         const bool c1 = hl >= 0 && wl >= 0, c2 = hl >= 0 && wl + 1 <= Wl - 1;
@@ -96,7 +123,7 @@ __global__ void __launch_bounds__(kBlock) msda_col2im_kernel(
           const A v1 = c1 ? (A)vb[o1 + c] : (A)0, v2 = c2 ? (A)vb[o2 + c] : (A)0;
           const A v3 = c3 ? (A)vb[o3 + c] : (A)0, v4 = c4 ? (A)vb[o4 + c] : (A)0;
           const A ta = top * a;
-          if (live) {
+          if (live && add) {
             if (c1) atomic_acc(gvb + o1 + c, w1 * ta);
             if (c2) atomic_acc(gvb + o2 + c, w2 * ta);
             if (c3) atomic_acc(gvb + o3 + c, w3 * ta);
@@ -125,6 +152,326 @@ __global__ void __launch_bounds__(kBlock) msda_col2im_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// grad_value without atomics for one-level grids whose queries are the grid cells
+// (BEVFormer temporal self-attention: q = y * W + x, D = 32, P <= 4). A persistent
+// workgroup owns kOwnT x kOwnT positions of one (batch, head) slice at a time and writes
+// their grad_value rows once, with plain stores:
+//   1. the candidate queries (cells within kOwnMargin of the tile) have their locations
+//      and attention weights loaded, all in flight together; every candidate sample that
+//      is near its query (all corners within kOwnMargin cells) and in the window
+//      (-1, H) x (-1, W) counts one pair for each of its corners inside the tile and the
+//      image (integer LDS atomic, whose result is the pair's rank in its position);
+//   2. a scan of the counts gives each position's range, and each corner kept from step 1
+//      (position, rank) stores its pair (query, bilinear weight x attention) there;
+//   3. half-wave r (32 lanes, one channel each) owns tile row r: for each position it
+//      sums weight x grad_output row of the pair's query over the position's pairs (rows
+//      read from L2, 8 in flight) and stores it.
+// A tile with more than kOwnCap pairs zeroes its rows and adds its pairs with atomics.
+// Every near sample's corner is found by exactly one owner (its query lies within
+// kOwnMargin of the corner, so among that tile's candidates); msda_grid_coord_kernel then
+// adds the remaining samples with atomics.
+// ---------------------------------------------------------------------------
+constexpr int kOwnT = 8;
+constexpr int kOwnThreads = 256;
+constexpr int kOwnSide = kOwnT + 2 * kOwnMargin;              // candidate query side
+constexpr int kOwnCand = kOwnSide * kOwnSide;
+constexpr int kOwnMaxP = 4;                                   // points per query
+// Pairs kept in LDS per tile: a tile of TSA-like data holds about 16 per position (4
+// points x 4 corners of ~one query per cell); a tile beyond this adds its pairs with
+// atomics instead (see the overflow branch).
+constexpr int kOwnCap = 2560;
+constexpr int kOwnBins = kOwnT * kOwnT;
+static_assert(kOwnBins == kWave, "one wave scans the position counts");
+static_assert(kOwnCand < 65536 && kOwnCap < 65536, "candidate index and rank in 16 bits");
+
+struct OwnParams {
+  const void *loc, *attn, *grad_out;
+  float *gv;  // grad_value (fp32) or the fp32 workspace of the 16-bit types
+  const int64_t *shapes;
+  int64_t go_sb, go_sq, go_sh, go_sc;
+  int B, NH, NQ, NP, S;
+  int blocks_per_xcd;
+};
+
+template <typename T, int NP>
+__global__ void __launch_bounds__(kOwnThreads) msda_gv_owner_kernel(const OwnParams p) {
+  constexpr int D = 32;
+  constexpr int kIter = (kOwnCand * NP + kOwnThreads - 1) / kOwnThreads;
+  __shared__ int bin_at[kOwnBins + 1];   // counts, then each position's first pair
+  __shared__ int lq[kOwnCap];      // pair: query
+  __shared__ float lw[kOwnCap];    // pair: bilinear weight x attention
+  const int H = (int)p.shapes[0], W = (int)p.shapes[1];
+  const int tiles_x = (W + kOwnT - 1) / kOwnT;
+  const int ntile = tiles_x * ((H + kOwnT - 1) / kOwnT);
+  const int nitems = p.B * p.NH * ntile;
+  const int xcd = blockIdx.x & 7;
+  const int per = (nitems + 7) / 8;
+  const int i_end = min(nitems, (xcd + 1) * per);
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave, half = (tid & (kWave - 1)) >> 5, ch = tid & 31;
+  const T *loc = static_cast<const T *>(p.loc);
+  const T *attn = static_cast<const T *>(p.attn);
+  const T *gout = static_cast<const T *>(p.grad_out);
+  for (int item = xcd * per + (blockIdx.x >> 3); item < i_end; item += p.blocks_per_xcd) {
+    const int tile = item % ntile;
+    const int bh = item / ntile;
+    const int h = bh % p.NH, b = bh / p.NH;
+    const int ty = tile / tiles_x, tx = tile - ty * tiles_x;
+    const int y0 = ty * kOwnT, x0 = tx * kOwnT;
+    const int cy0 = max(0, y0 - kOwnMargin), cy1 = min(H, y0 + kOwnT + kOwnMargin);
+    const int cx0 = max(0, x0 - kOwnMargin), cx1 = min(W, x0 + kOwnT + kOwnMargin);
+    const int cw = cx1 - cx0;
+    const int ncand = (cy1 - cy0) * cw;
+    const int nsamp = ncand * NP;
+    const float inv_cw = 1.f / (float)cw;
+    // Candidate c = row * cw + col of the (cy1 - cy0) x cw block (c < 2^10: the rounded
+    // float quotient is exact).
+    auto cand_row = [&](int c) { return (int)(((float)c + 0.5f) * inv_cw); };
+    // Loads of the item, all in flight together: the thread's candidate samples
+    // i = tid + k * kOwnThreads (locations, attention).
+    float slx[kIter], sly[kIter], sa[kIter];
+    int scy[kIter], scx[kIter];
+#pragma unroll
+    for (int k = 0; k < kIter; ++k) {
+      const int i = min(tid + k * kOwnThreads, nsamp - 1);
+      const int c = i / NP, pt = i - (i / NP) * NP;
+      const int cr = cand_row(c);
+      scy[k] = cy0 + cr;
+      scx[k] = cx0 + c - cr * cw;
+      const int64_t unit = ((int64_t)b * p.NQ + scy[k] * W + scx[k]) * p.NH + h;
+      slx[k] = (float)loc[(unit * NP + pt) * 2];
+      sly[k] = (float)loc[(unit * NP + pt) * 2 + 1];
+      sa[k] = (float)attn[unit * NP + pt];
+    }
+    __syncthreads();  // the previous item's readers are done
+    for (int i = tid; i < kOwnBins + 1; i += kOwnThreads) bin_at[i] = 0;
+    __syncthreads();
+    // Each near sample's corners inside the tile and the image: position and rank in the
+    // position (integer LDS atomic), kept for the placement below.
+    int pslot[kIter][4];
+    float pwt[kIter][4];
+#pragma unroll
+    for (int k = 0; k < kIter; ++k) {
+#pragma unroll
+      for (int cn = 0; cn < 4; ++cn) pslot[k][cn] = -1;
+      if (tid + k * kOwnThreads >= nsamp) continue;
+      float him, wim;
+      sample_coords<float>(slx[k], sly[k], H, W, him, wim);
+      if (!(him > -1.f && wim > -1.f && him < (float)H && wim < (float)W)) continue;
+      const float fh = floorf(him), fw = floorf(wim);
+      const int hl = (int)fh, wl = (int)fw;
+      if (!near_cell(hl, wl, scy[k], scx[k])) continue;
+      const float lh = him - fh, lw = wim - fw, hh = 1.f - lh, hw = 1.f - lw;
+#pragma unroll
+      for (int cn = 0; cn < 4; ++cn) {
+        const int yy = hl + (cn >> 1), xx = wl + (cn & 1);
+        const int ry = yy - y0, rx = xx - x0;
+        if (yy < 0 || yy >= H || xx < 0 || xx >= W || (unsigned)ry >= (unsigned)kOwnT ||
+            (unsigned)rx >= (unsigned)kOwnT)
+          continue;
+        const int bin = ry * kOwnT + rx;
+        pslot[k][cn] = (bin << 16) | atomicAdd(&bin_at[bin], 1);
+        pwt[k][cn] = ((cn >> 1) ? lh : hh) * ((cn & 1) ? lw : hw) * sa[k];
+      }
+    }
+    __syncthreads();
+    if (tid < kWave) {  // exclusive scan of the kOwnBins (= 64) counts by wave 0
+      const int c = bin_at[tid];
+      int incl = c;
+#pragma unroll
+      for (int d = 1; d < kWave; d <<= 1) {
+        const int v = __shfl_up(incl, d, kWave);
+        if (tid >= d) incl += v;
+      }
+      bin_at[tid] = incl - c;
+      if (tid == kWave - 1) bin_at[kOwnBins] = incl;
+    }
+    __syncthreads();
+    const int r = wave * 2 + half;
+    float *gvr = p.gv + ((int64_t)b * p.S + (int64_t)(y0 + r) * W + x0) * (p.NH * D) + h * D + ch;
+    const bool row_in = y0 + r < H;
+    if (bin_at[kOwnBins] > kOwnCap) {
+      // More pairs than the LDS list holds (inputs that crowd many samples into one
+      // tile): zero the tile's rows, then every pair adds its weighted grad_output row.
+#pragma unroll
+      for (int x = 0; x < kOwnT; ++x)
+        if (row_in && x0 + x < W) gvr[(int64_t)x * (p.NH * D)] = 0.f;
+      __syncthreads();
+      float *gvt = p.gv + ((int64_t)b * p.S + (int64_t)y0 * W + x0) * (p.NH * D) + h * D;
+#pragma unroll
+      for (int k = 0; k < kIter; ++k) {
+#pragma unroll
+        for (int cn = 0; cn < 4; ++cn)
+          if (pslot[k][cn] >= 0) {
+            const int bin = pslot[k][cn] >> 16;
+            float *dst = gvt + ((int64_t)(bin / kOwnT) * W + bin % kOwnT) * (p.NH * D);
+            const T *src = gout + b * p.go_sb + (int64_t)(scy[k] * W + scx[k]) * p.go_sq + h * p.go_sh;
+            for (int e = 0; e < D; ++e) unsafeAtomicAdd(dst + e, pwt[k][cn] * (float)src[e * p.go_sc]);
+          }
+      }
+      continue;
+    }
+#pragma unroll
+    for (int k = 0; k < kIter; ++k) {
+#pragma unroll
+      for (int cn = 0; cn < 4; ++cn)
+        if (pslot[k][cn] >= 0) {
+          const int slot = bin_at[pslot[k][cn] >> 16] + (pslot[k][cn] & 0xffff);
+          lq[slot] = scy[k] * W + scx[k];
+          lw[slot] = pwt[k][cn];
+        }
+    }
+    __syncthreads();
+    // Half-wave r owns tile row r, lane ch channel ch: one position after the other, the
+    // sum of weight x staged grad_output row over the position's pairs.
+    const T *gob = gout + b * p.go_sb + h * p.go_sh + ch * p.go_sc;
+    int bnd[kOwnT + 1];
+#pragma unroll
+    for (int x = 0; x <= kOwnT; ++x) bnd[x] = bin_at[r * kOwnT + x];
+#pragma unroll
+    for (int x = 0; x < kOwnT; ++x) {
+      float acc = 0.f;
+      for (int k0 = bnd[x]; k0 < bnd[x + 1]; k0 += 8) {
+        float w[8], v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int k = min(k0 + u, bnd[x + 1] - 1);
+          w[u] = lw[k];
+          v[u] = (float)gob[(int64_t)lq[k] * p.go_sq];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc += (k0 + u < bnd[x + 1]) ? w[u] * v[u] : 0.f;
+      }
+      if (row_in && x0 + x < W) gvr[(int64_t)x * (p.NH * D)] = acc;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// grad_sampling_loc / grad_attn_weight for the owner path (one level, queries = cells,
+// D = 32, P <= kOwnMaxP), plus the atomics of the samples the owner pass leaves out.
+// G = D * sizeof(T) / 16 lanes own a (b, q, head) unit, lane li holding the VEC = 16 /
+// sizeof(T) channels at li * VEC: the unit's P x 4 corner rows come in 16-byte pieces,
+// all in flight together through the buffer path (corners outside the level or samples
+// outside the window read zeros). The three outputs of a sample are fixed combinations
+// of the corner dot products S_k = sum_c top_c * v_k,c:
+//   grad_attn = sum_k w_k S_k,  grad_loc_x = W a (hh (S2 - S1) + lh (S4 - S3)),
+//   grad_loc_y = H a (hw (S3 - S1) + lw (S4 - S2)),
+// summed over the G lanes by a packed shuffle reduction.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ void __launch_bounds__(kBlock) msda_grid_coord_kernel(
+    const T *__restrict__ value, const T *__restrict__ loc, const T *__restrict__ attn,
+    const T *__restrict__ grad_out, float *__restrict__ gv, T *__restrict__ grad_loc,
+    T *__restrict__ grad_attn, BwdParams p) {
+  constexpr int D = 32;
+  constexpr int VEC = 16 / (int)sizeof(T);
+  constexpr int G = D / VEC;  // lanes per unit (8 fp32, 4 for 16-bit types)
+  constexpr uint32_t kPast = 0x80000000u;
+  const int64_t tid = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int64_t u_raw = tid / G;
+  const bool live = u_raw < p.units;
+  const int64_t unit = live ? u_raw : p.units - 1;
+  const int li = (int)(tid % G);
+  const int h = (int)(unit % p.NH);
+  const int64_t bq = unit / p.NH;
+  const int q = (int)(bq % p.NQ);
+  const int b = (int)(bq / p.NQ);
+  const int NP = p.NP, NH = p.NH;
+  const int H = (int)p.shapes[0], W = (int)p.shapes[1];
+  const int64_t row = (int64_t)NH * D;
+  const T *vb = value + ((int64_t)b * p.S + p.lsi[0]) * row;
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb, (uint32_t)((int64_t)H * W * row * sizeof(T)));
+  const uint32_t lane_off = (uint32_t)((h * D + li * VEC) * sizeof(T));
+  const T *go = grad_out + b * p.go_sb + (int64_t)q * p.go_sq + h * p.go_sh;
+  float top[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) top[e] = (float)go[(li * VEC + e) * p.go_sc];
+  float *gvb = gv + ((int64_t)b * p.S + p.lsi[0]) * row + h * D + li * VEC;
+  const T *lp = loc + unit * NP * 2;
+  const T *ap = attn + unit * NP;
+  T *glp = grad_loc + unit * NP * 2;
+  T *gap = grad_attn + unit * NP;
+
+  // Geometry and corner loads of every point first.
+  float wt[kOwnMaxP][4], lhs[kOwnMaxP], lws[kOwnMaxP], av[kOwnMaxP];
+  int hls[kOwnMaxP], wls[kOwnMaxP];
+  bool far[kOwnMaxP], okp[kOwnMaxP];
+  Vec<T, VEC> cv[kOwnMaxP][4];
+#pragma unroll
+  for (int pt = 0; pt < kOwnMaxP; ++pt) {
+    const int ps = pt < NP ? pt : 0;
+    const float lx = (float)lp[2 * ps], ly = (float)lp[2 * ps + 1];
+    av[pt] = (float)ap[ps];
+    float him, wim;
+    sample_coords<float>(lx, ly, H, W, him, wim);
+    const bool ok = pt < NP && him > -1.f && wim > -1.f && him < (float)H && wim < (float)W;
+    const float fh = ok ? floorf(him) : 0.f, fw = ok ? floorf(wim) : 0.f;
+    const int hl = (int)fh, wl = (int)fw;
+    const float lh = ok ? him - fh : 0.f, lw = ok ? wim - fw : 0.f;
+    const float hh = 1.f - lh, hw = 1.f - lw;
+    lhs[pt] = lh;
+    lws[pt] = lw;
+    hls[pt] = hl;
+    wls[pt] = wl;
+    okp[pt] = ok;
+    far[pt] = ok && !near_query(hl, wl, q, W);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int yy = hl + (k >> 1), xx = wl + (k & 1);
+      const bool in = ok && yy >= 0 && yy < H && xx >= 0 && xx < W;
+      wt[pt][k] = in ? ((k >> 1) ? lh : hh) * ((k & 1) ? lw : hw) : 0.f;
+      const uint32_t off = in ? (uint32_t)(((int64_t)yy * W + xx) * row * sizeof(T)) + lane_off : kPast;
+      cv[pt][k] = buffer_load_vec<T, VEC>(rv, off);
+    }
+  }
+#pragma unroll
+  for (int pt = 0; pt < kOwnMaxP; ++pt) {
+    if (pt < NP) {
+    float s[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      float acc = 0.f;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc = fmaf(top[e], (float)cv[pt][k].v[e], acc);
+      s[k] = acc;
+    }
+    // packed reduction of s[0..3] over the G lanes; lane 0 ends with all four sums
+    const int hf = G >> 1, qt = G >> 2;
+    const bool up = li & hf;
+    float x = up ? s[2] : s[0], y = up ? s[3] : s[1];
+    x += __shfl_xor(up ? s[0] : s[2], hf, kWave);
+    y += __shfl_xor(up ? s[1] : s[3], hf, kWave);
+    const bool up2 = li & qt;
+    float v = up2 ? y : x;
+    v += __shfl_xor(up2 ? x : y, qt, kWave);
+    for (int st = qt >> 1; st >= 1; st >>= 1) v += __shfl_xor(v, st, kWave);
+    const int base = (threadIdx.x & (kWave - 1)) & ~(G - 1);
+    const float S1 = v, S2 = __shfl(v, base + qt, kWave);
+    const float S3 = __shfl(v, base + hf, kWave), S4 = __shfl(v, base + hf + qt, kWave);
+    if (live && li == 0) {  // a sample outside the window writes zeros
+      const float lh = lhs[pt], lw = lws[pt], hh = 1.f - lh, hw = 1.f - lw, a = av[pt];
+      const bool ok = okp[pt];
+      glp[2 * pt] = (T)(ok ? (float)W * a * (hh * (S2 - S1) + lh * (S4 - S3)) : 0.f);
+      glp[2 * pt + 1] = (T)(ok ? (float)H * a * (hw * (S3 - S1) + lw * (S4 - S2)) : 0.f);
+      gap[pt] = (T)(ok ? wt[pt][0] * S1 + wt[pt][1] * S2 + wt[pt][2] * S3 + wt[pt][3] * S4 : 0.f);
+    }
+    if (live && far[pt]) {  // samples the owner pass does not take: atomics
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if (wt[pt][k] == 0.f) continue;
+        const int yy = hls[pt] + (k >> 1), xx = wls[pt] + (k & 1);
+        float *dst = gvb + ((int64_t)yy * W + xx) * row;
+        const float ta = wt[pt][k] * av[pt];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) unsafeAtomicAdd(dst + e, ta * top[e]);
+      }
+    }
+    }
+  }
+}
+
 __global__ void __launch_bounds__(kBlock) fill_zero_f32(float *__restrict__ p, int64_t n) {
   const int64_t stride = (int64_t)gridDim.x * kBlock;
   for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) p[i] = 0.f;
@@ -143,8 +490,45 @@ unsigned stream_grid(int64_t n) {
   return (unsigned)(g < 8192 ? (g > 0 ? g : 1) : 8192);
 }
 
+// One-level grid with one query per cell, D = 32, at most kOwnMaxP points: grad_value by
+// the owner pass (every element written) plus far samples' atomics.
+// (16-byte aligned value, one batch of value under 2 GiB for the 31-bit buffer offsets.)
+template <typename T>
+bool owner_path(const MsdaBwdArgs &a) {
+  return a.f.num_levels == 1 && a.f.num_query == a.f.spatial_size && a.f.channels == 32 &&
+         a.f.num_point >= 1 && a.f.num_point <= kOwnMaxP && a.f.spatial_size > 0 &&
+         reinterpret_cast<uintptr_t>(a.f.value) % 16 == 0 &&
+         (int64_t)a.f.spatial_size * a.f.num_heads * 32 * (int64_t)sizeof(T) < ((int64_t)1 << 31) &&
+         device_cus() >= 8;
+}
+
+template <typename T>
+hipError_t launch_owner(const MsdaBwdArgs &a, float *gv, hipStream_t stream) {
+  OwnParams p;
+  p.loc = a.f.sampling_loc;
+  p.attn = a.f.attn_weight;
+  p.grad_out = a.grad_output;
+  p.gv = gv;
+  p.shapes = a.f.spatial_shapes;
+  p.go_sb = a.go_stride[0]; p.go_sq = a.go_stride[1];
+  p.go_sh = a.go_stride[2]; p.go_sc = a.go_stride[3];
+  p.B = a.f.batch; p.NH = a.f.num_heads; p.NQ = a.f.num_query; p.NP = a.f.num_point;
+  p.S = a.f.spatial_size;
+  const int blocks = (device_cus() / 8) * 8 * 3;  // three workgroups per CU (VGPRs)
+  p.blocks_per_xcd = blocks / 8;
+  if (a.f.batch == 0 || a.f.num_heads == 0) return hipSuccess;
+  switch (a.f.num_point) {
+    case 1: hipLaunchKernelGGL((msda_gv_owner_kernel<T, 1>), dim3(blocks), dim3(kOwnThreads), 0, stream, p); break;
+    case 2: hipLaunchKernelGGL((msda_gv_owner_kernel<T, 2>), dim3(blocks), dim3(kOwnThreads), 0, stream, p); break;
+    case 3: hipLaunchKernelGGL((msda_gv_owner_kernel<T, 3>), dim3(blocks), dim3(kOwnThreads), 0, stream, p); break;
+    default: hipLaunchKernelGGL((msda_gv_owner_kernel<T, 4>), dim3(blocks), dim3(kOwnThreads), 0, stream, p); break;
+  }
+  return hipGetLastError();
+}
+
 template <typename T, typename A>
-hipError_t launch_t(const MsdaBwdArgs &a, A *grad_value, hipStream_t stream) {
+hipError_t launch_t(const MsdaBwdArgs &a, A *grad_value, hipStream_t stream,
+                    int gv_mode = kGvAll) {
   BwdParams p;
   p.shapes = a.f.spatial_shapes;
   p.lsi = a.f.level_start_index;
@@ -153,6 +537,7 @@ hipError_t launch_t(const MsdaBwdArgs &a, A *grad_value, hipStream_t stream) {
   p.units = (int64_t)a.f.batch * a.f.num_query * a.f.num_heads;
   p.S = a.f.spatial_size; p.NH = a.f.num_heads; p.D = a.f.channels;
   p.NL = a.f.num_levels; p.NQ = a.f.num_query; p.NP = a.f.num_point;
+  p.gv_mode = gv_mode;
   p.log2_g = 0;
   while ((1 << p.log2_g) < a.f.channels && p.log2_g < 6) ++p.log2_g;
   const int64_t threads = p.units << p.log2_g;
@@ -167,13 +552,52 @@ hipError_t launch_t(const MsdaBwdArgs &a, A *grad_value, hipStream_t stream) {
 }
 
 template <typename T>
+hipError_t launch_grid_coord(const MsdaBwdArgs &a, float *gv, hipStream_t stream) {
+  BwdParams p;
+  p.shapes = a.f.spatial_shapes;
+  p.lsi = a.f.level_start_index;
+  p.go_sb = a.go_stride[0]; p.go_sq = a.go_stride[1];
+  p.go_sh = a.go_stride[2]; p.go_sc = a.go_stride[3];
+  p.units = (int64_t)a.f.batch * a.f.num_query * a.f.num_heads;
+  p.S = a.f.spatial_size; p.NH = a.f.num_heads; p.D = a.f.channels;
+  p.NL = a.f.num_levels; p.NQ = a.f.num_query; p.NP = a.f.num_point;
+  p.gv_mode = kGvFar;
+  p.log2_g = 0;
+  constexpr int G = 32 * (int)sizeof(T) / 16;
+  const int64_t threads = p.units * G;
+  if (threads == 0) return hipSuccess;
+  hipLaunchKernelGGL((msda_grid_coord_kernel<T>), dim3((unsigned)((threads + kBlock - 1) / kBlock)),
+                     dim3(kBlock), 0, stream, static_cast<const T *>(a.f.value),
+                     static_cast<const T *>(a.f.sampling_loc), static_cast<const T *>(a.f.attn_weight),
+                     static_cast<const T *>(a.grad_output), gv, static_cast<T *>(a.grad_loc),
+                     static_cast<T *>(a.grad_attn), p);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_f32(const MsdaBwdArgs &a, hipStream_t stream) {
+  float *gv = static_cast<float *>(a.grad_value);
+  if (!owner_path<T>(a)) return launch_t<T, float>(a, gv, stream);
+  hipError_t e = launch_owner<T>(a, gv, stream);
+  if (e != hipSuccess) return e;
+  return launch_grid_coord<T>(a, gv, stream);
+}
+
+template <typename T>
 hipError_t launch_half(const MsdaBwdArgs &a, hipStream_t stream) {
   const int64_t n = (int64_t)a.f.batch * a.f.spatial_size * a.f.num_heads * a.f.channels;
   float *acc = static_cast<float *>(a.workspace);
-  hipLaunchKernelGGL(fill_zero_f32, dim3(stream_grid(n)), dim3(kBlock), 0, stream, acc, n);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  e = launch_t<T, float>(a, acc, stream);
+  hipError_t e;
+  if (owner_path<T>(a)) {  // the owner pass writes every element of the workspace
+    e = launch_owner<T>(a, acc, stream);
+    if (e != hipSuccess) return e;
+    e = launch_grid_coord<T>(a, acc, stream);
+  } else {
+    hipLaunchKernelGGL(fill_zero_f32, dim3(stream_grid(n)), dim3(kBlock), 0, stream, acc, n);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    e = launch_t<T, float>(a, acc, stream);
+  }
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL((narrow_f32<T>), dim3(stream_grid(n)), dim3(kBlock), 0, stream, acc,
                      static_cast<T *>(a.grad_value), n);
@@ -188,7 +612,7 @@ int64_t msda_backward_workspace_bytes(int dtype, int64_t value_elems) {
 
 hipError_t launch_msda_backward(int dtype, const MsdaBwdArgs &a, hipStream_t stream) {
   switch (dtype) {
-    case 0: return launch_t<float, float>(a, static_cast<float *>(a.grad_value), stream);
+    case 0: return launch_f32<float>(a, stream);
     case 1: return launch_half<f16>(a, stream);
     case 2: return launch_half<bf16>(a, stream);
     case 3: return launch_t<double, double>(a, static_cast<double *>(a.grad_value), stream);

@@ -742,20 +742,6 @@ hipError_t launch_wave_t(const MsdaArgs &a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// Compute units of the current device (cached per device).
-int device_cus() {
-  static int cus[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cus[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-      return 0;
-    cus[dev] = n;
-  }
-  return cus[dev];
-}
-
 int gcd_int(int x, int y) {
   while (y) { const int t = x % y; x = y; y = t; }
   return x;
@@ -1110,6 +1096,19 @@ hipError_t launch_msda_forward(int dtype, const MsdaArgs &a, bool force_generic,
     default:
       return hipErrorInvalidValue;
   }
+}
+
+int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return 0;
+    cus[dev] = n;
+  }
+  return cus[dev];
 }
 
 }  // namespace bevk

@@ -172,6 +172,87 @@ def test_generic_shapes(geom, dtype):
         _check3(got, ref, dtype, f"{geom} {dtype}")
 
 
+def _grid_queries(batch, H, W, heads, points, jitter_px, far_frac, seed):
+    """One level, one query per cell (q = y*W + x) sampling around its cell centre with
+    `jitter_px` pixels of Gaussian noise; a `far_frac` share of the samples is moved to a
+    random place in [-0.2, 1.2]^2 (far from its query, some outside the window)."""
+    g = torch.Generator().manual_seed(seed)
+    spatial_shapes, lsi, s = inputs.msda_meta([(H, W)])
+    value = torch.randn(batch, s, heads, 32, generator=g)
+    q = torch.arange(s)
+    ctr = torch.stack([((q % W).double() + 0.5) / W, ((q // W).double() + 0.5) / H], -1)
+    shape = (batch, s, heads, 1, points, 2)
+    loc = ctr.float().view(1, s, 1, 1, 1, 2).expand(*shape).clone()
+    loc[..., 0] += jitter_px / W * torch.randn(shape[:-1], generator=g)
+    loc[..., 1] += jitter_px / H * torch.randn(shape[:-1], generator=g)
+    far = torch.rand(shape[:-1], generator=g) < far_frac
+    wild = -0.2 + 1.4 * torch.rand(shape, generator=g)
+    loc = torch.where(far.unsqueeze(-1), wild, loc)
+    attn = torch.softmax(torch.randn(batch, s, heads, points, generator=g), -1)
+    return dict(value=value, spatial_shapes=spatial_shapes, level_start_index=lsi,
+                sampling_loc=loc, attn_weight=attn.view(batch, s, heads, 1, points))
+
+
+@pytest.mark.parametrize("geom", [
+    # batch, H, W, heads, points, jitter px, far share
+    (2, 23, 37, 2, 4, 2.0, 0.05),   # edge tiles on both axes
+    (1, 8, 8, 3, 1, 1.0, 0.0),      # one tile exactly, one point
+    (1, 9, 17, 1, 3, 3.0, 0.1),
+    (2, 40, 30, 2, 2, 4.0, 0.02),   # wide jitter: many samples beyond the owner margin
+])
+@pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
+def test_grid_queries(geom, dtype):
+    """Queries on the grid cells of a one-level map (the temporal self-attention form):
+    grad_value comes from the per-position owner pass plus atomics for the samples far
+    from their query; all three gradients are compared whole with the oracle."""
+    d = _grid_queries(*geom, seed=sum(geom[:5]))
+    go = _grad_output(d, seed=5)
+    _check3(_run(d, go, dtype), _ref(d, go, dtype), dtype, f"grid {geom} {dtype}")
+
+
+def _crowded_grid(H, W, heads, cy, cx, seed):
+    """Queries on the cells of an H x W map whose 4 samples move up to 5 cells towards
+    cell (cy, cx) (so every sample stays within the owner margin of its query): the 8 x 8
+    tile holding (cy, cx) receives several thousand corner pairs."""
+    g = torch.Generator().manual_seed(seed)
+    spatial_shapes, lsi, s = inputs.msda_meta([(H, W)])
+    value = torch.randn(1, s, heads, 32, generator=g)
+    q = torch.arange(s)
+    qy, qx = (q // W).double(), (q % W).double()
+    ty = qy + (cy - qy).clamp(-5, 5)
+    tx = qx + (cx - qx).clamp(-5, 5)
+    shape = (1, s, heads, 1, 4)
+    jy = ty.view(1, s, 1, 1, 1) + 0.5 + 0.3 * torch.randn(shape, generator=g, dtype=torch.float64)
+    jx = tx.view(1, s, 1, 1, 1) + 0.5 + 0.3 * torch.randn(shape, generator=g, dtype=torch.float64)
+    # keep every corner within 5 cells of its query (the jitter must not push it out)
+    jy = torch.minimum(torch.maximum(jy, qy.view(1, s, 1, 1, 1) - 4.4), qy.view(1, s, 1, 1, 1) + 5.4)
+    jx = torch.minimum(torch.maximum(jx, qx.view(1, s, 1, 1, 1) - 4.4), qx.view(1, s, 1, 1, 1) + 5.4)
+    loc = torch.stack([jx / W, jy / H], -1).float()
+    attn = torch.softmax(torch.randn(1, s, heads, 4, generator=g), -1)
+    d = dict(value=value, spatial_shapes=spatial_shapes, level_start_index=lsi,
+             sampling_loc=loc, attn_weight=attn.view(1, s, heads, 1, 4))
+    # corner pairs landing in the crowded tile (h_im = loc * H - 0.5, as the kernels)
+    hi = (loc[..., 1].double() * H - 0.5).floor()
+    wi = (loc[..., 0].double() * W - 0.5).floor()
+    t0y, t0x = cy // 8 * 8, cx // 8 * 8
+    n = 0
+    for dy in (0, 1):
+        for dx in (0, 1):
+            yy, xx = hi + dy, wi + dx
+            n += int(((yy >= t0y) & (yy < t0y + 8) & (xx >= t0x) & (xx < t0x + 8)).sum() // heads)
+    return d, n
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["fp32", "fp16"])
+def test_grid_queries_crowded_tile(dtype):
+    """A tile with more corner pairs than the owner pass keeps in LDS (2560) takes the
+    atomic branch; the result still matches the oracle."""
+    d, pairs = _crowded_grid(30, 28, 2, 12, 13, seed=4)
+    assert pairs > 2560, pairs
+    go = _grad_output(d, seed=6)
+    _check3(_run(d, go, dtype), _ref(d, go, dtype), dtype, f"crowded {dtype}")
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["fp32", "fp16"])
 def test_empty_queries(dtype):
     d = inputs.msda_random(2, [(3, 4)], 0, 2, 32, 2)
