@@ -155,8 +155,9 @@ __global__ void __launch_bounds__(kBlock) msda_col2im_kernel(
 // ---------------------------------------------------------------------------
 // grad_value without atomics for one-level grids whose queries are the grid cells
 // (BEVFormer temporal self-attention: q = y * W + x, D = 32, P <= 4). A persistent
-// workgroup owns kOwnT x kOwnT positions of one (batch, head) slice at a time and writes
-// their grad_value rows once, with plain stores:
+// workgroup owns kOwnT x kOwnT positions of one (batch, head) slice at a time and stores
+// their grad_value rows once, without atomics (fp32 grad_value: added to what it holds;
+// the fp32 workspace of the 16-bit types: written):
 //   1. the candidate queries (cells within kOwnMargin of the tile) have their locations
 //      and attention weights loaded, all in flight together; every candidate sample that
 //      is near its query (all corners within kOwnMargin cells) and in the window
@@ -187,7 +188,8 @@ static_assert(kOwnCand < 65536 && kOwnCap < 65536, "candidate index and rank in 
 
 struct OwnParams {
   const void *loc, *attn, *grad_out;
-  float *gv;  // grad_value (fp32) or the fp32 workspace of the 16-bit types
+  float *gv;       // grad_value (fp32) or the fp32 workspace of the 16-bit types
+  int accumulate;  // add to gv (fp32 grad_value, whose contract is accumulation) or write it
   const int64_t *shapes;
   int64_t go_sb, go_sq, go_sh, go_sc;
   int B, NH, NQ, NP, S;
@@ -293,10 +295,13 @@ __global__ void __launch_bounds__(kOwnThreads) msda_gv_owner_kernel(const OwnPar
     const bool row_in = y0 + r < H;
     if (bin_at[kOwnBins] > kOwnCap) {
       // More pairs than the LDS list holds (inputs that crowd many samples into one
-      // tile): zero the tile's rows, then every pair adds its weighted grad_output row.
+      // tile): zero the tile's rows (write mode), then every pair adds its weighted
+      // grad_output row.
+      if (!p.accumulate) {
 #pragma unroll
-      for (int x = 0; x < kOwnT; ++x)
-        if (row_in && x0 + x < W) gvr[(int64_t)x * (p.NH * D)] = 0.f;
+        for (int x = 0; x < kOwnT; ++x)
+          if (row_in && x0 + x < W) gvr[(int64_t)x * (p.NH * D)] = 0.f;
+      }
       __syncthreads();
       float *gvt = p.gv + ((int64_t)b * p.S + (int64_t)y0 * W + x0) * (p.NH * D) + h * D;
 #pragma unroll
@@ -329,6 +334,10 @@ __global__ void __launch_bounds__(kOwnThreads) msda_gv_owner_kernel(const OwnPar
     int bnd[kOwnT + 1];
 #pragma unroll
     for (int x = 0; x <= kOwnT; ++x) bnd[x] = bin_at[r * kOwnT + x];
+    float old[kOwnT];  // accumulate mode: the row's values, loaded before the sums
+#pragma unroll
+    for (int x = 0; x < kOwnT; ++x)
+      old[x] = (p.accumulate && row_in && x0 + x < W) ? gvr[(int64_t)x * (p.NH * D)] : 0.f;
 #pragma unroll
     for (int x = 0; x < kOwnT; ++x) {
       float acc = 0.f;
@@ -343,7 +352,7 @@ __global__ void __launch_bounds__(kOwnThreads) msda_gv_owner_kernel(const OwnPar
 #pragma unroll
         for (int u = 0; u < 8; ++u) acc += (k0 + u < bnd[x + 1]) ? w[u] * v[u] : 0.f;
       }
-      if (row_in && x0 + x < W) gvr[(int64_t)x * (p.NH * D)] = acc;
+      if (row_in && x0 + x < W) gvr[(int64_t)x * (p.NH * D)] = old[x] + acc;
     }
   }
 }
@@ -503,8 +512,9 @@ bool owner_path(const MsdaBwdArgs &a) {
 }
 
 template <typename T>
-hipError_t launch_owner(const MsdaBwdArgs &a, float *gv, hipStream_t stream) {
+hipError_t launch_owner(const MsdaBwdArgs &a, float *gv, bool accumulate, hipStream_t stream) {
   OwnParams p;
+  p.accumulate = accumulate ? 1 : 0;
   p.loc = a.f.sampling_loc;
   p.attn = a.f.attn_weight;
   p.grad_out = a.grad_output;
@@ -578,7 +588,7 @@ template <typename T>
 hipError_t launch_f32(const MsdaBwdArgs &a, hipStream_t stream) {
   float *gv = static_cast<float *>(a.grad_value);
   if (!owner_path<T>(a)) return launch_t<T, float>(a, gv, stream);
-  hipError_t e = launch_owner<T>(a, gv, stream);
+  hipError_t e = launch_owner<T>(a, gv, true, stream);
   if (e != hipSuccess) return e;
   return launch_grid_coord<T>(a, gv, stream);
 }
@@ -589,7 +599,7 @@ hipError_t launch_half(const MsdaBwdArgs &a, hipStream_t stream) {
   float *acc = static_cast<float *>(a.workspace);
   hipError_t e;
   if (owner_path<T>(a)) {  // the owner pass writes every element of the workspace
-    e = launch_owner<T>(a, acc, stream);
+    e = launch_owner<T>(a, acc, false, stream);
     if (e != hipSuccess) return e;
     e = launch_grid_coord<T>(a, acc, stream);
   } else {

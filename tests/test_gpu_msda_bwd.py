@@ -243,6 +243,25 @@ def _crowded_grid(H, W, heads, cy, cx, seed):
     return d, n
 
 
+def test_grid_queries_accumulate_fp32():
+    """Grid queries take the owner pass; fp32 grad_value is still added to what the caller
+    holds (here 3.0 everywhere), including in a crowded tile."""
+    import _modulated_deform_conv_ext as ext
+    for d in (_grid_queries(1, 19, 21, 2, 4, 2.0, 0.05, seed=8), _crowded_grid(30, 28, 2, 12, 13, seed=4)[0]):
+        go = _grad_output(d, seed=7)
+        dd = _dev(d, torch.float32)
+        gv = torch.full_like(dd["value"], 3.0)
+        gl = torch.empty_like(dd["sampling_loc"])
+        ga = torch.empty_like(dd["attn_weight"])
+        ext.backward(dd["value"], dd["spatial_shapes"], dd["level_start_index"],
+                     dd["sampling_loc"], dd["attn_weight"], go.to(DEV), gv, gl, ga)
+        torch.cuda.synchronize()
+        rv, rl, ra = _ref(d, go, torch.float32)
+        check(gv.cpu(), rv + 3.0, torch.float32, "grid grad_value accumulated")
+        check(gl.cpu(), rl, torch.float32, "grid grad_sampling_loc")
+        check(ga.cpu(), ra, torch.float32, "grid grad_attn_weight")
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["fp32", "fp16"])
 def test_grid_queries_crowded_tile(dtype):
     """A tile with more corner pairs than the owner pass keeps in LDS (2560) takes the
