@@ -44,10 +44,17 @@ __global__ void __launch_bounds__(kBlock) col2im_nhwc_kernel(
   // Lanes past the last pair still take part in the butterfly below; they do no work.
   const bool live = pair < HoWo * T_;
   const int pc = live ? pair : 0;
-  const int sp = pc / T_, t = pc - (pc / T_) * T_;
-  const int oh = sp / g.width_col, ow = sp - oh * g.width_col;
-  const int i = t / g.kernel_w, j = t - i * g.kernel_w;
-  const int64_t m = (int64_t)b * HoWo + sp;
+  // Quotients by the runtime sizes from a float reciprocal, corrected by one step (the
+  // launch keeps every quotient below 2^22, where the estimate is off by at most one).
+  auto qdiv = [](int a, int d) {
+    int q = (int)((float)a * __builtin_amdgcn_rcpf((float)d));
+    const int r = a - q * d;
+    return q + (r >= d) - (r < 0);
+  };
+  const int sp = qdiv(pc, T_), t = pc - sp * T_;
+  const int oh = qdiv(sp, g.width_col), ow = sp - oh * g.width_col;
+  const int i = qdiv(t, g.kernel_w), j = t - i * g.kernel_w;
+  const int m = b * HoWo + sp;  // 32-bit indices: the launch checks the tensor sizes
 
   float dy, dx, mk;
   if constexpr (FUSED_Y) {
@@ -235,8 +242,10 @@ hipError_t launch_nchw_t(const DcnGeom &g, const void *col, const void *im, cons
 // ---------------------------------------------------------------------------
 // NHWC grad_offset / grad_mask alone, 16-byte vectors: lane li of a pair's LPP lanes takes
 // the VEC = 16 / sizeof(T) consecutive channels at li*VEC (then + LPP*VEC), so one dcol
-// load and four corner loads move 16 bytes per lane; LPP = min(64, next power of two >=
-// C / VEC), two pairs share a wave when C*sizeof(T) is 512 bytes. Corners outside the
+// load and four corner loads move 16 bytes per lane; LPP = min(8, next power of two >=
+// C / VEC): eight pairs share a wave, so the per-pair geometry (the bulk of the VALU work)
+// is repeated on 8 lanes, not 64 (measured at res4: 8 lanes 51 / 107 us fp16 / fp32,
+// 64 lanes 68 / 142 us, 4 lanes 60 / 142 us). Corners outside the
 // image read zeros through the buffer path (their offset is set past the end of the
 // image), so there are no branches around the loads. The gradients are formed from the
 // four corner dot products once per (pixel, tap) after a shuffle butterfly.
@@ -256,10 +265,17 @@ __global__ void __launch_bounds__(kBlock) col2im_coord_nhwc_vec_kernel(
   const int li = threadIdx.x & (LPP - 1);
   const bool live = pair < HoWo * T_;
   const int pc = live ? pair : 0;
-  const int sp = pc / T_, t = pc - (pc / T_) * T_;
-  const int oh = sp / g.width_col, ow = sp - oh * g.width_col;
-  const int i = t / g.kernel_w, j = t - i * g.kernel_w;
-  const int64_t m = (int64_t)b * HoWo + sp;
+  // Quotients by the runtime sizes from a float reciprocal, corrected by one step (the
+  // launch keeps every quotient below 2^22, where the estimate is off by at most one).
+  auto qdiv = [](int a, int d) {
+    int q = (int)((float)a * __builtin_amdgcn_rcpf((float)d));
+    const int r = a - q * d;
+    return q + (r >= d) - (r < 0);
+  };
+  const int sp = qdiv(pc, T_), t = pc - sp * T_;
+  const int oh = qdiv(sp, g.width_col), ow = sp - oh * g.width_col;
+  const int i = qdiv(t, g.kernel_w), j = t - i * g.kernel_w;
+  const int m = b * HoWo + sp;  // 32-bit indices: the launch checks the tensor sizes
 
   float dy, dx, mk;
   if constexpr (FUSED_Y) {
@@ -283,13 +299,14 @@ __global__ void __launch_bounds__(kBlock) col2im_coord_nhwc_vec_kernel(
   const bool in_w0 = wl >= 0 && wl < g.width, in_w1 = wl + 1 >= 0 && wl + 1 < g.width;
   const bool fin = live && fh == fhc && fw == fwc;
   const int C = g.channels;
-  const int64_t img = (int64_t)b * g.height * g.width;
-  const int64_t e1 = (img + (int64_t)hl * g.width + wl) * C;  // element index of corner 1
+  const int img = b * g.height * g.width;
   const uint32_t eb = (uint32_t)sizeof(T);
-  const uint32_t o1 = (fin && in_h0 && in_w0) ? (uint32_t)(e1 * eb) : kPast;
-  const uint32_t o2 = (fin && in_h0 && in_w1) ? (uint32_t)((e1 + C) * eb) : kPast;
-  const uint32_t o3 = (fin && in_h1 && in_w0) ? (uint32_t)((e1 + (int64_t)g.width * C) * eb) : kPast;
-  const uint32_t o4 = (fin && in_h1 && in_w1) ? (uint32_t)((e1 + (int64_t)(g.width + 1) * C) * eb) : kPast;
+  const uint32_t e1 = (uint32_t)((img + hl * g.width + wl) * C) * eb;  // corner 1, bytes
+  const uint32_t rowb = (uint32_t)(g.width * C) * eb, colb = (uint32_t)C * eb;
+  const uint32_t o1 = (fin && in_h0 && in_w0) ? e1 : kPast;
+  const uint32_t o2 = (fin && in_h0 && in_w1) ? e1 + colb : kPast;
+  const uint32_t o3 = (fin && in_h1 && in_w0) ? e1 + rowb : kPast;
+  const uint32_t o4 = (fin && in_h1 && in_w1) ? e1 + rowb + colb : kPast;
   const float w1 = hh * hw, w2 = hh * lw, w3 = lh * hw, w4 = lh * lw;
   const __amdgpu_buffer_rsrc_t rim = make_rsrc(im, im_bytes);
   const T *drow = dcol + (m * T_ + t) * C;
@@ -690,8 +707,14 @@ hipError_t launch_t(const DcnGeom &g, const void *dcol, const void *im, const vo
   // the image fits the 31-bit buffer offsets; grad_x then goes separately.
   constexpr int VEC = 16 / sizeof(T);
   const int64_t im_bytes = (int64_t)g.batch * g.height * g.width * g.channels * sizeof(T);
+  const int64_t col_elems = (int64_t)g.batch * g.height_col * g.width_col *
+                            g.kernel_h * g.kernel_w * g.channels;
   const bool vec = goff != nullptr && (sizeof(T) == 2 || sizeof(T) == 4) && g.channels % VEC == 0 &&
-                   im_bytes < ((int64_t)1 << 31) && reinterpret_cast<uintptr_t>(dcol) % 16 == 0 &&
+                   im_bytes < ((int64_t)1 << 31) && col_elems < ((int64_t)1 << 31) &&
+                   (int64_t)g.batch * g.height_col * g.width_col * 3 * g.kernel_h * g.kernel_w <
+                       ((int64_t)1 << 31) &&
+                   (int64_t)g.height_col * g.width_col < ((int64_t)1 << 22) &&
+                   reinterpret_cast<uintptr_t>(dcol) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(im) % 16 == 0;
   if (gx != nullptr) {
     // grad_x through the binned kernel where it applies, else through the per-sample
@@ -718,7 +741,7 @@ hipError_t launch_t(const DcnGeom &g, const void *dcol, const void *im, const vo
   }
   if (vec) {
     int vl2 = 0;
-    while (vl2 < 6 && (1 << vl2) * VEC < g.channels) ++vl2;
+    while (vl2 < 3 && (1 << vl2) * VEC < g.channels) ++vl2;  // at most 8 lanes per pair
     const dim3 vgrid((unsigned)(((pairs << vl2) + kBlock - 1) / kBlock), g.batch);
     hipLaunchKernelGGL((col2im_coord_nhwc_vec_kernel<T, FY>), vgrid, dim3(kBlock), 0, stream, dc,
                        xim, of, mk, g, vl2, (uint32_t)im_bytes, goff, gmask);
