@@ -184,7 +184,7 @@ constexpr int kOwnMaxP = 4;                                   // points per quer
 constexpr int kOwnCap = 2560;
 constexpr int kOwnBins = kOwnT * kOwnT;
 static_assert(kOwnBins == kWave, "one wave scans the position counts");
-static_assert(kOwnCand < 65536 && kOwnCap < 65536, "candidate index and rank in 16 bits");
+static_assert(kOwnCand * kOwnMaxP * 4 < 65536, "a corner's rank in its position fits 16 bits");
 
 struct OwnParams {
   const void *loc, *attn, *grad_out;
@@ -329,7 +329,7 @@ __global__ void __launch_bounds__(kOwnThreads) msda_gv_owner_kernel(const OwnPar
     }
     __syncthreads();
     // Half-wave r owns tile row r, lane ch channel ch: one position after the other, the
-    // sum of weight x staged grad_output row over the position's pairs.
+    // sum of weight x grad_output row (of the pair's query) over the position's pairs.
     const T *gob = gout + b * p.go_sb + h * p.go_sh + ch * p.go_sc;
     int bnd[kOwnT + 1];
 #pragma unroll
