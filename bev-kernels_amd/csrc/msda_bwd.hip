@@ -165,16 +165,16 @@ __global__ void __launch_bounds__(kBlock) msda_col2im_kernel(
 //      image (integer LDS atomic, whose result is the pair's rank in its position);
 //   2. a scan of the counts gives each position's range, and each corner kept from step 1
 //      (position, rank) stores its pair (query, bilinear weight x attention) there;
-//   3. half-wave r (32 lanes, one channel each) owns tile row r: for each position it
-//      sums weight x grad_output row of the pair's query over the position's pairs (rows
-//      read from L2, 8 in flight) and stores it.
+//   3. each half-wave (32 lanes, one channel each) owns half a tile row: for each
+//      position it sums weight x grad_output row of the pair's query over the position's
+//      pairs (rows read from L2, 8 in flight) and stores it.
 // A tile with more than kOwnCap pairs zeroes its rows and adds its pairs with atomics.
 // Every near sample's corner is found by exactly one owner (its query lies within
 // kOwnMargin of the corner, so among that tile's candidates); msda_grid_coord_kernel then
 // adds the remaining samples with atomics.
 // ---------------------------------------------------------------------------
 constexpr int kOwnT = 8;
-constexpr int kOwnThreads = 256;
+constexpr int kOwnThreads = 512;
 constexpr int kOwnSide = kOwnT + 2 * kOwnMargin;              // candidate query side
 constexpr int kOwnCand = kOwnSide * kOwnSide;
 constexpr int kOwnMaxP = 4;                                   // points per query
@@ -290,8 +290,11 @@ __global__ void __launch_bounds__(kOwnThreads) msda_gv_owner_kernel(const OwnPar
       if (tid == kWave - 1) bin_at[kOwnBins] = incl;
     }
     __syncthreads();
-    const int r = wave * 2 + half;
-    float *gvr = p.gv + ((int64_t)b * p.S + (int64_t)(y0 + r) * W + x0) * (p.NH * D) + h * D + ch;
+    // Half-wave hw (0..15) owns positions [xb, xb + 4) of tile row r.
+    constexpr int kHX = kOwnT / 2;
+    const int hw = wave * 2 + half, r = hw >> 1, xb = (hw & 1) * kHX;
+    float *gvr =
+        p.gv + ((int64_t)b * p.S + (int64_t)(y0 + r) * W + x0 + xb) * (p.NH * D) + h * D + ch;
     const bool row_in = y0 + r < H;
     if (bin_at[kOwnBins] > kOwnCap) {
       // More pairs than the LDS list holds (inputs that crowd many samples into one
@@ -299,8 +302,8 @@ __global__ void __launch_bounds__(kOwnThreads) msda_gv_owner_kernel(const OwnPar
       // grad_output row.
       if (!p.accumulate) {
 #pragma unroll
-        for (int x = 0; x < kOwnT; ++x)
-          if (row_in && x0 + x < W) gvr[(int64_t)x * (p.NH * D)] = 0.f;
+        for (int x = 0; x < kHX; ++x)
+          if (row_in && x0 + xb + x < W) gvr[(int64_t)x * (p.NH * D)] = 0.f;
       }
       __syncthreads();
       float *gvt = p.gv + ((int64_t)b * p.S + (int64_t)y0 * W + x0) * (p.NH * D) + h * D;
@@ -328,18 +331,18 @@ __global__ void __launch_bounds__(kOwnThreads) msda_gv_owner_kernel(const OwnPar
         }
     }
     __syncthreads();
-    // Half-wave r owns tile row r, lane ch channel ch: one position after the other, the
-    // sum of weight x grad_output row (of the pair's query) over the position's pairs.
+    // Lane ch of half-wave hw: channel ch; one position after the other, the sum of
+    // weight x grad_output row (of the pair's query) over the position's pairs.
     const T *gob = gout + b * p.go_sb + h * p.go_sh + ch * p.go_sc;
-    int bnd[kOwnT + 1];
+    int bnd[kHX + 1];
 #pragma unroll
-    for (int x = 0; x <= kOwnT; ++x) bnd[x] = bin_at[r * kOwnT + x];
-    float old[kOwnT];  // accumulate mode: the row's values, loaded before the sums
+    for (int x = 0; x <= kHX; ++x) bnd[x] = bin_at[r * kOwnT + xb + x];
+    float old[kHX];  // accumulate mode: the positions' values, loaded before the sums
 #pragma unroll
-    for (int x = 0; x < kOwnT; ++x)
-      old[x] = (p.accumulate && row_in && x0 + x < W) ? gvr[(int64_t)x * (p.NH * D)] : 0.f;
+    for (int x = 0; x < kHX; ++x)
+      old[x] = (p.accumulate && row_in && x0 + xb + x < W) ? gvr[(int64_t)x * (p.NH * D)] : 0.f;
 #pragma unroll
-    for (int x = 0; x < kOwnT; ++x) {
+    for (int x = 0; x < kHX; ++x) {
       float acc = 0.f;
       for (int k0 = bnd[x]; k0 < bnd[x + 1]; k0 += 8) {
         float w[8], v[8];
@@ -352,7 +355,7 @@ __global__ void __launch_bounds__(kOwnThreads) msda_gv_owner_kernel(const OwnPar
 #pragma unroll
         for (int u = 0; u < 8; ++u) acc += (k0 + u < bnd[x + 1]) ? w[u] * v[u] : 0.f;
       }
-      if (row_in && x0 + x < W) gvr[(int64_t)x * (p.NH * D)] = old[x] + acc;
+      if (row_in && x0 + xb + x < W) gvr[(int64_t)x * (p.NH * D)] = old[x] + acc;
     }
   }
 }
@@ -524,7 +527,7 @@ hipError_t launch_owner(const MsdaBwdArgs &a, float *gv, bool accumulate, hipStr
   p.go_sh = a.go_stride[2]; p.go_sc = a.go_stride[3];
   p.B = a.f.batch; p.NH = a.f.num_heads; p.NQ = a.f.num_query; p.NP = a.f.num_point;
   p.S = a.f.spatial_size;
-  const int blocks = (device_cus() / 8) * 8 * 3;  // three workgroups per CU (VGPRs)
+  const int blocks = (device_cus() / 8) * 8 * 2;  // two 8-wave workgroups per CU
   p.blocks_per_xcd = blocks / 8;
   if (a.f.batch == 0 || a.f.num_heads == 0) return hipSuccess;
   switch (a.f.num_point) {
