@@ -20,6 +20,11 @@
 // grad_value is fp32 for f32/f16/bf16 inputs and fp64 for f64: 16-bit callers pass an
 // fp32 workspace that is cleared here, accumulated, and narrowed into grad_value at the
 // end (binding_musa.mu:456-510 does the same for fp16).
+//
+// One-level maps whose queries are the grid cells (temporal self-attention) take two other
+// kernels below: msda_gv_owner_kernel adds each grad_value row once per position owner,
+// without atomics, and msda_grid_coord_kernel computes grad_sampling_loc /
+// grad_attn_weight and adds the samples far from their query with atomics.
 #include "bevk_common.h"
 #include "bevk_launch.h"
 
@@ -38,11 +43,7 @@ struct BwdParams {
   int64_t go_sb, go_sq, go_sh, go_sc;  // grad_output strides, elements
   int64_t units;                       // batch * num_query * num_heads
   int S, NH, D, NL, NQ, NP, log2_g;
-  int gv_mode;                         // grad_value adds: kGvAll, or kGvFar after the owner pass
 };
-
-constexpr int kGvAll = 0;  // every sample adds to grad_value
-constexpr int kGvFar = 1;  // only samples the owner pass leaves out (not near their query)
 
 // Sampling coordinates of a sample, as fused multiply-adds so that every kernel that
 // classifies samples gets the same bits.
@@ -53,16 +54,13 @@ __device__ __forceinline__ void sample_coords(A lx, A ly, int Hl, int Wl, A &him
 }
 
 // One-level grids whose queries are the grid cells (q = y * W + x): a sample is "near"
-// when all four of its corners lie within kOwnMargin cells of its query's cell. The
-// owner pass adds near samples to grad_value without atomics; the others are added by
-// msda_col2im_kernel in kGvFar mode.
+// when all four of its corners lie within kOwnMargin cells of its query's cell (qy, qx).
+// The owner pass adds near samples to grad_value without atomics; the others are added
+// by msda_grid_coord_kernel.
 constexpr int kOwnMargin = 6;
 __device__ __forceinline__ bool near_cell(int hl, int wl, int qy, int qx) {
   return hl >= qy - kOwnMargin && hl + 1 <= qy + kOwnMargin && wl >= qx - kOwnMargin &&
          wl + 1 <= qx + kOwnMargin;
-}
-__device__ __forceinline__ bool near_query(int hl, int wl, int q, int Wl) {
-  return near_cell(hl, wl, q / Wl, q - (q / Wl) * Wl);
 }
 
 // T: input dtype; A: arithmetic / grad_value type.
@@ -109,7 +107,6 @@ __global__ void __launch_bounds__(kBlock) msda_col2im_kernel(
       if (him > (A)-1 && wim > (A)-1 && him < (A)Hl && wim < (A)Wl) {
         const A fh = floor(him), fw = floor(wim);
         const int hl = (int)fh, wl = (int)fw;
-        const bool add = p.gv_mode == kGvAll || !near_query(hl, wl, q, Wl);
         const A lh = him - fh, lw = wim - fw, hh = (A)1 - lh, hw = (A)1 - lw;
         const A w1 = hh * hw, w2 = hh * lw, w3 = lh * hw, w4 = lh * lw;
         const bool c1 = hl >= 0 && wl >= 0, c2 = hl >= 0 && wl + 1 <= Wl - 1;
@@ -123,7 +120,7 @@ __global__ void __launch_bounds__(kBlock) msda_col2im_kernel(
           const A v1 = c1 ? (A)vb[o1 + c] : (A)0, v2 = c2 ? (A)vb[o2 + c] : (A)0;
           const A v3 = c3 ? (A)vb[o3 + c] : (A)0, v4 = c4 ? (A)vb[o4 + c] : (A)0;
           const A ta = top * a;
-          if (live && add) {
+          if (live) {
             if (c1) atomic_acc(gvb + o1 + c, w1 * ta);
             if (c2) atomic_acc(gvb + o2 + c, w2 * ta);
             if (c3) atomic_acc(gvb + o3 + c, w3 * ta);
@@ -381,17 +378,25 @@ __global__ void __launch_bounds__(kBlock) msda_grid_coord_kernel(
   constexpr int VEC = 16 / (int)sizeof(T);
   constexpr int G = D / VEC;  // lanes per unit (8 fp32, 4 for 16-bit types)
   constexpr uint32_t kPast = 0x80000000u;
-  const int64_t tid = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-  const int64_t u_raw = tid / G;
-  const bool live = u_raw < p.units;
-  const int64_t unit = live ? u_raw : p.units - 1;
-  const int li = (int)(tid % G);
-  const int h = (int)(unit % p.NH);
-  const int64_t bq = unit / p.NH;
-  const int q = (int)(bq % p.NQ);
-  const int b = (int)(bq / p.NQ);
+  // 32-bit unit indices and quotients from a float reciprocal corrected by one step (the
+  // launch keeps units below 2^31 and every quotient below 2^22).
+  auto qdiv = [](int a, int d) {
+    int qq = (int)((float)a * __builtin_amdgcn_rcpf((float)d));
+    const int rr = a - qq * d;
+    return qq + (rr >= d) - (rr < 0);
+  };
+  const int tid = blockIdx.x * kBlock + threadIdx.x;
+  const int u_raw = tid / G;
+  const bool live = u_raw < (int)p.units;
+  const int unit = live ? u_raw : (int)p.units - 1;
+  const int li = tid % G;
+  const int bq = qdiv(unit, p.NH);
+  const int h = unit - bq * p.NH;
+  const int b = qdiv(bq, p.NQ);
+  const int q = bq - b * p.NQ;
   const int NP = p.NP, NH = p.NH;
   const int H = (int)p.shapes[0], W = (int)p.shapes[1];
+  const int qy = qdiv(q, W), qx = q - qy * W;
   const int64_t row = (int64_t)NH * D;
   const T *vb = value + ((int64_t)b * p.S + p.lsi[0]) * row;
   const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb, (uint32_t)((int64_t)H * W * row * sizeof(T)));
@@ -401,10 +406,10 @@ __global__ void __launch_bounds__(kBlock) msda_grid_coord_kernel(
 #pragma unroll
   for (int e = 0; e < VEC; ++e) top[e] = (float)go[(li * VEC + e) * p.go_sc];
   float *gvb = gv + ((int64_t)b * p.S + p.lsi[0]) * row + h * D + li * VEC;
-  const T *lp = loc + unit * NP * 2;
-  const T *ap = attn + unit * NP;
-  T *glp = grad_loc + unit * NP * 2;
-  T *gap = grad_attn + unit * NP;
+  const T *lp = loc + (int64_t)unit * NP * 2;
+  const T *ap = attn + (int64_t)unit * NP;
+  T *glp = grad_loc + (int64_t)unit * NP * 2;
+  T *gap = grad_attn + (int64_t)unit * NP;
 
   // Geometry and corner loads of every point first.
   float wt[kOwnMaxP][4], lhs[kOwnMaxP], lws[kOwnMaxP], av[kOwnMaxP];
@@ -428,7 +433,7 @@ __global__ void __launch_bounds__(kBlock) msda_grid_coord_kernel(
     hls[pt] = hl;
     wls[pt] = wl;
     okp[pt] = ok;
-    far[pt] = ok && !near_query(hl, wl, q, W);
+    far[pt] = ok && !near_cell(hl, wl, qy, qx);
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int yy = hl + (k >> 1), xx = wl + (k & 1);
@@ -511,7 +516,8 @@ bool owner_path(const MsdaBwdArgs &a) {
          a.f.num_point >= 1 && a.f.num_point <= kOwnMaxP && a.f.spatial_size > 0 &&
          reinterpret_cast<uintptr_t>(a.f.value) % 16 == 0 &&
          (int64_t)a.f.spatial_size * a.f.num_heads * 32 * (int64_t)sizeof(T) < ((int64_t)1 << 31) &&
-         device_cus() >= 8;
+         (int64_t)a.f.batch * a.f.num_query * a.f.num_heads * 8 < ((int64_t)1 << 31) &&
+         (int64_t)a.f.batch * a.f.num_query < ((int64_t)1 << 22) && device_cus() >= 8;
 }
 
 template <typename T>
@@ -540,8 +546,7 @@ hipError_t launch_owner(const MsdaBwdArgs &a, float *gv, bool accumulate, hipStr
 }
 
 template <typename T, typename A>
-hipError_t launch_t(const MsdaBwdArgs &a, A *grad_value, hipStream_t stream,
-                    int gv_mode = kGvAll) {
+hipError_t launch_t(const MsdaBwdArgs &a, A *grad_value, hipStream_t stream) {
   BwdParams p;
   p.shapes = a.f.spatial_shapes;
   p.lsi = a.f.level_start_index;
@@ -550,7 +555,6 @@ hipError_t launch_t(const MsdaBwdArgs &a, A *grad_value, hipStream_t stream,
   p.units = (int64_t)a.f.batch * a.f.num_query * a.f.num_heads;
   p.S = a.f.spatial_size; p.NH = a.f.num_heads; p.D = a.f.channels;
   p.NL = a.f.num_levels; p.NQ = a.f.num_query; p.NP = a.f.num_point;
-  p.gv_mode = gv_mode;
   p.log2_g = 0;
   while ((1 << p.log2_g) < a.f.channels && p.log2_g < 6) ++p.log2_g;
   const int64_t threads = p.units << p.log2_g;
@@ -574,7 +578,6 @@ hipError_t launch_grid_coord(const MsdaBwdArgs &a, float *gv, hipStream_t stream
   p.units = (int64_t)a.f.batch * a.f.num_query * a.f.num_heads;
   p.S = a.f.spatial_size; p.NH = a.f.num_heads; p.D = a.f.channels;
   p.NL = a.f.num_levels; p.NQ = a.f.num_query; p.NP = a.f.num_point;
-  p.gv_mode = kGvFar;
   p.log2_g = 0;
   constexpr int G = 32 * (int)sizeof(T) / 16;
   const int64_t threads = p.units * G;
