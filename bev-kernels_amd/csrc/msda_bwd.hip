@@ -43,7 +43,30 @@ struct BwdParams {
   int64_t go_sb, go_sq, go_sh, go_sc;  // grad_output strides, elements
   int64_t units;                       // batch * num_query * num_heads
   int S, NH, D, NL, NQ, NP, log2_g;
+  int coarse;  // msda_coarse_gv_kernel adds the coarse levels' grad_value (see below)
 };
+
+// Coarse levels: the longest run of final levels (l = LC .. NL - 1, stored one after the
+// other) whose positions number at most kCoarseBins. Both kernels of the coarse split
+// derive LC from the shapes with this function, so every sample is added by exactly one.
+constexpr int kCoarseBins = 2048;
+__device__ __forceinline__ int coarse_first_level(const int64_t *shapes, const int64_t *lsi,
+                                                  int NL, int S) {
+  int lc = NL;
+  int64_t end = 0;
+  for (int l = NL - 1; l >= 0; --l) {
+    const int64_t n = shapes[2 * l] * shapes[2 * l + 1];
+    if (l == NL - 1) {
+      if (lsi[l] < 0 || lsi[l] + n > S) break;
+      end = lsi[l] + n;
+    } else if (lsi[l] < 0 || lsi[l] + n != lsi[l + 1]) {
+      break;
+    }
+    if (end - lsi[l] > kCoarseBins) break;
+    lc = l;
+  }
+  return lc;
+}
 
 // Sampling coordinates of a sample, as fused multiply-adds so that every kernel that
 // classifies samples gets the same bits.
@@ -95,9 +118,11 @@ __global__ void __launch_bounds__(kBlock) msda_col2im_kernel(
   const T *ap = attn + unit * NS;
   T *glp = grad_loc + unit * NS * 2;
   T *gap = grad_attn + unit * NS;
+  const int LC = p.coarse ? coarse_first_level(p.shapes, p.lsi, p.NL, p.S) : p.NL;
   for (int l = 0; l < p.NL; ++l) {
     const int Hl = (int)p.shapes[2 * l], Wl = (int)p.shapes[2 * l + 1];
     const int64_t base = p.lsi[l];
+    const bool add = l < LC;  // coarse levels: msda_coarse_gv_kernel
     for (int pt = 0; pt < p.NP; ++pt) {
       const int s = l * p.NP + pt;
       const A lx = (A)lp[2 * s], ly = (A)lp[2 * s + 1], a = (A)ap[s];
@@ -120,7 +145,7 @@ __global__ void __launch_bounds__(kBlock) msda_col2im_kernel(
           const A v1 = c1 ? (A)vb[o1 + c] : (A)0, v2 = c2 ? (A)vb[o2 + c] : (A)0;
           const A v3 = c3 ? (A)vb[o3 + c] : (A)0, v4 = c4 ? (A)vb[o4 + c] : (A)0;
           const A ta = top * a;
-          if (live) {
+          if (live && add) {
             if (c1) atomic_acc(gvb + o1 + c, w1 * ta);
             if (c2) atomic_acc(gvb + o2 + c, w2 * ta);
             if (c3) atomic_acc(gvb + o3 + c, w3 * ta);
@@ -489,6 +514,190 @@ __global__ void __launch_bounds__(kBlock) msda_grid_coord_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// grad_value of the coarse levels (D = 32, fp32 accumulation) with one atomic per
+// (position, channel) per workgroup instead of one per (sample, corner, channel): a
+// persistent 8-wave workgroup takes kCoarseQ queries of one (batch, head) slice at a time,
+//   1. stages their grad_output rows in LDS and counts every valid corner of their
+//      coarse-level samples in its position (integer LDS atomic);
+//   2. scans the counts, and a second visit of the samples stores the pairs
+//      (position, query, bilinear weight x attention) in position order;
+//   3. half-wave r streams an equal share of the pairs, summing weight x staged row, and
+//      adds the sum to grad_value when the position changes.
+// SCA's levels 2 and 3 (1825 positions) receive ~4.5 corner adds per position and slice
+// from 128 queries, level 3 ~22: most of them collapse into one atomic. A workgroup whose
+// pairs exceed the LDS list adds them one by one.
+// ---------------------------------------------------------------------------
+constexpr int kCoarseQ = 128;
+constexpr int kCoarseThreads = 512;
+constexpr int kCoarseCap = 8192;  // pairs kept in LDS (SCA: 128 queries x 2 levels x 8 x 4)
+constexpr int kCoarseMaxSPU = 32;  // coarse samples per query the kernel takes (levels x points)
+constexpr int kCoarseIter = kCoarseQ * kCoarseMaxSPU / kCoarseThreads;  // samples per thread
+
+struct CoarseParams {
+  const void *loc, *attn, *grad_out;
+  float *gv;
+  const int64_t *shapes, *lsi;
+  int64_t go_sb, go_sq, go_sh, go_sc;
+  int B, NH, NQ, NL, NP, S;
+  int blocks_per_xcd;
+};
+
+template <typename T>
+__global__ void __launch_bounds__(kCoarseThreads) msda_coarse_gv_kernel(const CoarseParams p) {
+  constexpr int D = 32;
+  __shared__ float tst[kCoarseQ * D];       // grad_output rows of the item's queries
+  __shared__ int cnt[kCoarseBins + 1];      // counts, then each position's first pair
+  __shared__ int cur[kCoarseBins];          // placement cursors
+  __shared__ int2 list[kCoarseCap];         // {position << 8 | query in item, weight bits}
+  __shared__ int wsum[kCoarseThreads / kWave];
+  const int LC = coarse_first_level(p.shapes, p.lsi, p.NL, p.S);
+  if (LC >= p.NL) return;  // uniform: no coarse level
+  const int NLc = p.NL - LC;
+  const int64_t base = p.lsi[LC];
+  const int NB = (int)(p.lsi[p.NL - 1] + p.shapes[2 * (p.NL - 1)] * p.shapes[2 * p.NL - 1] - base);
+  const int qchunks = (p.NQ + kCoarseQ - 1) / kCoarseQ;
+  const int nitems = p.B * p.NH * qchunks;
+  const int xcd = blockIdx.x & 7;
+  const int per = (nitems + 7) / 8;
+  const int i_end = min(nitems, (xcd + 1) * per);
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int ch = tid & 31, hw = tid >> 5;  // half-wave index, 0..15
+  const T *loc = static_cast<const T *>(p.loc);
+  const T *attn = static_cast<const T *>(p.attn);
+  const T *gout = static_cast<const T *>(p.grad_out);
+  const int SPU = NLc * p.NP;  // coarse samples per query
+  for (int item = xcd * per + (blockIdx.x >> 3); item < i_end; item += p.blocks_per_xcd) {
+    const int qc = item % qchunks;
+    const int bh = item / qchunks;
+    const int h = bh % p.NH, b = bh / p.NH;
+    const int q0 = qc * kCoarseQ;
+    const int nq = min(kCoarseQ, p.NQ - q0);
+    const int nsamp = nq * SPU;
+    float *gvb = p.gv + ((int64_t)b * p.S + base) * (p.NH * D) + h * D;
+    // The thread's coarse samples i = tid + k * kCoarseThreads: locations, weights and
+    // level loaded once per item, all in flight together, for both visits below.
+    float slx[kCoarseIter], sly[kCoarseIter], sa[kCoarseIter];
+    int sl[kCoarseIter];
+#pragma unroll
+    for (int k = 0; k < kCoarseIter; ++k) {
+      const int i = min(tid + k * kCoarseThreads, nsamp - 1);
+      const int u = i / SPU, r = i - u * SPU;
+      const int lv = r / p.NP, pt = r - lv * p.NP;
+      sl[k] = LC + lv;
+      const int64_t unit = ((int64_t)b * p.NQ + q0 + u) * p.NH + h;
+      const int64_t si = (unit * p.NL + sl[k]) * p.NP + pt;
+      slx[k] = (float)loc[si * 2];
+      sly[k] = (float)loc[si * 2 + 1];
+      sa[k] = (float)attn[si];
+    }
+    // Calls fn(position, query in item, weight) for every valid corner of the thread's
+    // k-th coarse sample.
+    auto visit = [&](int k, auto &&fn) __attribute__((always_inline)) {
+      const int i = tid + k * kCoarseThreads;
+      if (i >= nsamp) return;
+      const int u = i / SPU;
+      const int l = sl[k];
+      const int Hl = (int)p.shapes[2 * l], Wl = (int)p.shapes[2 * l + 1];
+      float him, wim;
+      sample_coords<float>(slx[k], sly[k], Hl, Wl, him, wim);
+      if (!(him > -1.f && wim > -1.f && him < (float)Hl && wim < (float)Wl)) return;
+      const float fh = floorf(him), fw = floorf(wim);
+      const int hl = (int)fh, wl = (int)fw;
+      const float lh = him - fh, lw = wim - fw, hh = 1.f - lh, hwt = 1.f - lw;
+      const int lbase = (int)(p.lsi[l] - base);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int yy = hl + (c >> 1), xx = wl + (c & 1);
+        if (yy < 0 || yy >= Hl || xx < 0 || xx >= Wl) continue;
+        fn(lbase + yy * Wl + xx, u, ((c >> 1) ? lh : hh) * ((c & 1) ? lw : hwt) * sa[k]);
+      }
+    };
+    __syncthreads();  // the previous item's readers are done
+    for (int i = tid; i < nq * D; i += kCoarseThreads) {
+      const int u = i / D, c = i - u * D;
+      tst[i] = (float)gout[b * p.go_sb + (int64_t)(q0 + u) * p.go_sq + h * p.go_sh + c * p.go_sc];
+    }
+    for (int i = tid; i <= NB; i += kCoarseThreads) cnt[i] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kCoarseIter; ++k) visit(k, [&](int bin, int, float) { atomicAdd(&cnt[bin], 1); });
+    __syncthreads();
+    {  // exclusive scan of the NB counts: thread tid owns [tid*E, tid*E + E)
+      const int E = (NB + kCoarseThreads - 1) / kCoarseThreads;
+      const int e0 = min(tid * E, NB), e1 = min(e0 + E, NB);
+      int local = 0;
+      for (int e = e0; e < e1; ++e) local += cnt[e];
+      int incl = local;
+#pragma unroll
+      for (int d = 1; d < kWave; d <<= 1) {
+        const int v = __shfl_up(incl, d, kWave);
+        if (lane >= d) incl += v;
+      }
+      if (lane == kWave - 1) wsum[wave] = incl;
+      __syncthreads();
+      int run = incl - local;
+      for (int w2 = 0; w2 < wave; ++w2) run += wsum[w2];
+      for (int e = e0; e < e1; ++e) {
+        const int c = cnt[e];
+        cnt[e] = run;
+        cur[e] = run;
+        run += c;
+      }
+      if (tid == kCoarseThreads - 1) {
+        int tot = 0;
+        for (int w2 = 0; w2 < kCoarseThreads / kWave; ++w2) tot += wsum[w2];
+        cnt[NB] = tot;
+      }
+    }
+    __syncthreads();
+    const int total = cnt[NB];
+    if (total > kCoarseCap) {
+      // More pairs than the LDS list holds: every pair adds its weighted row directly.
+#pragma unroll
+      for (int k = 0; k < kCoarseIter; ++k)
+        visit(k, [&](int bin, int u, float w) {
+          for (int c = 0; c < D; ++c) unsafeAtomicAdd(gvb + (int64_t)bin * (p.NH * D) + c, w * tst[u * D + c]);
+        });
+      continue;
+    }
+#pragma unroll
+    for (int k = 0; k < kCoarseIter; ++k)
+      visit(k, [&](int bin, int u, float w) {
+        list[atomicAdd(&cur[bin], 1)] = int2{(bin << 8) | u, __builtin_bit_cast(int, w)};
+      });
+    __syncthreads();
+    // Half-wave hw streams pairs [total * hw / 16, total * (hw + 1) / 16); lane ch holds
+    // channel ch; a position cut by two half-waves is added in two parts.
+    const int lo = total * hw / (kCoarseThreads / 32), hi = total * (hw + 1) / (kCoarseThreads / 32);
+    if (lo < hi) {
+      int bin = list[lo].x >> 8;
+      float acc = 0.f;
+      for (int k0 = lo; k0 < hi; k0 += 8) {
+        int2 e[8];
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) e[u] = list[min(k0 + u, hi - 1)];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = tst[(e[u].x & 255) * D + ch];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (k0 + u < hi) {
+            const int bu = e[u].x >> 8;
+            if (bu != bin) {
+              unsafeAtomicAdd(gvb + (int64_t)bin * (p.NH * D) + ch, acc);
+              acc = 0.f;
+              bin = bu;
+            }
+            acc += __builtin_bit_cast(float, e[u].y) * v[u];
+          }
+        }
+      }
+      unsafeAtomicAdd(gvb + (int64_t)bin * (p.NH * D) + ch, acc);
+    }
+  }
+}
+
 __global__ void __launch_bounds__(kBlock) fill_zero_f32(float *__restrict__ p, int64_t n) {
   const int64_t stride = (int64_t)gridDim.x * kBlock;
   for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) p[i] = 0.f;
@@ -545,6 +754,34 @@ hipError_t launch_owner(const MsdaBwdArgs &a, float *gv, bool accumulate, hipStr
   return hipGetLastError();
 }
 
+// The coarse split (msda_coarse_gv_kernel + msda_col2im_kernel without the coarse levels'
+// atomics) for D = 32 and fp32 accumulation.
+template <typename T, typename A>
+bool coarse_split(const MsdaBwdArgs &a) {
+  return sizeof(A) == 4 && a.f.channels == 32 && a.f.num_levels >= 1 && device_cus() >= 8 &&
+         a.f.num_query > 0 && a.f.batch > 0 && a.f.num_heads > 0 &&
+         a.f.num_levels * a.f.num_point <= kCoarseMaxSPU;
+}
+
+template <typename T>
+hipError_t launch_coarse(const MsdaBwdArgs &a, float *gv, hipStream_t stream) {
+  CoarseParams p;
+  p.loc = a.f.sampling_loc;
+  p.attn = a.f.attn_weight;
+  p.grad_out = a.grad_output;
+  p.gv = gv;
+  p.shapes = a.f.spatial_shapes;
+  p.lsi = a.f.level_start_index;
+  p.go_sb = a.go_stride[0]; p.go_sq = a.go_stride[1];
+  p.go_sh = a.go_stride[2]; p.go_sc = a.go_stride[3];
+  p.B = a.f.batch; p.NH = a.f.num_heads; p.NQ = a.f.num_query; p.NL = a.f.num_levels;
+  p.NP = a.f.num_point; p.S = a.f.spatial_size;
+  const int blocks = (device_cus() / 8) * 8;  // one 8-wave workgroup per CU (LDS)
+  p.blocks_per_xcd = blocks / 8;
+  hipLaunchKernelGGL((msda_coarse_gv_kernel<T>), dim3(blocks), dim3(kCoarseThreads), 0, stream, p);
+  return hipGetLastError();
+}
+
 template <typename T, typename A>
 hipError_t launch_t(const MsdaBwdArgs &a, A *grad_value, hipStream_t stream) {
   BwdParams p;
@@ -555,10 +792,17 @@ hipError_t launch_t(const MsdaBwdArgs &a, A *grad_value, hipStream_t stream) {
   p.units = (int64_t)a.f.batch * a.f.num_query * a.f.num_heads;
   p.S = a.f.spatial_size; p.NH = a.f.num_heads; p.D = a.f.channels;
   p.NL = a.f.num_levels; p.NQ = a.f.num_query; p.NP = a.f.num_point;
+  p.coarse = coarse_split<T, A>(a) ? 1 : 0;
   p.log2_g = 0;
   while ((1 << p.log2_g) < a.f.channels && p.log2_g < 6) ++p.log2_g;
   const int64_t threads = p.units << p.log2_g;
   if (threads == 0) return hipSuccess;
+  if constexpr (sizeof(A) == 4) {
+    if (p.coarse) {
+      const hipError_t e = launch_coarse<T>(a, grad_value, stream);
+      if (e != hipSuccess) return e;
+    }
+  }
   hipLaunchKernelGGL((msda_col2im_kernel<T, A>),
                      dim3((unsigned)((threads + kBlock - 1) / kBlock)), dim3(kBlock), 0, stream,
                      static_cast<const T *>(a.f.value), static_cast<const T *>(a.f.sampling_loc),
@@ -578,6 +822,7 @@ hipError_t launch_grid_coord(const MsdaBwdArgs &a, float *gv, hipStream_t stream
   p.units = (int64_t)a.f.batch * a.f.num_query * a.f.num_heads;
   p.S = a.f.spatial_size; p.NH = a.f.num_heads; p.D = a.f.channels;
   p.NL = a.f.num_levels; p.NQ = a.f.num_query; p.NP = a.f.num_point;
+  p.coarse = 0;
   p.log2_g = 0;
   constexpr int G = 32 * (int)sizeof(T) / 16;
   const int64_t threads = p.units * G;

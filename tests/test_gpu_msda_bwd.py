@@ -272,6 +272,23 @@ def test_grid_queries_crowded_tile(dtype):
     _check3(_run(d, go, dtype), _ref(d, go, dtype), dtype, f"crowded {dtype}")
 
 
+@pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
+def test_coarse_levels_overflow(dtype):
+    """Small levels only (all of them "coarse": 96 positions), 8 points per level and D =
+    32: a workgroup's 128 queries bring more corner pairs than its LDS list holds (8192),
+    so it adds them one by one; the result matches the oracle."""
+    d = inputs.msda_random(1, [(6, 7), (4, 5), (3, 3), (2, 2)], 300, 2, 32, 8, seed=21,
+                           loc_lo=0.05, loc_hi=0.95)
+    loc = d["sampling_loc"][0, :128, 0]  # the first workgroup: queries 0..127, head 0
+    shapes = d["spatial_shapes"].double()
+    him = loc[..., 1].double() * shapes[:, 0].view(4, 1) - 0.5
+    wim = loc[..., 0].double() * shapes[:, 1].view(4, 1) - 0.5
+    inside = (him > -1) & (wim > -1) & (him < shapes[:, 0].view(4, 1)) & (wim < shapes[:, 1].view(4, 1))
+    assert int(inside.sum()) * 4 > 8192 * 1.3  # well over the list, even with corners cut
+    go = _grad_output(d, seed=9)
+    _check3(_run(d, go, dtype), _ref(d, go, dtype), dtype, f"coarse overflow {dtype}")
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["fp32", "fp16"])
 def test_empty_queries(dtype):
     d = inputs.msda_random(2, [(3, 4)], 0, 2, 32, 2)
