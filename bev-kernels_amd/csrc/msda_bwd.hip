@@ -698,6 +698,110 @@ __global__ void __launch_bounds__(kCoarseThreads) msda_coarse_gv_kernel(const Co
   }
 }
 
+// ---------------------------------------------------------------------------
+// msda_col2im_kernel for D = 32 and fp32 accumulation (the BEVFormer shapes): 32 lanes per
+// (b, q, head) unit, lane c on channel c, two units per wave. Same per-sample arithmetic;
+// 32-bit offsets (one batch of value under 2 GiB, checked at launch), quotients by the
+// runtime sizes from a reciprocal with one correction step, corner loads through the
+// buffer path with out-of-level corners reading zeros (no branches around the loads), and
+// the three channel sums of a sample reduced in 8 shuffles (each quarter of the 32 lanes
+// ends up holding one of them) instead of 15. The kernel was VALU-bound beside its
+// atomics: ~5,900 VALU instructions per wave at SCA.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ void __launch_bounds__(kBlock) msda_col2im_d32_kernel(
+    const T *__restrict__ value, const T *__restrict__ loc, const T *__restrict__ attn,
+    const T *__restrict__ grad_out, float *__restrict__ grad_value, T *__restrict__ grad_loc,
+    T *__restrict__ grad_attn, BwdParams p) {
+  constexpr int D = 32;
+  constexpr uint32_t kPast = 0x80000000u;
+  auto qdiv = [](int a, int d) {
+    int qq = (int)((float)a * __builtin_amdgcn_rcpf((float)d));
+    const int rr = a - qq * d;
+    return qq + (rr >= d) - (rr < 0);
+  };
+  const int tid = blockIdx.x * kBlock + threadIdx.x;
+  const int u_raw = tid >> 5;
+  const bool live = u_raw < (int)p.units;
+  const int unit = live ? u_raw : (int)p.units - 1;
+  const int lane = tid & 31;
+  const int bq = qdiv(unit, p.NH);
+  const int h = unit - bq * p.NH;
+  const int b = qdiv(bq, p.NQ);
+  const int q = bq - b * p.NQ;
+  const int NS = p.NL * p.NP;
+  const int row = p.NH * D;  // elements per spatial position
+  const float top = live ? (float)grad_out[b * p.go_sb + (int64_t)q * p.go_sq + h * p.go_sh +
+                                           lane * p.go_sc]
+                         : 0.f;
+  const T *vb = value + (int64_t)b * p.S * row + h * D;
+  float *gvb = grad_value + (int64_t)b * p.S * row + h * D;
+  const __amdgpu_buffer_rsrc_t rv =
+      make_rsrc(vb, (uint32_t)(((int64_t)p.S * row - h * D) * sizeof(T)));
+  const T *lp = loc + (int64_t)unit * NS * 2;
+  const T *ap = attn + (int64_t)unit * NS;
+  T *glp = grad_loc + (int64_t)unit * NS * 2;
+  T *gap = grad_attn + (int64_t)unit * NS;
+  const int LC = p.coarse ? coarse_first_level(p.shapes, p.lsi, p.NL, p.S) : p.NL;
+  const uint32_t lane_b = (uint32_t)(lane * sizeof(T));
+  for (int l = 0; l < p.NL; ++l) {
+    const int Hl = (int)p.shapes[2 * l], Wl = (int)p.shapes[2 * l + 1];
+    const int base = (int)p.lsi[l];
+    const bool add = live && l < LC;  // coarse levels: msda_coarse_gv_kernel
+    for (int pt = 0; pt < p.NP; ++pt) {
+      const int s = l * p.NP + pt;
+      const float lx = (float)lp[2 * s], ly = (float)lp[2 * s + 1], a = (float)ap[s];
+      float him, wim;
+      sample_coords<float>(lx, ly, Hl, Wl, him, wim);
+      float gh = 0.f, gw = 0.f, ga = 0.f;
+      if (him > -1.f && wim > -1.f && him < (float)Hl && wim < (float)Wl) {
+        const float fh = floorf(him), fw = floorf(wim);
+        const int hl = (int)fh, wl = (int)fw;
+        const float lh = him - fh, lw = wim - fw, hh = 1.f - lh, hw = 1.f - lw;
+        const float w1 = hh * hw, w2 = hh * lw, w3 = lh * hw, w4 = lh * lw;
+        const bool c1 = hl >= 0 && wl >= 0, c2 = hl >= 0 && wl + 1 <= Wl - 1;
+        const bool c3 = hl + 1 <= Hl - 1 && wl >= 0;
+        const bool c4 = hl + 1 <= Hl - 1 && wl + 1 <= Wl - 1;
+        const int e1 = (base + hl * Wl + wl) * row, e2 = e1 + row;
+        const int e3 = e1 + Wl * row, e4 = e3 + row;
+        const uint32_t eb = (uint32_t)sizeof(T);
+        const float v1 = (float)buffer_load_one<T>(rv, c1 ? (uint32_t)e1 * eb + lane_b : kPast);
+        const float v2 = (float)buffer_load_one<T>(rv, c2 ? (uint32_t)e2 * eb + lane_b : kPast);
+        const float v3 = (float)buffer_load_one<T>(rv, c3 ? (uint32_t)e3 * eb + lane_b : kPast);
+        const float v4 = (float)buffer_load_one<T>(rv, c4 ? (uint32_t)e4 * eb + lane_b : kPast);
+        const float ta = top * a;
+        if (add) {
+          if (c1) unsafeAtomicAdd(gvb + e1 + lane, w1 * ta);
+          if (c2) unsafeAtomicAdd(gvb + e2 + lane, w2 * ta);
+          if (c3) unsafeAtomicAdd(gvb + e3 + lane, w3 * ta);
+          if (c4) unsafeAtomicAdd(gvb + e4 + lane, w4 * ta);
+        }
+        gh = ta * (hw * (v3 - v1) + lw * (v4 - v2)) * (float)Hl;
+        gw = ta * (hh * (v2 - v1) + lh * (v4 - v3)) * (float)Wl;
+        ga = top * (w1 * v1 + w2 * v2 + w3 * v3 + w4 * v4);
+      }
+      // lanes 0-15 keep (gh, gw), 16-31 keep ga; then each quarter keeps one sum
+      const bool up = lane & 16;
+      float k1 = up ? ga : gh, k2 = up ? 0.f : gw;
+      k1 += __shfl_xor(up ? gh : ga, 16, kWave);
+      k2 += __shfl_xor(up ? gw : 0.f, 16, kWave);
+      const bool up2 = lane & 8;
+      float v = up2 ? k2 : k1;
+      v += __shfl_xor(up2 ? k1 : k2, 8, kWave);
+      v += __shfl_xor(v, 4, kWave);
+      v += __shfl_xor(v, 2, kWave);
+      v += __shfl_xor(v, 1, kWave);
+      const int base_lane = (threadIdx.x & (kWave - 1)) & ~31;
+      const float sgw = __shfl(v, base_lane + 8, kWave), sga = __shfl(v, base_lane + 16, kWave);
+      if (live && lane == 0) {
+        glp[2 * s] = (T)sgw;
+        glp[2 * s + 1] = (T)v;
+        gap[s] = (T)sga;
+      }
+    }
+  }
+}
+
 __global__ void __launch_bounds__(kBlock) fill_zero_f32(float *__restrict__ p, int64_t n) {
   const int64_t stride = (int64_t)gridDim.x * kBlock;
   for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) p[i] = 0.f;
@@ -801,6 +905,18 @@ hipError_t launch_t(const MsdaBwdArgs &a, A *grad_value, hipStream_t stream) {
     if (p.coarse) {
       const hipError_t e = launch_coarse<T>(a, grad_value, stream);
       if (e != hipSuccess) return e;
+    }
+    if (a.f.channels == 32 && p.units * 32 < ((int64_t)1 << 31) &&
+        (int64_t)a.f.batch * a.f.num_query < ((int64_t)1 << 22) &&
+        (int64_t)a.f.spatial_size * a.f.num_heads * 32 * (int64_t)sizeof(T) < ((int64_t)1 << 31)) {
+      hipLaunchKernelGGL((msda_col2im_d32_kernel<T>),
+                         dim3((unsigned)((p.units * 32 + kBlock - 1) / kBlock)), dim3(kBlock), 0,
+                         stream, static_cast<const T *>(a.f.value),
+                         static_cast<const T *>(a.f.sampling_loc),
+                         static_cast<const T *>(a.f.attn_weight),
+                         static_cast<const T *>(a.grad_output), grad_value,
+                         static_cast<T *>(a.grad_loc), static_cast<T *>(a.grad_attn), p);
+      return hipGetLastError();
     }
   }
   hipLaunchKernelGGL((msda_col2im_kernel<T, A>),

@@ -157,6 +157,7 @@ def test_grad_value_accumulates_fp32_and_is_written_fp16():
     (2, [(1, 1), (2, 3), (6, 2)], 9, 4, 8, 5),
     (1, [(9, 11)], 13, 1, 1, 1),
     (3, [(3, 3), (2, 2)], 6, 2, 64, 4),
+    (2, [(1, 1), (7, 3), (5, 9)], 11, 3, 32, 5),  # D = 32 kernel, ragged levels
 ])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16,
                                    torch.float64], ids=IDS + ["fp64"])
