@@ -521,16 +521,18 @@ __global__ void __launch_bounds__(kBlock) msda_grid_coord_kernel(
 //   1. stages their grad_output rows in LDS and counts every valid corner of their
 //      coarse-level samples in its position (integer LDS atomic);
 //   2. scans the counts, and a second visit of the samples stores the pairs
-//      (position, query, bilinear weight x attention) in position order;
+//      (query, bilinear weight x attention) in position order; the scanned counts give
+//      each position's range, so a pair does not carry its position;
 //   3. half-wave r streams an equal share of the pairs, summing weight x staged row, and
-//      adds the sum to grad_value when the position changes.
-// SCA's levels 2 and 3 (1825 positions) receive ~4.5 corner adds per position and slice
-// from 128 queries, level 3 ~22: most of them collapse into one atomic. A workgroup whose
+//      adds the sum to grad_value when the position changes (the position of its first
+//      pair found by a binary search of the ranges).
+// SCA's levels 2 and 3 (1825 positions) receive ~9 corner adds per position and slice
+// from 256 queries, level 3 ~44: most of them collapse into one atomic. A workgroup whose
 // pairs exceed the LDS list adds them one by one.
 // ---------------------------------------------------------------------------
-constexpr int kCoarseQ = 128;
+constexpr int kCoarseQ = 256;
 constexpr int kCoarseThreads = 512;
-constexpr int kCoarseCap = 8192;  // pairs kept in LDS (SCA: 128 queries x 2 levels x 8 x 4)
+constexpr int kCoarseCap = 16384;  // pairs kept in LDS (SCA: 256 queries x 2 levels x 8 x 4)
 constexpr int kCoarseMaxSPU = 32;  // coarse samples per query the kernel takes (levels x points)
 constexpr int kCoarseIter = kCoarseQ * kCoarseMaxSPU / kCoarseThreads;  // samples per thread
 
@@ -549,7 +551,8 @@ __global__ void __launch_bounds__(kCoarseThreads) msda_coarse_gv_kernel(const Co
   __shared__ float tst[kCoarseQ * D];       // grad_output rows of the item's queries
   __shared__ int cnt[kCoarseBins + 1];      // counts, then each position's first pair
   __shared__ int cur[kCoarseBins];          // placement cursors
-  __shared__ int2 list[kCoarseCap];         // {position << 8 | query in item, weight bits}
+  __shared__ float lwt[kCoarseCap];         // pairs in position order: weight
+  __shared__ unsigned short lq[kCoarseCap]; // and query in item
   __shared__ int wsum[kCoarseThreads / kWave];
   const int LC = coarse_first_level(p.shapes, p.lsi, p.NL, p.S);
   if (LC >= p.NL) return;  // uniform: no coarse level
@@ -664,32 +667,43 @@ __global__ void __launch_bounds__(kCoarseThreads) msda_coarse_gv_kernel(const Co
 #pragma unroll
     for (int k = 0; k < kCoarseIter; ++k)
       visit(k, [&](int bin, int u, float w) {
-        list[atomicAdd(&cur[bin], 1)] = int2{(bin << 8) | u, __builtin_bit_cast(int, w)};
+        const int slot = atomicAdd(&cur[bin], 1);
+        lwt[slot] = w;
+        lq[slot] = (unsigned short)u;
       });
     __syncthreads();
     // Half-wave hw streams pairs [total * hw / 16, total * (hw + 1) / 16); lane ch holds
     // channel ch; a position cut by two half-waves is added in two parts.
     const int lo = total * hw / (kCoarseThreads / 32), hi = total * (hw + 1) / (kCoarseThreads / 32);
     if (lo < hi) {
-      int bin = list[lo].x >> 8;
+      // the position holding pair lo: the last one whose range starts at or before lo
+      // (an empty position's successor starts where it does, so the last one is not empty)
+      int bin = 0;
+      for (int st = kCoarseBins / 2; st > 0; st >>= 1)
+        if (bin + st < NB && cnt[bin + st] <= lo) bin += st;
+      int next = cnt[bin + 1];  // first pair of the following position
       float acc = 0.f;
       for (int k0 = lo; k0 < hi; k0 += 8) {
-        int2 e[8];
-        float v[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) e[u] = list[min(k0 + u, hi - 1)];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = tst[(e[u].x & 255) * D + ch];
+        float w[8], v[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-          if (k0 + u < hi) {
-            const int bu = e[u].x >> 8;
-            if (bu != bin) {
+          const int k = min(k0 + u, hi - 1);
+          w[u] = lwt[k];
+          v[u] = tst[lq[k] * D + ch];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int k = k0 + u;
+          if (k < hi) {
+            if (k >= next) {  // pair k starts a later position (k < total ends the walk)
               unsafeAtomicAdd(gvb + (int64_t)bin * (p.NH * D) + ch, acc);
               acc = 0.f;
-              bin = bu;
+              do {
+                ++bin;
+                next = cnt[bin + 1];
+              } while (next <= k);
             }
-            acc += __builtin_bit_cast(float, e[u].y) * v[u];
+            acc += w[u] * v[u];
           }
         }
       }
