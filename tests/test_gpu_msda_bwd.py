@@ -290,6 +290,32 @@ def test_coarse_levels_overflow(dtype):
     _check3(_run(d, go, dtype), _ref(d, go, dtype), dtype, f"coarse overflow {dtype}")
 
 
+@pytest.mark.parametrize("num_query,heads", [((1 << 21) + 5, 8), ((1 << 22) + 3, 1)])
+def test_large_unit_counts(num_query, heads):
+    """Unit decoding at scale. The D = 32 kernel decodes (batch, query, head) from its unit
+    index with float reciprocals and one correction step, exact while batch x queries
+    < 2^22 (its launch bound): 8 heads x (2^21 + 5) queries put the unit index past 2^24,
+    where its float conversion rounds. 2^22 + 3 queries are past the bound and take the
+    general kernel. grad_sampling_loc / grad_attn_weight of queries spread over the range
+    (each depends on its own query and head only) against the oracle on that subset."""
+    d = inputs.msda_random(1, [(3, 5), (2, 2)], num_query, heads, 32, 1, seed=21,
+                           loc_lo=-0.3, loc_hi=1.3)
+    g = torch.Generator().manual_seed(4)
+    q_idx = torch.cat([torch.arange(16), torch.arange(num_query - 16, num_query),
+                       torch.randint(16, num_query - 16, (32,), generator=g)]).unique()
+    gen = torch.Generator(device=DEV).manual_seed(9)
+    go = torch.randn(1, num_query, heads * 32, generator=gen, device=DEV).half()
+    dd = _dev(d, torch.float16)
+    _, gl, ga = _api().ms_deform_attn_backward(**dd, grad_output=go)
+    torch.cuda.synchronize()
+    sub = dict(d, sampling_loc=d["sampling_loc"][:, q_idx], attn_weight=d["attn_weight"][:, q_idx])
+    go_sub = go[:, q_idx.to(DEV)].float().cpu()
+    del go, dd
+    _, rl, ra = _ref(sub, go_sub, torch.float16)
+    check(gl[:, q_idx.to(DEV)].cpu(), rl, torch.float16, f"{num_query}x{heads} grad_sampling_loc")
+    check(ga[:, q_idx.to(DEV)].cpu(), ra, torch.float16, f"{num_query}x{heads} grad_attn_weight")
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["fp32", "fp16"])
 def test_empty_queries(dtype):
     d = inputs.msda_random(2, [(3, 4)], 0, 2, 32, 2)
