@@ -21,6 +21,11 @@
 // fp32 workspace that is cleared here, accumulated, and narrowed into grad_value at the
 // end (binding_musa.mu:456-510 does the same for fp16).
 //
+// D = 32 with fp32 accumulation (every BEVFormer and DETR shape) runs the same mapping in
+// msda_col2im_d32_kernel (32-bit offsets, branch-free corner loads, shorter reduction), and
+// the levels of at most kCoarseBins positions leave its atomics for msda_coarse_gv_kernel,
+// which sums each position's corner adds of 256 queries before one atomic per channel.
+//
 // One-level maps whose queries are the grid cells (temporal self-attention) take two other
 // kernels below: msda_gv_owner_kernel adds each grad_value row once per position owner,
 // without atomics, and msda_grid_coord_kernel computes grad_sampling_loc /
