@@ -292,7 +292,8 @@ def main():
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the operators shard over cameras/batch with no communication; see DESIGN.md)",
+              "(the operators shard over cameras / batch with no communication: each GPU runs "
+              "its own share of the batch, so N GPUs give N times this throughput)",
               file=sys.stderr)
         sys.exit(2)
     import torch
