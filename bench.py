@@ -293,7 +293,7 @@ def main():
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
               "(the operators shard over cameras / batch with no communication: each GPU runs "
-              "its own share of the batch, so N GPUs give N times this throughput)",
+              "its own share of the batch; only the one-GPU rate is measured here)",
               file=sys.stderr)
         sys.exit(2)
     import torch
