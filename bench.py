@@ -15,7 +15,8 @@ Len_q 10000, 8 heads x 32, 8 points), fp32, with inputs resident in HBM:
              the backward kernels (MSDA backward, DCN NHWC column-to-image) in GB/s of
              compulsory bytes
   cpu_baseline  the CPU oracle (grid_sample form) on the same SCA workload, timed on the
-             host cores of this machine
+             host cores of this machine; `dcn` adds the DCN goldens (NCHW: configs[0]
+             and res4 / res5 fp32; NHWC: res4 / res5 on fp16-rounded inputs)
 Cold-cache protocol (default): a 1 GiB buffer is overwritten before every timed launch so
 L2 and the 256 MB MALL hold none of the inputs; --warm times back-to-back launches.
 """
@@ -131,6 +132,32 @@ def dcn_fused_case(name, dtype, cache):
     flops = 2.0 * B * H * W * 9 * C * Cout
     return (lambda: ext.dcn_fused_fwd_nhwc(x, off, msk, w_packed, None, B, C, H, W, H, W, Cout, 3, 3,
                                            1, 1, 1, 1, 1, 1, out)), flops
+
+
+def dcn_mega_case(name, dtype, cache):
+    """One-launch full forward (offset conv + sigmoid + deformable gather + GEMM) of one DCN
+    configuration, weights packed once (untimed). Work: 2*M*K*(Cout + 3T) flops (the offset
+    conv and the deformable conv)."""
+    import torch
+    import _modulated_deform_conv_ext as ext
+    from oracle import inputs
+    if name not in cache:
+        cache[name] = inputs.nchw_to_nhwc(inputs.dcn_inputs(name))
+    d = cache[name]
+    dev = torch.device("cuda")
+    x = d["x"].to(dtype).to(dev)
+    B, H, W, C = x.shape
+    Cout = d["weight"].shape[0]
+    g = torch.Generator().manual_seed(13)
+    w_off = (1.5 / (9 * C) ** 0.5 * torch.randn(27, C, 3, 3, generator=g)).to(dtype).to(dev)
+    b_off = (0.5 * torch.randn(27, generator=g)).to(dev)
+    wo_packed = ext.dcn_pack_weight(w_off.contiguous())
+    w_packed = ext.dcn_pack_weight(d["weight"].to(dtype).to(dev).contiguous())
+    y = torch.empty(B * H * W, 27, dtype=torch.float32, device=dev)
+    out = torch.empty(B, H, W, Cout, dtype=dtype, device=dev)
+    flops = 2.0 * B * H * W * 9 * C * (Cout + 27)
+    return (lambda: ext.dcn_mega_fwd_nhwc(x, wo_packed, b_off, w_packed, None, B, C, H, W, H, W,
+                                          Cout, 3, 3, 1, 1, 1, 1, 1, 1, False, y, out)), flops
 
 
 def dcn_front_case(name, dtype, cache):
@@ -285,7 +312,49 @@ def cpu_baseline(cache):
             "kind": "port",
             "sample": f"full SCA workload (6x10000x8 queries, fp32) through the oracle's "
                       f"grid_sample form, torch CPU, {cores} threads, median of 3 = "
-                      f"{t * 1e3:.0f} ms, {cpu}"}
+                      f"{t * 1e3:.0f} ms, {cpu}",
+            "dcn": dcn_cpu_baselines(cores)}
+
+
+def dcn_cpu_baselines(cores):
+    """The DCN CPU goldens on the BASELINE workloads, 1 warm-up + median of 3, fp32 on the
+    host cores: the NCHW golden (configs[0]; res4 / res5 fp32 NCHW on 2 of the 6 images)
+    and the NHWC golden (whole res4 / res5, fp32 on fp16-rounded inputs, the reference for
+    the fp16 / bf16 fused runs). GFLOP/s = 2*M*K*Cout of the sample / median time."""
+    import torch
+    from oracle import dcn as od
+    from oracle import inputs
+    rows = []
+    # (config, layout, images): the NCHW golden of res4 / res5 on a bounded sample of 2
+    # of the 6 images (its Python loop over channel x tap dominates); the rest whole
+    for name, layout, imgs in (("dcn_c1", "nchw", None), ("dcn_res4", "nchw", 2),
+                               ("dcn_res5", "nchw", 2), ("dcn_res4", "nhwc", None),
+                               ("dcn_res5", "nhwc", None)):
+        d = inputs.dcn_inputs(name, batch=imgs)
+        B, C, H, W = d["x"].shape
+        cout = d["weight"].shape[0]
+        flops = 2.0 * B * H * W * 9 * C * cout
+        if layout == "nchw":
+            args = (d["x"], d["offset"], d["mask"], d["weight"], d["bias"])
+            fn = lambda: od.forward_nchw(*args, (1, 1), (1, 1), (1, 1))  # noqa: E731
+        else:
+            dn = inputs.nchw_to_nhwc(d)
+            r = {k: (v.to(torch.float16).float() if torch.is_tensor(v) else v)
+                 for k, v in dn.items()}
+            fn = lambda: od.forward_nhwc(r["x"], r["offset"], r["mask"], r["weight"],  # noqa: E731
+                                         r["bias"], 1, 1, 1)
+        fn()
+        ts = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        t = statistics.median(ts)
+        rows.append({"config": f"{name}_{layout}_golden", "ms": round(t * 1e3, 1),
+                     "GFLOP/s": round(flops / t / 1e9, 1), "cores": cores,
+                     "sample": (f"{B} of the 6 images" if imgs else f"whole workload (B={B})")
+                               + ", fp32, median of 3"})
+    return rows
 
 
 def main():
@@ -314,6 +383,8 @@ def main():
             fn, _ = dcn_fused_case(name, dtype_of(dt), cache)
         elif kind == "dcn_nchw":
             fn, _ = dcn_nchw_case(name, cache)
+        elif kind == "dcn_mega":
+            fn, _ = dcn_mega_case(name, dtype_of(dt), cache)
         elif kind == "dcn_front":
             fn, _ = dcn_front_case(name, dtype_of(dt), cache)
         elif kind == "msda_bwd":
@@ -379,35 +450,43 @@ def main():
 
     if not args.no_configs:
         rows = []
+        reps, wu = max(100, steps), max(10, warmup)   # per row: >= 100 timed after >= 10
         for name in ("msda_sca", "msda_tsa", "msda_detr"):
             for dt in ("fp32", "fp16", "bf16"):
                 f, nb = msda_case(name, dtype_of(dt), cache)
-                m, _, _ = timer.run(f, max(10, steps // 2), 3)
+                m, _, _ = timer.run(f, reps, wu)
                 g = nb / (m * 1e-6) / 1e9
                 rows.append({"config": name, "dtype": dt, "us": round(m, 2),
                              "GB/s": round(g, 1), "frac_hbm": round(g / HBM_PEAK_GBS, 4)})
         for name in ("dcn_res4", "dcn_res5"):
             for dt in ("fp16", "bf16", "fp32"):
                 f, fl = dcn_fused_case(name, dtype_of(dt), cache)
-                m, _, _ = timer.run(f, max(10, steps // 2), 3)
+                m, _, _ = timer.run(f, reps, wu)
                 tf = fl / (m * 1e-6) / 1e12
                 rows.append({"config": name + "_nhwc_fused", "dtype": dt, "us": round(m, 2),
                              "TFLOP/s": round(tf, 2),
                              "frac_mfma": round(tf / MFMA_PEAK_TFLOPS[dt], 4)})
             f, fl = dcn_nchw_case(name, cache)
-            m, _, _ = timer.run(f, max(10, steps // 2), 3)
+            m, _, _ = timer.run(f, reps, wu)
             tf = fl / (m * 1e-6) / 1e12
             rows.append({"config": name + "_nchw_module", "dtype": "fp32", "us": round(m, 2),
                          "TFLOP/s": round(tf, 2),
                          "frac_mfma": round(tf / MFMA_PEAK_TFLOPS["fp32"], 4)})
+            for dt in ("fp16", "bf16"):
+                f, fl = dcn_mega_case(name, dtype_of(dt), cache)
+                m, _, _ = timer.run(f, reps, wu)
+                tf = fl / (m * 1e-6) / 1e12
+                rows.append({"config": name + "_mega_one_launch", "dtype": dt,
+                             "us": round(m, 2), "TFLOP/s": round(tf, 2),
+                             "frac_mfma": round(tf / MFMA_PEAK_TFLOPS[dt], 4)})
             f, nb = dcn_front_case(name, dtype_of("fp16"), cache)
-            m, _, _ = timer.run(f, max(10, steps // 2), 3)
+            m, _, _ = timer.run(f, reps, wu)
             g = nb / (m * 1e-6) / 1e9
             rows.append({"config": name + "_front_end", "dtype": "fp16", "us": round(m, 2),
                          "GB/s": round(g, 1), "frac_hbm": round(g / HBM_PEAK_GBS, 4)})
             for dt in ("fp16", "fp32"):
                 f, nb = dcn_bwd_case(name, dtype_of(dt), cache)
-                m, _, _ = timer.run(f, max(10, steps // 2), 3)
+                m, _, _ = timer.run(f, reps, wu)
                 g = nb / (m * 1e-6) / 1e9
                 rows.append({"config": name + "_col2im_nhwc_backward", "dtype": dt,
                              "us": round(m, 2), "GB/s": round(g, 1),
@@ -415,7 +494,7 @@ def main():
         for name in ("msda_sca", "msda_tsa", "msda_detr"):
             for dt in ("fp32", "fp16", "bf16"):
                 f, nb = msda_bwd_case(name, dtype_of(dt), cache)
-                m, _, _ = timer.run(f, max(10, steps // 2), 3)
+                m, _, _ = timer.run(f, reps, wu)
                 g = nb / (m * 1e-6) / 1e9
                 rows.append({"config": name + "_backward", "dtype": dt, "us": round(m, 2),
                              "GB/s": round(g, 1), "frac_hbm": round(g / HBM_PEAK_GBS, 4)})

@@ -45,6 +45,8 @@ _SIGNATURES = {
     "bevk_dcn_pack_weight": [_i, _vp] + [_i] * 4 + [_vp, _vp],
     "bevk_dcn_fused_fwd_nhwc": [_i, _vp, _vp, _i, _vp, _vp, _vp] + [_i] * 15 + [_vp, _vp],
     "bevk_transpose": [_i, _vp, _vp, _i, _i, _i, _vp],
+    "bevk_dcn_offset_conv_nhwc": [_i, _vp, _vp, _vp] + [_i] * 14 + [_vp, _vp],
+    "bevk_dcn_mega_fwd_nhwc": [_i, _vp, _vp, _vp, _vp, _vp] + [_i] * 16 + [_vp, _vp, _vp],
     "bevk_msda_forward": [_i, _vp, _vp, _vp, _vp, _vp] + [_i] * 9 + [_vp, _vp],
     "bevk_msda_backward_workspace_bytes": [_i] * 5,
     "bevk_msda_backward": [_i, _vp, _vp, _vp, _vp, _vp, _vp] + [ctypes.c_int64] * 4

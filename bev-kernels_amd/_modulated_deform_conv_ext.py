@@ -10,8 +10,10 @@ Unlike the reference launchers these wrappers check device, contiguity, dtype an
 element counts against the integer sizes before launching, and raise RuntimeError on
 a mismatch, so a kernel never indexes past a buffer.
 
-The backward entry points are kept as names only: the backward kernels are not part
-of this build and raise RuntimeError.
+The backward entry points (the col2im / col2im_coord names and MSDA ``backward``) run
+the column-to-image and MSDA backward kernels of the library with the reference's
+ownership rules: gradients the reference accumulates into caller-zeroed tensors are
+added to what the caller passes, everything else is written.
 """
 from __future__ import annotations
 
@@ -39,6 +41,8 @@ __all__ = [
     "dcn_packed_weight_numel",
     "dcn_pack_weight",
     "dcn_fused_fwd_nhwc",
+    "dcn_offset_conv_nhwc",
+    "dcn_mega_fwd_nhwc",
     "transpose",
     "nchw_to_nhwc",
     "nhwc_to_nchw",
@@ -142,8 +146,8 @@ def dcn_pack_weight(weight, packed=None):
 
     fp32: [Cout, kh, kw, C]; fp16 / bf16: MFMA-fragment blocks of 32 output channels x 16
     reduction elements (k = (i*kw + j)*C + c), zero padded. The reference permutes the
-    weight to [kh, kw, C, Cout] on every call (fused_tl.py:500-510); here it is packed
-    once per weight and reused."""
+    weight to [kh, kw, C, Cout] on every call (fused_tl.py:500-510); the operator layer
+    packs on every call as well (one small kernel)."""
     fn = "dcn_pack_weight"
     if weight.dim() != 4:
         raise RuntimeError(f"{fn}: weight must be [Cout, C, kh, kw], got {tuple(weight.shape)}")
@@ -222,6 +226,70 @@ def dcn_fused_fwd_nhwc(data_im, data_offset, data_mask, weight_packed, bias, bat
             _b.ptr(bias), batch_size, channels, height_im, width_im, height_col, width_col,
             channels_out, kernel_h, kernel_w, pad_h, pad_w, stride_h, stride_w, dilation_h,
             dilation_w, _b.ptr(out), _b.stream_of(data_im))
+
+
+def _offset_conv_checks(fn, data_im, w_off_packed, b_off, batch_size, channels, height_im,
+                        width_im, height_col, width_col, kernel_h, kernel_w, y):
+    _b.require_contiguous(fn, data_im=data_im, w_off_packed=w_off_packed, b_off=b_off, y=y)
+    _b.require_dtype(fn, data_im, w_off_packed=w_off_packed)
+    for name, t in (("b_off", b_off), ("y", y)):
+        if t is not None and t.dtype != torch.float32:
+            raise RuntimeError(f"{fn}: {name} must be float32, got {t.dtype}")
+    taps = kernel_h * kernel_w
+    m = batch_size * height_col * width_col
+    _b.require_numel(fn, "data_im", data_im, batch_size * height_im * width_im * channels)
+    _b.require_numel(fn, "w_off_packed", w_off_packed,
+                     dcn_packed_weight_numel(data_im.dtype, 3 * taps, kernel_h, kernel_w,
+                                             channels))
+    if b_off is not None:
+        _b.require_numel(fn, "b_off", b_off, 3 * taps)
+    _b.require_numel(fn, "y", y, m * 3 * taps)
+
+
+def dcn_offset_conv_nhwc(data_im, w_off_packed, b_off, batch_size, channels, height_im,
+                         width_im, height_col, width_col, kernel_h, kernel_w, pad_h, pad_w,
+                         stride_h, stride_w, dilation_h, dilation_w, y):
+    """Offset conv of the NHWC front end: y [B*Ho*Wo, 3T] (float32) = conv(x, w_off) +
+    b_off with fp32 accumulation (the kernel of fused_tl.offset_conv_forward_nhwc,
+    fused_tl.py:419-470). w_off_packed is dcn_pack_weight(w_off [3T, C, kh, kw]); b_off is
+    float32 [3T] or None."""
+    fn = "dcn_offset_conv_nhwc"
+    _b.require_device(fn, data_im, w_off_packed, b_off, y)
+    _offset_conv_checks(fn, data_im, w_off_packed, b_off, batch_size, channels, height_im,
+                        width_im, height_col, width_col, kernel_h, kernel_w, y)
+    _b.call("bevk_dcn_offset_conv_nhwc", _b.dtype_code(data_im), _b.ptr(data_im),
+            _b.ptr(w_off_packed), _b.ptr(b_off), batch_size, channels, height_im, width_im,
+            height_col, width_col, kernel_h, kernel_w, pad_h, pad_w, stride_h, stride_w,
+            dilation_h, dilation_w, _b.ptr(y), _b.stream_of(data_im))
+
+
+def dcn_mega_fwd_nhwc(data_im, w_off_packed, b_off, weight_packed, bias, batch_size, channels,
+                      height_im, width_im, height_col, width_col, channels_out, kernel_h,
+                      kernel_w, pad_h, pad_w, stride_h, stride_w, dilation_h, dilation_w,
+                      act_relu, y, out):
+    """Whole DCNv2 forward with the offset conv inside (fused_tl.py:565-766 and the
+    DCNSplitNHWCFunction forward with its ReLU epilogue, dcn_split_nhwc.py:158-204):
+    y [B*Ho*Wo, 3T] float32 = conv(x, w_off) + b_off (written), offsets y[:, :2T], mask
+    sigmoid(y[:, 2T:]), out [B, Ho, Wo, Cout] = deformable conv + bias (relu if act_relu).
+    One kernel launch on the shapes of the persistent fp16/bf16 kernel."""
+    fn = "dcn_mega_fwd_nhwc"
+    _b.require_device(fn, data_im, w_off_packed, b_off, weight_packed, bias, y, out)
+    _offset_conv_checks(fn, data_im, w_off_packed, b_off, batch_size, channels, height_im,
+                        width_im, height_col, width_col, kernel_h, kernel_w, y)
+    _b.require_contiguous(fn, weight_packed=weight_packed, bias=bias, out=out)
+    _b.require_dtype(fn, data_im, weight_packed=weight_packed, bias=bias, out=out)
+    m = batch_size * height_col * width_col
+    _b.require_numel(fn, "weight_packed", weight_packed,
+                     dcn_packed_weight_numel(data_im.dtype, channels_out, kernel_h, kernel_w,
+                                             channels))
+    if bias is not None:
+        _b.require_numel(fn, "bias", bias, channels_out)
+    _b.require_numel(fn, "out", out, m * channels_out)
+    _b.call("bevk_dcn_mega_fwd_nhwc", _b.dtype_code(data_im), _b.ptr(data_im),
+            _b.ptr(w_off_packed), _b.ptr(b_off), _b.ptr(weight_packed), _b.ptr(bias),
+            batch_size, channels, height_im, width_im, height_col, width_col, channels_out,
+            kernel_h, kernel_w, pad_h, pad_w, stride_h, stride_w, dilation_h, dilation_w,
+            1 if act_relu else 0, _b.ptr(y), _b.ptr(out), _b.stream_of(data_im))
 
 
 def _col2im_nchw(fn, data_col, data_im, data_offset, data_mask, batch_size, channels,

@@ -108,4 +108,43 @@ __device__ __forceinline__ T buffer_load_one(__amdgpu_buffer_rsrc_t r, uint32_t 
 // the pre-sigmoid mask.
 __device__ __forceinline__ float sigmoid_f32(float x) { return 1.f / (1.f + __expf(-x)); }
 
+// Sample geometry forms of the fused DCN kernels.
+enum DcnGeo {
+  kGeoMask = 0,     // offsets [M][2T] + mask [M][T], input dtype
+  kGeoY = 1,        // raw offset-conv output y [M][3T], input dtype; mask = sigmoid(y[2T + t])
+  kGeoRegular = 2,  // no offsets: a plain convolution (fp32 output; the offset conv)
+  kGeoYF32 = 3,     // y [M][3T] fp32 (+ fp32 bias [3T] when given); mask = sigmoid
+};
+
+// Offsets (dy, dx) and mask of tap t of output row m in the deformable forms
+// (dcn_fused_nhwc_kernel.cuh:126-134 and dcn_split_nhwc.py:131-132 for the y forms:
+// offset = y[..., :2T] with (dy, dx) interleaved per tap, mask = sigmoid(y[..., 2T:])).
+template <typename T, int GEO>
+__device__ __forceinline__ void tap_offsets(const void *off, const void *msk, const float *yb,
+                                            int64_t m, int t, int taps, float &dy, float &dx,
+                                            float &mk) {
+  if constexpr (GEO == kGeoY) {
+    const T *yp = static_cast<const T *>(off) + m * 3 * taps;
+    dy = (float)yp[2 * t];
+    dx = (float)yp[2 * t + 1];
+    mk = sigmoid_f32((float)yp[2 * taps + t]);
+  } else if constexpr (GEO == kGeoYF32) {
+    const float *yp = static_cast<const float *>(off) + m * 3 * taps;
+    float b0 = 0.f, b1 = 0.f, b2 = 0.f;
+    if (yb != nullptr) {
+      b0 = yb[2 * t];
+      b1 = yb[2 * t + 1];
+      b2 = yb[2 * taps + t];
+    }
+    dy = yp[2 * t] + b0;
+    dx = yp[2 * t + 1] + b1;
+    mk = sigmoid_f32(yp[2 * taps + t] + b2);
+  } else {
+    const T *op = static_cast<const T *>(off);
+    dy = (float)op[m * 2 * taps + 2 * t];
+    dx = (float)op[m * 2 * taps + 2 * t + 1];
+    mk = (float)static_cast<const T *>(msk)[m * taps + t];
+  }
+}
+
 }  // namespace bevk

@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "bevk_common.h"
+
 namespace bevk {
 
 // Compute units of the current device (cached per device; 0 when the query fails).
@@ -35,7 +37,10 @@ struct MsdaBwdArgs {
 
 // Bytes of fp32 accumulator the 16-bit backward needs (0 for f32 / f64).
 int64_t msda_backward_workspace_bytes(int dtype, int64_t value_elems);
-hipError_t launch_msda_backward(int dtype, const MsdaBwdArgs &a, hipStream_t stream);
+// force_generic: the per-unit atomic kernel for every level (no coarse split, no grid
+// owner pass, no D = 32 kernel).
+hipError_t launch_msda_backward(int dtype, const MsdaBwdArgs &a, bool force_generic,
+                                hipStream_t stream);
 
 struct DcnGeom {
   int batch, channels, height, width, height_col, width_col;
@@ -53,26 +58,35 @@ hipError_t launch_im2col_nhwc(int dtype, const DcnGeom &g, const void *data_im,
                               const void *data_offset, bool fused_y, const void *data_mask,
                               void *data_col, hipStream_t stream);
 
-// Sample geometry of the fused kernels.
-enum DcnGeo {
-  kGeoMask = 0,     // offsets [M][2T] + mask [M][T]
-  kGeoY = 1,        // raw offset-conv output y [M][3T]; mask = sigmoid(y[2T + t])
-  kGeoRegular = 2,  // no offsets: a plain convolution (fp32 output; offset conv)
-};
-
 // Fused NHWC implicit-GEMM forward (dg == 1). w_packed: layout of launch_dcn_pack_weight.
-// kGeoRegular writes fp32 `out` and ignores data_offset / data_mask / bias.
+// geo (DcnGeo): kGeoMask / kGeoY read data_offset (and data_mask) in the input dtype;
+// kGeoYF32 reads an fp32 y [M][3T] as data_offset and adds y_bias [3T] (fp32, may be
+// null); kGeoRegular ignores data_offset / data_mask and writes fp32 `out`, with an fp32
+// `bias`. relu: max(out, 0) in the epilogue (not for kGeoRegular).
 hipError_t launch_dcn_fused_nhwc(int dtype, const DcnGeom &g, int channels_out,
                                  const void *data_im, const void *data_offset, int geo,
                                  const void *data_mask, const void *w_packed,
-                                 const void *bias, void *out, hipStream_t stream);
+                                 const void *bias, void *out, hipStream_t stream,
+                                 const float *y_bias = nullptr, bool relu = false);
 
 // fp16 / bf16 implicit GEMM with the weight in MFMA-fragment blocks (<= 9 taps).
 bool dcn_fused_h_supported(const DcnGeom &g);
 hipError_t launch_dcn_fused_h(int dtype, const DcnGeom &g, int channels_out, const void *x,
                               const void *off, int geo, const void *msk,
                               const void *w_packed, const void *bias, void *out,
-                              hipStream_t stream);
+                              hipStream_t stream, const float *y_bias = nullptr,
+                              bool relu = false);
+
+// One-launch DCNv2 forward with the offset conv inside (fp16 / bf16 on the persistent
+// kernel): y = conv(x, w_off) + b_off (fp32, kept in LDS and written to y_out), offsets
+// y[:, :2T], mask sigmoid(y[:, 2T:]), then the deformable implicit GEMM (+ bias, relu).
+// Returns false (and launches nothing) when the shape does not take the persistent
+// kernel; the caller then runs the offset conv and launch_dcn_fused_nhwc (kGeoYF32).
+bool dcn_mega_supported(int dtype, const DcnGeom &g, int channels_out);
+hipError_t launch_dcn_mega(int dtype, const DcnGeom &g, int channels_out, const void *x,
+                           const void *w_off_packed, const float *b_off,
+                           const void *w_packed, const void *bias, bool relu, float *y_out,
+                           void *out, hipStream_t stream);
 
 // Elements of the packed weight: fp32 Cout * K; half types ceil(Cout/32) * ceil(K/16) * 512.
 int64_t dcn_packed_weight_elems(int dtype, int cout, int K);

@@ -204,6 +204,9 @@ int bevk_modulated_deformable_col2im_nchw(
   if (!data_col || !data_offset || !data_mask || (!grad_im && !grad_offset) ||
       (grad_offset && !data_im))
     return fail(BEVK_ERR_INVALID, "%s: null tensor pointer", fn);
+  // 16-bit grad_im takes packed pair atomics: its first element must start a pair
+  if (grad_im && dtype_size(dtype) == 2 && reinterpret_cast<uintptr_t>(grad_im) % 4 != 0)
+    return fail(BEVK_ERR_INVALID, "%s: 16-bit grad_im must be 4-byte aligned", fn);
   return hip_status(bevk::launch_col2im_nchw(dtype, g, data_col, data_im, data_offset, data_mask,
                                              grad_im, grad_offset, grad_mask,
                                              (hipStream_t)stream),
@@ -419,6 +422,90 @@ int bevk_dcn_fused_fwd_nhwc(int dtype, const void *data_im, const void *data_off
                     fn);
 }
 
+// Shared checks of the offset-conv entry points (dg == 1, fused-kernel dtypes, channel
+// vectors, 32-bit buffer offsets). Returns 0 or the failure code.
+static int check_offset_conv(const char *fn, int dtype, const bevk::DcnGeom &g) {
+  if (dtype != BEVK_F32 && dtype != BEVK_F16 && dtype != BEVK_BF16)
+    return fail(BEVK_ERR_UNSUPPORTED, "\"%s\" not implemented for '%s'", fn, dtype_name(dtype));
+  if (int rc = check_geom(fn, g)) return rc;
+  const int taps = g.kernel_h * g.kernel_w;
+  if (dtype != BEVK_F32 && taps > 9)
+    return fail(BEVK_ERR_UNSUPPORTED,
+                "%s: kernels of more than 9 taps are fp32-only for the offset conv", fn);
+  const int vec = 16 / dtype_size(dtype);
+  if (g.channels <= 0 || g.channels % vec != 0)
+    return fail(BEVK_ERR_UNSUPPORTED,
+                "%s: channels (%d) must be a positive multiple of %d for '%s'", fn, g.channels,
+                vec, dtype_name(dtype));
+  const long long m = (long long)g.batch * g.height_col * g.width_col;
+  if ((long long)g.batch * g.height * g.width * g.channels * dtype_size(dtype) >
+          kMaxBufferBytes ||
+      m >= (1LL << 30))
+    return fail(BEVK_ERR_INVALID, "%s: problem too large for 32-bit buffer offsets", fn);
+  return 0;
+}
+
+int bevk_dcn_offset_conv_nhwc(int dtype, const void *data_im, const void *w_off_packed,
+                              const float *b_off, int batch_size, int channels, int height_im,
+                              int width_im, int height_col, int width_col, int kernel_h,
+                              int kernel_w, int pad_h, int pad_w, int stride_h, int stride_w,
+                              int dilation_h, int dilation_w, float *y, void *stream) {
+  const char *fn = "dcn_offset_conv_nhwc";
+  g_last_error.clear();
+  const bevk::DcnGeom g =
+      make_geom(batch_size, channels, height_im, width_im, height_col, width_col, kernel_h,
+                kernel_w, pad_h, pad_w, stride_h, stride_w, dilation_h, dilation_w, 1);
+  if (int rc = check_offset_conv(fn, dtype, g)) return rc;
+  const int taps = kernel_h * kernel_w;
+  if ((long long)batch_size * height_col * width_col == 0) return ok();
+  if (!data_im || !w_off_packed || !y) return fail(BEVK_ERR_INVALID, "%s: null tensor pointer", fn);
+  return hip_status(bevk::launch_dcn_fused_nhwc(dtype, g, 3 * taps, data_im, nullptr,
+                                                bevk::kGeoRegular, nullptr, w_off_packed, b_off,
+                                                y, (hipStream_t)stream),
+                    fn);
+}
+
+int bevk_dcn_mega_fwd_nhwc(int dtype, const void *data_im, const void *w_off_packed,
+                           const float *b_off, const void *weight_packed, const void *bias,
+                           int batch_size, int channels, int height_im, int width_im,
+                           int height_col, int width_col, int channels_out, int kernel_h,
+                           int kernel_w, int pad_h, int pad_w, int stride_h, int stride_w,
+                           int dilation_h, int dilation_w, int act_relu, float *y, void *out,
+                           void *stream) {
+  const char *fn = "dcn_mega_fwd_nhwc";
+  g_last_error.clear();
+  const bevk::DcnGeom g =
+      make_geom(batch_size, channels, height_im, width_im, height_col, width_col, kernel_h,
+                kernel_w, pad_h, pad_w, stride_h, stride_w, dilation_h, dilation_w, 1);
+  if (int rc = check_offset_conv(fn, dtype, g)) return rc;
+  if (channels_out < 0) return fail(BEVK_ERR_INVALID, "%s: negative channels_out", fn);
+  const int taps = kernel_h * kernel_w;
+  const long long m = (long long)batch_size * height_col * width_col;
+  if (m == 0) return ok();
+  if ((long long)taps * channels * channels_out * dtype_size(dtype) > kMaxBufferBytes ||
+      bevk::dcn_packed_weight_elems(dtype, channels_out, taps * channels) * dtype_size(dtype) >
+          kMaxBufferBytes)
+    return fail(BEVK_ERR_INVALID, "%s: weight too large for 32-bit buffer offsets", fn);
+  if (!data_im || !w_off_packed || !y || (channels_out > 0 && (!weight_packed || !out)))
+    return fail(BEVK_ERR_INVALID, "%s: null tensor pointer", fn);
+  const hipStream_t st = (hipStream_t)stream;
+  if (channels_out > 0 && bevk::dcn_mega_supported(dtype, g, channels_out))
+    return hip_status(bevk::launch_dcn_mega(dtype, g, channels_out, data_im, w_off_packed, b_off,
+                                            weight_packed, bias, act_relu != 0, y, out, st),
+                      fn);
+  // Other shapes: the offset conv (with its bias) into y, then the fused kernel reading y.
+  if (int rc = hip_status(bevk::launch_dcn_fused_nhwc(dtype, g, 3 * taps, data_im, nullptr,
+                                                      bevk::kGeoRegular, nullptr, w_off_packed,
+                                                      b_off, y, st),
+                          fn))
+    return rc;
+  if (channels_out == 0) return ok();
+  return hip_status(bevk::launch_dcn_fused_nhwc(dtype, g, channels_out, data_im, y,
+                                                bevk::kGeoYF32, nullptr, weight_packed, bias,
+                                                out, st, nullptr, act_relu != 0),
+                    fn);
+}
+
 int bevk_msda_forward(int dtype, const void *value, const int64_t *spatial_shapes,
                       const int64_t *level_start_index, const void *sampling_loc,
                       const void *attn_weight, int batch, int spatial_size, int num_heads,
@@ -469,7 +556,6 @@ int bevk_msda_backward(int dtype, const void *value, const int64_t *spatial_shap
                        void *stream) {
   const char *fn = "msda_backward";
   g_last_error.clear();
-  (void)force_generic_col2im;
   if (!valid_dtype(dtype)) return fail(BEVK_ERR_INVALID, "%s: unknown dtype code %d", fn, dtype);
   if (batch < 0 || spatial_size < 0 || num_heads < 0 || channels < 0 || num_levels < 0 ||
       num_query < 0 || num_point < 0)
@@ -508,7 +594,8 @@ int bevk_msda_backward(int dtype, const void *value, const int64_t *spatial_shap
   a.go_stride[2] = go_stride_h; a.go_stride[3] = go_stride_c;
   a.grad_value = grad_value; a.grad_loc = grad_sampling_loc; a.grad_attn = grad_attn_weight;
   a.workspace = workspace;
-  return hip_status(bevk::launch_msda_backward(dtype, a, (hipStream_t)stream), fn);
+  return hip_status(
+      bevk::launch_msda_backward(dtype, a, force_generic_col2im != 0, (hipStream_t)stream), fn);
 }
 
 }  // extern "C"

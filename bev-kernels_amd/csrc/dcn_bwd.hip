@@ -143,19 +143,23 @@ __device__ __forceinline__ void atomic_add_elem(float *p, float v) { unsafeAtomi
 __device__ __forceinline__ void atomic_add_elem(double *p, double v) { unsafeAtomicAdd(p, v); }
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef short short2v __attribute__((ext_vector_type(2)));
-// 16-bit types: a packed add on the aligned pair, zero into the neighbour.
+// 16-bit types: a packed add on the aligned pair with -0.0 into the neighbour, the exact
+// additive identity (x + -0.0 == x for every x, -0.0 and +0.0 included), so the
+// neighbour keeps its bits. The entry point requires a 4-byte-aligned grad_im, so the
+// first element has no neighbour before the buffer.
+constexpr short kNegZero16 = (short)0x8000;  // -0.0 in fp16 and in bf16
 __device__ __forceinline__ void atomic_add_elem(f16 *p, float v) {
   const uintptr_t a = reinterpret_cast<uintptr_t>(p);
   half2v *pair = reinterpret_cast<half2v *>(a & ~(uintptr_t)3);
-  const f16 h = (f16)v;
-  half2v d = (a & 2) ? half2v{(f16)0.f, h} : half2v{h, (f16)0.f};
+  const f16 h = (f16)v, nz = __builtin_bit_cast(f16, kNegZero16);
+  half2v d = (a & 2) ? half2v{nz, h} : half2v{h, nz};
   __builtin_amdgcn_global_atomic_fadd_v2f16(pair, d);
 }
 __device__ __forceinline__ void atomic_add_elem(bf16 *p, float v) {
   const uintptr_t a = reinterpret_cast<uintptr_t>(p);
   short2v *pair = reinterpret_cast<short2v *>(a & ~(uintptr_t)3);
   const short b = __builtin_bit_cast(short, (bf16)v);
-  short2v d = (a & 2) ? short2v{0, b} : short2v{b, 0};
+  short2v d = (a & 2) ? short2v{kNegZero16, b} : short2v{b, kNegZero16};
   __builtin_amdgcn_global_atomic_fadd_v2bf16(pair, d);
 }
 

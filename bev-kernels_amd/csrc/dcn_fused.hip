@@ -40,6 +40,8 @@ struct FusedParams {
   const void *w;
   const void *bias;
   void *out;
+  const float *yb;  // kGeoYF32: fp32 bias of y (or null)
+  int relu;         // max(out, 0) in the epilogue
   int B, C, H, W, Ho, Wo, Cout, kh, kw, ph, pw, sh, sw, dh, dw;
   int M, K;
   int tiles_m;
@@ -72,8 +74,8 @@ template <> struct Mfma<float> {
 // chunk, lanes 32-63 the second).
 template <typename T> constexpr int lane_k() { return Mfma<T>::KSTEP / 2; }
 
-// GEO: kGeoMask, kGeoY or kGeoRegular (see bevk_launch.h); kGeoRegular is used with
-// T = float only (the fp32 offset conv of the fused front end).
+// GEO: kGeoMask, kGeoY, kGeoYF32 or kGeoRegular (bevk_common.h); kGeoRegular is used
+// with T = float only (the fp32 offset conv of the fused front end, fp32 bias).
 template <typename T, int BM, int BN, int BK, int WAVES_M, int WAVES_N, int GEO>
 __global__ void __launch_bounds__(kThreads) dcn_fused_nhwc_kernel(const FusedParams p) {
   constexpr int VEC = 16 / sizeof(T);
@@ -155,17 +157,7 @@ __global__ void __launch_bounds__(kThreads) dcn_fused_nhwc_kernel(const FusedPar
       }
     } else if (m >= 0 && t < T_) {
       float dy, dx, mk;
-      const T *offp = static_cast<const T *>(p.off);
-      if constexpr (GEO == kGeoY) {
-        const T *yp = offp + (int64_t)m * 3 * T_;
-        dy = (float)yp[2 * t];
-        dx = (float)yp[2 * t + 1];
-        mk = sigmoid_f32((float)yp[2 * T_ + t]);
-      } else {
-        dy = (float)offp[(int64_t)m * 2 * T_ + 2 * t];
-        dx = (float)offp[(int64_t)m * 2 * T_ + 2 * t + 1];
-        mk = (float)static_cast<const T *>(p.msk)[(int64_t)m * T_ + t];
-      }
+      tap_offsets<T, GEO>(p.off, p.msk, p.yb, m, t, T_, dy, dx, mk);
       const int ki = t / p.kw, kj = t - (t / p.kw) * p.kw;
       const float h = (float)(a_hb[i] + ki * p.dh) + dy;
       const float w = (float)(a_wb[i] + kj * p.dw) + dx;
@@ -296,7 +288,9 @@ __global__ void __launch_bounds__(kThreads) dcn_fused_nhwc_kernel(const FusedPar
       for (int e = 0; e < 16; ++e) {
         const int row = wm * WTM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
         const int m = m0 + row;
-        if (m < p.M && n < p.Cout) out[(int64_t)m * p.Cout + n] = static_cast<T>(acc[i][j][e] + bv);
+        float v = acc[i][j][e] + bv;
+        if (GEO != kGeoRegular && p.relu) v = v < 0.f ? 0.f : v;  // NaN stays NaN
+        if (m < p.M && n < p.Cout) out[(int64_t)m * p.Cout + n] = static_cast<T>(v);
       }
     }
   }
@@ -307,6 +301,9 @@ hipError_t launch_cfg(const FusedParams &p, int geo, hipStream_t stream) {
   dim3 grid(p.tiles_m, (p.Cout + BN - 1) / BN);
   if (geo == kGeoY)
     hipLaunchKernelGGL((dcn_fused_nhwc_kernel<T, BM, BN, BK, WM, WN, kGeoY>), grid,
+                       dim3(kThreads), 0, stream, p);
+  else if (geo == kGeoYF32)
+    hipLaunchKernelGGL((dcn_fused_nhwc_kernel<T, BM, BN, BK, WM, WN, kGeoYF32>), grid,
                        dim3(kThreads), 0, stream, p);
   else if (geo == kGeoRegular && sizeof(T) == 4)
     hipLaunchKernelGGL((dcn_fused_nhwc_kernel<T, BM, BN, BK, WM, WN, kGeoRegular>), grid,
@@ -334,13 +331,14 @@ hipError_t launch_t(FusedParams p, int geo, hipStream_t stream) {
 hipError_t launch_dcn_fused_nhwc(int dtype, const DcnGeom &g, int channels_out, const void *x,
                                  const void *off, int geo, const void *msk,
                                  const void *w_packed, const void *bias, void *out,
-                                 hipStream_t stream) {
+                                 hipStream_t stream, const float *y_bias, bool relu) {
   if (dtype != 0 && dcn_fused_h_supported(g))
     return launch_dcn_fused_h(dtype, g, channels_out, x, off, geo, msk, w_packed, bias, out,
-                              stream);
+                              stream, y_bias, relu);
   if (dtype != 0 && geo == kGeoRegular) return hipErrorInvalidValue;  // fp32 output only
   FusedParams p;
   p.x = x; p.off = off; p.msk = msk; p.w = w_packed; p.bias = bias; p.out = out;
+  p.yb = y_bias; p.relu = relu ? 1 : 0;
   p.B = g.batch; p.C = g.channels; p.H = g.height; p.W = g.width;
   p.Ho = g.height_col; p.Wo = g.width_col; p.Cout = channels_out;
   p.kh = g.kernel_h; p.kw = g.kernel_w; p.ph = g.pad_h; p.pw = g.pad_w;

@@ -9,8 +9,8 @@
 //     bilinear x mask weights, once, in LDS.
 //   * A operand: per K step (BK = 64 channels of one tap) each thread gathers 16-byte
 //     vectors of the four corner rows of its (row, k-vector) slots with buffer loads
-//     (8 lanes cover 128 contiguous bytes of a pixel), blends them (packed fp16 FMA, or
-//     fp32 FMA for bf16) and writes the A tile to double-buffered LDS.
+//     (8 lanes cover 128 contiguous bytes of a pixel), blends them in fp32 with one
+//     rounding to T (blend4) and writes the A tile to double-buffered LDS.
 //   * B operand: the weight is pre-packed in MFMA fragment order, so every B fragment is
 //     one coalesced 1 KB load straight into registers (double-buffered across K steps).
 //     LDS only carries the A tile.
@@ -21,13 +21,14 @@
 #include "bevk_common.h"
 #include "bevk_launch.h"
 
+#include <type_traits>
+
 namespace bevk {
 namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
-typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef int int4v __attribute__((ext_vector_type(4)));
 
 constexpr int kMaxTaps = 9;
@@ -35,10 +36,18 @@ constexpr int kMaxTaps = 9;
 struct HParams {
   const void *x, *off, *msk, *w, *bias;
   void *out;
+  const float *yb;               // kGeoYF32: fp32 bias of y (or null)
+  int relu;                      // max(out, 0) in the epilogue
   int C, H, W, Ho, Wo, Cout, kh, kw, ph, pw, sh, sw, dh, dw, M, K;
   int taps, nb_total, kb_total;  // packed weight blocks: [nb_total][kb_total][64][16 B]
   int mt, nt, tiles_per_xcd;     // output tiles (M x N) and tiles per XCD
   uint32_t x_bytes, w_bytes;
+  // offset conv of the one-launch forward: packed w_off (3T <= 32 columns, one 32-column
+  // fragment block), its fp32 bias and the fp32 y [M][3T] written out (or null)
+  const void *w2;
+  const float *b2;
+  float *y_out;
+  uint32_t w2_bytes;
 };
 
 template <typename T> __device__ __forceinline__ floatx16 mfma16(const T *a, int4v b, floatx16 c);
@@ -56,9 +65,89 @@ struct TapGeo {
   uint32_t o[4];
 };
 
+// A tap that contributes nothing: zero weights, every corner out of range.
+__device__ __forceinline__ TapGeo empty_geo(uint32_t oob) {
+  TapGeo G;
+  G.w[0] = G.w[1] = G.w[2] = G.w[3] = 0.f;
+  G.o[0] = G.o[1] = G.o[2] = G.o[3] = oob;
+  return G;
+}
+
+// Deformable sample at (h, w) of image b: corner byte offsets (row = C elements of T) and
+// mask-folded bilinear weights. The whole sample is zero unless -1 < h < H and -1 < w < W
+// (modulated_deform_conv.py:256-258); each corner outside the image is zero
+// (fused_tl.py:146-174, dcn_fused_nhwc_kernel.cuh:140-187).
+template <typename T>
+__device__ __forceinline__ TapGeo deform_geo(float h, float w, float mk, int b, int H, int W,
+                                             int C, uint32_t oob) {
+  TapGeo G = empty_geo(oob);
+  if (h > -1.f && w > -1.f && h < (float)H && w < (float)W) {
+    const float fh = floorf(h), fw = floorf(w);
+    const int hl = (int)fh, wl = (int)fw;
+    const float lh = h - fh, lw = w - fw, hh = 1.f - lh, hw = 1.f - lw;
+    const uint32_t rowb = (uint32_t)C * (uint32_t)sizeof(T);
+    const uint32_t base = (uint32_t)(b * H * W + hl * W + wl) * rowb;
+    const bool y0 = hl >= 0, y1 = hl + 1 <= H - 1, x0 = wl >= 0, x1 = wl + 1 <= W - 1;
+    if (y0 && x0) { G.w[0] = hh * hw * mk; G.o[0] = base; }
+    if (y0 && x1) { G.w[1] = hh * lw * mk; G.o[1] = base + rowb; }
+    if (y1 && x0) { G.w[2] = lh * hw * mk; G.o[2] = base + (uint32_t)W * rowb; }
+    if (y1 && x1) { G.w[3] = lh * lw * mk; G.o[3] = base + (uint32_t)(W + 1) * rowb; }
+  }
+  return G;
+}
+
+// Plain convolution tap (the offset conv): the one in-image pixel with weight 1.
+template <typename T>
+__device__ __forceinline__ TapGeo regular_geo(int h, int w, int b, int H, int W, int C,
+                                              uint32_t oob) {
+  TapGeo G = empty_geo(oob);
+  if (h >= 0 && h < H && w >= 0 && w < W) {
+    G.w[0] = 1.f;
+    G.o[0] = (uint32_t)(b * H * W + h * W + w) * (uint32_t)C * (uint32_t)sizeof(T);
+  }
+  return G;
+}
+
+// Geometry of tap t of output row m (m < M) in form GEO; for the y forms `off` is y.
+template <typename T, int GEO>
+__device__ __forceinline__ TapGeo tap_geo(const HParams &p, const void *off, int64_t ym, int m,
+                                          int t) {
+  const int HoWo = p.Ho * p.Wo;
+  const int b = m / HoWo, r = m - b * HoWo, oh = r / p.Wo, ow = r - (r / p.Wo) * p.Wo;
+  const int ki = t / p.kw, kj = t - (t / p.kw) * p.kw;
+  const int h0 = oh * p.sh - p.ph + ki * p.dh, w0 = ow * p.sw - p.pw + kj * p.dw;
+  if constexpr (GEO == kGeoRegular) {
+    return regular_geo<T>(h0, w0, b, p.H, p.W, p.C, p.x_bytes);
+  } else {
+    float dy, dx, mk;
+    tap_offsets<T, GEO>(off, p.msk, p.yb, ym, t, p.taps, dy, dx, mk);
+    return deform_geo<T>((float)h0 + dy, (float)w0 + dx, mk, b, p.H, p.W, p.C, p.x_bytes);
+  }
+}
+
+// One A-tile vector: sum_q w_q * corner_q in fp32 (the corners converted exactly), rounded
+// once to T, as the reference's gather does (dcn_fused_nhwc_kernel.cuh:185-187,
+// fused_tl.py:128-133). For fp16 the compiler takes the corners straight from their
+// halves (v_fma_mix_f32); the fma with a zero addend keeps the first product in that form.
+template <typename T>
+__device__ __forceinline__ Vec<T, 8> blend4(const Vec<T, 8> (&c)[4], float w0, float w1,
+                                            float w2, float w3) {
+  Vec<T, 8> o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float s = __builtin_fmaf(w0, (float)c[0].v[e], 0.f);
+    s = __builtin_fmaf(w1, (float)c[1].v[e], s);
+    s = __builtin_fmaf(w2, (float)c[2].v[e], s);
+    s = __builtin_fmaf(w3, (float)c[3].v[e], s);
+    o.v[e] = static_cast<T>(s);
+  }
+  return o;
+}
+
 // GEO: kGeoMask (offsets [M][2T] + mask [M][T]), kGeoY (raw offset-conv output [M][3T],
-// sigmoid of the mask part here) or kGeoRegular (no offsets: a plain convolution, used for
-// the offset conv of the fused front end). OutT: T, or float for the offset conv.
+// sigmoid of the mask part here), kGeoYF32 (the same from an fp32 y plus its fp32 bias) or
+// kGeoRegular (no offsets: a plain convolution, used for the offset conv; fp32 bias and
+// output). OutT: T, or float for the offset conv.
 // TAPSTEP: C % BK == 0, so every K step lies inside one tap and a thread keeps its corner
 // offsets and weights in registers from one tap to the next.
 template <typename T, typename OutT, int BM, int BN, int BK, int WM_, int WN_, int GEO,
@@ -80,7 +169,7 @@ dcn_fused_h_kernel(const HParams p) {
   if ((int)(blockIdx.x >> 3) >= p.tiles_per_xcd || tile >= p.mt * p.nt) return;
   const int mtile = tile / p.nt;
   const int m0 = mtile * BM, n0 = (tile - mtile * p.nt) * BN;
-  const int HoWo = p.Ho * p.Wo, TT = p.taps;
+  const int TT = p.taps;
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, p.x_bytes);
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, p.w_bytes);
   const uint32_t xoob = p.x_bytes, woob = p.w_bytes;
@@ -88,48 +177,7 @@ dcn_fused_h_kernel(const HParams p) {
   // ---- geometry table -------------------------------------------------------------
   for (int g = tid; g < BM * TT; g += NT) {
     const int row = g / TT, t = g - row * TT, m = m0 + row;
-    TapGeo G;
-    G.w[0] = G.w[1] = G.w[2] = G.w[3] = 0.f;
-    G.o[0] = G.o[1] = G.o[2] = G.o[3] = xoob;
-    if (GEO == kGeoRegular && m < p.M) {
-      const int b = m / HoWo, r = m - b * HoWo, oh = r / p.Wo, ow = r - (r / p.Wo) * p.Wo;
-      const int ki = t / p.kw, kj = t - (t / p.kw) * p.kw;
-      const int h = oh * p.sh - p.ph + ki * p.dh, w = ow * p.sw - p.pw + kj * p.dw;
-      if (h >= 0 && h < p.H && w >= 0 && w < p.W) {
-        G.w[0] = 1.f;
-        G.o[0] = (uint32_t)(b * p.H * p.W + h * p.W + w) * (uint32_t)p.C * (uint32_t)sizeof(T);
-      }
-    } else if (m < p.M) {
-      const int b = m / HoWo, r = m - b * HoWo, oh = r / p.Wo, ow = r - (r / p.Wo) * p.Wo;
-      float dy, dx, mk;
-      const T *op = static_cast<const T *>(p.off);
-      if constexpr (GEO == kGeoY) {
-        const T *yp = op + (int64_t)m * 3 * TT;
-        dy = (float)yp[2 * t];
-        dx = (float)yp[2 * t + 1];
-        mk = sigmoid_f32((float)yp[2 * TT + t]);
-      } else {
-        dy = (float)op[(int64_t)m * 2 * TT + 2 * t];
-        dx = (float)op[(int64_t)m * 2 * TT + 2 * t + 1];
-        mk = (float)static_cast<const T *>(p.msk)[(int64_t)m * TT + t];
-      }
-      const int ki = t / p.kw, kj = t - (t / p.kw) * p.kw;
-      const float h = (float)(oh * p.sh - p.ph + ki * p.dh) + dy;
-      const float w = (float)(ow * p.sw - p.pw + kj * p.dw) + dx;
-      if (h > -1.f && w > -1.f && h < (float)p.H && w < (float)p.W) {
-        const float fh = floorf(h), fw = floorf(w);
-        const int hl = (int)fh, wl = (int)fw;
-        const float lh = h - fh, lw = w - fw, hh = 1.f - lh, hw = 1.f - lw;
-        const uint32_t rowb = (uint32_t)p.C * (uint32_t)sizeof(T);
-        const uint32_t base = (uint32_t)(b * p.H * p.W + hl * p.W + wl) * rowb;
-        const bool y0 = hl >= 0, y1 = hl + 1 <= p.H - 1, x0 = wl >= 0, x1 = wl + 1 <= p.W - 1;
-        if (y0 && x0) { G.w[0] = hh * hw * mk; G.o[0] = base; }
-        if (y0 && x1) { G.w[1] = hh * lw * mk; G.o[1] = base + rowb; }
-        if (y1 && x0) { G.w[2] = lh * hw * mk; G.o[2] = base + (uint32_t)p.W * rowb; }
-        if (y1 && x1) { G.w[3] = lh * lw * mk; G.o[3] = base + (uint32_t)(p.W + 1) * rowb; }
-      }
-    }
-    geo[g] = G;
+    geo[g] = m < p.M ? tap_geo<T, GEO>(p, p.off, m, m, t) : empty_geo(xoob);
   }
   __syncthreads();
 
@@ -237,24 +285,8 @@ dcn_fused_h_kernel(const HParams p) {
       V o;
       if constexpr (GEO == kGeoRegular) {
         o = ra[i][0];  // weight 1 on the one in-range pixel; 0 (read as 0) outside
-      } else if constexpr (__is_same(T, f16)) {
-        const half2v w1 = {(f16)rw[i][0], (f16)rw[i][0]}, w2 = {(f16)rw[i][1], (f16)rw[i][1]};
-        const half2v w3 = {(f16)rw[i][2], (f16)rw[i][2]}, w4 = {(f16)rw[i][3], (f16)rw[i][3]};
-#pragma unroll
-        for (int e = 0; e < VEC; e += 2) {
-          const half2v v1 = {ra[i][0].v[e], ra[i][0].v[e + 1]};
-          const half2v v2 = {ra[i][1].v[e], ra[i][1].v[e + 1]};
-          const half2v v3 = {ra[i][2].v[e], ra[i][2].v[e + 1]};
-          const half2v v4 = {ra[i][3].v[e], ra[i][3].v[e + 1]};
-          const half2v r = w1 * v1 + w2 * v2 + w3 * v3 + w4 * v4;
-          o.v[e] = r.x;
-          o.v[e + 1] = r.y;
-        }
       } else {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e)
-          o.v[e] = static_cast<T>(rw[i][0] * (float)ra[i][0].v[e] + rw[i][1] * (float)ra[i][1].v[e] +
-                                  rw[i][2] * (float)ra[i][2].v[e] + rw[i][3] * (float)ra[i][3].v[e]);
+        o = blend4<T>(ra[i], rw[i][0], rw[i][1], rw[i][2], rw[i][3]);
       }
       store_vec<T, VEC>(&As[buf][a_row[i] * LDA + a_kv[i] * VEC], o);
     }
@@ -309,7 +341,8 @@ dcn_fused_h_kernel(const HParams p) {
 
   // ---- epilogue: lane holds col = lane % 32, rows 8*(e/4) + 4*(lane/32) + e%4 --------
   OutT *out = static_cast<OutT *>(p.out);
-  const T *bias = static_cast<const T *>(p.bias);
+  using BiasT = typename std::conditional<GEO == kGeoRegular, float, T>::type;
+  const BiasT *bias = static_cast<const BiasT *>(p.bias);
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const int n = n0 + (wn * TN + j) * 32 + lrow;
@@ -319,7 +352,9 @@ dcn_fused_h_kernel(const HParams p) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int m = m0 + wm * WTM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-        if (m < p.M && n < p.Cout) out[(int64_t)m * p.Cout + n] = static_cast<OutT>(acc[i][j][e] + bv);
+        float v = acc[i][j][e] + bv;
+        if (GEO != kGeoRegular && p.relu) v = v < 0.f ? 0.f : v;  // NaN stays NaN
+        if (m < p.M && n < p.Cout) out[(int64_t)m * p.Cout + n] = static_cast<OutT>(v);
       }
   }
 }
@@ -371,6 +406,9 @@ hipError_t launch_cfg(HParams p, int geo, hipStream_t stream) {
   if (geo == kGeoY)
     hipLaunchKernelGGL((dcn_fused_h_kernel<T, OutT, BM, BN, BK, WM, WN, kGeoY, TAPSTEP>), grid,
                        block, 0, stream, p);
+  else if (geo == kGeoYF32)
+    hipLaunchKernelGGL((dcn_fused_h_kernel<T, OutT, BM, BN, BK, WM, WN, kGeoYF32, TAPSTEP>),
+                       grid, block, 0, stream, p);
   else if (geo == kGeoRegular)
     hipLaunchKernelGGL((dcn_fused_h_kernel<T, OutT, BM, BN, BK, WM, WN, kGeoRegular, TAPSTEP>),
                        grid, block, 0, stream, p);
@@ -444,28 +482,33 @@ struct PParams {
   int halves;    // 256-column halves of Cout (1 or 2): XCDs 0-3 take half 0, 4-7 half 1
 };
 
+// B fragment of v_mfma_f32_16x16x32 read from the 32x32x16 fragment packing: lane l takes
+// column n and k = 32 kh + 8 (l >> 4) .. + 8 of a K step, i.e. block (n / 32, 2 kh +
+// (l >> 5)), lane (n % 32) + 32 ((l >> 4) & 1) of the packing.
+__device__ __forceinline__ uint32_t b_frag_offset(int n, int kh, int lane, int nb_total,
+                                                  int kb_total, uint32_t oob) {
+  const int nb = n >> 5;
+  return nb < nb_total ? ((uint32_t)(nb * kb_total + 2 * kh + (lane >> 5)) * 64u +
+                          (uint32_t)((n & 31) + 32 * ((lane >> 4) & 1))) * 16u
+                       : oob;
+}
+
 // Consumer wave c: B(k+1) issued at step k, MFMA(k) from A buffer k % 2, one barrier per
-// step; then the epilogue. Always 9 row blocks (compile-time, so the MFMA loop and the
-// accumulators carry no run-time conditions); nrb row blocks are stored.
+// step; then the epilogue (bias, relu, one rounding). Always NRB row blocks (compile-time,
+// so the MFMA loop and the accumulators carry no run-time conditions); nrb row blocks are
+// stored.
 template <typename T, int NRB>
 __device__ __forceinline__ void dcn_p_consumer(const HParams &p, T (*As)[NRB * 16 * kPLDA],
                                                int m0, int nrb, int n0, int nk, int lane,
                                                int wave) {
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, p.w_bytes);
-  const uint32_t woob = p.w_bytes;
-  // B fragments (16x16x32, read from the 32x32x16 fragment packing): lane l takes column
-  // n = 64 wave + 16 cb + (l & 15) and k = k0 + 8 (l >> 4) .. + 8 of the step.
   uint32_t bo[kPKH][4];
 #pragma unroll
   for (int kh = 0; kh < kPKH; ++kh)
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb) {
-      const int n = n0 + wave * 64 + cb * 16 + (lane & 15);
-      const int nb = n >> 5;
-      bo[kh][cb] = nb < p.nb_total ? ((uint32_t)(nb * p.kb_total + 2 * kh + (lane >> 5)) * 64u +
-                                      (uint32_t)((n & 31) + 32 * ((lane >> 4) & 1))) * 16u
-                                   : woob;
-    }
+    for (int cb = 0; cb < 4; ++cb)
+      bo[kh][cb] = b_frag_offset(n0 + wave * 64 + cb * 16 + (lane & 15), kh, lane, p.nb_total,
+                                 p.kb_total, p.w_bytes);
   auto issue_b = [&](int ks, int4v (&br)[kPKH][4]) __attribute__((always_inline)) {
 #pragma unroll
     for (int kh = 0; kh < kPKH; ++kh)
@@ -516,86 +559,152 @@ __device__ __forceinline__ void dcn_p_consumer(const HParams &p, T (*As)[NRB * 1
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int m = m0 + rbi * 16 + 4 * (lane >> 4) + e;
+        float v = acc[rbi][cb][e] + bv;
+        if (p.relu) v = v < 0.f ? 0.f : v;  // NaN stays NaN, as torch.relu
         if (rbi < nrb && m < p.M && n < p.Cout)
-          out[(int64_t)m * p.Cout + n] = static_cast<T>(acc[rbi][cb][e] + bv);
+          out[(int64_t)m * p.Cout + n] = static_cast<T>(v);
       }
+  }
+}
+
+// Offset conv of the one-launch forward, consumer side: y[row][n] = sum_k A[row, k] *
+// Woff[n, k] + b_off[n] for the workgroup's NRB * 16 rows and n < 32 (3T <= 27 used), in
+// fp32. Wave c takes the row blocks c, c + 4, c + 8 (a block past NRB repeats the last
+// one and is not stored, so no MFMA is conditional) and both 16-column blocks; every wave
+// loads the same B fragments (4 per step). At the end y goes to ys (LDS, row pitch 3T) and
+// to p.y_out when that is given. Same barrier sequence as dcn_p_consumer.
+template <typename T, int NRB>
+__device__ __forceinline__ void dcn_p_offset_consumer(const HParams &p,
+                                                      T (*As)[NRB * 16 * kPLDA], float *ys,
+                                                      int m0, int nrb, int nk, int lane,
+                                                      int wave) {
+  constexpr int RB = (NRB + 3) / 4;
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w2, p.w2_bytes);
+  const int kb2 = p.K / 16;
+  uint32_t bo[kPKH][2];
+#pragma unroll
+  for (int kh = 0; kh < kPKH; ++kh)
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+      bo[kh][cb] = b_frag_offset(cb * 16 + (lane & 15), kh, lane, 1, kb2, p.w2_bytes);
+  auto issue_b = [&](int ks, int4v (&br)[kPKH][2]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int kh = 0; kh < kPKH; ++kh)
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb)
+        br[kh][cb] = __builtin_amdgcn_raw_buffer_load_b128(
+            wr, bo[kh][cb], (uint32_t)ks * (uint32_t)(kPBK / 16) * 1024u, 0);
+  };
+  floatx4 acc[RB][2];
+#pragma unroll
+  for (int i = 0; i < RB; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  int4v br[kPKH][2];
+  issue_b(0, br);
+  __syncthreads();  // A(0) written by the producers
+  for (int ks = 0; ks < nk; ++ks) {
+    const int buf = ks & 1;
+#pragma unroll
+    for (int kh = 0; kh < kPKH; ++kh) {
+      int4v af[RB];
+#pragma unroll
+      for (int i = 0; i < RB; ++i) {
+        const int rb = min(wave + 4 * i, NRB - 1);
+        af[i] = *reinterpret_cast<const int4v *>(
+            &As[buf][(rb * 16 + (lane & 15)) * kPLDA + kh * 32 + 8 * (lane >> 4)]);
+      }
+#pragma unroll
+      for (int i = 0; i < RB; ++i)
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) acc[i][cb] = mfma16x16<T>(af[i], br[kh][cb], acc[i][cb]);
+    }
+    issue_b(ks + 1, br);
+    __syncthreads();
+  }
+  // The last barrier above ends every read and write of the A ring: ys may alias it.
+  const int n3 = 3 * p.taps;
+#pragma unroll
+  for (int i = 0; i < RB; ++i) {
+    const int rb = wave + 4 * i;
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      const int n = cb * 16 + (lane & 15);
+      const float bv = (n < n3 && p.b2 != nullptr) ? p.b2[n] : 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = rb * 16 + 4 * (lane >> 4) + e;
+        if (rb < nrb && n < n3) {
+          const float v = acc[i][cb][e] + bv;
+          ys[row * n3 + n] = v;
+          if (p.y_out != nullptr && m0 + row < p.M) p.y_out[(int64_t)(m0 + row) * n3 + n] = v;
+        }
+      }
+    }
   }
 }
 
 // Producer thread ptid (0..255) with NS gather slots: slot i is (row, k-vector) =
 // (s / KV, s % KV), s = ptid + 256 i. The gathers of step k + 2 are issued at step k into
 // register set k % 2 (blended at step k - 1); A(k+1) is blended at step k from set
-// (k+1) % 2 into buffer (k+1) % 2. Every
-// load is issued unconditionally (steps past the end read out of range), so the compiler's
-// wait counts stay exact and the gathers of the next steps stay in flight.
-template <typename T, int NS, int NRB>
+// (k+1) % 2 into buffer (k+1) % 2. Every load is issued unconditionally (steps past the end
+// read out of range), so the compiler's wait counts stay exact and the gathers of the next
+// steps stay in flight. REG: plain convolution taps (one pixel per slot, no blend).
+template <typename T, int NS, int NRB, bool REG>
 __device__ __forceinline__ void dcn_p_producer(const HParams &p, const TapGeo *geo,
                                                T (*As)[NRB * 16 * kPLDA], int nk, int ptid) {
   using V = Vec<T, 8>;
   constexpr int KV = kPBK / 8;
+  constexpr int NQ = REG ? 1 : 4;
   const int TT = p.taps;
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, p.x_bytes);
   const uint32_t xoob = p.x_bytes;
   const int kv = ptid % KV;
   const int spt = p.C / kPBK;  // K steps per tap
-  uint32_t go[NS][4];          // corner offsets of the tap being issued (+ k-vector)
+  uint32_t go[NS][NQ];         // corner offsets of the tap being issued (+ k-vector)
   auto load_geo = [&](int t) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
       if (t < TT) {
         const TapGeo &G = geo[((ptid + i * kPProd) / KV) * TT + t];
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
+        for (int q = 0; q < NQ; ++q)
           go[i][q] = G.o[q] == xoob ? xoob : G.o[q] + (uint32_t)(kv * 8 * sizeof(T));
       } else {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) go[i][q] = xoob;
+        for (int q = 0; q < NQ; ++q) go[i][q] = xoob;
       }
     }
   };
-  auto issue_gather = [&](int ks, V (&ra)[NS][4]) __attribute__((always_inline)) {
+  auto issue_gather = [&](int ks, V (&ra)[NS][NQ]) __attribute__((always_inline)) {
     const int t = ks / spt, cs = ks - t * spt;
     if (cs == 0) load_geo(t);
     const uint32_t so = (uint32_t)(cs * kPBK * sizeof(T));
 #pragma unroll
     for (int i = 0; i < NS; ++i)
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
+      for (int q = 0; q < NQ; ++q)
         ra[i][q] = __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(xr, go[i][q], so, 0));
   };
-  auto blend = [&](int ks, const V (&ra)[NS][4], int buf) __attribute__((always_inline)) {
+  auto blend = [&](int ks, const V (&ra)[NS][NQ], int buf) __attribute__((always_inline)) {
     // Past the last step the gathered corners are zero (out-of-range offsets); the tap is
     // clamped so the weight read stays inside the table.
     const int t = min(ks / spt, TT - 1);
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
       const int row = (ptid + i * kPProd) / KV;
-      const float4 w = *reinterpret_cast<const float4 *>(geo[row * TT + t].w);
       V o;
-      if constexpr (__is_same(T, f16)) {
-        const half2v w1 = {(f16)w.x, (f16)w.x}, w2 = {(f16)w.y, (f16)w.y};
-        const half2v w3 = {(f16)w.z, (f16)w.z}, w4 = {(f16)w.w, (f16)w.w};
-#pragma unroll
-        for (int e = 0; e < 8; e += 2) {
-          const half2v v1 = {ra[i][0].v[e], ra[i][0].v[e + 1]};
-          const half2v v2 = {ra[i][1].v[e], ra[i][1].v[e + 1]};
-          const half2v v3 = {ra[i][2].v[e], ra[i][2].v[e + 1]};
-          const half2v v4 = {ra[i][3].v[e], ra[i][3].v[e + 1]};
-          const half2v rr = w1 * v1 + w2 * v2 + w3 * v3 + w4 * v4;
-          o.v[e] = rr.x;
-          o.v[e + 1] = rr.y;
-        }
+      if constexpr (REG) {
+        o = ra[i][0];  // the in-image pixel, or zeros read out of range
       } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          o.v[e] = static_cast<T>(w.x * (float)ra[i][0].v[e] + w.y * (float)ra[i][1].v[e] +
-                                  w.z * (float)ra[i][2].v[e] + w.w * (float)ra[i][3].v[e]);
+        const float4 w = *reinterpret_cast<const float4 *>(geo[row * TT + t].w);
+        o = blend4<T>(ra[i], w.x, w.y, w.z, w.w);
       }
       store_vec<T, 8>(&As[buf][row * kPLDA + kv * 8], o);
     }
   };
-  V ra0[NS][4], ra1[NS][4];
-  auto step = [&](int ks, V (&ra_issue)[NS][4], const V (&ra_blend)[NS][4])
+  V ra0[NS][NQ], ra1[NS][NQ];
+  auto step = [&](int ks, V (&ra_issue)[NS][NQ], const V (&ra_blend)[NS][NQ])
       __attribute__((always_inline)) {
     issue_gather(ks + 2, ra_issue);
     blend(ks + 1, ra_blend, (ks + 1) & 1);
@@ -613,13 +722,20 @@ __device__ __forceinline__ void dcn_p_producer(const HParams &p, const TapGeo *g
   if (k0 < nk) step(k0, ra0, ra1);
 }
 
-template <typename T, int GEO, int NRB>
+// GEO: kGeoMask, kGeoY or kGeoYF32 (read from global memory). MEGA: the one-launch
+// forward; a first pass over K computes the offset conv of the workgroup's rows on the
+// matrix cores (dcn_p_offset_consumer + plain-convolution producers), its fp32 output
+// with bias is kept in LDS (aliasing the A ring) and the deformable geometry is built from
+// it, as the reference's single-kernel forward does (fused_tl.py:565-688).
+template <typename T, int GEO, int NRB, bool MEGA>
 __global__ void __launch_bounds__(kPThreads) dcn_fused_p_kernel(const PParams pp) {
   using SH = PShape<NRB>;
   constexpr int kPRows = SH::kRows;
   const HParams &p = pp.h;
   __shared__ __attribute__((aligned(16))) TapGeo geo[kPRows * kMaxTaps];
   __shared__ __attribute__((aligned(16))) T As[2][kPRows * kPLDA];
+  static_assert(!MEGA || sizeof(As) >= sizeof(float) * kPRows * 3 * kMaxTaps,
+                "the offset-conv output must fit in the A ring");
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -637,73 +753,63 @@ __global__ void __launch_bounds__(kPThreads) dcn_fused_p_kernel(const PParams pp
   const int n0 = half * kPCols;
   const int m0 = rb0 * 16;
   const int nrows = nrb * 16;
-  const int HoWo = p.Ho * p.Wo, TT = p.taps;
+  const int TT = p.taps;
   const uint32_t xoob = p.x_bytes;
+  const int nk = TT * (p.C / kPBK);
+  float *ys = reinterpret_cast<float *>(&As[0][0]);
+
+  if constexpr (MEGA) {
+    // Pass 1: the offset conv. Plain-convolution geometry (one pixel per row and tap).
+    for (int g = tid; g < kPRows * TT; g += kPThreads) {
+      const int row = g / TT, t = g - row * TT, m = m0 + row;
+      geo[g] = (row < nrows && m < p.M) ? tap_geo<T, kGeoRegular>(p, nullptr, 0, m, t)
+                                        : empty_geo(xoob);
+    }
+    __syncthreads();
+    if (wave < 4)
+      dcn_p_offset_consumer<T, NRB>(p, As, ys, m0, nrb, nk, lane, wave);
+    else if (wave - 4 < SH::kLastWaves)
+      dcn_p_producer<T, SH::kSPT, NRB, true>(p, geo, As, nk, tid - kPProd);
+    else
+      dcn_p_producer<T, SH::kSPT - 1, NRB, true>(p, geo, As, nk, tid - kPProd);
+    __syncthreads();  // y of every row in ys
+  }
 
   // Geometry table for all NRB * 16 rows (rows outside the range or past M: zero weights,
   // out-of-range offsets).
   for (int g = tid; g < kPRows * TT; g += kPThreads) {
     const int row = g / TT, t = g - row * TT, m = m0 + row;
-    TapGeo G;
-    G.w[0] = G.w[1] = G.w[2] = G.w[3] = 0.f;
-    G.o[0] = G.o[1] = G.o[2] = G.o[3] = xoob;
+    TapGeo G = empty_geo(xoob);
     if (row < nrows && m < p.M) {
-      const int b = m / HoWo, rr = m - b * HoWo, oh = rr / p.Wo, ow = rr - (rr / p.Wo) * p.Wo;
-      float dy, dx, mk;
-      const T *op = static_cast<const T *>(p.off);
-      if constexpr (GEO == kGeoY) {
-        const T *yp = op + (int64_t)m * 3 * TT;
-        dy = (float)yp[2 * t];
-        dx = (float)yp[2 * t + 1];
-        mk = sigmoid_f32((float)yp[2 * TT + t]);
-      } else {
-        dy = (float)op[(int64_t)m * 2 * TT + 2 * t];
-        dx = (float)op[(int64_t)m * 2 * TT + 2 * t + 1];
-        mk = (float)static_cast<const T *>(p.msk)[(int64_t)m * TT + t];
-      }
-      const int ki = t / p.kw, kj = t - (t / p.kw) * p.kw;
-      const float h = (float)(oh * p.sh - p.ph + ki * p.dh) + dy;
-      const float w = (float)(ow * p.sw - p.pw + kj * p.dw) + dx;
-      if (h > -1.f && w > -1.f && h < (float)p.H && w < (float)p.W) {
-        const float fh = floorf(h), fw = floorf(w);
-        const int hl = (int)fh, wl = (int)fw;
-        const float lh = h - fh, lw = w - fw, hh = 1.f - lh, hw = 1.f - lw;
-        const uint32_t rowb = (uint32_t)p.C * (uint32_t)sizeof(T);
-        const uint32_t base = (uint32_t)(b * p.H * p.W + hl * p.W + wl) * rowb;
-        const bool y0 = hl >= 0, y1 = hl + 1 <= p.H - 1, x0 = wl >= 0, x1 = wl + 1 <= p.W - 1;
-        if (y0 && x0) { G.w[0] = hh * hw * mk; G.o[0] = base; }
-        if (y0 && x1) { G.w[1] = hh * lw * mk; G.o[1] = base + rowb; }
-        if (y1 && x0) { G.w[2] = lh * hw * mk; G.o[2] = base + (uint32_t)p.W * rowb; }
-        if (y1 && x1) { G.w[3] = lh * lw * mk; G.o[3] = base + (uint32_t)(p.W + 1) * rowb; }
-      }
+      if constexpr (MEGA)
+        G = tap_geo<T, kGeoYF32>(p, ys, row, m, t);   // bias already in ys
+      else
+        G = tap_geo<T, GEO>(p, p.off, m, m, t);
     }
     geo[g] = G;
   }
-  __syncthreads();
-  const int nk = TT * (p.C / kPBK);
+  __syncthreads();  // MEGA: ys is dead from here, the A ring is written again
   // Always the NRB-block body: a range of NRB - 1 blocks has zero geometry in its last
   // block (see above) and does not store it; the kernel's time is set by the full ranges.
   // Consumers and producers run the same number of barriers (one per step + prologue).
   if (wave < 4)
     dcn_p_consumer<T, NRB>(p, As, m0, nrb, n0, nk, lane, wave);
   else if (wave - 4 < SH::kLastWaves)
-    dcn_p_producer<T, SH::kSPT, NRB>(p, geo, As, nk, tid - kPProd);
+    dcn_p_producer<T, SH::kSPT, NRB, false>(p, geo, As, nk, tid - kPProd);
   else
-    dcn_p_producer<T, SH::kSPT - 1, NRB>(p, geo, As, nk, tid - kPProd);
+    dcn_p_producer<T, SH::kSPT - 1, NRB, false>(p, geo, As, nk, tid - kPProd);
 }
 
 // The persistent kernel runs one workgroup per CU over one 256-column half of Cout and
 // NRB - 1 or NRB row blocks (NRB = 9: res4-like shapes; NRB = 5: res5-like, Cout 512).
+// The CU count is read once per device (device_cus).
 struct PConfig {
   int nblocks = 0, nrb = 0, halves = 0;
 };
 PConfig p_config_for(const HParams &p, int geo) {
   PConfig c;
   if (geo == kGeoRegular || p.C % 64 != 0 || p.Cout <= 128 || p.Cout > 2 * kPCols) return c;
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    return c;
+  const int cus = device_cus();
   const int nb = (cus / 8) * 8;
   const int halves = p.Cout > kPCols ? 2 : 1;
   const int64_t rb = (int64_t)((p.M + 15) / 16);
@@ -720,32 +826,35 @@ PConfig p_config_for(const HParams &p, int geo) {
   return c;
 }
 
-template <typename T, int GEO>
+template <typename T, int GEO, bool MEGA>
 hipError_t launch_p_geo(const PParams &pp, int nrb, hipStream_t stream) {
   if (nrb == 9)
-    hipLaunchKernelGGL((dcn_fused_p_kernel<T, GEO, 9>), dim3(pp.nblocks), dim3(kPThreads), 0,
-                       stream, pp);
+    hipLaunchKernelGGL((dcn_fused_p_kernel<T, GEO, 9, MEGA>), dim3(pp.nblocks), dim3(kPThreads),
+                       0, stream, pp);
   else
-    hipLaunchKernelGGL((dcn_fused_p_kernel<T, GEO, 5>), dim3(pp.nblocks), dim3(kPThreads), 0,
-                       stream, pp);
+    hipLaunchKernelGGL((dcn_fused_p_kernel<T, GEO, 5, MEGA>), dim3(pp.nblocks), dim3(kPThreads),
+                       0, stream, pp);
   return hipGetLastError();
 }
 
 template <typename T>
-hipError_t launch_p(const HParams &h, int geo, const PConfig &c, hipStream_t stream) {
+hipError_t launch_p(const HParams &h, int geo, const PConfig &c, bool mega,
+                    hipStream_t stream) {
   PParams pp;
   pp.h = h;
   pp.rb_total = (h.M + 15) / 16;
   pp.nblocks = c.nblocks;
   pp.halves = c.halves;
-  if (geo == kGeoY) return launch_p_geo<T, kGeoY>(pp, c.nrb, stream);
-  return launch_p_geo<T, kGeoMask>(pp, c.nrb, stream);
+  if (mega) return launch_p_geo<T, kGeoYF32, true>(pp, c.nrb, stream);
+  if (geo == kGeoY) return launch_p_geo<T, kGeoY, false>(pp, c.nrb, stream);
+  if (geo == kGeoYF32) return launch_p_geo<T, kGeoYF32, false>(pp, c.nrb, stream);
+  return launch_p_geo<T, kGeoMask, false>(pp, c.nrb, stream);
 }
 
 template <typename T>
 hipError_t launch_t(const HParams &p, int geo, hipStream_t stream) {
   const PConfig c = p_config_for(p, geo);
-  if (c.nblocks) return launch_p<T>(p, geo, c, stream);
+  if (c.nblocks) return launch_p<T>(p, geo, c, false, stream);
   return p.C % 64 == 0 ? launch_tt<T, true>(p, geo, stream) : launch_tt<T, false>(p, geo, stream);
 }
 
@@ -779,12 +888,13 @@ hipError_t launch_dcn_pack_weight(int dtype, const void *weight, int cout, int C
 
 bool dcn_fused_h_supported(const DcnGeom &g) { return g.kernel_h * g.kernel_w <= kMaxTaps; }
 
-hipError_t launch_dcn_fused_h(int dtype, const DcnGeom &g, int channels_out, const void *x,
-                              const void *off, int geo, const void *msk,
-                              const void *w_packed, const void *bias, void *out,
-                              hipStream_t stream) {
-  HParams p;
+namespace {
+HParams make_hparams(int dtype, const DcnGeom &g, int channels_out, const void *x,
+                     const void *off, const void *msk, const void *w_packed, const void *bias,
+                     void *out, const float *y_bias, bool relu) {
+  HParams p{};
   p.x = x; p.off = off; p.msk = msk; p.w = w_packed; p.bias = bias; p.out = out;
+  p.yb = y_bias; p.relu = relu ? 1 : 0;
   p.C = g.channels; p.H = g.height; p.W = g.width; p.Ho = g.height_col; p.Wo = g.width_col;
   p.Cout = channels_out; p.kh = g.kernel_h; p.kw = g.kernel_w;
   p.ph = g.pad_h; p.pw = g.pad_w; p.sh = g.stride_h; p.sw = g.stride_w;
@@ -796,9 +906,47 @@ hipError_t launch_dcn_fused_h(int dtype, const DcnGeom &g, int channels_out, con
   p.kb_total = (p.K + 15) / 16;
   p.x_bytes = (uint32_t)((int64_t)g.batch * g.height * g.width * g.channels * 2);
   p.w_bytes = (uint32_t)(dcn_packed_weight_elems(dtype, channels_out, p.K) * 2);
+  return p;
+}
+}  // namespace
+
+hipError_t launch_dcn_fused_h(int dtype, const DcnGeom &g, int channels_out, const void *x,
+                              const void *off, int geo, const void *msk,
+                              const void *w_packed, const void *bias, void *out,
+                              hipStream_t stream, const float *y_bias, bool relu) {
+  const HParams p =
+      make_hparams(dtype, g, channels_out, x, off, msk, w_packed, bias, out, y_bias, relu);
   switch (dtype) {
     case 1: return launch_t<f16>(p, geo, stream);
     case 2: return launch_t<bf16>(p, geo, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+bool dcn_mega_supported(int dtype, const DcnGeom &g, int channels_out) {
+  if ((dtype != 1 && dtype != 2) || g.deformable_group != 1 ||
+      g.kernel_h * g.kernel_w > kMaxTaps)
+    return false;
+  const HParams p = make_hparams(dtype, g, channels_out, nullptr, nullptr, nullptr, nullptr,
+                                 nullptr, nullptr, nullptr, false);
+  return p_config_for(p, kGeoYF32).nblocks != 0;
+}
+
+hipError_t launch_dcn_mega(int dtype, const DcnGeom &g, int channels_out, const void *x,
+                           const void *w_off_packed, const float *b_off,
+                           const void *w_packed, const void *bias, bool relu, float *y_out,
+                           void *out, hipStream_t stream) {
+  if (!dcn_mega_supported(dtype, g, channels_out)) return hipErrorInvalidValue;
+  HParams p = make_hparams(dtype, g, channels_out, x, nullptr, nullptr, w_packed, bias, out,
+                           nullptr, relu);
+  p.w2 = w_off_packed;
+  p.b2 = b_off;
+  p.y_out = y_out;
+  p.w2_bytes = (uint32_t)(dcn_packed_weight_elems(dtype, 3 * p.taps, p.K) * 2);
+  const PConfig c = p_config_for(p, kGeoYF32);
+  switch (dtype) {
+    case 1: return launch_p<f16>(p, kGeoYF32, c, true, stream);
+    case 2: return launch_p<bf16>(p, kGeoYF32, c, true, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -91,6 +91,14 @@ __device__ __forceinline__ bool near_cell(int hl, int wl, int qy, int qx) {
          wl + 1 <= qx + kOwnMargin;
 }
 
+// The one level is a grid of exactly num_query cells starting at position 0, so query q
+// is cell (q / W, q % W). The owner and the coordinate kernels both read this from the
+// device metadata (the host checks only num_level == 1 and num_query == spatial_size);
+// when it does not hold, every sample takes the atomic path.
+__device__ __forceinline__ bool grid_queries(const int64_t *shapes, const int64_t *lsi, int nq) {
+  return shapes[0] * shapes[1] == (int64_t)nq && lsi[0] == 0;
+}
+
 // T: input dtype; A: arithmetic / grad_value type.
 template <typename T, typename A>
 __global__ void __launch_bounds__(kBlock) msda_col2im_kernel(
@@ -217,7 +225,7 @@ struct OwnParams {
   const void *loc, *attn, *grad_out;
   float *gv;       // grad_value (fp32) or the fp32 workspace of the 16-bit types
   int accumulate;  // add to gv (fp32 grad_value, whose contract is accumulation) or write it
-  const int64_t *shapes;
+  const int64_t *shapes, *lsi;
   int64_t go_sb, go_sq, go_sh, go_sc;
   int B, NH, NQ, NP, S;
   int blocks_per_xcd;
@@ -231,13 +239,25 @@ __global__ void __launch_bounds__(kOwnThreads) msda_gv_owner_kernel(const OwnPar
   __shared__ int lq[kOwnCap];      // pair: query
   __shared__ float lw[kOwnCap];    // pair: bilinear weight x attention
   const int H = (int)p.shapes[0], W = (int)p.shapes[1];
+  const int tid = threadIdx.x;
+  if (!grid_queries(p.shapes, p.lsi, p.NQ)) {
+    // The shapes do not describe the queries as grid cells: no sample is near, so
+    // msda_grid_coord_kernel adds every sample with atomics; in write mode the workspace
+    // is cleared here first (this kernel runs before it on the same stream).
+    if (!p.accumulate) {
+      const int64_t n = (int64_t)p.B * p.S * p.NH * 32;
+      for (int64_t i = (int64_t)blockIdx.x * kOwnThreads + tid; i < n;
+           i += (int64_t)gridDim.x * kOwnThreads)
+        p.gv[i] = 0.f;
+    }
+    return;
+  }
   const int tiles_x = (W + kOwnT - 1) / kOwnT;
   const int ntile = tiles_x * ((H + kOwnT - 1) / kOwnT);
   const int nitems = p.B * p.NH * ntile;
   const int xcd = blockIdx.x & 7;
   const int per = (nitems + 7) / 8;
   const int i_end = min(nitems, (xcd + 1) * per);
-  const int tid = threadIdx.x;
   const int wave = tid / kWave, half = (tid & (kWave - 1)) >> 5, ch = tid & 31;
   const T *loc = static_cast<const T *>(p.loc);
   const T *attn = static_cast<const T *>(p.attn);
@@ -426,16 +446,21 @@ __global__ void __launch_bounds__(kBlock) msda_grid_coord_kernel(
   const int q = bq - b * p.NQ;
   const int NP = p.NP, NH = p.NH;
   const int H = (int)p.shapes[0], W = (int)p.shapes[1];
-  const int qy = qdiv(q, W), qx = q - qy * W;
+  const bool grid = grid_queries(p.shapes, p.lsi, p.NQ);
+  const int qy = grid ? qdiv(q, W) : 0, qx = q - qy * W;
   const int64_t row = (int64_t)NH * D;
-  const T *vb = value + ((int64_t)b * p.S + p.lsi[0]) * row;
-  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb, (uint32_t)((int64_t)H * W * row * sizeof(T)));
+  // positions of the level inside the batch's value slice (the level's first position is
+  // lsi[0]; corners at or past `avail` count as outside the level)
+  const int64_t lsi0 = min(max(p.lsi[0], (int64_t)0), (int64_t)p.S);
+  const int64_t avail = min((int64_t)H * W, (int64_t)p.S - lsi0);
+  const T *vb = value + ((int64_t)b * p.S + lsi0) * row;
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(vb, (uint32_t)(avail * row * sizeof(T)));
   const uint32_t lane_off = (uint32_t)((h * D + li * VEC) * sizeof(T));
   const T *go = grad_out + b * p.go_sb + (int64_t)q * p.go_sq + h * p.go_sh;
   float top[VEC];
 #pragma unroll
   for (int e = 0; e < VEC; ++e) top[e] = (float)go[(li * VEC + e) * p.go_sc];
-  float *gvb = gv + ((int64_t)b * p.S + p.lsi[0]) * row + h * D + li * VEC;
+  float *gvb = gv + ((int64_t)b * p.S + lsi0) * row + h * D + li * VEC;
   const T *lp = loc + (int64_t)unit * NP * 2;
   const T *ap = attn + (int64_t)unit * NP;
   T *glp = grad_loc + (int64_t)unit * NP * 2;
@@ -463,11 +488,12 @@ __global__ void __launch_bounds__(kBlock) msda_grid_coord_kernel(
     hls[pt] = hl;
     wls[pt] = wl;
     okp[pt] = ok;
-    far[pt] = ok && !near_cell(hl, wl, qy, qx);
+    far[pt] = ok && (!grid || !near_cell(hl, wl, qy, qx));
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int yy = hl + (k >> 1), xx = wl + (k & 1);
-      const bool in = ok && yy >= 0 && yy < H && xx >= 0 && xx < W;
+      const bool in = ok && yy >= 0 && yy < H && xx >= 0 && xx < W &&
+                      (int64_t)yy * W + xx < avail;
       wt[pt][k] = in ? ((k >> 1) ? lh : hh) * ((k & 1) ? lw : hw) : 0.f;
       const uint32_t off = in ? (uint32_t)(((int64_t)yy * W + xx) * row * sizeof(T)) + lane_off : kPast;
       cv[pt][k] = buffer_load_vec<T, VEC>(rv, off);
@@ -861,6 +887,7 @@ hipError_t launch_owner(const MsdaBwdArgs &a, float *gv, bool accumulate, hipStr
   p.grad_out = a.grad_output;
   p.gv = gv;
   p.shapes = a.f.spatial_shapes;
+  p.lsi = a.f.level_start_index;
   p.go_sb = a.go_stride[0]; p.go_sq = a.go_stride[1];
   p.go_sh = a.go_stride[2]; p.go_sc = a.go_stride[3];
   p.B = a.f.batch; p.NH = a.f.num_heads; p.NQ = a.f.num_query; p.NP = a.f.num_point;
@@ -905,8 +932,10 @@ hipError_t launch_coarse(const MsdaBwdArgs &a, float *gv, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// generic: the per-unit kernel alone (msda_col2im_kernel, every level's grad_value by
+// atomics), the reference's force_generic_col2im.
 template <typename T, typename A>
-hipError_t launch_t(const MsdaBwdArgs &a, A *grad_value, hipStream_t stream) {
+hipError_t launch_t(const MsdaBwdArgs &a, A *grad_value, bool generic, hipStream_t stream) {
   BwdParams p;
   p.shapes = a.f.spatial_shapes;
   p.lsi = a.f.level_start_index;
@@ -915,7 +944,7 @@ hipError_t launch_t(const MsdaBwdArgs &a, A *grad_value, hipStream_t stream) {
   p.units = (int64_t)a.f.batch * a.f.num_query * a.f.num_heads;
   p.S = a.f.spatial_size; p.NH = a.f.num_heads; p.D = a.f.channels;
   p.NL = a.f.num_levels; p.NQ = a.f.num_query; p.NP = a.f.num_point;
-  p.coarse = coarse_split<T, A>(a) ? 1 : 0;
+  p.coarse = !generic && coarse_split<T, A>(a) ? 1 : 0;
   p.log2_g = 0;
   while ((1 << p.log2_g) < a.f.channels && p.log2_g < 6) ++p.log2_g;
   const int64_t threads = p.units << p.log2_g;
@@ -925,7 +954,7 @@ hipError_t launch_t(const MsdaBwdArgs &a, A *grad_value, hipStream_t stream) {
       const hipError_t e = launch_coarse<T>(a, grad_value, stream);
       if (e != hipSuccess) return e;
     }
-    if (a.f.channels == 32 && p.units * 32 < ((int64_t)1 << 31) &&
+    if (!generic && a.f.channels == 32 && p.units * 32 < ((int64_t)1 << 31) &&
         (int64_t)a.f.batch * a.f.num_query < ((int64_t)1 << 22) &&
         (int64_t)a.f.spatial_size * a.f.num_heads * 32 * (int64_t)sizeof(T) < ((int64_t)1 << 31)) {
       hipLaunchKernelGGL((msda_col2im_d32_kernel<T>),
@@ -971,20 +1000,20 @@ hipError_t launch_grid_coord(const MsdaBwdArgs &a, float *gv, hipStream_t stream
 }
 
 template <typename T>
-hipError_t launch_f32(const MsdaBwdArgs &a, hipStream_t stream) {
+hipError_t launch_f32(const MsdaBwdArgs &a, bool generic, hipStream_t stream) {
   float *gv = static_cast<float *>(a.grad_value);
-  if (!owner_path<T>(a)) return launch_t<T, float>(a, gv, stream);
+  if (generic || !owner_path<T>(a)) return launch_t<T, float>(a, gv, generic, stream);
   hipError_t e = launch_owner<T>(a, gv, true, stream);
   if (e != hipSuccess) return e;
   return launch_grid_coord<T>(a, gv, stream);
 }
 
 template <typename T>
-hipError_t launch_half(const MsdaBwdArgs &a, hipStream_t stream) {
+hipError_t launch_half(const MsdaBwdArgs &a, bool generic, hipStream_t stream) {
   const int64_t n = (int64_t)a.f.batch * a.f.spatial_size * a.f.num_heads * a.f.channels;
   float *acc = static_cast<float *>(a.workspace);
   hipError_t e;
-  if (owner_path<T>(a)) {  // the owner pass writes every element of the workspace
+  if (!generic && owner_path<T>(a)) {  // the owner pass writes every element of the workspace
     e = launch_owner<T>(a, acc, false, stream);
     if (e != hipSuccess) return e;
     e = launch_grid_coord<T>(a, acc, stream);
@@ -992,7 +1021,7 @@ hipError_t launch_half(const MsdaBwdArgs &a, hipStream_t stream) {
     hipLaunchKernelGGL(fill_zero_f32, dim3(stream_grid(n)), dim3(kBlock), 0, stream, acc, n);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
-    e = launch_t<T, float>(a, acc, stream);
+    e = launch_t<T, float>(a, acc, generic, stream);
   }
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL((narrow_f32<T>), dim3(stream_grid(n)), dim3(kBlock), 0, stream, acc,
@@ -1006,12 +1035,14 @@ int64_t msda_backward_workspace_bytes(int dtype, int64_t value_elems) {
   return (dtype == 1 || dtype == 2) ? value_elems * (int64_t)sizeof(float) : 0;
 }
 
-hipError_t launch_msda_backward(int dtype, const MsdaBwdArgs &a, hipStream_t stream) {
+hipError_t launch_msda_backward(int dtype, const MsdaBwdArgs &a, bool force_generic,
+                                hipStream_t stream) {
   switch (dtype) {
-    case 0: return launch_f32<float>(a, stream);
-    case 1: return launch_half<f16>(a, stream);
-    case 2: return launch_half<bf16>(a, stream);
-    case 3: return launch_t<double, double>(a, static_cast<double *>(a.grad_value), stream);
+    case 0: return launch_f32<float>(a, force_generic, stream);
+    case 1: return launch_half<f16>(a, force_generic, stream);
+    case 2: return launch_half<bf16>(a, force_generic, stream);
+    case 3:
+      return launch_t<double, double>(a, static_cast<double *>(a.grad_value), true, stream);
     default: return hipErrorInvalidValue;
   }
 }

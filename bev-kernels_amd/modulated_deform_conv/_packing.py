@@ -1,16 +1,15 @@
-"""Packed main weight for the fused NHWC kernel, cached on the weight tensor.
+"""Packed main weight for the fused NHWC kernel.
 
 The fused kernel reads the weight in the layout dcn_pack_weight produces (MFMA-fragment
-blocks for fp16 / bf16). A module's weight changes rarely, so the packed copy is kept on
-the weight tensor itself and rebuilt when the tensor's storage, version counter (bumped
-by every in-place update, optimizer steps included), dtype or device differs from the
-one it was packed from.
+blocks for fp16 / bf16, [Cout][kh][kw][C] for fp32). The weight is packed on every call,
+as the reference flattens its weight on every call (dcn_split_nhwc.py:143,
+fused_tl.py:399): one small kernel (a few microseconds for a 256 x 256 x 3 x 3 weight)
+beside the convolution, and no cached copy that a write through ``weight.data``, an EMA
+swap or another kernel could leave stale.
 """
 from __future__ import annotations
 
 import torch
-
-_ATTR = "_bevk_packed_weight"
 
 
 def _ext():
@@ -19,20 +18,5 @@ def _ext():
 
 
 def pack_weight(weight: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
-    """Pack weight [Cout, C, kh, kw] converted to `dtype` (no caching)."""
+    """Pack weight [Cout, C, kh, kw] converted to `dtype`."""
     return _ext().dcn_pack_weight(weight.detach().to(dtype).contiguous())
-
-
-def packed_weight(weight: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
-    """Packed copy of weight [Cout, C, kh, kw] in `dtype`, reused while the weight is
-    unchanged."""
-    key = (weight.data_ptr(), weight._version, dtype, tuple(weight.shape), weight.device)
-    hit = getattr(weight, _ATTR, None)
-    if hit is not None and hit[0] == key:
-        return hit[1]
-    packed = pack_weight(weight, dtype)
-    try:
-        setattr(weight, _ATTR, (key, packed))
-    except (AttributeError, RuntimeError):
-        pass
-    return packed

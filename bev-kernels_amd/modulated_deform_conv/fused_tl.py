@@ -1,10 +1,12 @@
-"""Fused NHWC DCNv2 forward with the public names of naotic/bev-kernels
-modulated_deform_conv/fused_tl.py, running on the gfx950 implicit-GEMM kernel.
+"""Fused NHWC DCNv2 with the public names of naotic/bev-kernels
+modulated_deform_conv/fused_tl.py, running on the gfx950 kernels of libbevk.so.
 
 The reference builds these on TileLang JIT kernels; here every entry point runs on the
-hand-written kernel of libbevk.so: the deformable bilinear x mask taps are produced
-straight into LDS tiles and multiplied on the matrix cores, so the [M, K] column matrix
-never reaches HBM.
+hand-written kernels: the deformable bilinear x mask taps are produced straight into LDS
+tiles and multiplied on the matrix cores, so the [M, K] column matrix never reaches HBM;
+the offset conv runs on the matrix cores too (fp32 accumulation), inside the same kernel
+for the single-kernel forward. The backward (dcn_col2im_nhwc, dcn_split) runs the NHWC
+column-to-image kernels.
 
 Layout:
   data_im  [B, H, W, Cin]
@@ -20,7 +22,7 @@ import torch
 import torch.nn.functional as F
 
 from . import dcn_split_nhwc as _split
-from ._packing import packed_weight
+from ._packing import pack_weight
 
 
 def out_size(H, pad, dil, k, stride):
@@ -139,7 +141,7 @@ def fused_dcn_forward_nhwc(data_im, offset, mask, weight, bias=None, stride=1, p
     vec = 16 // data_im.element_size()
     if Cin % vec == 0 and dt != torch.float64:
         _ext().dcn_fused_fwd_nhwc(data_im.contiguous(), offset.contiguous(), mask.contiguous(),
-                                  packed_weight(weight, dt), b, B, Cin, H, W, Ho, Wo, Cout, kH, kW, ph, pw, sh, sw,
+                                  pack_weight(weight, dt), b, B, Cin, H, W, Ho, Wo, Cout, kH, kW, ph, pw, sh, sw,
                                   dh, dw, out)
     else:
         cols = dcn_gather_cols_nhwc(data_im, offset, mask, kH, kW, (sh, sw), (ph, pw), (dh, dw))
@@ -167,76 +169,115 @@ def dcn_gather_cols_nhwc(data_im, offset, mask, kH, kW, stride=1, padding=0, dil
 
 def offset_conv_forward_nhwc(data_im, w_off, b_off, kH, kW, stride=1, padding=0, dilation=1,
                              block_M=64, block_N=32, block_K=32, num_stages=2, threads=256):
-    """Offset conv -> (offset [B,Ho,Wo,2T], mask [B,Ho,Wo,T]) as in mmcv's Pack:
-    offset = y[..., :2T], mask = sigmoid(y[..., 2T:3T]) (library convolution)."""
-    (sh, sw), (ph, pw), (dh, dw) = _triple(stride, padding, dilation)
+    """Offset conv -> (offset [B,Ho,Wo,2T], mask [B,Ho,Wo,T]) in the input dtype, as
+    mmcv's Pack splits it (fused_tl.py:419-470): y = conv(x, w_off) + b_off accumulated
+    and kept in fp32 (the matrix-core kernel dcn_offset_conv_nhwc), offset = y[..., :2T],
+    mask = sigmoid(y[..., 2T:3T]), both rounded once to the input dtype. The block_* /
+    num_stages / threads arguments of the TileLang version are accepted and ignored."""
     Tt = kH * kW
-    Noff = w_off.size(0)
-    if Noff != 3 * Tt or w_off.size(1) != data_im.size(-1):
+    if w_off.size(0) != 3 * Tt or w_off.size(1) != data_im.size(-1):
         raise RuntimeError("offset conv weight must be [3*kH*kW, Cin, kH, kW]")
-    y = F.conv2d(data_im.permute(0, 3, 1, 2), w_off.to(data_im.dtype),
-                 b_off.to(data_im.dtype) if b_off is not None else None, (sh, sw), (ph, pw),
-                 (dh, dw)).permute(0, 2, 3, 1)
-    offset = y[..., :2 * Tt].contiguous()
-    mask = torch.sigmoid(y[..., 2 * Tt:]).contiguous()
+    dt = data_im.dtype
+    if _split.offset_conv_supported(data_im, w_off):
+        y = _split.offset_conv_y(data_im, w_off, b_off, stride, padding, dilation)
+    else:
+        (sh, sw), (ph, pw), (dh, dw) = _triple(stride, padding, dilation)
+        y = F.conv2d(data_im.permute(0, 3, 1, 2).float(), w_off.float(),
+                     b_off.float() if b_off is not None else None, (sh, sw), (ph, pw),
+                     (dh, dw)).permute(0, 2, 3, 1)
+    offset = y[..., :2 * Tt].to(dt).contiguous()
+    mask = torch.sigmoid(y[..., 2 * Tt:]).to(dt).contiguous()
     return offset, mask
-
-
-def _raw_offset_conv(data_im, w_off, b_off, stride, padding, dilation):
-    y = F.conv2d(data_im.permute(0, 3, 1, 2), w_off.to(data_im.dtype),
-                 b_off.to(data_im.dtype) if b_off is not None else None, stride, padding,
-                 dilation)
-    return y.permute(0, 2, 3, 1).contiguous()   # [B,Ho,Wo,3T]: offsets, pre-sigmoid mask
 
 
 def dcn_forward_split_nhwc(data_im, w_off, b_off, weight, bias=None, stride=1, padding=0,
                            dilation=1):
-    """Full DCNv2 forward (NHWC): offset conv, then the fused deformable kernel reading
-    the raw offset-conv output."""
-    (sh, sw), (ph, pw), (dh, dw) = _triple(stride, padding, dilation)
+    """Full DCNv2 forward (NHWC, groups=1, dg=1; fused_tl.py:373-403): offset conv and the
+    deformable conv in one kernel (the offsets stay fp32 between them)."""
     _check_single_group(data_im, weight)
-    if sh != sw or ph != pw or dh != dw:
-        raise RuntimeError("dcn_forward_split_nhwc needs uniform stride/padding/dilation")
-    y = _raw_offset_conv(data_im, w_off, b_off, (sh, sw), (ph, pw), (dh, dw))
-    return _split._fused_forward(data_im, y, None, weight, bias, sh, ph, dh)
+    if _split.mega_supported(data_im, w_off, weight):
+        return _split.mega_forward(data_im, w_off, b_off, weight, bias, stride, padding,
+                                   dilation)[0]
+    offset, mask = offset_conv_forward_nhwc(data_im, w_off, b_off, weight.size(2),
+                                            weight.size(3), stride, padding, dilation)
+    return fused_dcn_forward_nhwc(data_im, offset, mask, weight, bias, stride, padding,
+                                  dilation)
 
 
 def fused_dcn_full_forward_nhwc(data_im, w_off, b_off, weight, bias=None, stride=1, padding=0,
                                 dilation=1):
-    """Full DCNv2 forward (NHWC): offset conv + fused deformable kernel."""
-    return dcn_forward_split_nhwc(data_im, w_off, b_off, weight, bias, stride, padding,
+    """Full DCNv2 forward (NHWC) as the reference composes it (fused_tl.py:473-484): the
+    offset conv (offset and mask rounded to the input dtype), then the fused deformable
+    kernel."""
+    _, _, kH, kW = weight.shape
+    offset, mask = offset_conv_forward_nhwc(data_im, w_off, b_off, kH, kW, stride, padding,
+                                            dilation)
+    return fused_dcn_forward_nhwc(data_im, offset, mask, weight, bias, stride, padding,
                                   dilation)
 
 
 def fused_dcn_mega_forward_nhwc(data_im, w_off, b_off, weight, bias=None, stride=1, padding=0,
                                 dilation=1, block_M=32, block_N=None, block_K=64, num_stages=2,
                                 threads=256):
-    """Full DCNv2 forward (NHWC): offset conv + fused deformable kernel (sigmoid of the
-    mask applied inside the kernel)."""
-    return dcn_forward_split_nhwc(data_im, w_off, b_off, weight, bias, stride, padding,
-                                  dilation)
+    """Single-kernel full DCNv2 forward (NHWC, groups=1, dg=1; fused_tl.py:565-766): offset
+    conv (fp32 accumulation, kept in fp32), sigmoid, deformable gather and main GEMM in one
+    launch on the persistent fp16/bf16 kernel (two launches on other shapes)."""
+    _check_single_group(data_im, weight)
+    if not _split.mega_supported(data_im, w_off, weight):
+        return dcn_forward_split_nhwc(data_im, w_off, b_off, weight, bias, stride, padding,
+                                      dilation)
+    return _split.mega_forward(data_im, w_off, b_off, weight, bias, stride, padding,
+                               dilation)[0]
 
 
 def dcn_col2im_nhwc(dCol, X, offset, mask, kH, kW, stride=1, padding=0, dilation=1, block=256):
-    """Backward col2im of the reference; the backward kernels are not part of this build."""
-    raise RuntimeError("dcn_col2im_nhwc: the backward kernels are not part of this build "
-                       "(forward operators only)")
+    """Backward column-to-image (fused_tl.py:792-862): dCol [M, T*Cin], X [B,H,W,Cin],
+    offset [B,Ho,Wo,2T], mask [B,Ho,Wo,T] -> (grad_X [B,H,W,Cin], grad_offset
+    [B,Ho,Wo,2T], grad_mask [B,Ho,Wo,T]), all float32, computed in fp32 on fp32 copies of
+    the inputs as the reference does. `block` is accepted and ignored."""
+    (sh, sw), (ph, pw), (dh, dw) = _triple(stride, padding, dilation)
+    B, H, W, Cin = X.shape
+    Ho = out_size(H, ph, dh, kH, sh)
+    Wo = out_size(W, pw, dw, kW, sw)
+    Tt = kH * kW
+    dev = X.device
+    gX = torch.zeros(B, H, W, Cin, device=dev, dtype=torch.float32)
+    gOff = torch.empty(B, Ho, Wo, 2 * Tt, device=dev, dtype=torch.float32)
+    gMask = torch.empty(B, Ho, Wo, Tt, device=dev, dtype=torch.float32)
+    _ext().modulated_deformable_col2im_nhwc_cuda(
+        dCol.float().contiguous(), X.float().contiguous(), offset.float().contiguous(),
+        mask.float().contiguous(), B, Cin, H, W, Ho, Wo, kH, kW, ph, pw, sh, sw, dh, dw, 1, gX,
+        gOff, gMask)
+    return gX, gOff, gMask
 
 
 class _DCNSplitFunction(torch.autograd.Function):
+    """Differentiable full DCNv2 (NHWC; fused_tl.py:866-943): forward = the one-kernel
+    forward, backward = the NHWC split composition (re-gathered columns, dCol = dO @ W,
+    column-to-image kernel, library offset-conv backward)."""
+
     @staticmethod
     def forward(ctx, x_nhwc, w_off, b_off, weight, bias, stride, padding, dilation):
-        return dcn_forward_split_nhwc(x_nhwc, w_off, b_off, weight, bias, stride, padding,
-                                      dilation)
+        (sh, sw), (ph, pw), (dh, dw) = _triple(stride, padding, dilation)
+        if sh != sw or ph != pw or dh != dw:
+            raise RuntimeError("dcn_split needs uniform stride/padding/dilation")
+        _check_single_group(x_nhwc, weight)
+        out, y = _split._split_forward(x_nhwc, w_off, b_off, weight, bias, sh, ph, dh)
+        ctx.save_for_backward(x_nhwc, y, w_off, weight)
+        ctx.stride, ctx.padding, ctx.dilation = sh, ph, dh
+        ctx.with_bias = bias is not None
+        return out
 
     @staticmethod
     def backward(ctx, grad_out):
-        raise RuntimeError("dcn_split backward: the backward kernels are not part of this "
-                           "build (forward operators only)")
+        x, y, w_off, weight = ctx.saved_tensors
+        grads = _split.split_backward(grad_out, x, y, w_off, weight, ctx.stride, ctx.padding,
+                                      ctx.dilation, ctx.with_bias)
+        return grads + (None, None, None)
 
 
 def dcn_split(x_nhwc, w_off, b_off, weight, bias=None, stride=1, padding=0, dilation=1):
-    """Full DCNv2 forward (NHWC)."""
+    """Autograd-enabled full DCNv2 forward (NHWC)."""
     return _DCNSplitFunction.apply(x_nhwc, w_off, b_off, weight, bias, stride, padding, dilation)
 
 

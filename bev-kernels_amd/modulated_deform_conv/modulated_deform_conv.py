@@ -16,7 +16,7 @@ import torch.nn as nn
 from torch.autograd import Function
 from torch.autograd.function import once_differentiable
 from torch.nn.modules.utils import _pair, _single
-from ._packing import packed_weight
+from ._packing import pack_weight
 
 _ext = None
 
@@ -346,7 +346,7 @@ def _modulated_deform_conv2d_forward(input, offset, mask, weight, bias, stride, 
         x_nhwc = ext.nchw_to_nhwc(input)
         off_nhwc = ext.nchw_to_nhwc(offset)
         msk_nhwc = ext.nchw_to_nhwc(mask)
-        w_packed = packed_weight(weight, input.dtype)
+        w_packed = pack_weight(weight, input.dtype)
         b = bias.to(input.dtype).contiguous() if bias is not None else None
         out = input.new_empty(batch, ho, wo, channels_out)
         ext.dcn_fused_fwd_nhwc(x_nhwc, off_nhwc, msk_nhwc, w_packed, b, batch, channels, height,

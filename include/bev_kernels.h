@@ -1,7 +1,7 @@
 /*
  * bev_kernels.h — C ABI of libbevk.so, the MI355X (gfx950) implementation of the
  * BEVFormer deformable-conv (DCNv2) and multi-scale deformable attention (MSDA)
- * forward operators.
+ * operators: forward, backward and the layout / weight-packing helpers.
  *
  * Conventions shared by every entry point:
  *   - All data pointers are DEVICE pointers to dense, contiguous (row-major) buffers.
@@ -102,8 +102,10 @@ int bevk_modulated_deformable_im2col_nhwc(
  *   data_im      [B, C, H, W] (may be NULL when grad_offset is NULL)
  *   data_offset  [B, dg*2T, Ho, Wo], data_mask [B, dg*T, Ho, Wo]
  *   grad_im      [B, C, H, W] dtype, ACCUMULATED with atomics (zero it first), or NULL. For
- *                F16 / BF16 the adds are packed pairs with 0 added to the neighbour element,
- *                so the buffer must be allocated to a multiple of 4 bytes.
+ *                F16 / BF16 the adds are packed pairs with -0.0 (the exact identity) added
+ *                to the neighbour element, so grad_im must be 4-byte aligned
+ *                (BEVK_ERR_INVALID otherwise) and, with an odd element count, the 2 bytes
+ *                after it must be addressable (they keep their bits).
  *   grad_offset  [B, dg*2T, Ho, Wo] and grad_mask [B, dg*T, Ho, Wo] dtype, written, or NULL
  * Replaces binding.cpp:13-19, :29-58 (modulated_deformable_col2im[_opt|_smem]_cuda and
  * modulated_deformable_col2im_coord[_opt]_cuda; modulated_deform_conv_cuda_kernel.cuh:
@@ -171,8 +173,9 @@ int64_t bevk_dcn_packed_weight_bytes(int dtype, int channels_out, int kernel_h, 
  *   F32:       [Cout, kh, kw, C]
  *   F16, BF16: MFMA-fragment blocks: block (n/32, k/16) of 64 lanes x 8 elements, lane
  *              (n%32) + 32*((k%16)/8), k = (i*kw + j)*C + c; zero padded to whole blocks.
- * Done once per weight; the reference repacks per call (weight.permute(2,3,1,0), e.g.
- * fused_tl.py:500-510, dcn_split_nhwc.py:143). */
+ * The reference flattens its weight on every call (weight.permute(2,3,1,0), e.g.
+ * fused_tl.py:500-510, dcn_split_nhwc.py:143); the Python operators pack on every call
+ * too, a caller with a fixed weight may pack once. */
 int bevk_dcn_pack_weight(int dtype, const void *weight, int channels_out, int kernel_h,
                          int kernel_w, int channels, void *packed, void *stream);
 
@@ -206,6 +209,42 @@ int bevk_dcn_fused_fwd_nhwc(
 /* ------------------------------------------------------------------------- */
 /* Multi-scale deformable attention                                            */
 /* ------------------------------------------------------------------------- */
+
+/* Offset conv of the NHWC front end on the matrix cores:
+ *   data_im       [B, H, W, C]
+ *   w_off_packed  bevk_dcn_pack_weight of the offset-conv weight [3T, C, kh, kw]
+ *                 (channels_out = 3T)
+ *   b_off         [3T] fp32, or NULL
+ *   y             [B*Ho*Wo, 3T] fp32, written: conv(x, w_off) + b_off, accumulated in fp32
+ * Offsets are y[:, :2T] ((dy, dx) per tap) and the pre-sigmoid mask y[:, 2T:].
+ * Replaces fused_tl.offset_conv_forward_nhwc's kernel (fused_tl.py:419-470: fp32
+ * accumulation, fp32 output, bias added in fp32). dg == 1. dtypes F32 (any kernel size),
+ * F16 / BF16 (at most 9 taps); C a multiple of 16 bytes' worth of elements. */
+int bevk_dcn_offset_conv_nhwc(int dtype, const void *data_im, const void *w_off_packed,
+                              const float *b_off, int batch_size, int channels, int height_im,
+                              int width_im, int height_col, int width_col, int kernel_h,
+                              int kernel_w, int pad_h, int pad_w, int stride_h, int stride_w,
+                              int dilation_h, int dilation_w, float *y, void *stream);
+
+/* Whole DCNv2 forward with the offset conv inside (the reference's single-kernel
+ * fused_dcn_mega_forward_nhwc, fused_tl.py:565-766, and the forward of
+ * DCNSplitNHWCFunction with its FrozenBN + ReLU epilogue, dcn_split_nhwc.py:158-204):
+ *   y = conv(x, w_off) + b_off in fp32 (as bevk_dcn_offset_conv_nhwc; written to y,
+ *   [B*Ho*Wo, 3T] fp32, which the backward needs), offsets y[:, :2T], mask
+ *   sigmoid(y[:, 2T:]), then out = deformable conv (+ bias) as bevk_dcn_fused_fwd_nhwc,
+ *   with max(out, 0) when act_relu != 0.
+ *   weight_packed / bias / out: as bevk_dcn_fused_fwd_nhwc (channels_out may be 0: y only).
+ * F16 / BF16 shapes that take the persistent kernel (C % 64 == 0, 128 < Cout <= 512, the
+ * row counts of the BEVFormer res4/res5 layers on a 256-CU device) run as ONE launch: y
+ * stays in LDS for the gather and never returns from HBM. Other shapes run the offset conv
+ * and then the fused kernel reading y. dtypes F32, F16, BF16; dg == 1. */
+int bevk_dcn_mega_fwd_nhwc(int dtype, const void *data_im, const void *w_off_packed,
+                           const float *b_off, const void *weight_packed, const void *bias,
+                           int batch_size, int channels, int height_im, int width_im,
+                           int height_col, int width_col, int channels_out, int kernel_h,
+                           int kernel_w, int pad_h, int pad_w, int stride_h, int stride_w,
+                           int dilation_h, int dilation_w, int act_relu, float *y, void *out,
+                           void *stream);
 
 /* MSDA forward.
  *   value              [B, spatial_size, num_heads, channels]
@@ -247,8 +286,12 @@ int64_t bevk_msda_backward_workspace_bytes(int dtype, int batch, int spatial_siz
  *   grad_sampling_loc  [B, num_query, num_heads, num_levels, num_point, 2]; written.
  *   grad_attn_weight   [B, num_query, num_heads, num_levels, num_point]; written.
  *   workspace          bevk_msda_backward_workspace_bytes(...) bytes, device memory.
- * im2col_step keeps the reference's contract; force_generic_col2im is accepted for
- * compatibility (one kernel serves every geometry).
+ * im2col_step keeps the reference's contract. force_generic_col2im != 0 runs the
+ * per-(batch, query, head) kernel alone, adding every level's grad_value with atomics
+ * (the reference's generic col2im, binding_musa.mu:459); otherwise the D = 32 kernel,
+ * the coarse-level sort and the grid-query owner pass are used where they apply.
+ * spatial_shapes / level_start_index must describe value (lsi[l] + H_l * W_l <=
+ * spatial_size), as in the reference; they are read on the device only.
  * Replaces _msda_opt2_musa.backward (binding_musa.mu:414-543, :550-556).
  * dtypes: F32, F16, BF16 (fp32 arithmetic and accumulation), F64. */
 int bevk_msda_backward(

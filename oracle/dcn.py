@@ -215,6 +215,29 @@ def fused_front_end_columns(x, w_off_tc, b_off, kh, kw, stride=1, padding=0, dil
     return _round_cols(cols, col_dtype)
 
 
+def offset_conv_nhwc(x, w_off, b_off=None, stride=1, padding=0, dilation=1):
+    """Offset conv of the NHWC front end (fused_tl.py:419-470, dcn_split_nhwc.py:168-172):
+    y [B, Ho, Wo, 3T] = conv(x, w_off) + b_off, x [B, H, W, C], w_off [3T, C, kh, kw] (the
+    library convolution in the caller's precision: float64 here)."""
+    def two(v):
+        return (v, v) if isinstance(v, int) else tuple(v)
+    y = F.conv2d(x.permute(0, 3, 1, 2), w_off, b_off, two(stride), two(padding), two(dilation))
+    return y.permute(0, 2, 3, 1)
+
+
+def mega_forward_nhwc(x, w_off, b_off, weight, bias=None, stride=1, padding=0, dilation=1,
+                      col_dtype=None, relu=False):
+    """Whole NHWC forward with the offset conv inside (fused_tl.py:565-766): y =
+    offset_conv_nhwc, offsets y[..., :2T], mask sigmoid(y[..., 2T:]) (split_y_nhwc), then
+    forward_nhwc; relu: the ReLU epilogue of dcn_split_nhwc.py:190-196."""
+    kh, kw = weight.shape[2], weight.shape[3]
+    y = offset_conv_nhwc(x, w_off, b_off, stride, padding, dilation)
+    off, mask = split_y_nhwc(y, kh * kw)
+    out = forward_nhwc(x, off, mask, weight, bias, stride, padding, dilation,
+                       col_dtype=col_dtype)
+    return torch.relu(out) if relu else out
+
+
 def split_y_nhwc(y, taps):
     """Raw offset-conv output y [..., 3T] -> (offset y[..., :2T], mask sigmoid(y[..., 2T:]))
     (dcn_split_nhwc.py:131-132; dcn_fused_nhwc_kernel.cuh:126-131)."""

@@ -179,3 +179,38 @@ def test_call_raises_runtime_error_with_message():
     with pytest.raises(RuntimeError, match="batch must divide im2col_step"):
         _bevk.call("bevk_msda_forward", 0, NULL, NULL, NULL, NULL, NULL, 6, 10, 8, 32, 1, 4, 4,
                    4, 0, NULL, NULL)
+
+
+def test_col2im_nchw_rejects_misaligned_half_grad_im():
+    """16-bit grad_im is added to with packed pair atomics, so it must start a 4-byte
+    pair; a view at an odd element offset is rejected before any launch (fake device
+    addresses: nothing is dereferenced)."""
+    f = _bevk.lib().bevk_modulated_deformable_col2im_nchw
+    p = ctypes.c_void_p
+    args = [p(0x10000), p(0x20000), p(0x30000), p(0x40000), 1, 4, 5, 5, 5, 5, 3, 3, 1, 1, 1, 1,
+            1, 1, 1]
+    for dtype in (1, 2):
+        assert f(dtype, *args, p(0x50002), NULL, NULL, NULL) == INVALID
+        assert "aligned" in _err()
+
+
+def _offset_conv(entry, dtype=1, **kw):
+    a = dict(b=1, c=64, h=5, w=5, ho=5, wo=5, kh=3, kw=3, ph=1, pw=1, sh=1, sw=1, dh=1, dw=1)
+    a.update(kw)
+    sizes = [a[k] for k in ("b", "c", "h", "w", "ho", "wo")]
+    geom = [a[k] for k in ("kh", "kw", "ph", "pw", "sh", "sw", "dh", "dw")]
+    lib = _bevk.lib()
+    if entry == "bevk_dcn_offset_conv_nhwc":
+        return lib.bevk_dcn_offset_conv_nhwc(dtype, NULL, NULL, NULL, *sizes, *geom, NULL, NULL)
+    return lib.bevk_dcn_mega_fwd_nhwc(dtype, NULL, NULL, NULL, NULL, NULL, *sizes,
+                                      a.get("cout", 16), *geom, 0, NULL, NULL, NULL)
+
+
+@pytest.mark.parametrize("entry", ["bevk_dcn_offset_conv_nhwc", "bevk_dcn_mega_fwd_nhwc"])
+def test_offset_conv_validation(entry):
+    assert _offset_conv(entry, dtype=3) == UNSUPPORTED and "not implemented" in _err()
+    assert _offset_conv(entry, c=12) == UNSUPPORTED and "multiple of 8" in _err()
+    assert _offset_conv(entry, kh=5, kw=5, ph=2, pw=2) == UNSUPPORTED and "9 taps" in _err()
+    assert _offset_conv(entry, ho=4) == INVALID and "does not match" in _err()
+    assert _offset_conv(entry) == INVALID and "null" in _err()
+    assert _offset_conv(entry, b=0) == 0          # nothing to do

@@ -213,8 +213,9 @@ def test_pack_weight_layout(dtype, shape):
     assert torch.equal(packed.cpu(), ref)                            # bit-exact permutation
 
 
-def test_packed_weight_cache_follows_updates():
-    """The module caches its packed weight; an in-place update must be seen next call."""
+def test_packed_weight_follows_updates():
+    """The weight is packed on every call: in-place updates (autograd-visible or through
+    .data, as EMA swaps and weight syncs do) are seen by the next call."""
     from modulated_deform_conv import ModulatedDeformConv2d
     torch.manual_seed(1)
     mod = ModulatedDeformConv2d(16, 32, 3, padding=1).half().to(DEV)
@@ -225,10 +226,14 @@ def test_packed_weight_cache_follows_updates():
         a = mod(x, off, msk)
         mod.weight.mul_(-2.0)
         b = mod(x, off, msk)
+        w0 = mod.weight.detach().clone()
+        mod.weight.data.copy_(-0.5 * w0)      # no version bump, same storage
+        c = mod(x, off, msk)
     torch.cuda.synchronize()
     bias = mod.bias.view(1, -1, 1, 1).float()
     torch.testing.assert_close((b.float() - bias), -2.0 * (a.float() - bias), rtol=2e-3,
                                atol=2e-3)
+    torch.testing.assert_close((c.float() - bias), (a.float() - bias), rtol=2e-3, atol=2e-3)
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
@@ -242,11 +247,11 @@ def test_dcn_split_nhwc_half_3t(dtype):
     weight = (0.1 * torch.randn(96, 64, 3, 3, generator=g)).to(dtype)
     bias = torch.randn(96, generator=g).to(dtype)
     out = dsn.dcn_split_nhwc(*(t.to(DEV) for t in (x, w_off, b_off, weight, bias)), 1, 1, 1)
-    y = F.conv2d(x.to(DEV).permute(0, 3, 1, 2), w_off.to(DEV), b_off.to(DEV), 1, 1, 1)
     torch.cuda.synchronize()
-    off, msk = od.split_y_nhwc(y.permute(0, 2, 3, 1).double().cpu(), 9)
-    ref = od.forward_nhwc(x.double(), off, msk, weight.double(), bias.double(), 1, 1, 1,
-                          col_dtype=dtype)
+    # the offset conv is accumulated and kept in fp32 inside the kernel: the oracle's
+    # float64 offset conv, not a library convolution rounded to the input dtype
+    ref = od.mega_forward_nhwc(x.double(), w_off.double(), b_off.double(), weight.double(),
+                               bias.double(), 1, 1, 1, col_dtype=dtype)
     check(out.cpu(), ref, dtype, "split 3T half")
 
 
@@ -482,3 +487,193 @@ def test_transpose_layouts(dtype, shape):
     assert torch.equal(y, x.permute(0, 2, 3, 1).contiguous())
     z = ext.nhwc_to_nchw(y)
     assert torch.equal(z, x)
+
+
+# ---------------------------------------------------------------------------------------
+# Arithmetic of the A operand: one rounding of an fp32 blend
+# ---------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", HALF, ids=["fp16", "bf16"])
+@pytest.mark.parametrize("shape", [(2, 64, 256, 9, 11), (1, 64, 256, 130, 128)],
+                         ids=["tiled", "persistent"])
+def test_fused_columns_single_rounding(dtype, shape):
+    """A selector weight (W[n] = 1 at one k_n, 0 elsewhere) makes every output element one
+    element of the deformable A operand, passed exactly through the fp32 MFMA accumulation.
+    The kernel blends the four corners in fp32 and rounds once to the input dtype (the
+    reference's gather, dcn_fused_nhwc_kernel.cuh:185-187): against the float64 columns
+    rounded once, every element is within one ulp and almost all are equal (only values
+    within fp32 rounding of a tie may differ). A blend in 16-bit arithmetic (weights
+    rounded, partial sums rounded) fails the equality count."""
+    from modulated_deform_conv import fused_tl
+    b, cin, cout, h, w = shape
+    d = inputs.nchw_to_nhwc(_rand_problem(b, cin, cout, h, w, dtype=dtype, seed=31))
+    K = 9 * cin
+    sel = (torch.arange(cout) * 37 + 5) % K                  # distinct k per output column
+    w_nk = torch.zeros(cout, K)
+    w_nk[torch.arange(cout), sel] = 1.0
+    weight = w_nk.view(cout, 3, 3, cin).permute(0, 3, 1, 2).contiguous().to(dtype)
+    out = fused_tl.fused_dcn_forward_nhwc(d["x"].to(DEV), d["offset"].to(DEV),
+                                          d["mask"].to(DEV), weight.to(DEV), None, 1, 1, 1)
+    torch.cuda.synchronize()
+    got = out.cpu().reshape(-1, cout)
+    cols = od.columns_nhwc(d["x"].double(), d["offset"].double(), d["mask"].double(), 3, 3, 1,
+                           1, 1, 1, 1, 1)
+    ref = cols[:, sel].to(dtype)                              # one rounding
+    diff = got != ref
+    frac = diff.double().mean().item()
+    assert frac < 1e-3, f"{frac:.2e} of the A elements differ from one rounding"
+    if diff.any():
+        a, r = got[diff].double(), ref[diff].double()
+        ulp = (r.abs() * (2.0 ** -10 if dtype == torch.float16 else 2.0 ** -7)).clamp_min(
+            2.0 ** -24)
+        far = (a - r).abs() > ulp * 1.0001
+        assert not far.any(), (
+            f"{int(far.sum())} of {a.numel()} differing elements beyond one ulp; first "
+            f"(got, want): {list(zip(a[far][:6].tolist(), r[far][:6].tolist()))}")
+
+
+# ---------------------------------------------------------------------------------------
+# Offset conv inside: offset_conv_forward_nhwc, the single-kernel forward and its callers
+# ---------------------------------------------------------------------------------------
+
+def _mega_problem(b, cin, cout, h, w, dtype, seed, k=3):
+    g = torch.Generator().manual_seed(seed)
+    T = k * k
+    x = torch.randn(b, h, w, cin, generator=g).to(dtype)
+    # a trained offset conv gives offsets of a few pixels and mask logits around 0
+    w_off = ((1.5 / (T * cin) ** 0.5) * torch.randn(3 * T, cin, k, k, generator=g)).to(dtype)
+    b_off = 0.5 * torch.randn(3 * T, generator=g)
+    weight = (0.1 * torch.randn(cout, cin, k, k, generator=g)).to(dtype)
+    bias = torch.randn(cout, generator=g).to(dtype)
+    return x, w_off, b_off, weight, bias
+
+
+def _mega_ref(x, w_off, b_off, weight, bias, dtype, s=1, p=1, dl=1, relu=False):
+    return od.mega_forward_nhwc(x.double(), w_off.double(), b_off.double(), weight.double(),
+                                None if bias is None else bias.double(), s, p, dl,
+                                col_dtype=_cols_dtype(dtype), relu=relu)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16],
+                         ids=["fp32", "fp16", "bf16"])
+@pytest.mark.parametrize("geom", [
+    # b, cin, h, w, stride, pad, dil
+    (2, 64, 9, 11, 1, 1, 1),
+    (1, 32, 12, 10, 2, 1, 1),
+    (1, 16, 10, 9, 1, 2, 2),
+])
+def test_offset_conv_forward_nhwc(dtype, geom):
+    """fused_tl.offset_conv_forward_nhwc: y accumulated and kept in fp32 on the matrix
+    cores, offset = y[..., :2T] and mask = sigmoid(y[..., 2T:]) rounded once to the input
+    dtype (fused_tl.py:419-470); the fp32 y itself against the float64 conv."""
+    from modulated_deform_conv import fused_tl, dcn_split_nhwc as dsn
+    b, cin, h, w, s, p, dl = geom
+    x, w_off, b_off, _, _ = _mega_problem(b, cin, 8, h, w, dtype, seed=sum(geom))
+    off, mask = fused_tl.offset_conv_forward_nhwc(x.to(DEV), w_off.to(DEV), b_off.to(DEV), 3,
+                                                  3, s, p, dl)
+    y = dsn.offset_conv_y(x.to(DEV), w_off.to(DEV), b_off.to(DEV), s, p, dl)
+    torch.cuda.synchronize()
+    y_ref = od.offset_conv_nhwc(x.double(), w_off.double(), b_off.double(), s, p, dl)
+    check(y.cpu(), y_ref, torch.float32, f"offset conv y {geom}")
+    o_ref, m_ref = od.split_y_nhwc(y_ref, 9)
+    assert off.dtype == mask.dtype == dtype
+    check(off.cpu(), o_ref, dtype, "offset")
+    check(mask.cpu(), m_ref, dtype, "mask")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16],
+                         ids=["fp32", "fp16", "bf16"])
+@pytest.mark.parametrize("shape", [
+    # batch, cin, cout, h, w: persistent one-launch shapes on a 256-CU device, then tiled
+    (2, 64, 200, 130, 128),   # one column half, 8- and 9-block row ranges, column tail
+    (1, 64, 320, 90, 100),    # two column halves, 4- and 5-block ranges
+    (2, 32, 48, 11, 13),      # the offset conv, then the fused kernel reading y
+], ids=["half1", "half2-tail", "small"])
+def test_mega_forward(dtype, shape):
+    """fused_tl.fused_dcn_mega_forward_nhwc (fused_tl.py:565-766): offset conv, sigmoid,
+    deformable gather and main GEMM in one launch (fp16 / bf16 persistent shapes). Every
+    output element against the float64 oracle (offset conv in float64, columns rounded to
+    the input dtype as the kernel's A tile), and the fp32 y the kernel writes for the
+    backward against the float64 conv."""
+    from modulated_deform_conv import fused_tl, dcn_split_nhwc as dsn
+    b, cin, cout, h, w = shape
+    x, w_off, b_off, weight, bias = _mega_problem(b, cin, cout, h, w, dtype, seed=cin + cout)
+    dv = [t.to(DEV) for t in (x, w_off, b_off, weight, bias)]
+    out = fused_tl.fused_dcn_mega_forward_nhwc(*dv, 1, 1, 1)
+    out2, y = dsn.mega_forward(*dv, 1, 1, 1)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2)
+    y_ref = od.offset_conv_nhwc(x.double(), w_off.double(), b_off.double(), 1, 1, 1)
+    check(y.cpu(), y_ref, torch.float32, f"mega y {shape}")
+    ref = _mega_ref(x, w_off, b_off, weight, bias, dtype)
+    check(out.cpu(), ref, dtype, f"mega {shape}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+def test_mega_bn_relu_persistent(dtype):
+    """dcn_split_nhwc with the FrozenBN + ReLU epilogue on a one-launch shape: BN folded
+    into the packed weight and bias, ReLU in the kernel's store (dcn_split_nhwc.py:178-204)."""
+    from modulated_deform_conv import dcn_split_nhwc as dsn
+    b, cin, cout, h, w = 2, 64, 200, 130, 128
+    x, w_off, b_off, weight, bias = _mega_problem(b, cin, cout, h, w, dtype, seed=9)
+    g = torch.Generator().manual_seed(2)
+    scale = 0.5 + torch.rand(cout, generator=g)
+    shift = torch.randn(cout, generator=g)
+    out = dsn.dcn_split_nhwc(*(t.to(DEV) for t in (x, w_off, b_off, weight, bias)), 1, 1, 1,
+                             scale.to(DEV), shift.to(DEV), True)
+    torch.cuda.synchronize()
+    w_eff = (weight.double() * scale.to(dtype).double().view(-1, 1, 1, 1)).to(dtype)
+    b_eff = (shift + bias.float() * scale).to(dtype)
+    ref = _mega_ref(x, w_off, b_off, w_eff, b_eff, dtype, relu=True)
+    assert (out >= 0).all()
+    check(out.cpu(), ref, dtype, "mega bn relu")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["fp32", "fp16"])
+def test_full_split_forward_entry_points(dtype):
+    """fused_dcn_full_forward_nhwc (offset conv, offsets rounded, fused kernel),
+    dcn_forward_split_nhwc and dcn_split_forward_nhwc (one kernel), fused_tl.dcn_split and
+    both dcn_apply_nchw adapters against the float64 oracle."""
+    from modulated_deform_conv import fused_tl, dcn_split_nhwc as dsn
+    x, w_off, b_off, weight, bias = _mega_problem(2, 64, 96, 12, 14, dtype, seed=12)
+    dv = [t.to(DEV) for t in (x, w_off, b_off, weight, bias)]
+    ref = _mega_ref(x, w_off, b_off, weight, bias, dtype)
+    for name, fn in (("full", fused_tl.fused_dcn_full_forward_nhwc),
+                     ("split", fused_tl.dcn_forward_split_nhwc),
+                     ("split_forward", dsn.dcn_split_forward_nhwc),
+                     ("dcn_split", fused_tl.dcn_split)):
+        out = fn(*dv, 1, 1, 1)
+        torch.cuda.synchronize()
+        check(out.detach().cpu(), ref, dtype, name)
+    x_nchw = dv[0].permute(0, 3, 1, 2).contiguous()
+    for name, fn in (("tl nchw", fused_tl.dcn_apply_nchw), ("fuse_c nchw", dsn.dcn_apply_nchw)):
+        out = fn(x_nchw, *dv[1:], 1, 1, 1)
+        torch.cuda.synchronize()
+        assert out.is_contiguous()
+        check(out.detach().permute(0, 2, 3, 1).cpu(), ref, dtype, name)
+
+
+def test_pack_cuda_channels_last(monkeypatch):
+    """Pack(backend='cuda') with ENABLE_CHANNEL_LAST (modulated_deform_conv.py:614-621): the
+    NCHW path on contiguous copies, output in channels_last memory format, same values."""
+    from modulated_deform_conv import ModulatedDeformConv2dPack
+    torch.manual_seed(4)
+    mod = ModulatedDeformConv2dPack(32, 40, 3, stride=1, padding=1, backend="cuda")
+    with torch.no_grad():
+        mod.conv_offset.weight.normal_(0, 0.05)
+        mod.conv_offset.bias.normal_(0, 0.5)
+    mod = mod.to(DEV)
+    x = torch.randn(2, 32, 11, 13).to(DEV).to(memory_format=torch.channels_last)
+    with torch.no_grad():
+        monkeypatch.setenv("ENABLE_CHANNEL_LAST", "1")
+        out_cl = mod(x)
+        monkeypatch.setenv("ENABLE_CHANNEL_LAST", "0")
+        out = mod(x)
+        y = mod.conv_offset(x)
+    torch.cuda.synchronize()
+    assert out_cl.is_contiguous(memory_format=torch.channels_last)
+    off, msk = od.split_y_nchw(y.double().cpu(), 9)
+    ref = od.forward_nchw(x.double().cpu(), off, msk, mod.weight.double().cpu(),
+                          mod.bias.double().cpu(), (1, 1), (1, 1), (1, 1))
+    check(out_cl.cpu(), ref, torch.float32, "channels_last")
+    check(out.cpu(), ref, torch.float32, "contiguous")

@@ -253,19 +253,88 @@ def test_dcn_split_nhwc_backward(dtype, bn, relu):
     # float64 reference of the same composition, by autograd. The derivative of a bilinear
     # sample with respect to its position jumps at cell edges, so the reference evaluates
     # it at the kernel's own sample positions: the forward value of y is the one the
-    # library convolution produced in the input dtype, its gradient that of the exact conv.
+    # backward reads (the kernel's fp32 offset conv rounded to the input dtype), its
+    # gradient that of the exact conv.
     r = [t.to(dtype).double().requires_grad_() for t in (x, w_off, b_off, weight, bias)]
     y = F.conv2d(r[0].permute(0, 3, 1, 2), r[1], r[2], 1, 1, 1)
     with torch.no_grad():
-        y_kernel = F.conv2d(leaves[0].permute(0, 3, 1, 2), leaves[1], leaves[2], 1, 1, 1)
-    y = (y + (y_kernel.cpu().double() - y).detach()).permute(0, 2, 3, 1)
+        assert dsn.mega_supported(leaves[0], leaves[1], leaves[3])
+        y_kernel = dsn.offset_conv_y(leaves[0], leaves[1], leaves[2], 1, 1, 1).to(dtype)
+    y = y + (y_kernel.permute(0, 3, 1, 2).cpu().double() - y).detach()
+    y = y.permute(0, 2, 3, 1)
     o, m = od.split_y_nhwc(y, 9)
     ref = od.forward_nhwc(r[0], o, m, r[3], r[4], 1, 1, 1, gate=False)
     if bn:
         ref = ref * scale.double() + shift.double()
         if relu:
-            ref = torch.relu(ref)
+            # the backward takes the ReLU mask the forward saved (dcn_split_nhwc.py:
+            # 190-196, 245-250): outputs within rounding of 0 follow the kernel's sign
+            ref = ref * (out.detach().cpu() > 0)
     ref.backward(go.to(dtype).double())
     tol_dtype = torch.float32 if dtype == torch.float32 else dtype
     for name, a, rr in zip(("x", "w_off", "b_off", "weight", "bias"), leaves, r):
         check(a.grad.cpu(), rr.grad, tol_dtype, f"grad {name} bn{bn} relu{relu}")
+
+
+# ---------------------------------------------------------------------------------------
+# fused_tl backward: dcn_col2im_nhwc and the autograd dcn_split / Pack(backend='tilelang')
+# ---------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["fp32", "fp16"])
+def test_fused_tl_col2im_nhwc(dtype):
+    """fused_tl.dcn_col2im_nhwc (fused_tl.py:831-862): fp32 gradients of X, offset and the
+    (post-sigmoid) mask, against autograd of the oracle columns weighted by dCol."""
+    from modulated_deform_conv import fused_tl
+    x, off, mask, _, _, ho, wo = _problem(2, 64, 11, 13, 3, 1, 1, 1, seed=8, dtype=dtype)
+    b, cin, h, w = x.shape
+    xh, oh, mh = _nhwc(x), _nhwc(off), _nhwc(mask)
+    g = torch.Generator().manual_seed(2)
+    dcol = torch.randn(b * ho * wo, 9 * cin, generator=g).to(dtype)
+    gx, goff, gmask = fused_tl.dcn_col2im_nhwc(dcol.to(DEV), xh.to(DEV), oh.to(DEV),
+                                               mh.to(DEV), 3, 3, 1, 1, 1)
+    torch.cuda.synchronize()
+    assert gx.dtype == goff.dtype == gmask.dtype == torch.float32
+    leaves = [t.double().requires_grad_() for t in (xh, oh, mh)]
+    cols = od.columns_nhwc(*leaves, 3, 3, 1, 1, 1, 1, 1, 1, gate=False)
+    grads = torch.autograd.grad((cols * dcol.double()).sum(), leaves)
+    tol = torch.float32 if dtype == torch.float32 else dtype
+    for name, a, r in zip(("grad_X", "grad_offset", "grad_mask"), (gx, goff, gmask), grads):
+        check(a.cpu(), r, tol, f"dcn_col2im_nhwc {name}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["fp32", "fp16"])
+def test_pack_tilelang_backward(dtype):
+    """ModulatedDeformConv2dPack(backend='tilelang') trains: fused_tl.dcn_apply_nchw ->
+    _DCNSplitFunction. Gradients of the input and of all four parameters against autograd
+    of the float64 oracle evaluated at the kernel's sample positions (see
+    test_dcn_split_nhwc_backward)."""
+    from modulated_deform_conv import ModulatedDeformConv2dPack
+    from modulated_deform_conv import dcn_split_nhwc as dsn
+    torch.manual_seed(3)
+    mod = ModulatedDeformConv2dPack(64, 48, 3, stride=1, padding=1, backend="tilelang")
+    with torch.no_grad():
+        mod.conv_offset.weight.normal_(0, 0.03)
+        mod.conv_offset.bias.normal_(0, 0.5)
+        mod.bias.normal_()
+    mod = mod.to(dtype).to(DEV)
+    x = torch.randn(2, 64, 9, 10).to(dtype).to(DEV).requires_grad_()
+    out = mod(x)
+    g = torch.Generator().manual_seed(4)
+    go = torch.randn(out.shape, generator=g).to(dtype)
+    out.backward(go.to(DEV))
+    torch.cuda.synchronize()
+    params = [mod.conv_offset.weight, mod.conv_offset.bias, mod.weight, mod.bias]
+    r = [t.detach().cpu().double().requires_grad_() for t in [x] + params]
+    xr = r[0].permute(0, 2, 3, 1)
+    y = F.conv2d(r[0], r[1], r[2], 1, 1, 1)
+    with torch.no_grad():
+        xk = x.detach().permute(0, 2, 3, 1).contiguous()
+        y_kernel = dsn.offset_conv_y(xk, mod.conv_offset.weight, mod.conv_offset.bias, 1, 1,
+                                     1).to(dtype)
+    y = (y + (y_kernel.permute(0, 3, 1, 2).cpu().double() - y).detach()).permute(0, 2, 3, 1)
+    o, m = od.split_y_nhwc(y, 9)
+    ref = od.forward_nhwc(xr, o, m, r[3], r[4], 1, 1, 1, gate=False).permute(0, 3, 1, 2)
+    ref.backward(go.double())
+    tol = torch.float32 if dtype == torch.float32 else dtype
+    for name, a, rr in zip(("x", "w_off", "b_off", "weight", "bias"), [x] + params, r):
+        check(a.grad.cpu(), rr.grad, tol, f"tilelang Pack grad {name}")
