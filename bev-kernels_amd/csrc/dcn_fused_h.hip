@@ -493,7 +493,7 @@ __device__ __forceinline__ uint32_t b_frag_offset(int n, int kh, int lane, int n
                        : oob;
 }
 
-// Consumer wave c: B(k+1) issued at step k, MFMA(k) from A buffer k % 2, one barrier per
+// Consumer wave c: B(k+2) issued at step k, MFMA(k) from A buffer k % 2, one barrier per
 // step; then the epilogue (bias, relu, one rounding). Always NRB row blocks (compile-time,
 // so the MFMA loop and the accumulators carry no run-time conditions); nrb row blocks are
 // stored.
@@ -517,15 +517,17 @@ __device__ __forceinline__ void dcn_p_consumer(const HParams &p, T (*As)[NRB * 1
         br[kh][cb] = __builtin_amdgcn_raw_buffer_load_b128(
             wr, bo[kh][cb], (uint32_t)ks * (uint32_t)(kPBK / 16) * 1024u, 0);
   };
+  // The matrix-core waves go first when both waves of a SIMD are ready to issue.
+  __builtin_amdgcn_s_setprio(1);
   floatx4 acc[NRB][4];
 #pragma unroll
   for (int i = 0; i < NRB; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-  // One B register set: B(k+1) is loaded right after step k's MFMAs (it has the barrier
-  // and the next step's A-fragment reads to arrive).
-  int4v br[kPKH][4];
-  auto step = [&](int ks) __attribute__((always_inline)) {
+  // Two B register sets: B(k+2) is loaded right after step k's MFMAs, so a weight load
+  // queued behind the producers' gathers has a whole step to arrive.
+  int4v br0[kPKH][4], br1[kPKH][4];
+  auto step = [&](int ks, int4v (&br)[kPKH][4]) __attribute__((always_inline)) {
     const int buf = ks & 1;
 #pragma unroll
     for (int kh = 0; kh < kPKH; ++kh) {
@@ -540,12 +542,19 @@ __device__ __forceinline__ void dcn_p_consumer(const HParams &p, T (*As)[NRB * 1
         for (int cb = 0; cb < 4; ++cb)
           acc[rbi][cb] = mfma16x16<T>(af[rbi], br[kh][cb], acc[rbi][cb]);
     }
-    issue_b(ks + 1, br);
+    issue_b(ks + 2, br);
     __syncthreads();
   };
-  issue_b(0, br);
+  issue_b(0, br0);
+  issue_b(1, br1);
   __syncthreads();  // A(0) written by the producers
-  for (int ks = 0; ks < nk; ++ks) step(ks);
+  int ks = 0;
+  for (; ks + 2 <= nk; ks += 2) {
+    step(ks, br0);
+    step(ks + 1, br1);
+  }
+  if (ks < nk) step(ks, br0);
+  __builtin_amdgcn_s_setprio(0);
 
   // Epilogue: lane holds column 64 wave + 16 cb + (lane & 15), rows 4 (lane >> 4) + e.
   T *out = static_cast<T *>(p.out);

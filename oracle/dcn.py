@@ -156,8 +156,16 @@ def bilinear_nhwc(im_b, h, w, gate=True):
     return torch.where(outer.unsqueeze(-1), out, torch.zeros_like(out))
 
 
-def columns_nhwc(x, offset, mask, kh, kw, sh, sw, ph, pw, dh, dw, gate=True):
-    """fused_tl.py:177-201: columns [B*Ho*Wo, T*C], k = t*C + c (gate: see bilinear_nhwc)."""
+def columns_nhwc(x, offset, mask, kh, kw, sh, sw, ph, pw, dh, dw, gate=True,
+                 coord_dtype=None):
+    """fused_tl.py:177-201: columns [B*Ho*Wo, T*C], k = t*C + c (gate: see bilinear_nhwc).
+
+    coord_dtype=torch.float32 rounds each sampling coordinate (integer tap position +
+    offset) once to fp32 and evaluates everything else in x's dtype: the reference's
+    kernels hold the coordinate in a float (dcn_fused_nhwc_kernel.cuh:140-141,
+    fused_tl.py:114-115), and an fp16 / fp32 offset added to a tap position can need more
+    than 24 significant bits (39 - 0.00173 needs 26). The rounding is an identity for
+    autograd, so gradients are those at the rounded coordinate."""
     B, H, W, C = x.shape
     T = kh * kw
     Ho = out_size(H, ph, dh, kh, sh)
@@ -171,16 +179,19 @@ def columns_nhwc(x, offset, mask, kh, kw, sh, sw, ph, pw, dh, dw, gate=True):
             ki, kj = t // kw, t % kw
             h_im = oh * sh - ph + ki * dh + offset[b, :, :, 2 * t].reshape(-1)
             w_im = ow * sw - pw + kj * dw + offset[b, :, :, 2 * t + 1].reshape(-1)
+            if coord_dtype is not None:
+                h_im = h_im + (h_im.detach().to(coord_dtype).to(dt) - h_im.detach())
+                w_im = w_im + (w_im.detach().to(coord_dtype).to(dt) - w_im.detach())
             samp = bilinear_nhwc(x[b], h_im, w_im, gate)
             cols[b, :, t, :] = samp * mask[b, :, :, t].reshape(-1, 1)
     return cols.reshape(B * Ho * Wo, T * C)
 
 
 def forward_nhwc(x, offset, mask, weight, bias=None, stride=1, padding=0, dilation=1,
-                 col_dtype=None, gate=True):
+                 col_dtype=None, gate=True, coord_dtype=None):
     """fused_tl.py:204-227: cols @ weight.permute(2,3,1,0).reshape(K, Cout) (+ bias).
     col_dtype: round the columns to this dtype first (see _round_cols); gate: see
-    bilinear_nhwc."""
+    bilinear_nhwc; coord_dtype: see columns_nhwc."""
     def two(v):
         return (v, v) if isinstance(v, int) else tuple(v)
     (sh, sw), (ph, pw), (dh, dw) = two(stride), two(padding), two(dilation)
@@ -188,8 +199,8 @@ def forward_nhwc(x, offset, mask, weight, bias=None, stride=1, padding=0, dilati
     Cout, _, kh, kw = weight.shape
     Ho = out_size(H, ph, dh, kh, sh)
     Wo = out_size(W, pw, dw, kw, sw)
-    cols = _round_cols(columns_nhwc(x, offset, mask, kh, kw, sh, sw, ph, pw, dh, dw, gate),
-                       col_dtype)
+    cols = _round_cols(columns_nhwc(x, offset, mask, kh, kw, sh, sw, ph, pw, dh, dw, gate,
+                                    coord_dtype), col_dtype)
     out = (cols @ weight.permute(2, 3, 1, 0).reshape(kh * kw * C, Cout)).view(B, Ho, Wo, Cout)
     if bias is not None:
         out = out + bias.view(1, 1, 1, -1)

@@ -501,9 +501,11 @@ def test_fused_columns_single_rounding(dtype, shape):
     element of the deformable A operand, passed exactly through the fp32 MFMA accumulation.
     The kernel blends the four corners in fp32 and rounds once to the input dtype (the
     reference's gather, dcn_fused_nhwc_kernel.cuh:185-187): against the float64 columns
-    rounded once, every element is within one ulp and almost all are equal (only values
-    within fp32 rounding of a tie may differ). A blend in 16-bit arithmetic (weights
-    rounded, partial sums rounded) fails the equality count."""
+    rounded once (at the kernel's fp32 sampling coordinate), almost all elements are equal (a difference needs the exact value within
+    fp32 rounding of a rounding boundary), and each differing one is within one ulp plus
+    the fp32 blend's own error (a few 2^-24 of sum |w_q * corner_q|, which shows when the
+    corners cancel). A blend in 16-bit arithmetic (weights rounded, partial sums rounded)
+    fails both the equality count and the per-element bound."""
     from modulated_deform_conv import fused_tl
     b, cin, cout, h, w = shape
     d = inputs.nchw_to_nhwc(_rand_problem(b, cin, cout, h, w, dtype=dtype, seed=31))
@@ -516,9 +518,13 @@ def test_fused_columns_single_rounding(dtype, shape):
                                           d["mask"].to(DEV), weight.to(DEV), None, 1, 1, 1)
     torch.cuda.synchronize()
     got = out.cpu().reshape(-1, cout)
+    # the sampling coordinate is an fp32 sum in the kernel, as in the reference's kernels
     cols = od.columns_nhwc(d["x"].double(), d["offset"].double(), d["mask"].double(), 3, 3, 1,
-                           1, 1, 1, 1, 1)
+                           1, 1, 1, 1, 1, coord_dtype=torch.float32)
     ref = cols[:, sel].to(dtype)                              # one rounding
+    # sum_q |w_q * corner_q|: the columns of |x| (bilinear weights and mask are >= 0)
+    mag = od.columns_nhwc(d["x"].double().abs(), d["offset"].double(), d["mask"].double(),
+                          3, 3, 1, 1, 1, 1, 1, 1, coord_dtype=torch.float32)[:, sel]
     diff = got != ref
     frac = diff.double().mean().item()
     assert frac < 1e-3, f"{frac:.2e} of the A elements differ from one rounding"
@@ -526,9 +532,10 @@ def test_fused_columns_single_rounding(dtype, shape):
         a, r = got[diff].double(), ref[diff].double()
         ulp = (r.abs() * (2.0 ** -10 if dtype == torch.float16 else 2.0 ** -7)).clamp_min(
             2.0 ** -24)
-        far = (a - r).abs() > ulp * 1.0001
+        bound = ulp * 1.0001 + 8 * 2.0 ** -24 * mag[diff]
+        far = (a - r).abs() > bound
         assert not far.any(), (
-            f"{int(far.sum())} of {a.numel()} differing elements beyond one ulp; first "
+            f"{int(far.sum())} of {a.numel()} differing elements beyond the bound; first "
             f"(got, want): {list(zip(a[far][:6].tolist(), r[far][:6].tolist()))}")
 
 

@@ -295,3 +295,35 @@ def test_gradcheck_front_end_columns():
     f = lambda x, w, b: od.fused_front_end_columns(x, w, b, 3, 3, 1, 1, 1)
     assert torch.autograd.gradcheck(f, (x.requires_grad_(), w_off.requires_grad_(),
                                         b_off.requires_grad_()))
+
+
+def test_fp32_coordinates():
+    """coord_dtype=torch.float32 evaluates the sample at fp32(tap position + offset):
+    (1) offsets whose sum with the tap position is exact in fp32 leave the columns
+    unchanged; (2) an offset that needs more than 24 bits (39 - 0.00172901153...) gives
+    the columns of the explicitly rounded coordinate, and so a different value from the
+    exact one; (3) gradients flow to the offset as through the identity."""
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(1, 6, 45, 3, generator=g, dtype=torch.float64)
+    off = torch.round(4 * torch.randn(1, 6, 45, 18, generator=g, dtype=torch.float64)) / 256
+    mask = torch.rand(1, 6, 45, 9, generator=g, dtype=torch.float64)
+    exact = od.columns_nhwc(x, off, mask, 3, 3, 1, 1, 1, 1, 1, 1)
+    rounded = od.columns_nhwc(x, off, mask, 3, 3, 1, 1, 1, 1, 1, 1, coord_dtype=torch.float32)
+    assert torch.equal(exact, rounded)
+    # pixel (0, 40), tap t = 3 (ki = 1, kj = 0): w = 40 - 1 + 0 + dx = 39 + dx
+    dx = -0.0017290115356445312            # an fp16 value; 39 + dx is not an fp32
+    off2 = off.clone()
+    off2[0, 0, 40, 2 * 3 + 1] = dx
+    w32 = float(torch.tensor(39.0 + dx, dtype=torch.float64).float())
+    assert w32 != 39.0 + dx
+    off3 = off2.clone()
+    off3[0, 0, 40, 2 * 3 + 1] = w32 - 39.0  # exact in float64: the rounded coordinate
+    got = od.columns_nhwc(x, off2, mask, 3, 3, 1, 1, 1, 1, 1, 1, coord_dtype=torch.float32)
+    want = od.columns_nhwc(x, off3, mask, 3, 3, 1, 1, 1, 1, 1, 1)
+    assert torch.equal(got, want)
+    assert not torch.equal(got, od.columns_nhwc(x, off2, mask, 3, 3, 1, 1, 1, 1, 1, 1))
+    o = off2.clone().requires_grad_()
+    od.columns_nhwc(x, o, mask, 3, 3, 1, 1, 1, 1, 1, 1, coord_dtype=torch.float32).sum().backward()
+    o3 = off3.clone().requires_grad_()
+    od.columns_nhwc(x, o3, mask, 3, 3, 1, 1, 1, 1, 1, 1).sum().backward()
+    assert torch.allclose(o.grad, o3.grad, rtol=0, atol=1e-12)
