@@ -41,6 +41,8 @@ _SIGNATURES = {
     "bevk_dcn_fused_im2col_nhwc_workspace_bytes": [_i] * 7,
     "bevk_modulated_deformable_fused_im2col_nhwc": [_i, _vp, _vp, _vp] + [_i] * 15
     + [_vp, ctypes.c_int64, _vp, _vp],
+    "bevk_modulated_deformable_fused_im2col_nhwc_noalloc": [_i, _vp, _vp, _vp] + [_i] * 15
+    + [_vp, _vp],
     "bevk_dcn_packed_weight_bytes": [_i] * 5,
     "bevk_dcn_pack_weight": [_i, _vp] + [_i] * 4 + [_vp, _vp],
     "bevk_dcn_fused_fwd_nhwc": [_i, _vp, _vp, _i, _vp, _vp, _vp] + [_i] * 15 + [_vp, _vp],

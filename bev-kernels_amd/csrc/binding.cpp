@@ -6,6 +6,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "../../include/bev_kernels.h"
@@ -249,6 +250,36 @@ int bevk_modulated_deformable_col2im_nhwc(
                     fn);
 }
 
+// Static scratch of the allocation-free front end
+// (bevk_modulated_deformable_fused_im2col_nhwc_noalloc): the packed offset-conv weight and
+// the fp32 offset-conv output y [M][3T] of one call. Every GPU the library runs on holds
+// its own copy until the process ends; calls that overlap on one GPU share it and race.
+static constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+// The device address of `scratch` on the current device, looked up once per device (the
+// host-side name is not a device address: kernels and copies take this pointer).
+static constexpr int kMaxScratchDevices = 64;
+static std::mutex g_scratch_mutex;
+static void *g_scratch_ptr[kMaxScratchDevices];
+
+static int device_scratch(const char *fn, void **out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices)
+    return fail(BEVK_ERR_HIP, "%s: no usable current HIP device", fn);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void *ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return fail(BEVK_ERR_HIP, "%s: hipGetSymbolAddress(scratch) failed: %s", fn,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
 // Workspace of the fused front end: packed offset-conv weight, then y [M][3T] fp32.
 static long long fused_im2col_ws_parts(int dtype, long long m, int taps, int channels,
                                        long long *y_offset) {
@@ -270,13 +301,15 @@ int64_t bevk_dcn_fused_im2col_nhwc_workspace_bytes(int dtype, int batch_size, in
                                kernel_h * kernel_w, channels, &y_offset);
 }
 
-int bevk_modulated_deformable_fused_im2col_nhwc(
-    int dtype, const void *data_im, const void *w_off, const float *b_off, int batch_size,
-    int channels, int height_im, int width_im, int height_col, int width_col, int kernel_h,
-    int kernel_w, int pad_h, int pad_w, int stride_h, int stride_w, int dilation_h,
-    int dilation_w, int deformable_group, void *workspace, int64_t workspace_bytes,
-    void *data_col, void *stream) {
-  const char *fn = "modulated_deformable_fused_im2col_nhwc";
+// The fused front end (offset conv + sigmoid + gather into the columns) with its scratch
+// in the caller's `workspace`, or (static_scratch) in the library's static scratch, whose
+// capacity is then workspace_bytes: a larger need is an error.
+static int fused_im2col_run(
+    const char *fn, bool static_scratch, int dtype, const void *data_im, const void *w_off, const float *b_off,
+    int batch_size, int channels, int height_im, int width_im, int height_col, int width_col,
+    int kernel_h, int kernel_w, int pad_h, int pad_w, int stride_h, int stride_w,
+    int dilation_h, int dilation_w, int deformable_group, void *workspace,
+    int64_t workspace_bytes, void *data_col, void *stream) {
   g_last_error.clear();
   // dcn_fused_nhwc_cuda.cu:99-100
   if (deformable_group != 1)
@@ -308,10 +341,18 @@ int bevk_modulated_deformable_fused_im2col_nhwc(
   long long y_offset = 0;
   const long long need = fused_im2col_ws_parts(dtype, m, taps, channels, &y_offset);
   if (workspace_bytes < need)
-    return fail(BEVK_ERR_INVALID, "%s: workspace of %lld bytes, %lld needed", fn,
-                (long long)workspace_bytes, need);
-  if (!data_im || !w_off || !b_off || !workspace || !data_col)
+    return static_scratch
+               ? fail(BEVK_ERR_INVALID,
+                      "%s: this shape needs %lld bytes of scratch; the library's static "
+                      "scratch holds %lld (use the workspace entry point)",
+                      fn, need, (long long)workspace_bytes)
+               : fail(BEVK_ERR_INVALID, "%s: workspace of %lld bytes, %lld needed", fn,
+                      (long long)workspace_bytes, need);
+  if (!data_im || !w_off || !b_off || !data_col || (!static_scratch && !workspace))
     return fail(BEVK_ERR_INVALID, "%s: null tensor pointer", fn);
+  if (static_scratch) {
+    if (int rc = device_scratch(fn, &workspace)) return rc;
+  }
   const hipStream_t st = (hipStream_t)stream;
   void *packed = workspace;
   float *y = reinterpret_cast<float *>(static_cast<char *>(workspace) + y_offset);
@@ -329,6 +370,31 @@ int bevk_modulated_deformable_fused_im2col_nhwc(
   // 3. sigmoid, bias and the deformable gather into the columns
   return hip_status(bevk::launch_im2col_nhwc_yf32(dtype, g, data_im, y, b_off, data_col, st),
                     fn);
+}
+
+int bevk_modulated_deformable_fused_im2col_nhwc(
+    int dtype, const void *data_im, const void *w_off, const float *b_off, int batch_size,
+    int channels, int height_im, int width_im, int height_col, int width_col, int kernel_h,
+    int kernel_w, int pad_h, int pad_w, int stride_h, int stride_w, int dilation_h,
+    int dilation_w, int deformable_group, void *workspace, int64_t workspace_bytes,
+    void *data_col, void *stream) {
+  return fused_im2col_run("modulated_deformable_fused_im2col_nhwc", false, dtype, data_im,
+                          w_off, b_off, batch_size, channels, height_im, width_im, height_col,
+                          width_col, kernel_h, kernel_w, pad_h, pad_w, stride_h, stride_w,
+                          dilation_h, dilation_w, deformable_group, workspace,
+                          workspace_bytes, data_col, stream);
+}
+
+int bevk_modulated_deformable_fused_im2col_nhwc_noalloc(
+    int dtype, const void *data_im, const void *w_off, const float *b_off, int batch_size,
+    int channels, int height_im, int width_im, int height_col, int width_col, int kernel_h,
+    int kernel_w, int pad_h, int pad_w, int stride_h, int stride_w, int dilation_h,
+    int dilation_w, int deformable_group, void *data_col, void *stream) {
+  return fused_im2col_run("modulated_deformable_fused_im2col_nhwc_noalloc", true, dtype, data_im,
+                          w_off, b_off, batch_size, channels, height_im, width_im, height_col,
+                          width_col, kernel_h, kernel_w, pad_h, pad_w, stride_h, stride_w,
+                          dilation_h, dilation_w, deformable_group, nullptr,
+                          (int64_t)kNoAllocScratchBytes, data_col, stream);
 }
 
 int64_t bevk_dcn_packed_weight_bytes(int dtype, int channels_out, int kernel_h, int kernel_w,

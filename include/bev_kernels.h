@@ -163,6 +163,21 @@ int bevk_modulated_deformable_fused_im2col_nhwc(
     int dilation_w, int deformable_group, void *workspace, int64_t workspace_bytes,
     void *data_col, void *stream);
 
+/* The fused NHWC front end above without a workspace argument: it allocates nothing
+ * (no hipMalloc / hipFree, no allocating library call) and keeps the packed offset-conv
+ * weight and the fp32 offset-conv output in a 16 MiB static device array of the library
+ * (one copy per GPU, held until the process ends). No counterpart in the reference: it is
+ * for callers that cannot allocate (code under HIP graph capture, tight serving loops).
+ * Shapes whose scratch need (bevk_dcn_fused_im2col_nhwc_workspace_bytes) exceeds 16 MiB
+ * return BEVK_ERR_INVALID before any device work. Calls that overlap on one GPU share the
+ * array and race; everything in it is written before it is read, so nothing carries over
+ * between calls. Arguments and results as bevk_modulated_deformable_fused_im2col_nhwc. */
+int bevk_modulated_deformable_fused_im2col_nhwc_noalloc(
+    int dtype, const void *data_im, const void *w_off, const float *b_off, int batch_size,
+    int channels, int height_im, int width_im, int height_col, int width_col, int kernel_h,
+    int kernel_w, int pad_h, int pad_w, int stride_h, int stride_w, int dilation_h,
+    int dilation_w, int deformable_group, void *data_col, void *stream);
+
 /* Bytes of the packed weight that bevk_dcn_fused_fwd_nhwc consumes for this shape
  * (-1 for an unsupported dtype). */
 int64_t bevk_dcn_packed_weight_bytes(int dtype, int channels_out, int kernel_h, int kernel_w,

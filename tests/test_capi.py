@@ -214,3 +214,14 @@ def test_offset_conv_validation(entry):
     assert _offset_conv(entry, ho=4) == INVALID and "does not match" in _err()
     assert _offset_conv(entry) == INVALID and "null" in _err()
     assert _offset_conv(entry, b=0) == 0          # nothing to do
+
+
+def test_noalloc_front_end_rejects_oversize_before_device_work():
+    """The allocation-free front end checks its scratch need (here y alone: 160000 x 27 x
+    4 bytes) against its 16 MiB static scratch before touching the device (fake
+    addresses: nothing is dereferenced, no HIP call is made)."""
+    f = _bevk.lib().bevk_modulated_deformable_fused_im2col_nhwc_noalloc
+    p = ctypes.c_void_p
+    rc = f(1, p(0x10000), p(0x20000), p(0x30000), 1, 16, 400, 400, 400, 400, 3, 3, 1, 1, 1, 1,
+           1, 1, 1, p(0x40000), NULL)
+    assert rc == INVALID and "static scratch" in _err()
