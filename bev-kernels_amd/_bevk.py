@@ -50,7 +50,7 @@ _SIGNATURES = {
     "bevk_dcn_offset_conv_nhwc": [_i, _vp, _vp, _vp] + [_i] * 14 + [_vp, _vp],
     "bevk_dcn_mega_fwd_nhwc": [_i, _vp, _vp, _vp, _vp, _vp] + [_i] * 16 + [_vp, _vp, _vp],
     "bevk_msda_forward": [_i, _vp, _vp, _vp, _vp, _vp] + [_i] * 9 + [_vp, _vp],
-    "bevk_msda_backward_workspace_bytes": [_i] * 5,
+    "bevk_msda_backward_workspace_bytes": [_i] * 8,
     "bevk_msda_backward": [_i, _vp, _vp, _vp, _vp, _vp, _vp] + [ctypes.c_int64] * 4
     + [_i] * 9 + [_vp, _vp, _vp, _vp, ctypes.c_int64, _vp],
 }

@@ -584,7 +584,8 @@ def backward(value, spatial_shapes, level_start_index, sampling_loc, attn_weight
     g4 = grad_output.view(batch, num_query, heads, channels)
     sb, sq, sh, sc = g4.stride()
     code = _b.dtype_code(value)
-    nbytes = _b.lib().bevk_msda_backward_workspace_bytes(code, batch, spatial, heads, channels)
+    nbytes = _b.lib().bevk_msda_backward_workspace_bytes(code, batch, spatial, heads, channels,
+                                                          num_levels, num_query, num_point)
     if nbytes < 0:
         raise RuntimeError(f"{fn}: invalid sizes")
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=value.device)

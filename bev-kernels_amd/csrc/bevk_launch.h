@@ -32,11 +32,17 @@ struct MsdaBwdArgs {
   const void *grad_output;
   int64_t go_stride[4];  // grad_output strides over (batch, query, head, channel), elements
   void *grad_value, *grad_loc, *grad_attn;
-  void *workspace;       // fp32 accumulator for 16-bit dtypes
+  void *workspace;       // fp32 accumulator for 16-bit dtypes, then the sorted path's buffers
+  int64_t workspace_bytes;
 };
 
-// Bytes of fp32 accumulator the 16-bit backward needs (0 for f32 / f64).
-int64_t msda_backward_workspace_bytes(int dtype, int64_t value_elems);
+// Bytes of fp32 accumulator the 16-bit backward needs at least (0 for f32 / f64).
+int64_t msda_backward_workspace_min(int dtype, int64_t value_elems);
+// Bytes that also hold the buffers of the sorted grad_value path (D = 32), which runs when
+// the workspace is at least this large.
+int64_t msda_backward_workspace_bytes(int dtype, int64_t batch, int64_t spatial_size,
+                                      int64_t num_heads, int64_t channels, int64_t num_levels,
+                                      int64_t num_query, int64_t num_point);
 // force_generic: the per-unit atomic kernel for every level (no coarse split, no grid
 // owner pass, no D = 32 kernel).
 hipError_t launch_msda_backward(int dtype, const MsdaBwdArgs &a, bool force_generic,

@@ -604,11 +604,13 @@ int bevk_msda_forward(int dtype, const void *value, const int64_t *spatial_shape
 }
 
 int64_t bevk_msda_backward_workspace_bytes(int dtype, int batch, int spatial_size,
-                                           int num_heads, int channels) {
-  if (!valid_dtype(dtype) || batch < 0 || spatial_size < 0 || num_heads < 0 || channels < 0)
+                                           int num_heads, int channels, int num_levels,
+                                           int num_query, int num_point) {
+  if (!valid_dtype(dtype) || batch < 0 || spatial_size < 0 || num_heads < 0 || channels < 0 ||
+      num_levels < 0 || num_query < 0 || num_point < 0)
     return -1;
-  return bevk::msda_backward_workspace_bytes(
-      dtype, (int64_t)batch * spatial_size * num_heads * channels);
+  return bevk::msda_backward_workspace_bytes(dtype, batch, spatial_size, num_heads, channels,
+                                             num_levels, num_query, num_point);
 }
 
 int bevk_msda_backward(int dtype, const void *value, const int64_t *spatial_shapes,
@@ -632,7 +634,7 @@ int bevk_msda_backward(int dtype, const void *value, const int64_t *spatial_shap
   if (step > 0 && batch % step != 0)
     return fail(BEVK_ERR_INVALID, "batch must divide im2col_step");
   const int64_t value_elems = (int64_t)batch * spatial_size * num_heads * channels;
-  const int64_t need = bevk::msda_backward_workspace_bytes(dtype, value_elems);
+  const int64_t need = bevk::msda_backward_workspace_min(dtype, value_elems);
   if (workspace_bytes < need)
     return fail(BEVK_ERR_INVALID, "%s: workspace of %lld bytes, %lld needed", fn,
                 (long long)workspace_bytes, (long long)need);
@@ -660,6 +662,7 @@ int bevk_msda_backward(int dtype, const void *value, const int64_t *spatial_shap
   a.go_stride[2] = go_stride_h; a.go_stride[3] = go_stride_c;
   a.grad_value = grad_value; a.grad_loc = grad_sampling_loc; a.grad_attn = grad_attn_weight;
   a.workspace = workspace;
+  a.workspace_bytes = workspace_bytes;
   return hip_status(
       bevk::launch_msda_backward(dtype, a, force_generic_col2im != 0, (hipStream_t)stream), fn);
 }

@@ -35,6 +35,8 @@
 
 #include <hip/amd_detail/amd_hip_unsafe_atomics.h>
 
+#include <type_traits>
+
 namespace bevk {
 namespace {
 
@@ -847,6 +849,489 @@ __global__ void __launch_bounds__(kBlock) msda_col2im_d32_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Sorted grad_value path (D = 32, fp32 accumulation, every level). The fp32 atomics of
+// msda_col2im_d32_kernel add one 128-byte row per valid corner (30.7 M rows for the fine
+// levels of SCA), at the L2's atomic line rate. Here the corner adds are bucketed by
+// position instead, and every bucket of kBkPos consecutive positions of a (batch, head)
+// slice is summed by one workgroup that owns those grad_value rows:
+//   1. msda_bkt_count_kernel: the valid corners of every sample counted per bucket (LDS
+//      histogram per block, one global add per bucket and block);
+//   2. msda_bkt_scan_kernel: bucket offsets and placement cursors, and the non-empty
+//      buckets listed per XCD (slice % 8, or bucket % 8 with fewer than 8 slices);
+//   3. msda_bkt_place_kernel: the corners again, staged in LDS in bucket order, each
+//      bucket's range reserved once per block, then written as contiguous runs of
+//      (weight, query << kBkShift | position in bucket);
+//   4. msda_bkt_acc_kernel: per bucket, chunks of at most kAccChunk corners sorted by
+//      position in LDS; each half-wave takes whole positions (about 1/16 of the chunk's
+//      corners), sums weight x grad_output row in registers and adds the sum to the
+//      bucket's LDS accumulator, which is added to grad_value once at the end (no atomics:
+//      no other workgroup writes these rows).
+// grad_sampling_loc / grad_attn_weight come from msda_coord_kernel (no atomics).
+// Corner set and weights are those of the reference (ms_deform_attn_kernels.cuh:427-490):
+// the same in-window test and per-corner bounds, weight = bilinear weight x attention.
+// ---------------------------------------------------------------------------
+constexpr int kBkShift = 8;
+constexpr int kBkPos = 1 << kBkShift;      // positions per bucket
+constexpr int kBkMaxPerSlice = 1024;       // buckets per slice (spatial_size <= 256 Ki)
+constexpr int kBkThreads = 256;
+constexpr int kPlaceCap = 4096;            // corners a place block stages (2 blocks per CU)
+constexpr int kAccThreads = 512;
+constexpr int kAccChunk = 12288;           // corners per accumulate pass (LDS)
+constexpr int kAccPerThread = kAccChunk / kAccThreads;
+constexpr int kAccBatch = 16;              // grad_output rows in flight per half-wave
+
+struct BktParams {
+  const void *loc, *attn, *grad_out;
+  const int64_t *shapes, *lsi;
+  float *gv;
+  int *count;       // [nbk] corners per bucket
+  int *cursor;      // [nbk] next free slot (offsets after the scan)
+  int *offset;      // [nbk + 1]
+  int *nitems;      // [8] buckets per XCD list
+  int2 *items;      // [8][item_cap] (bucket, first corner of the chunk)
+  float *pw;        // [capacity] corner weights
+  uint32_t *pq;     // [capacity] (query << kBkShift) | position in bucket
+  int64_t go_sb, go_sq, go_sh, go_sc;
+  uint32_t go_rows_bytes;  // bytes from row (b, 0, h, 0) past row (b, NQ - 1, h, 31)
+  int B, NH, NQ, NL, NP, S, NBS, nbk, item_cap, qpb;
+  int by_bucket;    // fewer than 8 slices: buckets go to XCD bucket % 8, else slice % 8
+  int blocks_per_xcd;
+};
+
+// Calls fn(position, weight) for every valid corner of sample (unit, l, pt) of the
+// slice's value map. Positions outside [0, S) (inconsistent metadata) are skipped.
+template <typename T, typename F>
+__device__ __forceinline__ void for_corners(const BktParams &p, int64_t unit, int l, int pt,
+                                            F &&fn) {
+  const T *loc = static_cast<const T *>(p.loc);
+  const T *attn = static_cast<const T *>(p.attn);
+  const int64_t si = (unit * p.NL + l) * p.NP + pt;
+  const float lx = (float)loc[si * 2], ly = (float)loc[si * 2 + 1], a = (float)attn[si];
+  const int Hl = (int)p.shapes[2 * l], Wl = (int)p.shapes[2 * l + 1];
+  float him, wim;
+  sample_coords<float>(lx, ly, Hl, Wl, him, wim);
+  if (!(him > -1.f && wim > -1.f && him < (float)Hl && wim < (float)Wl)) return;
+  const float fh = floorf(him), fw = floorf(wim);
+  const int hl = (int)fh, wl = (int)fw;
+  const float lh = him - fh, lw = wim - fw, hh = 1.f - lh, hw = 1.f - lw;
+  const int64_t base = p.lsi[l];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int yy = hl + (c >> 1), xx = wl + (c & 1);
+    if (yy < 0 || yy >= Hl || xx < 0 || xx >= Wl) continue;
+    const int64_t pos = base + (int64_t)yy * Wl + xx;
+    if (pos < 0 || pos >= p.S) continue;
+    fn((int)pos, ((c >> 1) ? lh : hh) * ((c & 1) ? lw : hw) * a);
+  }
+}
+
+// Block -> (slice, chunk of qpb queries); samples i = (query in chunk, level, point).
+template <typename T>
+__global__ void __launch_bounds__(kBkThreads) msda_bkt_count_kernel(const BktParams p) {
+  __shared__ int lcnt[kBkMaxPerSlice];
+  const int qchunks = (p.NQ + p.qpb - 1) / p.qpb;
+  const int slice = blockIdx.x / qchunks, qc = blockIdx.x - slice * qchunks;
+  const int b = slice / p.NH, h = slice - b * p.NH;
+  const int q0 = qc * p.qpb, nq = min(p.qpb, p.NQ - q0);
+  const int NS = p.NL * p.NP;
+  for (int k = threadIdx.x; k < p.NBS; k += kBkThreads) lcnt[k] = 0;
+  __syncthreads();
+  for (int i = threadIdx.x; i < nq * NS; i += kBkThreads) {
+    const int u = i / NS, r = i - u * NS, l = r / p.NP, pt = r - l * p.NP;
+    const int64_t unit = ((int64_t)b * p.NQ + q0 + u) * p.NH + h;
+    for_corners<T>(p, unit, l, pt, [&](int pos, float) { atomicAdd(&lcnt[pos >> kBkShift], 1); });
+  }
+  __syncthreads();
+  for (int k = threadIdx.x; k < p.NBS; k += kBkThreads)
+    if (lcnt[k] > 0) atomicAdd(&p.count[slice * p.NBS + k], lcnt[k]);
+}
+
+// One block: exclusive scan of the bucket counts (offset, cursor), then the chunks of at
+// most kAccChunk corners of the buckets of XCD x in list x.
+__global__ void __launch_bounds__(1024) msda_bkt_scan_kernel(const BktParams p) {
+  __shared__ int wsum[16];
+  __shared__ int carry;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  // block-wide exclusive scan of one value per thread (excl) and the block total
+  auto block_scan = [&](int v, int &excl, int &total) __attribute__((always_inline)) {
+    int incl = v;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const int t = __shfl_up(incl, d, kWave);
+      if (lane >= d) incl += t;
+    }
+    if (lane == kWave - 1) wsum[wave] = incl;
+    __syncthreads();
+    int before = 0, tot = 0;
+    for (int w = 0; w < 16; ++w) {
+      if (w < wave) before += wsum[w];
+      tot += wsum[w];
+    }
+    excl = incl - v + before;
+    total = tot;
+    __syncthreads();
+  };
+  if (tid == 0) carry = 0;
+  __syncthreads();
+  for (int k0 = 0; k0 < p.nbk; k0 += 1024) {
+    const int k = k0 + tid;
+    const int c = k < p.nbk ? p.count[k] : 0;
+    int excl, total;
+    block_scan(c, excl, total);
+    const int base = carry;
+    if (k < p.nbk) {
+      p.offset[k] = base + excl;
+      p.cursor[k] = base + excl;
+    }
+    __syncthreads();
+    if (tid == 0) carry = base + total;
+    __syncthreads();
+  }
+  if (tid == 0) p.offset[p.nbk] = carry;
+  for (int x = 0; x < 8; ++x) {
+    if (tid == 0) carry = 0;
+    __syncthreads();
+    for (int k0 = 0; k0 < p.nbk; k0 += 1024) {
+      const int k = k0 + tid;
+      const bool mine = k < p.nbk && ((p.by_bucket ? k : k / p.NBS) & 7) == x;
+      const int c = mine ? p.count[k] : 0;
+      const int nch = (c + kAccChunk - 1) / kAccChunk;
+      int excl, total;
+      block_scan(nch, excl, total);
+      const int base = carry;
+      if (mine) {
+        const int first = p.offset[k];
+        for (int j = 0; j < nch; ++j)
+          if (base + excl + j < p.item_cap)
+            p.items[x * p.item_cap + base + excl + j] = make_int2(k, first + j * kAccChunk);
+      }
+      __syncthreads();
+      if (tid == 0) carry = base + total;
+      __syncthreads();
+    }
+    if (tid == 0) p.nitems[x] = min(carry, p.item_cap);
+    __syncthreads();
+  }
+}
+
+// Same blocks as the count kernel (qpb * L * P * 4 <= kPlaceCap): count again, stage the
+// corners in LDS in bucket order, reserve each bucket's range once, write the runs.
+template <typename T>
+__global__ void __launch_bounds__(kBkThreads) msda_bkt_place_kernel(const BktParams p) {
+  __shared__ int lcnt[kBkMaxPerSlice];   // counts, then staging cursors
+  __shared__ int lst[kBkMaxPerSlice];    // first staged corner of each bucket
+  __shared__ int gbase[kBkMaxPerSlice];  // first global slot of each bucket
+  __shared__ float sw[kPlaceCap];
+  __shared__ uint32_t sq[kPlaceCap];
+  __shared__ unsigned short sb[kPlaceCap];
+  __shared__ int wsum[kBkThreads / kWave];
+  const int qchunks = (p.NQ + p.qpb - 1) / p.qpb;
+  const int slice = blockIdx.x / qchunks, qc = blockIdx.x - slice * qchunks;
+  const int b = slice / p.NH, h = slice - b * p.NH;
+  const int q0 = qc * p.qpb, nq = min(p.qpb, p.NQ - q0);
+  const int NS = p.NL * p.NP;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  for (int k = tid; k < p.NBS; k += kBkThreads) lcnt[k] = 0;
+  __syncthreads();
+  for (int i = tid; i < nq * NS; i += kBkThreads) {
+    const int u = i / NS, r = i - u * NS, l = r / p.NP, pt = r - l * p.NP;
+    const int64_t unit = ((int64_t)b * p.NQ + q0 + u) * p.NH + h;
+    for_corners<T>(p, unit, l, pt, [&](int pos, float) { atomicAdd(&lcnt[pos >> kBkShift], 1); });
+  }
+  __syncthreads();
+  {  // exclusive scan of the NBS counts: thread tid owns [tid*E, tid*E + E)
+    const int E = (p.NBS + kBkThreads - 1) / kBkThreads;
+    const int e0 = min(tid * E, p.NBS), e1 = min(e0 + E, p.NBS);
+    int local = 0;
+    for (int e = e0; e < e1; ++e) local += lcnt[e];
+    int incl = local;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const int v = __shfl_up(incl, d, kWave);
+      if (lane >= d) incl += v;
+    }
+    if (lane == kWave - 1) wsum[wave] = incl;
+    __syncthreads();
+    int run = incl - local;
+    for (int w2 = 0; w2 < wave; ++w2) run += wsum[w2];
+    for (int e = e0; e < e1; ++e) {
+      const int c = lcnt[e];
+      lst[e] = run;
+      gbase[e] = c > 0 ? atomicAdd(&p.cursor[slice * p.NBS + e], c) : 0;
+      lcnt[e] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < nq * NS; i += kBkThreads) {
+    const int u = i / NS, r = i - u * NS, l = r / p.NP, pt = r - l * p.NP;
+    const int64_t unit = ((int64_t)b * p.NQ + q0 + u) * p.NH + h;
+    const uint32_t qbits = (uint32_t)(q0 + u) << kBkShift;
+    for_corners<T>(p, unit, l, pt, [&](int pos, float w) {
+      const int k = pos >> kBkShift;
+      const int slot = atomicAdd(&lcnt[k], 1);
+      sw[slot] = w;
+      sq[slot] = qbits | (uint32_t)(pos & (kBkPos - 1));
+      sb[slot] = (unsigned short)k;
+    });
+  }
+  __syncthreads();
+  const int total = lcnt[p.NBS - 1];  // the last bucket's cursor ends at the staged total
+  for (int i = tid; i < total; i += kBkThreads) {
+    const int k = sb[i];
+    const int dst = gbase[k] + (i - lst[k]);
+    p.pw[dst] = sw[i];
+    p.pq[dst] = sq[i];
+  }
+}
+
+// Persistent: block j of XCD x takes chunks j, j + blocks_per_xcd, ... of list x. A bucket
+// of one chunk adds its sums to grad_value with plain stores (no other workgroup writes
+// those rows); the chunks of a larger bucket add theirs with atomics.
+template <typename T>
+__global__ void __launch_bounds__(kAccThreads) msda_bkt_acc_kernel(const BktParams p) {
+  constexpr int D = 32;
+  constexpr int NHW = kAccThreads / 32;     // half-waves
+  constexpr int BT = 16;                    // corners per batch of a half-wave
+  __shared__ float accs[kBkPos * D];        // the chunk's sums per position
+  __shared__ int cnt[kBkPos + 1];           // counts, then each position's first corner
+  __shared__ int cur[kBkPos];
+  __shared__ float lw[kAccChunk];
+  __shared__ uint32_t lq[kAccChunk];
+  __shared__ int pcut[NHW + 1];             // first position of each half-wave
+  __shared__ int wsum[kAccThreads / kWave];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int ch = tid & 31, hw = tid >> 5;
+  const int xcd = blockIdx.x & 7;
+  const int n_items = p.nitems[xcd];
+  const T *gout = static_cast<const T *>(p.grad_out);
+  for (int m = blockIdx.x >> 3; m < n_items; m += p.blocks_per_xcd) {
+    const int2 it = p.items[xcd * p.item_cap + m];
+    const int k = it.x, first = it.y;
+    const int bstart = p.offset[k], bend = p.offset[k + 1];
+    const int n = min(kAccChunk, bend - first);
+    const bool whole = bend - bstart <= kAccChunk;  // the bucket is this one chunk
+    const int slice = k / p.NBS, kb = k - slice * p.NBS;
+    const int b = slice / p.NH, h = slice - b * p.NH;
+    // grad_output rows of (b, ., h) through a buffer over the batch's rows (32-bit offsets)
+    const T *gob = gout + b * p.go_sb + h * p.go_sh;
+    const __amdgpu_buffer_rsrc_t gr = make_rsrc(gob, p.go_rows_bytes);
+    const uint32_t go_q_bytes = (uint32_t)(p.go_sq * (int64_t)sizeof(T));
+    const uint32_t ch_bytes = (uint32_t)(ch * p.go_sc * (int64_t)sizeof(T));
+    __syncthreads();  // the previous chunk's readers are done
+    for (int i = tid; i < kBkPos * D; i += kAccThreads) accs[i] = 0.f;
+    for (int i = tid; i <= kBkPos; i += kAccThreads) cnt[i] = 0;
+    __syncthreads();
+    float rw[kAccPerThread];
+    uint32_t rq[kAccPerThread];
+#pragma unroll
+    for (int j = 0; j < kAccPerThread; ++j) {
+      const int i = min(tid + j * kAccThreads, n - 1);
+      rw[j] = p.pw[first + i];
+      rq[j] = p.pq[first + i];
+    }
+#pragma unroll
+    for (int j = 0; j < kAccPerThread; ++j)
+      if (tid + j * kAccThreads < n) atomicAdd(&cnt[rq[j] & (kBkPos - 1)], 1);
+    __syncthreads();
+    {  // exclusive scan of the kBkPos counts, one per thread of waves 0-3
+      int v = 0, incl = 0;
+      if (tid < kBkPos) {
+        v = cnt[tid];
+        incl = v;
+#pragma unroll
+        for (int d = 1; d < kWave; d <<= 1) {
+          const int t = __shfl_up(incl, d, kWave);
+          if (lane >= d) incl += t;
+        }
+        if (lane == kWave - 1) wsum[wave] = incl;
+      }
+      __syncthreads();
+      if (tid < kBkPos) {
+        for (int w2 = 0; w2 < wave; ++w2) incl += wsum[w2];
+        cur[tid] = incl - v;
+      }
+    }
+    __syncthreads();
+    if (tid < kBkPos) cnt[tid] = cur[tid];
+    if (tid == 0) cnt[kBkPos] = n;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kAccPerThread; ++j)
+      if (tid + j * kAccThreads < n) {
+        const int slot = atomicAdd(&cur[rq[j] & (kBkPos - 1)], 1);
+        lw[slot] = rw[j];
+        lq[slot] = rq[j] >> kBkShift;
+      }
+    // half-wave cut points: pcut[w] = first position whose corners start at or after
+    // n * w / NHW (whole positions per half-wave)
+    if (tid <= NHW) {
+      const int target = n * tid / NHW;
+      int lo = 0, hi = kBkPos;  // smallest pos with cnt[pos] >= target (cnt[kBkPos] = n)
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (cnt[mid] >= target) hi = mid; else lo = mid + 1;
+      }
+      pcut[tid] = tid == NHW ? kBkPos : lo;
+    }
+    __syncthreads();
+    const int p0 = pcut[hw], p1 = pcut[hw + 1];
+    if (p0 < p1) {
+      // corners [k0, k1) of the half-wave's positions, BT at a time, the next batch's
+      // weights, queries and grad_output rows loaded while this one is summed
+      const int k0 = cnt[p0], k1 = cnt[p1];
+      int pos = p0, next = cnt[p0 + 1];
+      float acc = 0.f;
+      float wa[BT], va[BT], wb[BT], vb[BT];
+      auto fetch = [&](int kk0, float (&w)[BT], float (&v)[BT]) __attribute__((always_inline)) {
+        uint32_t qv[BT];
+#pragma unroll
+        for (int u = 0; u < BT; ++u) {
+          const int kk = min(kk0 + u, k1 - 1);
+          w[u] = lw[kk];
+          qv[u] = lq[kk];
+        }
+#pragma unroll
+        for (int u = 0; u < BT; ++u) v[u] = (float)buffer_load_one<T>(gr, qv[u] * go_q_bytes + ch_bytes);
+      };
+      auto consume = [&](int kk0, const float (&w)[BT], const float (&v)[BT]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < BT; ++u) {
+          const int kk = kk0 + u;
+          if (kk < k1) {
+            if (kk >= next) {  // corner kk starts a later position of this half-wave
+              accs[pos * D + ch] += acc;
+              acc = 0.f;
+              do {
+                ++pos;
+                next = cnt[pos + 1];
+              } while (next <= kk);
+            }
+            acc += w[u] * v[u];
+          }
+        }
+      };
+      fetch(k0, wa, va);
+      int kk0 = k0;
+      for (; kk0 + BT < k1; kk0 += 2 * BT) {
+        fetch(kk0 + BT, wb, vb);
+        consume(kk0, wa, va);
+        if (kk0 + 2 * BT < k1) fetch(kk0 + 2 * BT, wa, va);
+        consume(kk0 + BT, wb, vb);
+      }
+      if (kk0 < k1) consume(kk0, wa, va);
+      accs[pos * D + ch] += acc;
+    }
+    __syncthreads();
+    // the chunk's rows (positions past S do not exist; positions without corners skipped)
+    float *gvb = p.gv + ((int64_t)b * p.S + (int64_t)kb * kBkPos) * (p.NH * D) + h * D;
+    const int npos = min(kBkPos, p.S - kb * kBkPos);
+    for (int i = tid; i < npos * D; i += kAccThreads) {
+      const int pp = i / D, c = i - pp * D;
+      if (cnt[pp + 1] > cnt[pp]) {
+        float *dst = gvb + (int64_t)pp * (p.NH * D) + c;
+        if (whole) *dst += accs[i];
+        else unsafeAtomicAdd(dst, accs[i]);
+      }
+    }
+  }
+}
+
+// grad_sampling_loc / grad_attn_weight for D = 32 without grad_value: one wave per
+// (b, q, head) unit, 8 lanes per sample (lane owns 4 channels), 8 samples per pass and 4
+// passes per group, so the 16 corner loads of a lane are in flight together. Per sample the
+// lanes form S_k = sum_c top_c * v_k,c over their channels for the four corners; the three
+// gradients are linear in S_k and are reduced over the 8 lanes.
+template <typename T>
+__global__ void __launch_bounds__(kBlock) msda_coord_kernel(
+    const T *__restrict__ value, const T *__restrict__ loc, const T *__restrict__ attn,
+    const T *__restrict__ grad_out, T *__restrict__ grad_loc, T *__restrict__ grad_attn,
+    BwdParams p) {
+  constexpr int D = 32, VEC = 4, PG = 4;
+  constexpr uint32_t kPast = 0x80000000u;
+  const int64_t wg = ((int64_t)blockIdx.x * kBlock + threadIdx.x) >> 6;
+  if (wg >= p.units) return;  // uniform over the wave
+  const int unit = (int)wg;
+  const int lane = threadIdx.x & (kWave - 1), g = lane >> 3, cl = lane & 7;
+  const int bq = unit / p.NH, h = unit - bq * p.NH;
+  const int b = bq / p.NQ, q = bq - b * p.NQ;
+  const int NS = p.NL * p.NP;
+  const int row = p.NH * D;
+  float top[VEC];
+#pragma unroll
+  for (int j = 0; j < VEC; ++j)
+    top[j] = (float)grad_out[b * p.go_sb + (int64_t)q * p.go_sq + h * p.go_sh + (cl * VEC + j) * p.go_sc];
+  const T *vb = value + (int64_t)b * p.S * row + h * D;
+  const __amdgpu_buffer_rsrc_t rv =
+      make_rsrc(vb, (uint32_t)(((int64_t)p.S * row - h * D) * sizeof(T)));
+  const uint32_t lane_b = (uint32_t)(cl * VEC * sizeof(T));
+  const T *lp = loc + (int64_t)unit * NS * 2;
+  const T *ap = attn + (int64_t)unit * NS;
+  for (int s0 = 0; s0 < NS; s0 += 8 * PG) {
+    float lhv[PG], lwv[PG], av[PG], Hf[PG], Wf[PG];
+    bool inw[PG];
+    Vec<T, VEC> cv[PG][4];
+#pragma unroll
+    for (int j = 0; j < PG; ++j) {
+      const int s = s0 + j * 8 + g;
+      const int sc = s < NS ? s : NS - 1;
+      const int l = sc / p.NP;
+      const int Hl = (int)p.shapes[2 * l], Wl = (int)p.shapes[2 * l + 1];
+      const int base = (int)p.lsi[l];
+      const float lx = (float)lp[2 * sc], ly = (float)lp[2 * sc + 1];
+      av[j] = (float)ap[sc];
+      Hf[j] = (float)Hl;
+      Wf[j] = (float)Wl;
+      float him, wim;
+      sample_coords<float>(lx, ly, Hl, Wl, him, wim);
+      inw[j] = s < NS && him > -1.f && wim > -1.f && him < (float)Hl && wim < (float)Wl;
+      const float fh = floorf(him), fw = floorf(wim);
+      const int hl = (int)fh, wl = (int)fw;
+      lhv[j] = him - fh;
+      lwv[j] = wim - fw;
+      const bool c1 = inw[j] && hl >= 0 && wl >= 0;
+      const bool c2 = inw[j] && hl >= 0 && wl + 1 <= Wl - 1;
+      const bool c3 = inw[j] && hl + 1 <= Hl - 1 && wl >= 0;
+      const bool c4 = inw[j] && hl + 1 <= Hl - 1 && wl + 1 <= Wl - 1;
+      const uint32_t e1 = (uint32_t)((base + hl * Wl + wl) * row) * (uint32_t)sizeof(T) + lane_b;
+      const uint32_t dx = (uint32_t)(row * sizeof(T)), dy = (uint32_t)(Wl * row * sizeof(T));
+      cv[j][0] = buffer_load_vec<T, VEC>(rv, c1 ? e1 : kPast);
+      cv[j][1] = buffer_load_vec<T, VEC>(rv, c2 ? e1 + dx : kPast);
+      cv[j][2] = buffer_load_vec<T, VEC>(rv, c3 ? e1 + dy : kPast);
+      cv[j][3] = buffer_load_vec<T, VEC>(rv, c4 ? e1 + dy + dx : kPast);
+    }
+#pragma unroll
+    for (int j = 0; j < PG; ++j) {
+      const int s = s0 + j * 8 + g;
+      float s1 = 0.f, s2 = 0.f, s3 = 0.f, s4 = 0.f;
+#pragma unroll
+      for (int c = 0; c < VEC; ++c) {
+        s1 += top[c] * (float)cv[j][0].v[c];
+        s2 += top[c] * (float)cv[j][1].v[c];
+        s3 += top[c] * (float)cv[j][2].v[c];
+        s4 += top[c] * (float)cv[j][3].v[c];
+      }
+      const float lh = lhv[j], lw = lwv[j], hh = 1.f - lh, hwt = 1.f - lw, a = av[j];
+      float gh = inw[j] ? a * (hwt * (s3 - s1) + lw * (s4 - s2)) * Hf[j] : 0.f;
+      float gw = inw[j] ? a * (hh * (s2 - s1) + lh * (s4 - s3)) * Wf[j] : 0.f;
+      float ga = inw[j] ? hh * hwt * s1 + hh * lw * s2 + lh * hwt * s3 + lh * lw * s4 : 0.f;
+#pragma unroll
+      for (int m = 1; m < 8; m <<= 1) {
+        gh += __shfl_xor(gh, m, kWave);
+        gw += __shfl_xor(gw, m, kWave);
+        ga += __shfl_xor(ga, m, kWave);
+      }
+      if (s < NS && cl == 0) {
+        T *glp = grad_loc + ((int64_t)unit * NS + s) * 2;
+        glp[0] = (T)gw;
+        glp[1] = (T)gh;
+        grad_attn[(int64_t)unit * NS + s] = (T)ga;
+      }
+    }
+  }
+}
+
 __global__ void __launch_bounds__(kBlock) fill_zero_f32(float *__restrict__ p, int64_t n) {
   const int64_t stride = (int64_t)gridDim.x * kBlock;
   for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) p[i] = 0.f;
@@ -863,6 +1348,126 @@ __global__ void __launch_bounds__(kBlock) narrow_f32(const float *__restrict__ s
 unsigned stream_grid(int64_t n) {
   const int64_t g = (n + kBlock - 1) / kBlock;
   return (unsigned)(g < 8192 ? (g > 0 ? g : 1) : 8192);
+}
+
+// Workspace of the sorted grad_value path (bytes, after the 16-bit accumulator).
+struct BktLayout {
+  int NBS = 0, nbk = 0, item_cap = 0;
+  int64_t cap = 0;  // corner slots
+  int64_t off_count = 0, off_cursor = 0, off_offset = 0, off_nitems = 0, off_items = 0,
+          off_pw = 0, off_pq = 0, bytes = 0;
+};
+
+BktLayout bkt_layout(int64_t B, int64_t S, int64_t NH, int64_t NL, int64_t NQ, int64_t NP) {
+  BktLayout L;
+  auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
+  const int64_t nbs = (S + kBkPos - 1) / kBkPos;
+  const int64_t cap = B * NQ * NH * NL * NP * 4;
+  const int64_t nbk = B * NH * nbs;
+  const int64_t item_cap = (cap + kAccChunk - 1) / kAccChunk + nbk;  // chunks of one list
+  if (nbs <= 0 || nbs > kBkMaxPerSlice || cap <= 0 || cap >= ((int64_t)1 << 31) ||
+      nbk >= ((int64_t)1 << 26) || item_cap >= ((int64_t)1 << 26) || NQ >= ((int64_t)1 << 22) ||
+      NL * NP * 4 > kPlaceCap)
+    return L;  // bytes == 0: not applicable
+  L.NBS = (int)nbs; L.nbk = (int)nbk; L.item_cap = (int)item_cap; L.cap = cap;
+  int64_t o = 0;
+  L.off_count = o;  o += up(nbk * 4);
+  L.off_cursor = o; o += up(nbk * 4);
+  L.off_offset = o; o += up((nbk + 1) * 4);
+  L.off_nitems = o; o += up(8 * 4);
+  L.off_items = o;  o += up(8 * item_cap * 8);
+  L.off_pw = o;     o += up(cap * 4);
+  L.off_pq = o;     o += up(cap * 4);
+  L.bytes = o;
+  return L;
+}
+
+int64_t half_acc_bytes(int dtype, int64_t value_elems) {
+  return (dtype == 1 || dtype == 2) ? (value_elems * (int64_t)sizeof(float) + 255) / 256 * 256 : 0;
+}
+
+// The sorted path: D = 32, fp32 accumulation (f32 / f16 / bf16 inputs), one batch of value
+// under 2 GiB (32-bit buffer offsets), and a workspace that holds its buffers.
+template <typename T>
+bool sorted_path(const MsdaBwdArgs &a, int dtype, BktLayout &L) {
+  if (a.f.channels != 32 || a.f.batch <= 0 || a.f.num_heads <= 0 || a.f.num_query <= 0 ||
+      a.f.num_levels <= 0 || a.f.num_point <= 0 || device_cus() < 8)
+    return false;
+  if ((int64_t)a.f.spatial_size * a.f.num_heads * 32 * (int64_t)sizeof(T) >= ((int64_t)1 << 31))
+    return false;
+  if ((int64_t)a.f.batch * a.f.num_query * a.f.num_heads >= ((int64_t)1 << 31) / 64) return false;
+  // grad_output rows through 32-bit buffer offsets
+  if (a.go_stride[1] < 0 || a.go_stride[3] < 0 ||
+      ((int64_t)(a.f.num_query - 1) * a.go_stride[1] + 31 * a.go_stride[3] + 1) * (int64_t)sizeof(T) >=
+          ((int64_t)1 << 31))
+    return false;
+  L = bkt_layout(a.f.batch, a.f.spatial_size, a.f.num_heads, a.f.num_levels, a.f.num_query,
+                 a.f.num_point);
+  if (L.bytes == 0) return false;
+  const int64_t value_elems = (int64_t)a.f.batch * a.f.spatial_size * a.f.num_heads * 32;
+  return a.workspace != nullptr &&
+         a.workspace_bytes >= half_acc_bytes(dtype, value_elems) + L.bytes;
+}
+
+// grad_value (fp32, added to gv) by the four bucket kernels, then the coordinate kernel.
+template <typename T>
+hipError_t launch_sorted(const MsdaBwdArgs &a, const BktLayout &L, char *ws, float *gv,
+                         hipStream_t stream) {
+  BktParams p;
+  p.loc = a.f.sampling_loc;
+  p.attn = a.f.attn_weight;
+  p.grad_out = a.grad_output;
+  p.shapes = a.f.spatial_shapes;
+  p.lsi = a.f.level_start_index;
+  p.gv = gv;
+  p.count = reinterpret_cast<int *>(ws + L.off_count);
+  p.cursor = reinterpret_cast<int *>(ws + L.off_cursor);
+  p.offset = reinterpret_cast<int *>(ws + L.off_offset);
+  p.nitems = reinterpret_cast<int *>(ws + L.off_nitems);
+  p.items = reinterpret_cast<int2 *>(ws + L.off_items);
+  p.pw = reinterpret_cast<float *>(ws + L.off_pw);
+  p.pq = reinterpret_cast<uint32_t *>(ws + L.off_pq);
+  p.go_sb = a.go_stride[0]; p.go_sq = a.go_stride[1];
+  p.go_sh = a.go_stride[2]; p.go_sc = a.go_stride[3];
+  p.B = a.f.batch; p.NH = a.f.num_heads; p.NQ = a.f.num_query; p.NL = a.f.num_levels;
+  p.NP = a.f.num_point; p.S = a.f.spatial_size;
+  p.go_rows_bytes = (uint32_t)(((int64_t)(a.f.num_query - 1) * a.go_stride[1] + 31 * a.go_stride[3] + 1) *
+                               (int64_t)sizeof(T));
+  p.NBS = L.NBS; p.nbk = L.nbk; p.item_cap = L.item_cap;
+  p.by_bucket = (int64_t)a.f.batch * a.f.num_heads < 8 ? 1 : 0;
+  const int blocks = (device_cus() / 8) * 8;  // one 8-wave workgroup per CU (LDS)
+  p.blocks_per_xcd = blocks / 8;
+  p.qpb = kPlaceCap / (4 * a.f.num_levels * a.f.num_point);
+  const int qchunks = (a.f.num_query + p.qpb - 1) / p.qpb;
+  const unsigned cblocks = (unsigned)((int64_t)a.f.batch * a.f.num_heads * qchunks);
+  hipLaunchKernelGGL(fill_zero_f32, dim3(stream_grid(L.nbk)), dim3(kBlock), 0, stream,
+                     reinterpret_cast<float *>(p.count), (int64_t)L.nbk);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((msda_bkt_count_kernel<T>), dim3(cblocks), dim3(kBkThreads), 0, stream, p);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL(msda_bkt_scan_kernel, dim3(1), dim3(1024), 0, stream, p);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL((msda_bkt_place_kernel<T>), dim3(cblocks), dim3(kBkThreads), 0, stream, p);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  hipLaunchKernelGGL((msda_bkt_acc_kernel<T>), dim3(blocks), dim3(kAccThreads), 0, stream, p);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  BwdParams q;
+  q.shapes = a.f.spatial_shapes;
+  q.lsi = a.f.level_start_index;
+  q.go_sb = a.go_stride[0]; q.go_sq = a.go_stride[1];
+  q.go_sh = a.go_stride[2]; q.go_sc = a.go_stride[3];
+  q.units = (int64_t)a.f.batch * a.f.num_query * a.f.num_heads;
+  q.S = a.f.spatial_size; q.NH = a.f.num_heads; q.D = 32;
+  q.NL = a.f.num_levels; q.NQ = a.f.num_query; q.NP = a.f.num_point;
+  q.coarse = 0; q.log2_g = 0;
+  hipLaunchKernelGGL((msda_coord_kernel<T>), dim3((unsigned)((q.units * 64 + kBlock - 1) / kBlock)),
+                     dim3(kBlock), 0, stream, static_cast<const T *>(a.f.value),
+                     static_cast<const T *>(a.f.sampling_loc),
+                     static_cast<const T *>(a.f.attn_weight),
+                     static_cast<const T *>(a.grad_output), static_cast<T *>(a.grad_loc),
+                     static_cast<T *>(a.grad_attn), q);
+  return hipGetLastError();
 }
 
 // One-level grid with one query per cell, D = 32, at most kOwnMaxP points: grad_value by
@@ -1002,6 +1607,9 @@ hipError_t launch_grid_coord(const MsdaBwdArgs &a, float *gv, hipStream_t stream
 template <typename T>
 hipError_t launch_f32(const MsdaBwdArgs &a, bool generic, hipStream_t stream) {
   float *gv = static_cast<float *>(a.grad_value);
+  BktLayout L;
+  if (!generic && !owner_path<T>(a) && sorted_path<T>(a, 0, L))
+    return launch_sorted<T>(a, L, static_cast<char *>(a.workspace), gv, stream);
   if (generic || !owner_path<T>(a)) return launch_t<T, float>(a, gv, generic, stream);
   hipError_t e = launch_owner<T>(a, gv, true, stream);
   if (e != hipSuccess) return e;
@@ -1013,7 +1621,15 @@ hipError_t launch_half(const MsdaBwdArgs &a, bool generic, hipStream_t stream) {
   const int64_t n = (int64_t)a.f.batch * a.f.spatial_size * a.f.num_heads * a.f.channels;
   float *acc = static_cast<float *>(a.workspace);
   hipError_t e;
-  if (!generic && owner_path<T>(a)) {  // the owner pass writes every element of the workspace
+  BktLayout L;
+  const int dtype = std::is_same<T, f16>::value ? 1 : 2;
+  if (!generic && !owner_path<T>(a) && sorted_path<T>(a, dtype, L)) {
+    hipLaunchKernelGGL(fill_zero_f32, dim3(stream_grid(n)), dim3(kBlock), 0, stream, acc, n);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    e = launch_sorted<T>(a, L, static_cast<char *>(a.workspace) + half_acc_bytes(dtype, n), acc,
+                         stream);
+  } else if (!generic && owner_path<T>(a)) {  // the owner pass writes every element of the workspace
     e = launch_owner<T>(a, acc, false, stream);
     if (e != hipSuccess) return e;
     e = launch_grid_coord<T>(a, acc, stream);
@@ -1031,8 +1647,18 @@ hipError_t launch_half(const MsdaBwdArgs &a, bool generic, hipStream_t stream) {
 
 }  // namespace
 
-int64_t msda_backward_workspace_bytes(int dtype, int64_t value_elems) {
+int64_t msda_backward_workspace_min(int dtype, int64_t value_elems) {
   return (dtype == 1 || dtype == 2) ? value_elems * (int64_t)sizeof(float) : 0;
+}
+
+int64_t msda_backward_workspace_bytes(int dtype, int64_t batch, int64_t spatial_size,
+                                      int64_t num_heads, int64_t channels, int64_t num_levels,
+                                      int64_t num_query, int64_t num_point) {
+  const int64_t value_elems = batch * spatial_size * num_heads * channels;
+  if (dtype == 3 || channels != 32) return msda_backward_workspace_min(dtype, value_elems);
+  const BktLayout L = bkt_layout(batch, spatial_size, num_heads, num_levels, num_query, num_point);
+  if (L.bytes == 0) return msda_backward_workspace_min(dtype, value_elems);
+  return half_acc_bytes(dtype, value_elems) + L.bytes;
 }
 
 hipError_t launch_msda_backward(int dtype, const MsdaBwdArgs &a, bool force_generic,

@@ -281,12 +281,17 @@ int bevk_msda_forward(
     int num_query, int num_point, int im2col_step, int force_generic, void *output,
     void *stream);
 
-/* Bytes of workspace bevk_msda_backward needs: an fp32 accumulator of
- * batch*spatial_size*num_heads*channels elements for F16/BF16, 0 for F32/F64, -1 for an
- * unknown dtype or a negative size. The reference allocates this buffer inside its
- * fp16 backward (binding_musa.mu:456-463); here the caller owns it. */
+/* Bytes of workspace for bevk_msda_backward, -1 for an unknown dtype or a negative size.
+ * F16/BF16 need at least an fp32 accumulator of batch*spatial_size*num_heads*channels
+ * elements (the reference allocates it inside its fp16 backward, binding_musa.mu:456-463;
+ * here the caller owns it); F32/F64 need none. With channels == 32 the value returned
+ * also holds the buffers of the sorted grad_value path (every valid corner of every
+ * sample, 8 bytes each, bucketed by position), which bevk_msda_backward takes whenever
+ * the workspace it is given is at least this large; a smaller workspace (at least the
+ * accumulator) runs the atomic kernels instead. */
 int64_t bevk_msda_backward_workspace_bytes(int dtype, int batch, int spatial_size,
-                                           int num_heads, int channels);
+                                           int num_heads, int channels, int num_levels,
+                                           int num_query, int num_point);
 
 /* MSDA backward.
  *   value, spatial_shapes, level_start_index, sampling_loc, attn_weight: as the forward.
@@ -303,8 +308,9 @@ int64_t bevk_msda_backward_workspace_bytes(int dtype, int batch, int spatial_siz
  *   workspace          bevk_msda_backward_workspace_bytes(...) bytes, device memory.
  * im2col_step keeps the reference's contract. force_generic_col2im != 0 runs the
  * per-(batch, query, head) kernel alone, adding every level's grad_value with atomics
- * (the reference's generic col2im, binding_musa.mu:459); otherwise the D = 32 kernel,
- * the coarse-level sort and the grid-query owner pass are used where they apply.
+ * (the reference's generic col2im, binding_musa.mu:459); otherwise the grid-query owner
+ * pass, the sorted grad_value path (D = 32, full workspace) or the D = 32 kernel with the
+ * coarse-level sort are used where they apply.
  * spatial_shapes / level_start_index must describe value (lsi[l] + H_l * W_l <=
  * spatial_size), as in the reference; they are read on the device only.
  * Replaces _msda_opt2_musa.backward (binding_musa.mu:414-543, :550-556).

@@ -154,14 +154,34 @@ def _msda_bwd(dtype=0, step=64, b=2, nq=4, ws=0):
                                           0, NULL, NULL, NULL, NULL, ws, NULL)
 
 
+def _sorted_bytes(b, s, h, nl, nq, np_):
+    """Buffers of the sorted grad_value path: bucket counts, cursors and offsets (buckets of
+    256 positions per (batch, head) slice), 8 per-XCD lists of chunks of at most 12288
+    corners, and 8 bytes for every possible corner (4 per sample); each region 256-byte
+    aligned."""
+    up = lambda x: -(-x // 256) * 256  # noqa: E731
+    nbs = -(-s // 256)
+    cap = b * nq * h * nl * np_ * 4
+    nbk = b * h * nbs
+    items = -(-cap // 12288) + nbk
+    return 2 * up(nbk * 4) + up((nbk + 1) * 4) + up(32) + up(8 * items * 8) + 2 * up(cap * 4)
+
+
 def test_msda_backward_workspace_bytes():
     f = _bevk.lib().bevk_msda_backward_workspace_bytes
-    assert f(0, 2, 10, 8, 32) == 0
-    assert f(3, 2, 10, 8, 32) == 0
-    assert f(1, 2, 10, 8, 32) == 2 * 10 * 8 * 32 * 4
-    assert f(2, 6, 30825, 8, 32) == 6 * 30825 * 8 * 32 * 4
-    assert f(4, 2, 10, 8, 32) == -1
-    assert f(1, -1, 10, 8, 32) == -1
+    acc = lambda n: -(-n * 4 // 256) * 256  # noqa: E731
+    # D != 32 and float64: only the 16-bit accumulator
+    assert f(0, 2, 10, 8, 16, 1, 4, 4) == 0
+    assert f(3, 2, 10, 8, 32, 1, 4, 4) == 0
+    assert f(1, 2, 10, 8, 16, 1, 4, 4) == 2 * 10 * 8 * 16 * 4
+    # D == 32: the sorted path's buffers (after the accumulator for 16-bit types)
+    assert f(0, 2, 10, 8, 32, 1, 4, 4) == _sorted_bytes(2, 10, 8, 1, 4, 4)
+    assert f(1, 2, 10, 8, 32, 1, 4, 4) == acc(2 * 10 * 8 * 32) + _sorted_bytes(2, 10, 8, 1, 4, 4)
+    assert f(2, 6, 30825, 8, 32, 4, 10000, 8) == (acc(6 * 30825 * 8 * 32)
+                                                 + _sorted_bytes(6, 30825, 8, 4, 10000, 8))
+    assert f(4, 2, 10, 8, 32, 1, 4, 4) == -1
+    assert f(1, -1, 10, 8, 32, 1, 4, 4) == -1
+    assert f(1, 2, 10, 8, 32, 1, -4, 4) == -1
 
 
 def test_msda_backward_validation():
