@@ -877,7 +877,7 @@ constexpr int kBkMaxPerSlice = 1024;       // buckets per slice (spatial_size <=
 constexpr int kBkThreads = 256;
 constexpr int kPlaceCap = 4096;            // corners a place block stages (2 blocks per CU)
 constexpr int kAccThreads = 512;
-constexpr int kAccChunk = 12288;           // corners per accumulate pass (LDS)
+constexpr int kAccChunk = 4096;            // corners per accumulate item (LDS; 2 blocks per CU)
 constexpr int kAccPerThread = kAccChunk / kAccThreads;
 constexpr int kAccBatch = 16;              // grad_output rows in flight per half-wave
 
@@ -947,71 +947,61 @@ __global__ void __launch_bounds__(kBkThreads) msda_bkt_count_kernel(const BktPar
     if (lcnt[k] > 0) atomicAdd(&p.count[slice * p.NBS + k], lcnt[k]);
 }
 
-// One block: exclusive scan of the bucket counts (offset, cursor), then the chunks of at
-// most kAccChunk corners of the buckets of XCD x in list x.
+// Block x (of 8): exclusive scan of the bucket counts (block 0 stores offset and cursor),
+// then the chunks of at most kAccChunk corners of the buckets of XCD x in list x.
 __global__ void __launch_bounds__(1024) msda_bkt_scan_kernel(const BktParams p) {
   __shared__ int wsum[16];
-  __shared__ int carry;
+  __shared__ int carry, carry2;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-  // block-wide exclusive scan of one value per thread (excl) and the block total
-  auto block_scan = [&](int v, int &excl, int &total) __attribute__((always_inline)) {
-    int incl = v;
+  const int x = blockIdx.x;
+  // block-wide exclusive scans of two values per thread (excl) and the block totals
+  __shared__ int wsum2[16];
+  auto block_scan2 = [&](int v, int v2, int &excl, int &total, int &excl2, int &total2)
+      __attribute__((always_inline)) {
+    int incl = v, incl2 = v2;
 #pragma unroll
     for (int d = 1; d < kWave; d <<= 1) {
-      const int t = __shfl_up(incl, d, kWave);
-      if (lane >= d) incl += t;
+      const int t = __shfl_up(incl, d, kWave), t2 = __shfl_up(incl2, d, kWave);
+      if (lane >= d) { incl += t; incl2 += t2; }
     }
-    if (lane == kWave - 1) wsum[wave] = incl;
+    if (lane == kWave - 1) { wsum[wave] = incl; wsum2[wave] = incl2; }
     __syncthreads();
-    int before = 0, tot = 0;
+    int before = 0, tot = 0, before2 = 0, tot2 = 0;
     for (int w = 0; w < 16; ++w) {
-      if (w < wave) before += wsum[w];
+      if (w < wave) { before += wsum[w]; before2 += wsum2[w]; }
       tot += wsum[w];
+      tot2 += wsum2[w];
     }
     excl = incl - v + before;
     total = tot;
+    excl2 = incl2 - v2 + before2;
+    total2 = tot2;
     __syncthreads();
   };
-  if (tid == 0) carry = 0;
+  if (tid == 0) { carry = 0; carry2 = 0; }
   __syncthreads();
   for (int k0 = 0; k0 < p.nbk; k0 += 1024) {
     const int k = k0 + tid;
     const int c = k < p.nbk ? p.count[k] : 0;
-    int excl, total;
-    block_scan(c, excl, total);
-    const int base = carry;
-    if (k < p.nbk) {
+    const bool mine = k < p.nbk && ((p.by_bucket ? k : k / p.NBS) & 7) == x;
+    const int nch = mine ? (c + kAccChunk - 1) / kAccChunk : 0;
+    int excl, total, excl2, total2;
+    block_scan2(c, nch, excl, total, excl2, total2);
+    const int base = carry, base2 = carry2;
+    if (x == 0 && k < p.nbk) {
       p.offset[k] = base + excl;
       p.cursor[k] = base + excl;
     }
+    for (int j = 0; j < nch; ++j)
+      if (base2 + excl2 + j < p.item_cap)
+        p.items[x * p.item_cap + base2 + excl2 + j] = make_int2(k, base + excl + j * kAccChunk);
     __syncthreads();
-    if (tid == 0) carry = base + total;
+    if (tid == 0) { carry = base + total; carry2 = base2 + total2; }
     __syncthreads();
   }
-  if (tid == 0) p.offset[p.nbk] = carry;
-  for (int x = 0; x < 8; ++x) {
-    if (tid == 0) carry = 0;
-    __syncthreads();
-    for (int k0 = 0; k0 < p.nbk; k0 += 1024) {
-      const int k = k0 + tid;
-      const bool mine = k < p.nbk && ((p.by_bucket ? k : k / p.NBS) & 7) == x;
-      const int c = mine ? p.count[k] : 0;
-      const int nch = (c + kAccChunk - 1) / kAccChunk;
-      int excl, total;
-      block_scan(nch, excl, total);
-      const int base = carry;
-      if (mine) {
-        const int first = p.offset[k];
-        for (int j = 0; j < nch; ++j)
-          if (base + excl + j < p.item_cap)
-            p.items[x * p.item_cap + base + excl + j] = make_int2(k, first + j * kAccChunk);
-      }
-      __syncthreads();
-      if (tid == 0) carry = base + total;
-      __syncthreads();
-    }
-    if (tid == 0) p.nitems[x] = min(carry, p.item_cap);
-    __syncthreads();
+  if (tid == 0) {
+    if (x == 0) p.offset[p.nbk] = carry;
+    p.nitems[x] = min(carry2, p.item_cap);
   }
 }
 
@@ -1090,10 +1080,10 @@ __global__ void __launch_bounds__(kBkThreads) msda_bkt_place_kernel(const BktPar
 // of one chunk adds its sums to grad_value with plain stores (no other workgroup writes
 // those rows); the chunks of a larger bucket add theirs with atomics.
 template <typename T>
-__global__ void __launch_bounds__(kAccThreads) msda_bkt_acc_kernel(const BktParams p) {
+__global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktParams p) {
   constexpr int D = 32;
   constexpr int NHW = kAccThreads / 32;     // half-waves
-  constexpr int BT = 16;                    // corners per batch of a half-wave
+  constexpr int BT = 8;                     // corners per batch of a half-wave
   __shared__ float accs[kBkPos * D];        // the chunk's sums per position
   __shared__ int cnt[kBkPos + 1];           // counts, then each position's first corner
   __shared__ int cur[kBkPos];
@@ -1239,8 +1229,8 @@ __global__ void __launch_bounds__(kAccThreads) msda_bkt_acc_kernel(const BktPara
 }
 
 // grad_sampling_loc / grad_attn_weight for D = 32 without grad_value: one wave per
-// (b, q, head) unit, 8 lanes per sample (lane owns 4 channels), 8 samples per pass and 4
-// passes per group, so the 16 corner loads of a lane are in flight together. Per sample the
+// (b, q, head) unit, 8 lanes per sample (lane owns 4 channels), 8 samples per pass and 2
+// passes per group, so the 8 corner loads of a lane are in flight together. Per sample the
 // lanes form S_k = sum_c top_c * v_k,c over their channels for the four corners; the three
 // gradients are linear in S_k and are reduced over the 8 lanes.
 template <typename T>
@@ -1248,7 +1238,7 @@ __global__ void __launch_bounds__(kBlock) msda_coord_kernel(
     const T *__restrict__ value, const T *__restrict__ loc, const T *__restrict__ attn,
     const T *__restrict__ grad_out, T *__restrict__ grad_loc, T *__restrict__ grad_attn,
     BwdParams p) {
-  constexpr int D = 32, VEC = 4, PG = 4;
+  constexpr int D = 32, VEC = 4, PG = 2;
   constexpr uint32_t kPast = 0x80000000u;
   const int64_t wg = ((int64_t)blockIdx.x * kBlock + threadIdx.x) >> 6;
   if (wg >= p.units) return;  // uniform over the wave
@@ -1435,7 +1425,7 @@ hipError_t launch_sorted(const MsdaBwdArgs &a, const BktLayout &L, char *ws, flo
                                (int64_t)sizeof(T));
   p.NBS = L.NBS; p.nbk = L.nbk; p.item_cap = L.item_cap;
   p.by_bucket = (int64_t)a.f.batch * a.f.num_heads < 8 ? 1 : 0;
-  const int blocks = (device_cus() / 8) * 8;  // one 8-wave workgroup per CU (LDS)
+  const int blocks = (device_cus() / 8) * 8 * 2;  // two 8-wave workgroups per CU (LDS)
   p.blocks_per_xcd = blocks / 8;
   p.qpb = kPlaceCap / (4 * a.f.num_levels * a.f.num_point);
   const int qchunks = (a.f.num_query + p.qpb - 1) / p.qpb;
@@ -1446,7 +1436,7 @@ hipError_t launch_sorted(const MsdaBwdArgs &a, const BktLayout &L, char *ws, flo
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL((msda_bkt_count_kernel<T>), dim3(cblocks), dim3(kBkThreads), 0, stream, p);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  hipLaunchKernelGGL(msda_bkt_scan_kernel, dim3(1), dim3(1024), 0, stream, p);
+  hipLaunchKernelGGL(msda_bkt_scan_kernel, dim3(8), dim3(1024), 0, stream, p);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   hipLaunchKernelGGL((msda_bkt_place_kernel<T>), dim3(cblocks), dim3(kBkThreads), 0, stream, p);
   if ((e = hipGetLastError()) != hipSuccess) return e;
