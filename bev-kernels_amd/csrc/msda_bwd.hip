@@ -862,11 +862,12 @@ __global__ void __launch_bounds__(kBlock) msda_col2im_d32_kernel(
 //   3. msda_bkt_place_kernel: the corners again, staged in LDS in bucket order, each
 //      bucket's range reserved once per block, then written as contiguous runs of
 //      (weight, query << kBkShift | position in bucket);
-//   4. msda_bkt_acc_kernel: per bucket, chunks of at most kAccChunk corners sorted by
-//      position in LDS; each half-wave takes whole positions (about 1/16 of the chunk's
-//      corners), sums weight x grad_output row in registers and adds the sum to the
-//      bucket's LDS accumulator, which is added to grad_value once at the end (no atomics:
-//      no other workgroup writes these rows).
+//   4. msda_bkt_acc_kernel: per chunk of at most kAccChunk corners of one bucket, a
+//      counting sort by position in LDS; each 8-lane group takes whole positions (about
+//      1/64 of the chunk's corners), sums weight x grad_output row in registers (4
+//      channels per lane) and adds the sums to an LDS accumulator, which is added to
+//      grad_value at the end: with plain stores when the bucket is one chunk (no other
+//      workgroup writes these rows), else with atomics.
 // grad_sampling_loc / grad_attn_weight come from msda_coord_kernel (no atomics).
 // Corner set and weights are those of the reference (ms_deform_attn_kernels.cuh:427-490):
 // the same in-window test and per-corner bounds, weight = bilinear weight x attention.
@@ -1081,18 +1082,18 @@ __global__ void __launch_bounds__(kBkThreads) msda_bkt_place_kernel(const BktPar
 // those rows); the chunks of a larger bucket add theirs with atomics.
 template <typename T>
 __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktParams p) {
-  constexpr int D = 32;
-  constexpr int NHW = kAccThreads / 32;     // half-waves
-  constexpr int BT = 8;                     // corners per batch of a half-wave
+  constexpr int D = 32, VEC = 4;
+  constexpr int NGR = kAccThreads / 8;      // 8-lane groups (lane: 4 channels of a row)
+  constexpr int BT = sizeof(T) == 4 ? 4 : 6;  // corners per batch of a group (no spills)
   __shared__ float accs[kBkPos * D];        // the chunk's sums per position
   __shared__ int cnt[kBkPos + 1];           // counts, then each position's first corner
   __shared__ int cur[kBkPos];
   __shared__ float lw[kAccChunk];
   __shared__ uint32_t lq[kAccChunk];
-  __shared__ int pcut[NHW + 1];             // first position of each half-wave
+  __shared__ int pcut[NGR + 1];             // first position of each group
   __shared__ int wsum[kAccThreads / kWave];
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-  const int ch = tid & 31, hw = tid >> 5;
+  const int cl = tid & 7, gi = tid >> 3;
   const int xcd = blockIdx.x & 7;
   const int n_items = p.nitems[xcd];
   const T *gout = static_cast<const T *>(p.grad_out);
@@ -1108,7 +1109,7 @@ __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktP
     const T *gob = gout + b * p.go_sb + h * p.go_sh;
     const __amdgpu_buffer_rsrc_t gr = make_rsrc(gob, p.go_rows_bytes);
     const uint32_t go_q_bytes = (uint32_t)(p.go_sq * (int64_t)sizeof(T));
-    const uint32_t ch_bytes = (uint32_t)(ch * p.go_sc * (int64_t)sizeof(T));
+    const uint32_t ch_bytes = (uint32_t)(cl * VEC * sizeof(T));  // channels are contiguous
     __syncthreads();  // the previous chunk's readers are done
     for (int i = tid; i < kBkPos * D; i += kAccThreads) accs[i] = 0.f;
     for (int i = tid; i <= kBkPos; i += kAccThreads) cnt[i] = 0;
@@ -1154,27 +1155,29 @@ __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktP
         lw[slot] = rw[j];
         lq[slot] = rq[j] >> kBkShift;
       }
-    // half-wave cut points: pcut[w] = first position whose corners start at or after
-    // n * w / NHW (whole positions per half-wave)
-    if (tid <= NHW) {
-      const int target = n * tid / NHW;
+    // group cut points: pcut[g] = first position whose corners start at or after n * g /
+    // NGR (whole positions per group; a chunk holds ~16 corners per position)
+    if (tid <= NGR) {
+      const int target = n * tid / NGR;
       int lo = 0, hi = kBkPos;  // smallest pos with cnt[pos] >= target (cnt[kBkPos] = n)
       while (lo < hi) {
         const int mid = (lo + hi) >> 1;
         if (cnt[mid] >= target) hi = mid; else lo = mid + 1;
       }
-      pcut[tid] = tid == NHW ? kBkPos : lo;
+      pcut[tid] = tid == NGR ? kBkPos : lo;
     }
     __syncthreads();
-    const int p0 = pcut[hw], p1 = pcut[hw + 1];
+    const int p0 = pcut[gi], p1 = pcut[gi + 1];
     if (p0 < p1) {
-      // corners [k0, k1) of the half-wave's positions, BT at a time, the next batch's
-      // weights, queries and grad_output rows loaded while this one is summed
+      // corners [k0, k1) of the group's positions, BT at a time (one 4-channel piece of
+      // each corner's grad_output row per lane), the next batch loaded while this one is
+      // summed
       const int k0 = cnt[p0], k1 = cnt[p1];
       int pos = p0, next = cnt[p0 + 1];
-      float acc = 0.f;
-      float wa[BT], va[BT], wb[BT], vb[BT];
-      auto fetch = [&](int kk0, float (&w)[BT], float (&v)[BT]) __attribute__((always_inline)) {
+      float acc[VEC] = {0.f, 0.f, 0.f, 0.f};
+      float wa[BT], wb[BT];
+      Vec<T, VEC> va[BT], vb[BT];
+      auto fetch = [&](int kk0, float (&w)[BT], Vec<T, VEC> (&v)[BT]) __attribute__((always_inline)) {
         uint32_t qv[BT];
 #pragma unroll
         for (int u = 0; u < BT; ++u) {
@@ -1183,22 +1186,29 @@ __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktP
           qv[u] = lq[kk];
         }
 #pragma unroll
-        for (int u = 0; u < BT; ++u) v[u] = (float)buffer_load_one<T>(gr, qv[u] * go_q_bytes + ch_bytes);
+        for (int u = 0; u < BT; ++u) v[u] = buffer_load_vec<T, VEC>(gr, qv[u] * go_q_bytes + ch_bytes);
       };
-      auto consume = [&](int kk0, const float (&w)[BT], const float (&v)[BT]) __attribute__((always_inline)) {
+      auto flush = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int c = 0; c < VEC; ++c) {
+          accs[pos * D + cl * VEC + c] += acc[c];
+          acc[c] = 0.f;
+        }
+      };
+      auto consume = [&](int kk0, const float (&w)[BT], const Vec<T, VEC> (&v)[BT]) __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < BT; ++u) {
           const int kk = kk0 + u;
           if (kk < k1) {
-            if (kk >= next) {  // corner kk starts a later position of this half-wave
-              accs[pos * D + ch] += acc;
-              acc = 0.f;
+            if (kk >= next) {  // corner kk starts a later position of this group
+              flush();
               do {
                 ++pos;
                 next = cnt[pos + 1];
               } while (next <= kk);
             }
-            acc += w[u] * v[u];
+#pragma unroll
+            for (int c = 0; c < VEC; ++c) acc[c] += w[u] * (float)v[u].v[c];
           }
         }
       };
@@ -1211,7 +1221,7 @@ __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktP
         consume(kk0 + BT, wb, vb);
       }
       if (kk0 < k1) consume(kk0, wa, va);
-      accs[pos * D + ch] += acc;
+      flush();
     }
     __syncthreads();
     // the chunk's rows (positions past S do not exist; positions without corners skipped)
@@ -1228,6 +1238,17 @@ __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktP
   }
 }
 
+// Sum over each 8-lane group with DPP moves (no LDS traffic): lanes 4-7 of the group end
+// with the group's total. xor 1 and xor 2 inside each quad (quad_perm [1,0,3,2] and
+// [2,3,0,1]), then row_shr:4 adds the lower quad's sum to the upper quad (lanes whose
+// source is outside the 16-lane row read 0).
+__device__ __forceinline__ float sum8_upper(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x114, 0xF, 0xF, true));
+  return v;
+}
+
 // grad_sampling_loc / grad_attn_weight for D = 32 without grad_value: one wave per
 // (b, q, head) unit, 8 lanes per sample (lane owns 4 channels), 8 samples per pass and 2
 // passes per group, so the 8 corner loads of a lane are in flight together. Per sample the
@@ -1240,9 +1261,10 @@ __global__ void __launch_bounds__(kBlock) msda_coord_kernel(
     BwdParams p) {
   constexpr int D = 32, VEC = 4, PG = 2;
   constexpr uint32_t kPast = 0x80000000u;
-  const int64_t wg = ((int64_t)blockIdx.x * kBlock + threadIdx.x) >> 6;
-  if (wg >= p.units) return;  // uniform over the wave
-  const int unit = (int)wg;
+  // the unit is uniform over the wave: read it into a scalar register so the buffer
+  // descriptors built from it stay scalar
+  const int unit = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * (kBlock / kWave) + (threadIdx.x >> 6)));
+  if ((int64_t)unit >= p.units) return;
   const int lane = threadIdx.x & (kWave - 1), g = lane >> 3, cl = lane & 7;
   const int bq = unit / p.NH, h = unit - bq * p.NH;
   const int b = bq / p.NQ, q = bq - b * p.NQ;
@@ -1306,13 +1328,10 @@ __global__ void __launch_bounds__(kBlock) msda_coord_kernel(
       float gh = inw[j] ? a * (hwt * (s3 - s1) + lw * (s4 - s2)) * Hf[j] : 0.f;
       float gw = inw[j] ? a * (hh * (s2 - s1) + lh * (s4 - s3)) * Wf[j] : 0.f;
       float ga = inw[j] ? hh * hwt * s1 + hh * lw * s2 + lh * hwt * s3 + lh * lw * s4 : 0.f;
-#pragma unroll
-      for (int m = 1; m < 8; m <<= 1) {
-        gh += __shfl_xor(gh, m, kWave);
-        gw += __shfl_xor(gw, m, kWave);
-        ga += __shfl_xor(ga, m, kWave);
-      }
-      if (s < NS && cl == 0) {
+      gh = sum8_upper(gh);
+      gw = sum8_upper(gw);
+      ga = sum8_upper(ga);
+      if (s < NS && cl == 4) {
         T *glp = grad_loc + ((int64_t)unit * NS + s) * 2;
         glp[0] = (T)gw;
         glp[1] = (T)gh;
@@ -1387,7 +1406,7 @@ bool sorted_path(const MsdaBwdArgs &a, int dtype, BktLayout &L) {
     return false;
   if ((int64_t)a.f.batch * a.f.num_query * a.f.num_heads >= ((int64_t)1 << 31) / 64) return false;
   // grad_output rows through 32-bit buffer offsets
-  if (a.go_stride[1] < 0 || a.go_stride[3] < 0 ||
+  if (a.go_stride[1] < 0 || a.go_stride[3] != 1 || (a.go_stride[1] * (int64_t)sizeof(T)) % 16 != 0 ||
       ((int64_t)(a.f.num_query - 1) * a.go_stride[1] + 31 * a.go_stride[3] + 1) * (int64_t)sizeof(T) >=
           ((int64_t)1 << 31))
     return false;
