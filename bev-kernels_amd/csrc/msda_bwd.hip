@@ -900,19 +900,28 @@ struct BktParams {
   int blocks_per_xcd;
 };
 
-// Calls fn(position, weight) for every valid corner of sample (unit, l, pt) of the
-// slice's value map. Positions outside [0, S) (inconsistent metadata) are skipped.
-template <typename T, typename F>
-__device__ __forceinline__ void for_corners(const BktParams &p, int64_t unit, int l, int pt,
-                                            F &&fn) {
+// a / d for 0 <= a < 2^24 and 0 < d: a reciprocal estimate and one correction step
+__device__ __forceinline__ int fast_div(int a, int d) {
+  int q = (int)((float)a * __builtin_amdgcn_rcpf((float)d));
+  const int r = a - q * d;
+  return q + (r >= d) - (r < 0);
+}
+
+// The four corners of sample (unit, l, pt) of the slice's value map: position (-1 for an
+// invalid corner or a sample outside the window) and weight. Positions outside [0, S)
+// (inconsistent metadata) count as invalid.
+template <typename T>
+__device__ __forceinline__ void sample_corners(const BktParams &p, int64_t unit, int l, int pt,
+                                               int (&pos)[4], float (&wt)[4]) {
   const T *loc = static_cast<const T *>(p.loc);
   const T *attn = static_cast<const T *>(p.attn);
   const int64_t si = (unit * p.NL + l) * p.NP + pt;
-  const float lx = (float)loc[si * 2], ly = (float)loc[si * 2 + 1], a = (float)attn[si];
+  const Vec<T, 2> xy = *reinterpret_cast<const Vec<T, 2> *>(loc + si * 2);
+  const float lx = (float)xy.v[0], ly = (float)xy.v[1], a = (float)attn[si];
   const int Hl = (int)p.shapes[2 * l], Wl = (int)p.shapes[2 * l + 1];
   float him, wim;
   sample_coords<float>(lx, ly, Hl, Wl, him, wim);
-  if (!(him > -1.f && wim > -1.f && him < (float)Hl && wim < (float)Wl)) return;
+  const bool in = him > -1.f && wim > -1.f && him < (float)Hl && wim < (float)Wl;
   const float fh = floorf(him), fw = floorf(wim);
   const int hl = (int)fh, wl = (int)fw;
   const float lh = him - fh, lw = wim - fw, hh = 1.f - lh, hw = 1.f - lw;
@@ -920,10 +929,10 @@ __device__ __forceinline__ void for_corners(const BktParams &p, int64_t unit, in
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     const int yy = hl + (c >> 1), xx = wl + (c & 1);
-    if (yy < 0 || yy >= Hl || xx < 0 || xx >= Wl) continue;
-    const int64_t pos = base + (int64_t)yy * Wl + xx;
-    if (pos < 0 || pos >= p.S) continue;
-    fn((int)pos, ((c >> 1) ? lh : hh) * ((c & 1) ? lw : hw) * a);
+    const int64_t ps = base + (int64_t)yy * Wl + xx;
+    const bool ok = in && yy >= 0 && yy < Hl && xx >= 0 && xx < Wl && ps >= 0 && ps < p.S;
+    pos[c] = ok ? (int)ps : -1;
+    wt[c] = ((c >> 1) ? lh : hh) * ((c & 1) ? lw : hw) * a;
   }
 }
 
@@ -939,9 +948,14 @@ __global__ void __launch_bounds__(kBkThreads) msda_bkt_count_kernel(const BktPar
   for (int k = threadIdx.x; k < p.NBS; k += kBkThreads) lcnt[k] = 0;
   __syncthreads();
   for (int i = threadIdx.x; i < nq * NS; i += kBkThreads) {
-    const int u = i / NS, r = i - u * NS, l = r / p.NP, pt = r - l * p.NP;
+    const int u = fast_div(i, NS), r = i - u * NS, l = fast_div(r, p.NP), pt = r - l * p.NP;
     const int64_t unit = ((int64_t)b * p.NQ + q0 + u) * p.NH + h;
-    for_corners<T>(p, unit, l, pt, [&](int pos, float) { atomicAdd(&lcnt[pos >> kBkShift], 1); });
+    int pos[4];
+    float wt[4];
+    sample_corners<T>(p, unit, l, pt, pos, wt);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      if (pos[c] >= 0) atomicAdd(&lcnt[pos[c] >> kBkShift], 1);
   }
   __syncthreads();
   for (int k = threadIdx.x; k < p.NBS; k += kBkThreads)
@@ -1006,10 +1020,12 @@ __global__ void __launch_bounds__(1024) msda_bkt_scan_kernel(const BktParams p) 
   }
 }
 
-// Same blocks as the count kernel (qpb * L * P * 4 <= kPlaceCap): count again, stage the
-// corners in LDS in bucket order, reserve each bucket's range once, write the runs.
+// Same blocks as the count kernel (qpb * L * P * 4 <= kPlaceCap): the corners of the
+// thread's samples (kept in registers), counted per bucket, staged in LDS in bucket order,
+// each bucket's range reserved once, then written as contiguous runs.
 template <typename T>
 __global__ void __launch_bounds__(kBkThreads) msda_bkt_place_kernel(const BktParams p) {
+  constexpr int SPT = kPlaceCap / 4 / kBkThreads;  // samples per thread
   __shared__ int lcnt[kBkMaxPerSlice];   // counts, then staging cursors
   __shared__ int lst[kBkMaxPerSlice];    // first staged corner of each bucket
   __shared__ int gbase[kBkMaxPerSlice];  // first global slot of each bucket
@@ -1025,11 +1041,27 @@ __global__ void __launch_bounds__(kBkThreads) msda_bkt_place_kernel(const BktPar
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   for (int k = tid; k < p.NBS; k += kBkThreads) lcnt[k] = 0;
   __syncthreads();
-  for (int i = tid; i < nq * NS; i += kBkThreads) {
-    const int u = i / NS, r = i - u * NS, l = r / p.NP, pt = r - l * p.NP;
-    const int64_t unit = ((int64_t)b * p.NQ + q0 + u) * p.NH + h;
-    for_corners<T>(p, unit, l, pt, [&](int pos, float) { atomicAdd(&lcnt[pos >> kBkShift], 1); });
+  int rpos[SPT][4];
+  float rwt[SPT][4];
+  uint32_t rq[SPT];
+#pragma unroll
+  for (int j = 0; j < SPT; ++j) {
+    const int i = tid + j * kBkThreads;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) rpos[j][c] = -1;
+    rq[j] = 0;
+    if (i < nq * NS) {
+      const int u = fast_div(i, NS), r = i - u * NS, l = fast_div(r, p.NP), pt = r - l * p.NP;
+      const int64_t unit = ((int64_t)b * p.NQ + q0 + u) * p.NH + h;
+      sample_corners<T>(p, unit, l, pt, rpos[j], rwt[j]);
+      rq[j] = (uint32_t)(q0 + u) << kBkShift;
+    }
   }
+#pragma unroll
+  for (int j = 0; j < SPT; ++j)
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      if (rpos[j][c] >= 0) atomicAdd(&lcnt[rpos[j][c] >> kBkShift], 1);
   __syncthreads();
   {  // exclusive scan of the NBS counts: thread tid owns [tid*E, tid*E + E)
     const int E = (p.NBS + kBkThreads - 1) / kBkThreads;
@@ -1055,18 +1087,17 @@ __global__ void __launch_bounds__(kBkThreads) msda_bkt_place_kernel(const BktPar
     }
   }
   __syncthreads();
-  for (int i = tid; i < nq * NS; i += kBkThreads) {
-    const int u = i / NS, r = i - u * NS, l = r / p.NP, pt = r - l * p.NP;
-    const int64_t unit = ((int64_t)b * p.NQ + q0 + u) * p.NH + h;
-    const uint32_t qbits = (uint32_t)(q0 + u) << kBkShift;
-    for_corners<T>(p, unit, l, pt, [&](int pos, float w) {
-      const int k = pos >> kBkShift;
-      const int slot = atomicAdd(&lcnt[k], 1);
-      sw[slot] = w;
-      sq[slot] = qbits | (uint32_t)(pos & (kBkPos - 1));
-      sb[slot] = (unsigned short)k;
-    });
-  }
+#pragma unroll
+  for (int j = 0; j < SPT; ++j)
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      if (rpos[j][c] >= 0) {
+        const int k = rpos[j][c] >> kBkShift;
+        const int slot = atomicAdd(&lcnt[k], 1);
+        sw[slot] = rwt[j][c];
+        sq[slot] = rq[j] | (uint32_t)(rpos[j][c] & (kBkPos - 1));
+        sb[slot] = (unsigned short)k;
+      }
   __syncthreads();
   const int total = lcnt[p.NBS - 1];  // the last bucket's cursor ends at the staged total
   for (int i = tid; i < total; i += kBkThreads) {
@@ -1250,10 +1281,13 @@ __device__ __forceinline__ float sum8_upper(float v) {
 }
 
 // grad_sampling_loc / grad_attn_weight for D = 32 without grad_value: one wave per
-// (b, q, head) unit, 8 lanes per sample (lane owns 4 channels), 8 samples per pass and 2
-// passes per group, so the 8 corner loads of a lane are in flight together. Per sample the
-// lanes form S_k = sum_c top_c * v_k,c over their channels for the four corners; the three
-// gradients are linear in S_k and are reduced over the 8 lanes.
+// (b, q, head) unit. Lane i loads sample i's location and attention weight (64 samples per
+// load instruction); then 8 lanes per sample (lane owns 4 channels), 8 samples per pass and
+// 2 passes per group, take them by lane permutes, so the vector-memory path carries only
+// the corner rows and one grad_output row per unit. Per sample the lanes form
+// S_k = sum_c top_c * v_k,c over their channels for the four corners; the three gradients
+// are linear in S_k and are reduced over the 8 lanes. Needs contiguous grad_output
+// channels (16-byte pieces).
 template <typename T>
 __global__ void __launch_bounds__(kBlock) msda_coord_kernel(
     const T *__restrict__ value, const T *__restrict__ loc, const T *__restrict__ attn,
@@ -1270,72 +1304,81 @@ __global__ void __launch_bounds__(kBlock) msda_coord_kernel(
   const int b = bq / p.NQ, q = bq - b * p.NQ;
   const int NS = p.NL * p.NP;
   const int row = p.NH * D;
+  const Vec<T, VEC> tv = *reinterpret_cast<const Vec<T, VEC> *>(
+      grad_out + b * p.go_sb + (int64_t)q * p.go_sq + h * p.go_sh + cl * VEC);
   float top[VEC];
 #pragma unroll
-  for (int j = 0; j < VEC; ++j)
-    top[j] = (float)grad_out[b * p.go_sb + (int64_t)q * p.go_sq + h * p.go_sh + (cl * VEC + j) * p.go_sc];
+  for (int j = 0; j < VEC; ++j) top[j] = (float)tv.v[j];
   const T *vb = value + (int64_t)b * p.S * row + h * D;
   const __amdgpu_buffer_rsrc_t rv =
       make_rsrc(vb, (uint32_t)(((int64_t)p.S * row - h * D) * sizeof(T)));
   const uint32_t lane_b = (uint32_t)(cl * VEC * sizeof(T));
   const T *lp = loc + (int64_t)unit * NS * 2;
   const T *ap = attn + (int64_t)unit * NS;
-  for (int s0 = 0; s0 < NS; s0 += 8 * PG) {
-    float lhv[PG], lwv[PG], av[PG], Hf[PG], Wf[PG];
-    bool inw[PG];
-    Vec<T, VEC> cv[PG][4];
+  for (int c0 = 0; c0 < NS; c0 += kWave) {
+    // lane i: sample c0 + i
+    const int si = min(c0 + lane, NS - 1);
+    const Vec<T, 2> xy = *reinterpret_cast<const Vec<T, 2> *>(lp + 2 * si);
+    const float mx = (float)xy.v[0], my = (float)xy.v[1], ma = (float)ap[si];
+    const int cn = min(kWave, NS - c0);
+    for (int s0 = 0; s0 < cn; s0 += 8 * PG) {
+      float lhv[PG], lwv[PG], av[PG], Hf[PG], Wf[PG];
+      bool inw[PG];
+      Vec<T, VEC> cv[PG][4];
 #pragma unroll
-    for (int j = 0; j < PG; ++j) {
-      const int s = s0 + j * 8 + g;
-      const int sc = s < NS ? s : NS - 1;
-      const int l = sc / p.NP;
-      const int Hl = (int)p.shapes[2 * l], Wl = (int)p.shapes[2 * l + 1];
-      const int base = (int)p.lsi[l];
-      const float lx = (float)lp[2 * sc], ly = (float)lp[2 * sc + 1];
-      av[j] = (float)ap[sc];
-      Hf[j] = (float)Hl;
-      Wf[j] = (float)Wl;
-      float him, wim;
-      sample_coords<float>(lx, ly, Hl, Wl, him, wim);
-      inw[j] = s < NS && him > -1.f && wim > -1.f && him < (float)Hl && wim < (float)Wl;
-      const float fh = floorf(him), fw = floorf(wim);
-      const int hl = (int)fh, wl = (int)fw;
-      lhv[j] = him - fh;
-      lwv[j] = wim - fw;
-      const bool c1 = inw[j] && hl >= 0 && wl >= 0;
-      const bool c2 = inw[j] && hl >= 0 && wl + 1 <= Wl - 1;
-      const bool c3 = inw[j] && hl + 1 <= Hl - 1 && wl >= 0;
-      const bool c4 = inw[j] && hl + 1 <= Hl - 1 && wl + 1 <= Wl - 1;
-      const uint32_t e1 = (uint32_t)((base + hl * Wl + wl) * row) * (uint32_t)sizeof(T) + lane_b;
-      const uint32_t dx = (uint32_t)(row * sizeof(T)), dy = (uint32_t)(Wl * row * sizeof(T));
-      cv[j][0] = buffer_load_vec<T, VEC>(rv, c1 ? e1 : kPast);
-      cv[j][1] = buffer_load_vec<T, VEC>(rv, c2 ? e1 + dx : kPast);
-      cv[j][2] = buffer_load_vec<T, VEC>(rv, c3 ? e1 + dy : kPast);
-      cv[j][3] = buffer_load_vec<T, VEC>(rv, c4 ? e1 + dy + dx : kPast);
-    }
-#pragma unroll
-    for (int j = 0; j < PG; ++j) {
-      const int s = s0 + j * 8 + g;
-      float s1 = 0.f, s2 = 0.f, s3 = 0.f, s4 = 0.f;
-#pragma unroll
-      for (int c = 0; c < VEC; ++c) {
-        s1 += top[c] * (float)cv[j][0].v[c];
-        s2 += top[c] * (float)cv[j][1].v[c];
-        s3 += top[c] * (float)cv[j][2].v[c];
-        s4 += top[c] * (float)cv[j][3].v[c];
+      for (int j = 0; j < PG; ++j) {
+        const int sl = s0 + j * 8 + g;        // sample within the chunk
+        const int src = min(sl, cn - 1);
+        const float lx = __shfl(mx, src, kWave), ly = __shfl(my, src, kWave);
+        av[j] = __shfl(ma, src, kWave);
+        const int l = (c0 + src) / p.NP;
+        const int Hl = (int)p.shapes[2 * l], Wl = (int)p.shapes[2 * l + 1];
+        const int base = (int)p.lsi[l];
+        Hf[j] = (float)Hl;
+        Wf[j] = (float)Wl;
+        float him, wim;
+        sample_coords<float>(lx, ly, Hl, Wl, him, wim);
+        inw[j] = sl < cn && him > -1.f && wim > -1.f && him < (float)Hl && wim < (float)Wl;
+        const float fh = floorf(him), fw = floorf(wim);
+        const int hl = (int)fh, wl = (int)fw;
+        lhv[j] = him - fh;
+        lwv[j] = wim - fw;
+        const bool c1 = inw[j] && hl >= 0 && wl >= 0;
+        const bool c2 = inw[j] && hl >= 0 && wl + 1 <= Wl - 1;
+        const bool c3 = inw[j] && hl + 1 <= Hl - 1 && wl >= 0;
+        const bool c4 = inw[j] && hl + 1 <= Hl - 1 && wl + 1 <= Wl - 1;
+        const uint32_t e1 = (uint32_t)((base + hl * Wl + wl) * row) * (uint32_t)sizeof(T) + lane_b;
+        const uint32_t dx = (uint32_t)(row * sizeof(T)), dy = (uint32_t)(Wl * row * sizeof(T));
+        cv[j][0] = buffer_load_vec<T, VEC>(rv, c1 ? e1 : kPast);
+        cv[j][1] = buffer_load_vec<T, VEC>(rv, c2 ? e1 + dx : kPast);
+        cv[j][2] = buffer_load_vec<T, VEC>(rv, c3 ? e1 + dy : kPast);
+        cv[j][3] = buffer_load_vec<T, VEC>(rv, c4 ? e1 + dy + dx : kPast);
       }
-      const float lh = lhv[j], lw = lwv[j], hh = 1.f - lh, hwt = 1.f - lw, a = av[j];
-      float gh = inw[j] ? a * (hwt * (s3 - s1) + lw * (s4 - s2)) * Hf[j] : 0.f;
-      float gw = inw[j] ? a * (hh * (s2 - s1) + lh * (s4 - s3)) * Wf[j] : 0.f;
-      float ga = inw[j] ? hh * hwt * s1 + hh * lw * s2 + lh * hwt * s3 + lh * lw * s4 : 0.f;
-      gh = sum8_upper(gh);
-      gw = sum8_upper(gw);
-      ga = sum8_upper(ga);
-      if (s < NS && cl == 4) {
-        T *glp = grad_loc + ((int64_t)unit * NS + s) * 2;
-        glp[0] = (T)gw;
-        glp[1] = (T)gh;
-        grad_attn[(int64_t)unit * NS + s] = (T)ga;
+#pragma unroll
+      for (int j = 0; j < PG; ++j) {
+        const int sl = s0 + j * 8 + g;
+        float s1 = 0.f, s2 = 0.f, s3 = 0.f, s4 = 0.f;
+#pragma unroll
+        for (int c = 0; c < VEC; ++c) {
+          s1 += top[c] * (float)cv[j][0].v[c];
+          s2 += top[c] * (float)cv[j][1].v[c];
+          s3 += top[c] * (float)cv[j][2].v[c];
+          s4 += top[c] * (float)cv[j][3].v[c];
+        }
+        const float lh = lhv[j], lw = lwv[j], hh = 1.f - lh, hwt = 1.f - lw, a = av[j];
+        float gh = inw[j] ? a * (hwt * (s3 - s1) + lw * (s4 - s2)) * Hf[j] : 0.f;
+        float gw = inw[j] ? a * (hh * (s2 - s1) + lh * (s4 - s3)) * Wf[j] : 0.f;
+        float ga = inw[j] ? hh * hwt * s1 + hh * lw * s2 + lh * hwt * s3 + lh * lw * s4 : 0.f;
+        gh = sum8_upper(gh);
+        gw = sum8_upper(gw);
+        ga = sum8_upper(ga);
+        if (sl < cn && cl == 4) {
+          const int s = c0 + sl;
+          T *glp = grad_loc + ((int64_t)unit * NS + s) * 2;
+          glp[0] = (T)gw;
+          glp[1] = (T)gh;
+          grad_attn[(int64_t)unit * NS + s] = (T)ga;
+        }
       }
     }
   }
@@ -1406,6 +1449,11 @@ bool sorted_path(const MsdaBwdArgs &a, int dtype, BktLayout &L) {
     return false;
   if ((int64_t)a.f.batch * a.f.num_query * a.f.num_heads >= ((int64_t)1 << 31) / 64) return false;
   // grad_output rows through 32-bit buffer offsets
+  // (16-byte pieces of grad_output rows: contiguous channels, aligned rows)
+  if (reinterpret_cast<uintptr_t>(a.grad_output) % 16 != 0 || a.go_stride[0] < 0 ||
+      a.go_stride[2] < 0 || (a.go_stride[0] * (int64_t)sizeof(T)) % 16 != 0 ||
+      (a.go_stride[2] * (int64_t)sizeof(T)) % 16 != 0)
+    return false;
   if (a.go_stride[1] < 0 || a.go_stride[3] != 1 || (a.go_stride[1] * (int64_t)sizeof(T)) % 16 != 0 ||
       ((int64_t)(a.f.num_query - 1) * a.go_stride[1] + 31 * a.go_stride[3] + 1) * (int64_t)sizeof(T) >=
           ((int64_t)1 << 31))
