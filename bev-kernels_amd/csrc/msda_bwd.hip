@@ -861,7 +861,7 @@ __global__ void __launch_bounds__(kBlock) msda_col2im_d32_kernel(
 //      buckets listed per XCD (slice % 8, or bucket % 8 with fewer than 8 slices);
 //   3. msda_bkt_place_kernel: the corners again, staged in LDS in bucket order, each
 //      bucket's range reserved once per block, then written as contiguous runs of
-//      (weight, query << kBkShift | position in bucket);
+//      8-byte (weight, query << kBkShift | position in bucket) records;
 //   4. msda_bkt_acc_kernel: per chunk of at most kAccChunk corners of one bucket, a
 //      counting sort by position in LDS; each 8-lane group takes whole positions (about
 //      1/64 of the chunk's corners), sums weight x grad_output row in registers (4
@@ -891,8 +891,7 @@ struct BktParams {
   int *offset;      // [nbk + 1]
   int *nitems;      // [8] buckets per XCD list
   int2 *items;      // [8][item_cap] (bucket, first corner of the chunk)
-  float *pw;        // [capacity] corner weights
-  uint32_t *pq;     // [capacity] (query << kBkShift) | position in bucket
+  int2 *pc;         // [capacity] corners: (weight bits, query << kBkShift | position in bucket)
   int64_t go_sb, go_sq, go_sh, go_sc;
   uint32_t go_rows_bytes;  // bytes from row (b, 0, h, 0) past row (b, NQ - 1, h, 31)
   int B, NH, NQ, NL, NP, S, NBS, nbk, item_cap, qpb;
@@ -1103,8 +1102,7 @@ __global__ void __launch_bounds__(kBkThreads) msda_bkt_place_kernel(const BktPar
   for (int i = tid; i < total; i += kBkThreads) {
     const int k = sb[i];
     const int dst = gbase[k] + (i - lst[k]);
-    p.pw[dst] = sw[i];
-    p.pq[dst] = sq[i];
+    p.pc[dst] = make_int2(__builtin_bit_cast(int, sw[i]), (int)sq[i]);
   }
 }
 
@@ -1150,8 +1148,11 @@ __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktP
 #pragma unroll
     for (int j = 0; j < kAccPerThread; ++j) {
       const int i = min(tid + j * kAccThreads, n - 1);
-      rw[j] = p.pw[first + i];
-      rq[j] = p.pq[first + i];
+      // streamed once: a non-temporal load keeps the grad_output rows in the L2
+      typedef int i2v __attribute__((ext_vector_type(2)));
+      const i2v c = __builtin_nontemporal_load(reinterpret_cast<const i2v *>(p.pc + first + i));
+      rw[j] = __builtin_bit_cast(float, c.x);
+      rq[j] = (uint32_t)c.y;
     }
 #pragma unroll
     for (int j = 0; j < kAccPerThread; ++j)
@@ -1407,7 +1408,7 @@ struct BktLayout {
   int NBS = 0, nbk = 0, item_cap = 0;
   int64_t cap = 0;  // corner slots
   int64_t off_count = 0, off_cursor = 0, off_offset = 0, off_nitems = 0, off_items = 0,
-          off_pw = 0, off_pq = 0, bytes = 0;
+          off_pc = 0, bytes = 0;
 };
 
 BktLayout bkt_layout(int64_t B, int64_t S, int64_t NH, int64_t NL, int64_t NQ, int64_t NP) {
@@ -1428,8 +1429,7 @@ BktLayout bkt_layout(int64_t B, int64_t S, int64_t NH, int64_t NL, int64_t NQ, i
   L.off_offset = o; o += up((nbk + 1) * 4);
   L.off_nitems = o; o += up(8 * 4);
   L.off_items = o;  o += up(8 * item_cap * 8);
-  L.off_pw = o;     o += up(cap * 4);
-  L.off_pq = o;     o += up(cap * 4);
+  L.off_pc = o;     o += up(cap * 8);
   L.bytes = o;
   return L;
 }
@@ -1482,8 +1482,7 @@ hipError_t launch_sorted(const MsdaBwdArgs &a, const BktLayout &L, char *ws, flo
   p.offset = reinterpret_cast<int *>(ws + L.off_offset);
   p.nitems = reinterpret_cast<int *>(ws + L.off_nitems);
   p.items = reinterpret_cast<int2 *>(ws + L.off_items);
-  p.pw = reinterpret_cast<float *>(ws + L.off_pw);
-  p.pq = reinterpret_cast<uint32_t *>(ws + L.off_pq);
+  p.pc = reinterpret_cast<int2 *>(ws + L.off_pc);
   p.go_sb = a.go_stride[0]; p.go_sq = a.go_stride[1];
   p.go_sh = a.go_stride[2]; p.go_sc = a.go_stride[3];
   p.B = a.f.batch; p.NH = a.f.num_heads; p.NQ = a.f.num_query; p.NL = a.f.num_levels;

@@ -164,7 +164,7 @@ def _sorted_bytes(b, s, h, nl, nq, np_):
     cap = b * nq * h * nl * np_ * 4
     nbk = b * h * nbs
     items = -(-cap // 4096) + nbk
-    return 2 * up(nbk * 4) + up((nbk + 1) * 4) + up(32) + up(8 * items * 8) + 2 * up(cap * 4)
+    return 2 * up(nbk * 4) + up((nbk + 1) * 4) + up(32) + up(8 * items * 8) + up(cap * 8)
 
 
 def test_msda_backward_workspace_bytes():
