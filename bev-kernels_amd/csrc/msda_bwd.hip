@@ -1270,117 +1270,197 @@ __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktP
   }
 }
 
-// Sum over each 8-lane group with DPP moves (no LDS traffic): lanes 4-7 of the group end
-// with the group's total. xor 1 and xor 2 inside each quad (quad_perm [1,0,3,2] and
-// [2,3,0,1]), then row_shr:4 adds the lower quad's sum to the upper quad (lanes whose
-// source is outside the 16-lane row read 0).
-__device__ __forceinline__ float sum8_upper(float v) {
+// grad_sampling_loc / grad_attn_weight for D = 32 without grad_value. A wave takes a tile
+// of queries of one (batch, head) slice, `upi` units at a time (upi * L * P <= 64 samples,
+// one per lane; more samples than 64 go in chunks of 64 with upi = 1):
+//   1. lane i takes sample i: loads its location and attention weight, and writes the four
+//      corner offsets (an out-of-range offset for a corner outside the level or a sample
+//      outside the window, so the load returns zeros) and (lh, lw, a * H, a * W) to LDS;
+//   2. groups of LPS lanes (LPS * 16 bytes = one corner row) take the samples in steps,
+//      each group staying on one unit so that its grad_output piece stays in registers,
+//      form S_k = sum_c top_c * v_k,c for the four corners, reduce the three gradients
+//      (linear in S_k) over the group and leave them in LDS;
+//   3. lane i stores sample i's gradients (contiguous stores).
+// Tiles are ordered slice by slice and XCD x takes the x-th eighth of them, so the
+// workgroups of one XCD gather from one slice of value at a time (a slice of the SCA map
+// is 3.9 MB in fp32, the size of an XCD's L2).
+constexpr int kCoWaves = 4;  // waves per workgroup
+constexpr int kCoIters = 4;  // unit groups per tile
+
+struct CoordParams {
+  const void *value, *loc, *attn, *grad_out;
+  void *grad_loc, *grad_attn;
+  const int64_t *shapes, *lsi;
+  int64_t go_sb, go_sq, go_sh;  // grad_output strides, elements (channels contiguous)
+  int NH, NQ, NL, NP, S;
+  int upi;     // units per pass
+  int tps;     // tiles per slice
+  int nt8;     // tiles per XCD
+  int ntiles;
+};
+
+// Sum over each LPS-lane group (4 or 8) with DPP moves, no LDS traffic: xor 1 and xor 2
+// inside each quad (quad_perm [1,0,3,2] and [2,3,0,1]); for 8 lanes, row_shr:4 then adds
+// the lower quad's sum to the upper quad (lanes whose source is outside the 16-lane row
+// read 0). Lane LPS - 1 of the group ends with the group's total.
+template <int LPS>
+__device__ __forceinline__ float group_sum(float v) {
   v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
   v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
-  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x114, 0xF, 0xF, true));
+  if constexpr (LPS == 8)
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x114, 0xF, 0xF, true));
   return v;
 }
 
-// grad_sampling_loc / grad_attn_weight for D = 32 without grad_value: one wave per
-// (b, q, head) unit. Lane i loads sample i's location and attention weight (64 samples per
-// load instruction); then 8 lanes per sample (lane owns 4 channels), 8 samples per pass and
-// 2 passes per group, take them by lane permutes, so the vector-memory path carries only
-// the corner rows and one grad_output row per unit. Per sample the lanes form
-// S_k = sum_c top_c * v_k,c over their channels for the four corners; the three gradients
-// are linear in S_k and are reduced over the 8 lanes. Needs contiguous grad_output
-// channels (16-byte pieces).
+// LDS stores by one lane become visible to loads by other lanes of the same wave once
+// issued (a wave's LDS instructions execute in order); this keeps the compiler from
+// moving memory accesses across the hand-over.
+__device__ __forceinline__ void wave_lds_handover() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 template <typename T>
-__global__ void __launch_bounds__(kBlock) msda_coord_kernel(
-    const T *__restrict__ value, const T *__restrict__ loc, const T *__restrict__ attn,
-    const T *__restrict__ grad_out, T *__restrict__ grad_loc, T *__restrict__ grad_attn,
-    BwdParams p) {
-  constexpr int D = 32, VEC = 4, PG = 2;
+__global__ void __launch_bounds__(kCoWaves * kWave) msda_coord_kernel(const CoordParams p) {
+  constexpr int D = 32, VEC = 16 / (int)sizeof(T), LPS = D / VEC, G = kWave / LPS;
   constexpr uint32_t kPast = 0x80000000u;
-  // the unit is uniform over the wave: read it into a scalar register so the buffer
-  // descriptors built from it stay scalar
-  const int unit = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * (kBlock / kWave) + (threadIdx.x >> 6)));
-  if ((int64_t)unit >= p.units) return;
-  const int lane = threadIdx.x & (kWave - 1), g = lane >> 3, cl = lane & 7;
-  const int bq = unit / p.NH, h = unit - bq * p.NH;
-  const int b = bq / p.NQ, q = bq - b * p.NQ;
-  const int NS = p.NL * p.NP;
+  __shared__ uint4 s_off[kCoWaves][kWave];   // corner byte offsets
+  __shared__ float4 s_par[kCoWaves][kWave];  // lh, lw, a * H, a * W
+  __shared__ float4 s_res[kCoWaves][kWave];  // grad_w, grad_h, grad_attn
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & (kWave - 1);
+  const int xcd = blockIdx.x & 7, r = blockIdx.x >> 3;
+  // the wave's tile is uniform: kept in scalar registers
+  const int tloc = __builtin_amdgcn_readfirstlane(r * kCoWaves + wave);
+  const int tile = xcd * p.nt8 + tloc;
+  if (tloc >= p.nt8 || tile >= p.ntiles) return;
+  const int slice = tile / p.tps;
+  const int tq = tile - slice * p.tps;
+  const int b = slice / p.NH, h = slice - b * p.NH;
+  const int NS = p.NL * p.NP, upi = p.upi;
+  const int q_begin = tq * upi * kCoIters, q_end = min(p.NQ, q_begin + upi * kCoIters);
   const int row = p.NH * D;
-  const Vec<T, VEC> tv = *reinterpret_cast<const Vec<T, VEC> *>(
-      grad_out + b * p.go_sb + (int64_t)q * p.go_sq + h * p.go_sh + cl * VEC);
-  float top[VEC];
-#pragma unroll
-  for (int j = 0; j < VEC; ++j) top[j] = (float)tv.v[j];
-  const T *vb = value + (int64_t)b * p.S * row + h * D;
+  const T *vb = static_cast<const T *>(p.value) + (int64_t)b * p.S * row + h * D;
   const __amdgpu_buffer_rsrc_t rv =
       make_rsrc(vb, (uint32_t)(((int64_t)p.S * row - h * D) * sizeof(T)));
+  const T *loc = static_cast<const T *>(p.loc);
+  const T *attn = static_cast<const T *>(p.attn);
+  T *gloc = static_cast<T *>(p.grad_loc);
+  T *gattn = static_cast<T *>(p.grad_attn);
+  const T *gob = static_cast<const T *>(p.grad_out) + b * p.go_sb + h * p.go_sh;
+  // group lanes: unit slot ug, sample column gq of GPU per unit, channels cl * VEC ..
+  const int g = lane / LPS, cl = lane - g * LPS;
+  const int ug = g % upi, gq = g / upi, GPU = G / upi;
   const uint32_t lane_b = (uint32_t)(cl * VEC * sizeof(T));
-  const T *lp = loc + (int64_t)unit * NS * 2;
-  const T *ap = attn + (int64_t)unit * NS;
   for (int c0 = 0; c0 < NS; c0 += kWave) {
-    // lane i: sample c0 + i
-    const int si = min(c0 + lane, NS - 1);
-    const Vec<T, 2> xy = *reinterpret_cast<const Vec<T, 2> *>(lp + 2 * si);
-    const float mx = (float)xy.v[0], my = (float)xy.v[1], ma = (float)ap[si];
-    const int cn = min(kWave, NS - c0);
-    for (int s0 = 0; s0 < cn; s0 += 8 * PG) {
-      float lhv[PG], lwv[PG], av[PG], Hf[PG], Wf[PG];
-      bool inw[PG];
-      Vec<T, VEC> cv[PG][4];
+    const int nsc = upi > 1 ? NS : min(kWave, NS - c0);  // samples per unit in this pass
+    // sample lanes: unit slot ui, sample s; the level geometry is fixed for the pass
+    const int ui = lane / nsc, s = c0 + lane - ui * nsc;
+    const bool lane_on = ui < upi;
+    const int l = lane_on ? s / p.NP : 0;
+    const int Hl = (int)p.shapes[2 * l], Wl = (int)p.shapes[2 * l + 1];
+    const int lbase = (int)p.lsi[l];
+    const float Hf = (float)Hl, Wf = (float)Wl;
+    const uint32_t dx = (uint32_t)(row * sizeof(T)), dy = (uint32_t)(Wl * row * sizeof(T));
+    const int steps = (nsc + GPU - 1) / GPU;
+    // sample index of lane (ui, s) in the pass at q0: si0 + (q0 - q_begin) * NH * NS (32-bit:
+    // the launch checks units * NS * 2 < 2^31); lanes past the units read sample 0 of unit 0
+    const int uq = lane_on ? ui : 0;
+    const int si0 = ((b * p.NQ + q_begin + uq) * p.NH + h) * NS + (lane_on ? s : c0);
+    const int dsi = p.NH * NS;
+    const int qlast = q_end - 1 - q_begin - uq;  // pass offset of the tile's last query
+    // the next pass's location, attention weight and grad_output piece are loaded while
+    // this pass runs
+    Vec<T, 2> xy_n;
+    T a_n;
+    Vec<T, VEC> tv_n;
+    auto fetch = [&](int q0) __attribute__((always_inline)) {
+      const int si = si0 + min(q0 - q_begin, qlast) * dsi;
+      xy_n = *reinterpret_cast<const Vec<T, 2> *>(loc + (int64_t)si * 2);
+      a_n = attn[si];
+      const int qg = min(q0 + ug, q_end - 1);
+      tv_n = *reinterpret_cast<const Vec<T, VEC> *>(gob + (int64_t)qg * p.go_sq + cl * VEC);
+    };
+    fetch(q_begin);
+    for (int q0 = q_begin; q0 < q_end; q0 += upi) {
+      // 1. sample lanes
+      const int qs = q0 + ui;
+      const bool on = lane_on && qs < q_end;
+      const int si = si0 + (q0 - q_begin) * dsi;
+      const Vec<T, 2> xy = xy_n;
+      const float a = (float)a_n;
+      float top[VEC];
 #pragma unroll
-      for (int j = 0; j < PG; ++j) {
-        const int sl = s0 + j * 8 + g;        // sample within the chunk
-        const int src = min(sl, cn - 1);
-        const float lx = __shfl(mx, src, kWave), ly = __shfl(my, src, kWave);
-        av[j] = __shfl(ma, src, kWave);
-        const int l = (c0 + src) / p.NP;
-        const int Hl = (int)p.shapes[2 * l], Wl = (int)p.shapes[2 * l + 1];
-        const int base = (int)p.lsi[l];
-        Hf[j] = (float)Hl;
-        Wf[j] = (float)Wl;
-        float him, wim;
-        sample_coords<float>(lx, ly, Hl, Wl, him, wim);
-        inw[j] = sl < cn && him > -1.f && wim > -1.f && him < (float)Hl && wim < (float)Wl;
+      for (int c = 0; c < VEC; ++c) top[c] = (float)tv_n.v[c];
+      if (q0 + upi < q_end) fetch(q0 + upi);
+      uint4 off = make_uint4(kPast, kPast, kPast, kPast);
+      float4 par = make_float4(0.f, 0.f, 0.f, 0.f);
+      float him, wim;
+      sample_coords<float>((float)xy.v[0], (float)xy.v[1], Hl, Wl, him, wim);
+      if (on && him > -1.f && wim > -1.f && him < Hf && wim < Wf) {
         const float fh = floorf(him), fw = floorf(wim);
         const int hl = (int)fh, wl = (int)fw;
-        lhv[j] = him - fh;
-        lwv[j] = wim - fw;
-        const bool c1 = inw[j] && hl >= 0 && wl >= 0;
-        const bool c2 = inw[j] && hl >= 0 && wl + 1 <= Wl - 1;
-        const bool c3 = inw[j] && hl + 1 <= Hl - 1 && wl >= 0;
-        const bool c4 = inw[j] && hl + 1 <= Hl - 1 && wl + 1 <= Wl - 1;
-        const uint32_t e1 = (uint32_t)((base + hl * Wl + wl) * row) * (uint32_t)sizeof(T) + lane_b;
-        const uint32_t dx = (uint32_t)(row * sizeof(T)), dy = (uint32_t)(Wl * row * sizeof(T));
-        cv[j][0] = buffer_load_vec<T, VEC>(rv, c1 ? e1 : kPast);
-        cv[j][1] = buffer_load_vec<T, VEC>(rv, c2 ? e1 + dx : kPast);
-        cv[j][2] = buffer_load_vec<T, VEC>(rv, c3 ? e1 + dy : kPast);
-        cv[j][3] = buffer_load_vec<T, VEC>(rv, c4 ? e1 + dy + dx : kPast);
+        const uint32_t e1 = (uint32_t)((lbase + hl * Wl + wl) * row) * (uint32_t)sizeof(T);
+        const bool y0 = hl >= 0, y1 = hl + 1 <= Hl - 1, x0 = wl >= 0, x1 = wl + 1 <= Wl - 1;
+        off.x = y0 && x0 ? e1 : kPast;
+        off.y = y0 && x1 ? e1 + dx : kPast;
+        off.z = y1 && x0 ? e1 + dy : kPast;
+        off.w = y1 && x1 ? e1 + dy + dx : kPast;
+        par = make_float4(him - fh, wim - fw, a * Hf, a * Wf);
       }
+      s_off[wave][lane] = off;
+      s_par[wave][lane] = par;
+      wave_lds_handover();
+      // 2. group lanes, two steps at a time
+      for (int t = 0; t < steps; t += 2) {
+        Vec<T, VEC> cv[2][4];
+        float4 pr[2];
+        int slot[2];
+        bool ok[2];
 #pragma unroll
-      for (int j = 0; j < PG; ++j) {
-        const int sl = s0 + j * 8 + g;
-        float s1 = 0.f, s2 = 0.f, s3 = 0.f, s4 = 0.f;
-#pragma unroll
-        for (int c = 0; c < VEC; ++c) {
-          s1 += top[c] * (float)cv[j][0].v[c];
-          s2 += top[c] * (float)cv[j][1].v[c];
-          s3 += top[c] * (float)cv[j][2].v[c];
-          s4 += top[c] * (float)cv[j][3].v[c];
+        for (int j = 0; j < 2; ++j) {
+          const int sl = (t + j) * GPU + gq;
+          ok[j] = sl < nsc && t + j < steps;
+          slot[j] = ug * nsc + min(sl, nsc - 1);
+          const uint4 o = s_off[wave][slot[j]];
+          pr[j] = s_par[wave][slot[j]];
+          cv[j][0] = buffer_load_vec<T, VEC>(rv, (ok[j] ? o.x : kPast) + lane_b);
+          cv[j][1] = buffer_load_vec<T, VEC>(rv, (ok[j] ? o.y : kPast) + lane_b);
+          cv[j][2] = buffer_load_vec<T, VEC>(rv, (ok[j] ? o.z : kPast) + lane_b);
+          cv[j][3] = buffer_load_vec<T, VEC>(rv, (ok[j] ? o.w : kPast) + lane_b);
         }
-        const float lh = lhv[j], lw = lwv[j], hh = 1.f - lh, hwt = 1.f - lw, a = av[j];
-        float gh = inw[j] ? a * (hwt * (s3 - s1) + lw * (s4 - s2)) * Hf[j] : 0.f;
-        float gw = inw[j] ? a * (hh * (s2 - s1) + lh * (s4 - s3)) * Wf[j] : 0.f;
-        float ga = inw[j] ? hh * hwt * s1 + hh * lw * s2 + lh * hwt * s3 + lh * lw * s4 : 0.f;
-        gh = sum8_upper(gh);
-        gw = sum8_upper(gw);
-        ga = sum8_upper(ga);
-        if (sl < cn && cl == 4) {
-          const int s = c0 + sl;
-          T *glp = grad_loc + ((int64_t)unit * NS + s) * 2;
-          glp[0] = (T)gw;
-          glp[1] = (T)gh;
-          grad_attn[(int64_t)unit * NS + s] = (T)ga;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          float s1 = 0.f, s2 = 0.f, s3 = 0.f, s4 = 0.f;
+#pragma unroll
+          for (int c = 0; c < VEC; ++c) {
+            s1 += top[c] * (float)cv[j][0].v[c];
+            s2 += top[c] * (float)cv[j][1].v[c];
+            s3 += top[c] * (float)cv[j][2].v[c];
+            s4 += top[c] * (float)cv[j][3].v[c];
+          }
+          const float lh = pr[j].x, lw = pr[j].y, hh = 1.f - lh, hw = 1.f - lw;
+          // a sample outside the window has no valid corner: S_k = 0 and all three are 0
+          float gh = pr[j].z * (hw * (s3 - s1) + lw * (s4 - s2));
+          float gw = pr[j].w * (hh * (s2 - s1) + lh * (s4 - s3));
+          float ga = hh * hw * s1 + hh * lw * s2 + lh * hw * s3 + lh * lw * s4;
+          gh = group_sum<LPS>(gh);
+          gw = group_sum<LPS>(gw);
+          ga = group_sum<LPS>(ga);
+          if (ok[j] && cl == LPS - 1) s_res[wave][slot[j]] = make_float4(gw, gh, ga, 0.f);
         }
       }
+      wave_lds_handover();
+      // 3. sample lanes
+      if (on) {
+        const float4 rr = s_res[wave][lane];
+        Vec<T, 2> gl;
+        gl.v[0] = (T)rr.x;
+        gl.v[1] = (T)rr.y;
+        *reinterpret_cast<Vec<T, 2> *>(gloc + (int64_t)si * 2) = gl;
+        gattn[si] = (T)rr.z;
+      }
+      wave_lds_handover();
     }
   }
 }
@@ -1448,6 +1528,15 @@ bool sorted_path(const MsdaBwdArgs &a, int dtype, BktLayout &L) {
   if ((int64_t)a.f.spatial_size * a.f.num_heads * 32 * (int64_t)sizeof(T) >= ((int64_t)1 << 31))
     return false;
   if ((int64_t)a.f.batch * a.f.num_query * a.f.num_heads >= ((int64_t)1 << 31) / 64) return false;
+  // sample indices of loc / grad_loc in 32 bits
+  if ((int64_t)a.f.batch * a.f.num_query * a.f.num_heads * a.f.num_levels * a.f.num_point * 2 >=
+      ((int64_t)1 << 31))
+    return false;
+  // 16-byte corner rows; (x, y) pairs of loc / grad_loc read and written as one access
+  if (reinterpret_cast<uintptr_t>(a.f.value) % 16 != 0 ||
+      reinterpret_cast<uintptr_t>(a.f.sampling_loc) % (2 * sizeof(T)) != 0 ||
+      reinterpret_cast<uintptr_t>(a.grad_loc) % (2 * sizeof(T)) != 0)
+    return false;
   // grad_output rows through 32-bit buffer offsets
   // (16-byte pieces of grad_output rows: contiguous channels, aligned rows)
   if (reinterpret_cast<uintptr_t>(a.grad_output) % 16 != 0 || a.go_stride[0] < 0 ||
@@ -1508,21 +1597,26 @@ hipError_t launch_sorted(const MsdaBwdArgs &a, const BktLayout &L, char *ws, flo
   if ((e = hipGetLastError()) != hipSuccess) return e;
   hipLaunchKernelGGL((msda_bkt_acc_kernel<T>), dim3(blocks), dim3(kAccThreads), 0, stream, p);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  BwdParams q;
-  q.shapes = a.f.spatial_shapes;
-  q.lsi = a.f.level_start_index;
-  q.go_sb = a.go_stride[0]; q.go_sq = a.go_stride[1];
-  q.go_sh = a.go_stride[2]; q.go_sc = a.go_stride[3];
-  q.units = (int64_t)a.f.batch * a.f.num_query * a.f.num_heads;
-  q.S = a.f.spatial_size; q.NH = a.f.num_heads; q.D = 32;
-  q.NL = a.f.num_levels; q.NQ = a.f.num_query; q.NP = a.f.num_point;
-  q.coarse = 0; q.log2_g = 0;
-  hipLaunchKernelGGL((msda_coord_kernel<T>), dim3((unsigned)((q.units * 64 + kBlock - 1) / kBlock)),
-                     dim3(kBlock), 0, stream, static_cast<const T *>(a.f.value),
-                     static_cast<const T *>(a.f.sampling_loc),
-                     static_cast<const T *>(a.f.attn_weight),
-                     static_cast<const T *>(a.grad_output), static_cast<T *>(a.grad_loc),
-                     static_cast<T *>(a.grad_attn), q);
+  CoordParams c;
+  c.value = a.f.value;
+  c.loc = a.f.sampling_loc;
+  c.attn = a.f.attn_weight;
+  c.grad_out = a.grad_output;
+  c.grad_loc = a.grad_loc;
+  c.grad_attn = a.grad_attn;
+  c.shapes = a.f.spatial_shapes;
+  c.lsi = a.f.level_start_index;
+  c.go_sb = a.go_stride[0]; c.go_sq = a.go_stride[1]; c.go_sh = a.go_stride[2];
+  c.NH = a.f.num_heads; c.NQ = a.f.num_query; c.NL = a.f.num_levels; c.NP = a.f.num_point;
+  c.S = a.f.spatial_size;
+  const int ns = a.f.num_levels * a.f.num_point;
+  c.upi = ns <= 16 ? 4 : ns <= 32 ? 2 : 1;
+  c.tps = (a.f.num_query + c.upi * kCoIters - 1) / (c.upi * kCoIters);
+  const int64_t ntiles = (int64_t)a.f.batch * a.f.num_heads * c.tps;
+  c.ntiles = (int)ntiles;
+  c.nt8 = (int)((ntiles + 7) / 8);
+  const unsigned cgrid = 8u * (unsigned)((c.nt8 + kCoWaves - 1) / kCoWaves);
+  hipLaunchKernelGGL((msda_coord_kernel<T>), dim3(cgrid), dim3(kCoWaves * kWave), 0, stream, c);
   return hipGetLastError();
 }
 
