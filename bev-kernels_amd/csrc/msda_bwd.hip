@@ -1140,7 +1140,6 @@ __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktP
     const uint32_t go_q_bytes = (uint32_t)(p.go_sq * (int64_t)sizeof(T));
     const uint32_t ch_bytes = (uint32_t)(cl * VEC * sizeof(T));  // channels are contiguous
     __syncthreads();  // the previous chunk's readers are done
-    for (int i = tid; i < kBkPos * D; i += kAccThreads) accs[i] = 0.f;
     for (int i = tid; i <= kBkPos; i += kAccThreads) cnt[i] = 0;
     __syncthreads();
     float rw[kAccPerThread];
@@ -1220,12 +1219,12 @@ __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktP
 #pragma unroll
         for (int u = 0; u < BT; ++u) v[u] = buffer_load_vec<T, VEC>(gr, qv[u] * go_q_bytes + ch_bytes);
       };
+      // each position is flushed once, by the group that owns it: a plain store (the
+      // rows of positions without corners are never read)
       auto flush = [&]() __attribute__((always_inline)) {
+        *reinterpret_cast<float4 *>(&accs[pos * D + cl * VEC]) = make_float4(acc[0], acc[1], acc[2], acc[3]);
 #pragma unroll
-        for (int c = 0; c < VEC; ++c) {
-          accs[pos * D + cl * VEC + c] += acc[c];
-          acc[c] = 0.f;
-        }
+        for (int c = 0; c < VEC; ++c) acc[c] = 0.f;
       };
       auto consume = [&](int kk0, const float (&w)[BT], const Vec<T, VEC> (&v)[BT]) __attribute__((always_inline)) {
 #pragma unroll
@@ -1256,15 +1255,26 @@ __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktP
       flush();
     }
     __syncthreads();
-    // the chunk's rows (positions past S do not exist; positions without corners skipped)
+    // the chunk's rows (positions past S do not exist; positions without corners skipped):
+    // 4 channels per thread for the plain read-modify-write; atomics on consecutive floats
+    // across the lanes (the L2 works per line of each atomic instruction)
     float *gvb = p.gv + ((int64_t)b * p.S + (int64_t)kb * kBkPos) * (p.NH * D) + h * D;
     const int npos = min(kBkPos, p.S - kb * kBkPos);
-    for (int i = tid; i < npos * D; i += kAccThreads) {
-      const int pp = i / D, c = i - pp * D;
-      if (cnt[pp + 1] > cnt[pp]) {
-        float *dst = gvb + (int64_t)pp * (p.NH * D) + c;
-        if (whole) *dst += accs[i];
-        else unsafeAtomicAdd(dst, accs[i]);
+    if (whole) {
+      for (int i = tid; i < npos * (D / 4); i += kAccThreads) {
+        const int pp = i / (D / 4), c = (i - pp * (D / 4)) * 4;
+        if (cnt[pp + 1] > cnt[pp]) {
+          const float4 v = *reinterpret_cast<const float4 *>(&accs[pp * D + c]);
+          float *dst = gvb + (int64_t)pp * (p.NH * D) + c;
+          float4 o = *reinterpret_cast<const float4 *>(dst);
+          o.x += v.x; o.y += v.y; o.z += v.z; o.w += v.w;
+          *reinterpret_cast<float4 *>(dst) = o;
+        }
+      }
+    } else {
+      for (int i = tid; i < npos * D; i += kAccThreads) {
+        const int pp = i / D, c = i - pp * D;
+        if (cnt[pp + 1] > cnt[pp]) unsafeAtomicAdd(gvb + (int64_t)pp * (p.NH * D) + c, accs[i]);
       }
     }
   }
@@ -1312,6 +1322,34 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+// sum_c a_c * b_c over one 16-byte piece of a row, in fp32: fused multiply-adds for fp32,
+// v_dot2 (two exact 16-bit products and an fp32 accumulator per instruction) for f16 / bf16
+template <typename T, int VEC>
+__device__ __forceinline__ float piece_dot(const Vec<T, VEC> &a, const Vec<T, VEC> &b) {
+  if constexpr (sizeof(T) == 4) {
+    float s = 0.f;
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) s = fmaf((float)a.v[c], (float)b.v[c], s);
+    return s;
+  } else if constexpr (std::is_same<T, f16>::value) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    struct P { h2 v[VEC / 2]; };
+    const P pa = __builtin_bit_cast(P, a), pb = __builtin_bit_cast(P, b);
+    float s = 0.f;
+#pragma unroll
+    for (int c = 0; c < VEC / 2; ++c) s = __builtin_amdgcn_fdot2(pa.v[c], pb.v[c], s, false);
+    return s;
+  } else {
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    struct P { b2 v[VEC / 2]; };
+    const P pa = __builtin_bit_cast(P, a), pb = __builtin_bit_cast(P, b);
+    float s = 0.f;
+#pragma unroll
+    for (int c = 0; c < VEC / 2; ++c) s = __builtin_amdgcn_fdot2_f32_bf16(pa.v[c], pb.v[c], s, false);
+    return s;
+  }
+}
+
 // LDS stores by one lane become visible to loads by other lanes of the same wave once
 // issued (a wave's LDS instructions execute in order); this keeps the compiler from
 // moving memory accesses across the hand-over.
@@ -1354,15 +1392,18 @@ __global__ void __launch_bounds__(kCoWaves * kWave) msda_coord_kernel(const Coor
   const uint32_t lane_b = (uint32_t)(cl * VEC * sizeof(T));
   for (int c0 = 0; c0 < NS; c0 += kWave) {
     const int nsc = upi > 1 ? NS : min(kWave, NS - c0);  // samples per unit in this pass
+    // slot i = ui * stride + k holds sample k of unit slot ui; stride = the samples the
+    // GPU groups of a unit take in `steps` steps (a multiple of GPU, upi * stride <= 64:
+    // upi * nsc <= 64 and G divides 64); slots k >= nsc hold no sample (zero loads)
+    const int steps = (nsc + GPU - 1) / GPU, stride = steps * GPU;
     // sample lanes: unit slot ui, sample s; the level geometry is fixed for the pass
-    const int ui = lane / nsc, s = c0 + lane - ui * nsc;
-    const bool lane_on = ui < upi;
+    const int ui = lane / stride, k = lane - ui * stride, s = c0 + k;
+    const bool lane_on = ui < upi && k < nsc;
     const int l = lane_on ? s / p.NP : 0;
     const int Hl = (int)p.shapes[2 * l], Wl = (int)p.shapes[2 * l + 1];
     const int lbase = (int)p.lsi[l];
     const float Hf = (float)Hl, Wf = (float)Wl;
     const uint32_t dx = (uint32_t)(row * sizeof(T)), dy = (uint32_t)(Wl * row * sizeof(T));
-    const int steps = (nsc + GPU - 1) / GPU;
     // sample index of lane (ui, s) in the pass at q0: si0 + (q0 - q_begin) * NH * NS (32-bit:
     // the launch checks units * NS * 2 < 2^31); lanes past the units read sample 0 of unit 0
     const int uq = lane_on ? ui : 0;
@@ -1389,9 +1430,7 @@ __global__ void __launch_bounds__(kCoWaves * kWave) msda_coord_kernel(const Coor
       const int si = si0 + (q0 - q_begin) * dsi;
       const Vec<T, 2> xy = xy_n;
       const float a = (float)a_n;
-      float top[VEC];
-#pragma unroll
-      for (int c = 0; c < VEC; ++c) top[c] = (float)tv_n.v[c];
+      const Vec<T, VEC> top = tv_n;
       if (q0 + upi < q_end) fetch(q0 + upi);
       uint4 off = make_uint4(kPast, kPast, kPast, kPast);
       float4 par = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1411,34 +1450,27 @@ __global__ void __launch_bounds__(kCoWaves * kWave) msda_coord_kernel(const Coor
       s_off[wave][lane] = off;
       s_par[wave][lane] = par;
       wave_lds_handover();
-      // 2. group lanes, two steps at a time
+      // 2. group lanes, two steps at a time (a step past `steps` reads slot 0 of its unit
+      // again and writes the same result there)
       for (int t = 0; t < steps; t += 2) {
         Vec<T, VEC> cv[2][4];
         float4 pr[2];
         int slot[2];
-        bool ok[2];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          const int sl = (t + j) * GPU + gq;
-          ok[j] = sl < nsc && t + j < steps;
-          slot[j] = ug * nsc + min(sl, nsc - 1);
+          const int tj = t + j < steps ? t + j : 0;
+          slot[j] = ug * stride + tj * GPU + gq;
           const uint4 o = s_off[wave][slot[j]];
           pr[j] = s_par[wave][slot[j]];
-          cv[j][0] = buffer_load_vec<T, VEC>(rv, (ok[j] ? o.x : kPast) + lane_b);
-          cv[j][1] = buffer_load_vec<T, VEC>(rv, (ok[j] ? o.y : kPast) + lane_b);
-          cv[j][2] = buffer_load_vec<T, VEC>(rv, (ok[j] ? o.z : kPast) + lane_b);
-          cv[j][3] = buffer_load_vec<T, VEC>(rv, (ok[j] ? o.w : kPast) + lane_b);
+          cv[j][0] = buffer_load_vec<T, VEC>(rv, o.x + lane_b);
+          cv[j][1] = buffer_load_vec<T, VEC>(rv, o.y + lane_b);
+          cv[j][2] = buffer_load_vec<T, VEC>(rv, o.z + lane_b);
+          cv[j][3] = buffer_load_vec<T, VEC>(rv, o.w + lane_b);
         }
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          float s1 = 0.f, s2 = 0.f, s3 = 0.f, s4 = 0.f;
-#pragma unroll
-          for (int c = 0; c < VEC; ++c) {
-            s1 += top[c] * (float)cv[j][0].v[c];
-            s2 += top[c] * (float)cv[j][1].v[c];
-            s3 += top[c] * (float)cv[j][2].v[c];
-            s4 += top[c] * (float)cv[j][3].v[c];
-          }
+          const float s1 = piece_dot<T, VEC>(top, cv[j][0]), s2 = piece_dot<T, VEC>(top, cv[j][1]);
+          const float s3 = piece_dot<T, VEC>(top, cv[j][2]), s4 = piece_dot<T, VEC>(top, cv[j][3]);
           const float lh = pr[j].x, lw = pr[j].y, hh = 1.f - lh, hw = 1.f - lw;
           // a sample outside the window has no valid corner: S_k = 0 and all three are 0
           float gh = pr[j].z * (hw * (s3 - s1) + lw * (s4 - s2));
@@ -1447,7 +1479,7 @@ __global__ void __launch_bounds__(kCoWaves * kWave) msda_coord_kernel(const Coor
           gh = group_sum<LPS>(gh);
           gw = group_sum<LPS>(gw);
           ga = group_sum<LPS>(ga);
-          if (ok[j] && cl == LPS - 1) s_res[wave][slot[j]] = make_float4(gw, gh, ga, 0.f);
+          if (cl == LPS - 1) s_res[wave][slot[j]] = make_float4(gw, gh, ga, 0.f);
         }
       }
       wave_lds_handover();
@@ -1535,7 +1567,8 @@ bool sorted_path(const MsdaBwdArgs &a, int dtype, BktLayout &L) {
   // 16-byte corner rows; (x, y) pairs of loc / grad_loc read and written as one access
   if (reinterpret_cast<uintptr_t>(a.f.value) % 16 != 0 ||
       reinterpret_cast<uintptr_t>(a.f.sampling_loc) % (2 * sizeof(T)) != 0 ||
-      reinterpret_cast<uintptr_t>(a.grad_loc) % (2 * sizeof(T)) != 0)
+      reinterpret_cast<uintptr_t>(a.grad_loc) % (2 * sizeof(T)) != 0 ||
+      reinterpret_cast<uintptr_t>(a.grad_value) % 16 != 0)
     return false;
   // grad_output rows through 32-bit buffer offsets
   // (16-byte pieces of grad_output rows: contiguous channels, aligned rows)
