@@ -890,7 +890,7 @@ struct BktParams {
   int *cursor;      // [nbk] next free slot (offsets after the scan)
   int *offset;      // [nbk + 1]
   int *nitems;      // [8] buckets per XCD list
-  int2 *items;      // [8][item_cap] (bucket, first corner of the chunk)
+  int4 *items;      // [8][item_cap] (bucket, first corner, corners, 1 if the bucket is one chunk)
   int2 *pc;         // [capacity] corners: (weight bits, query << kBkShift | position in bucket)
   int64_t go_sb, go_sq, go_sh, go_sc;
   uint32_t go_rows_bytes;  // bytes from row (b, 0, h, 0) past row (b, NQ - 1, h, 31)
@@ -962,60 +962,59 @@ __global__ void __launch_bounds__(kBkThreads) msda_bkt_count_kernel(const BktPar
 }
 
 // Block x (of 8): exclusive scan of the bucket counts (block 0 stores offset and cursor),
-// then the chunks of at most kAccChunk corners of the buckets of XCD x in list x.
+// then the chunks of at most kAccChunk corners of the buckets of XCD x in list x. Thread t
+// owns a contiguous run of buckets: one pass to sum them, one block scan of the run sums,
+// one pass to write.
 __global__ void __launch_bounds__(1024) msda_bkt_scan_kernel(const BktParams p) {
-  __shared__ int wsum[16];
-  __shared__ int carry, carry2;
+  __shared__ int wsum[16], wsum2[16];
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   const int x = blockIdx.x;
-  // block-wide exclusive scans of two values per thread (excl) and the block totals
-  __shared__ int wsum2[16];
-  auto block_scan2 = [&](int v, int v2, int &excl, int &total, int &excl2, int &total2)
-      __attribute__((always_inline)) {
-    int incl = v, incl2 = v2;
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-      const int t = __shfl_up(incl, d, kWave), t2 = __shfl_up(incl2, d, kWave);
-      if (lane >= d) { incl += t; incl2 += t2; }
-    }
-    if (lane == kWave - 1) { wsum[wave] = incl; wsum2[wave] = incl2; }
-    __syncthreads();
-    int before = 0, tot = 0, before2 = 0, tot2 = 0;
-    for (int w = 0; w < 16; ++w) {
-      if (w < wave) { before += wsum[w]; before2 += wsum2[w]; }
-      tot += wsum[w];
-      tot2 += wsum2[w];
-    }
-    excl = incl - v + before;
-    total = tot;
-    excl2 = incl2 - v2 + before2;
-    total2 = tot2;
-    __syncthreads();
+  const int E = (p.nbk + 1023) / 1024;
+  const int k0 = min(tid * E, p.nbk), k1 = min(k0 + E, p.nbk);
+  auto mine = [&](int k) __attribute__((always_inline)) {
+    return ((p.by_bucket ? k : k / p.NBS) & 7) == x;
   };
-  if (tid == 0) { carry = 0; carry2 = 0; }
-  __syncthreads();
-  for (int k0 = 0; k0 < p.nbk; k0 += 1024) {
-    const int k = k0 + tid;
-    const int c = k < p.nbk ? p.count[k] : 0;
-    const bool mine = k < p.nbk && ((p.by_bucket ? k : k / p.NBS) & 7) == x;
-    const int nch = mine ? (c + kAccChunk - 1) / kAccChunk : 0;
-    int excl, total, excl2, total2;
-    block_scan2(c, nch, excl, total, excl2, total2);
-    const int base = carry, base2 = carry2;
-    if (x == 0 && k < p.nbk) {
-      p.offset[k] = base + excl;
-      p.cursor[k] = base + excl;
+  int sum = 0, nch = 0;
+  for (int k = k0; k < k1; k += 4) {
+    int c[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) c[j] = k + j < k1 ? p.count[k + j] : 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      sum += c[j];
+      if (k + j < k1 && mine(k + j)) nch += (c[j] + kAccChunk - 1) / kAccChunk;
     }
-    for (int j = 0; j < nch; ++j)
-      if (base2 + excl2 + j < p.item_cap)
-        p.items[x * p.item_cap + base2 + excl2 + j] = make_int2(k, base + excl + j * kAccChunk);
-    __syncthreads();
-    if (tid == 0) { carry = base + total; carry2 = base2 + total2; }
-    __syncthreads();
+  }
+  int incl = sum, incl2 = nch;
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int t = __shfl_up(incl, d, kWave), t2 = __shfl_up(incl2, d, kWave);
+    if (lane >= d) { incl += t; incl2 += t2; }
+  }
+  if (lane == kWave - 1) { wsum[wave] = incl; wsum2[wave] = incl2; }
+  __syncthreads();
+  int run = incl - sum, run2 = incl2 - nch, total = 0, total2 = 0;
+  for (int w = 0; w < 16; ++w) {
+    if (w < wave) { run += wsum[w]; run2 += wsum2[w]; }
+    total += wsum[w];
+    total2 += wsum2[w];
+  }
+  for (int k = k0; k < k1; ++k) {
+    const int c = p.count[k];
+    if (x == 0) {
+      p.offset[k] = run;
+      p.cursor[k] = run;
+    }
+    if (mine(k))
+      for (int j = 0; j * kAccChunk < c; ++j, ++run2)
+        if (run2 < p.item_cap)
+          p.items[x * p.item_cap + run2] =
+              make_int4(k, run + j * kAccChunk, min(kAccChunk, c - j * kAccChunk), c <= kAccChunk);
+    run += c;
   }
   if (tid == 0) {
-    if (x == 0) p.offset[p.nbk] = carry;
-    p.nitems[x] = min(carry2, p.item_cap);
+    if (x == 0) p.offset[p.nbk] = total;
+    p.nitems[x] = min(total2, p.item_cap);
   }
 }
 
@@ -1111,9 +1110,11 @@ __global__ void __launch_bounds__(kBkThreads) msda_bkt_place_kernel(const BktPar
 // those rows); the chunks of a larger bucket add theirs with atomics.
 template <typename T>
 __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktParams p) {
-  constexpr int D = 32, VEC = 4;
-  constexpr int NGR = kAccThreads / 8;      // 8-lane groups (lane: 4 channels of a row)
-  constexpr int BT = sizeof(T) == 4 ? 4 : 6;  // corners per batch of a group (no spills)
+  // a group of LPC lanes reads one 128-byte (fp32) or 64-byte (16-bit) grad_output row,
+  // 16 bytes per lane
+  constexpr int D = 32, VEC = 16 / (int)sizeof(T), LPC = D / VEC;
+  constexpr int NGR = kAccThreads / LPC;
+  constexpr int BT = 4;                     // corners per batch of a group (no spills)
   __shared__ float accs[kBkPos * D];        // the chunk's sums per position
   __shared__ int cnt[kBkPos + 1];           // counts, then each position's first corner
   __shared__ int cur[kBkPos];
@@ -1122,16 +1123,30 @@ __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktP
   __shared__ int pcut[NGR + 1];             // first position of each group
   __shared__ int wsum[kAccThreads / kWave];
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-  const int cl = tid & 7, gi = tid >> 3;
+  const int cl = tid % LPC, gi = tid / LPC;
   const int xcd = blockIdx.x & 7;
   const int n_items = p.nitems[xcd];
+  const int4 *items = p.items + (int64_t)xcd * p.item_cap;
   const T *gout = static_cast<const T *>(p.grad_out);
+  // the corner records of a chunk, 8 per thread (streamed once: non-temporal loads keep the
+  // grad_output rows in L2)
+  float rw[kAccPerThread];
+  uint32_t rq[kAccPerThread];
+  auto load_records = [&](const int4 &h) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < kAccPerThread; ++j) {
+      const int i = min(tid + j * kAccThreads, h.z - 1);
+      typedef int i2v __attribute__((ext_vector_type(2)));
+      const i2v c = __builtin_nontemporal_load(reinterpret_cast<const i2v *>(p.pc + h.y + i));
+      rw[j] = __builtin_bit_cast(float, c.x);
+      rq[j] = (uint32_t)c.y;
+    }
+  };
   for (int m = blockIdx.x >> 3; m < n_items; m += p.blocks_per_xcd) {
-    const int2 it = p.items[xcd * p.item_cap + m];
-    const int k = it.x, first = it.y;
-    const int bstart = p.offset[k], bend = p.offset[k + 1];
-    const int n = min(kAccChunk, bend - first);
-    const bool whole = bend - bstart <= kAccChunk;  // the bucket is this one chunk
+    const int4 it = items[m];  // (bucket, first corner, corners, whole)
+    load_records(it);
+    const int k = it.x, n = it.z;
+    const bool whole = it.w != 0;  // the bucket is this one chunk
     const int slice = k / p.NBS, kb = k - slice * p.NBS;
     const int b = slice / p.NH, h = slice - b * p.NH;
     // grad_output rows of (b, ., h) through a buffer over the batch's rows (32-bit offsets)
@@ -1142,17 +1157,6 @@ __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktP
     __syncthreads();  // the previous chunk's readers are done
     for (int i = tid; i <= kBkPos; i += kAccThreads) cnt[i] = 0;
     __syncthreads();
-    float rw[kAccPerThread];
-    uint32_t rq[kAccPerThread];
-#pragma unroll
-    for (int j = 0; j < kAccPerThread; ++j) {
-      const int i = min(tid + j * kAccThreads, n - 1);
-      // streamed once: a non-temporal load keeps the grad_output rows in the L2
-      typedef int i2v __attribute__((ext_vector_type(2)));
-      const i2v c = __builtin_nontemporal_load(reinterpret_cast<const i2v *>(p.pc + first + i));
-      rw[j] = __builtin_bit_cast(float, c.x);
-      rq[j] = (uint32_t)c.y;
-    }
 #pragma unroll
     for (int j = 0; j < kAccPerThread; ++j)
       if (tid + j * kAccThreads < n) atomicAdd(&cnt[rq[j] & (kBkPos - 1)], 1);
@@ -1205,7 +1209,9 @@ __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktP
       // summed
       const int k0 = cnt[p0], k1 = cnt[p1];
       int pos = p0, next = cnt[p0 + 1];
-      float acc[VEC] = {0.f, 0.f, 0.f, 0.f};
+      float acc[VEC];
+#pragma unroll
+      for (int c = 0; c < VEC; ++c) acc[c] = 0.f;
       float wa[BT], wb[BT];
       Vec<T, VEC> va[BT], vb[BT];
       auto fetch = [&](int kk0, float (&w)[BT], Vec<T, VEC> (&v)[BT]) __attribute__((always_inline)) {
@@ -1222,7 +1228,10 @@ __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktP
       // each position is flushed once, by the group that owns it: a plain store (the
       // rows of positions without corners are never read)
       auto flush = [&]() __attribute__((always_inline)) {
-        *reinterpret_cast<float4 *>(&accs[pos * D + cl * VEC]) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+#pragma unroll
+        for (int c = 0; c < VEC; c += 4)
+          *reinterpret_cast<float4 *>(&accs[pos * D + cl * VEC + c]) =
+              make_float4(acc[c], acc[c + 1], acc[c + 2], acc[c + 3]);
 #pragma unroll
         for (int c = 0; c < VEC; ++c) acc[c] = 0.f;
       };
@@ -1254,12 +1263,12 @@ __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktP
       if (kk0 < k1) consume(kk0, wa, va);
       flush();
     }
-    __syncthreads();
     // the chunk's rows (positions past S do not exist; positions without corners skipped):
     // 4 channels per thread for the plain read-modify-write; atomics on consecutive floats
     // across the lanes (the L2 works per line of each atomic instruction)
     float *gvb = p.gv + ((int64_t)b * p.S + (int64_t)kb * kBkPos) * (p.NH * D) + h * D;
     const int npos = min(kBkPos, p.S - kb * kBkPos);
+    __syncthreads();
     if (whole) {
       for (int i = tid; i < npos * (D / 4); i += kAccThreads) {
         const int pp = i / (D / 4), c = (i - pp * (D / 4)) * 4;
@@ -1540,7 +1549,7 @@ BktLayout bkt_layout(int64_t B, int64_t S, int64_t NH, int64_t NL, int64_t NQ, i
   L.off_cursor = o; o += up(nbk * 4);
   L.off_offset = o; o += up((nbk + 1) * 4);
   L.off_nitems = o; o += up(8 * 4);
-  L.off_items = o;  o += up(8 * item_cap * 8);
+  L.off_items = o;  o += up(8 * item_cap * 16);
   L.off_pc = o;     o += up(cap * 8);
   L.bytes = o;
   return L;
@@ -1603,7 +1612,7 @@ hipError_t launch_sorted(const MsdaBwdArgs &a, const BktLayout &L, char *ws, flo
   p.cursor = reinterpret_cast<int *>(ws + L.off_cursor);
   p.offset = reinterpret_cast<int *>(ws + L.off_offset);
   p.nitems = reinterpret_cast<int *>(ws + L.off_nitems);
-  p.items = reinterpret_cast<int2 *>(ws + L.off_items);
+  p.items = reinterpret_cast<int4 *>(ws + L.off_items);
   p.pc = reinterpret_cast<int2 *>(ws + L.off_pc);
   p.go_sb = a.go_stride[0]; p.go_sq = a.go_stride[1];
   p.go_sh = a.go_stride[2]; p.go_sc = a.go_stride[3];
