@@ -897,6 +897,7 @@ struct BktParams {
   int B, NH, NQ, NL, NP, S, NBS, nbk, item_cap, qpb;
   int by_bucket;    // fewer than 8 slices: buckets go to XCD bucket % 8, else slice % 8
   int blocks_per_xcd;
+  int cblk8;        // count / place blocks per XCD
 };
 
 // a / d for 0 <= a < 2^24 and 0 < d: a reciprocal estimate and one correction step
@@ -935,12 +936,24 @@ __device__ __forceinline__ void sample_corners(const BktParams &p, int64_t unit,
   }
 }
 
+// Count / place block -> (slice, chunk of qpb queries). The chunks are numbered slice by
+// slice and XCD x (block index % 8) takes the x-th eighth of them, so the blocks of one XCD
+// work on one or two slices at a time and a bucket's records are written through one L2.
+__device__ __forceinline__ bool bkt_block(const BktParams &p, int &slice, int &qc) {
+  const int qchunks = (p.NQ + p.qpb - 1) / p.qpb;
+  const int r = blockIdx.x >> 3, lb = (int)(blockIdx.x & 7) * p.cblk8 + r;
+  if (r >= p.cblk8 || lb >= p.B * p.NH * qchunks) return false;
+  slice = lb / qchunks;
+  qc = lb - slice * qchunks;
+  return true;
+}
+
 // Block -> (slice, chunk of qpb queries); samples i = (query in chunk, level, point).
 template <typename T>
 __global__ void __launch_bounds__(kBkThreads) msda_bkt_count_kernel(const BktParams p) {
   __shared__ int lcnt[kBkMaxPerSlice];
-  const int qchunks = (p.NQ + p.qpb - 1) / p.qpb;
-  const int slice = blockIdx.x / qchunks, qc = blockIdx.x - slice * qchunks;
+  int slice, qc;
+  if (!bkt_block(p, slice, qc)) return;
   const int b = slice / p.NH, h = slice - b * p.NH;
   const int q0 = qc * p.qpb, nq = min(p.qpb, p.NQ - q0);
   const int NS = p.NL * p.NP;
@@ -1031,8 +1044,8 @@ __global__ void __launch_bounds__(kBkThreads) msda_bkt_place_kernel(const BktPar
   __shared__ uint32_t sq[kPlaceCap];
   __shared__ unsigned short sb[kPlaceCap];
   __shared__ int wsum[kBkThreads / kWave];
-  const int qchunks = (p.NQ + p.qpb - 1) / p.qpb;
-  const int slice = blockIdx.x / qchunks, qc = blockIdx.x - slice * qchunks;
+  int slice, qc;
+  if (!bkt_block(p, slice, qc)) return;
   const int b = slice / p.NH, h = slice - b * p.NH;
   const int q0 = qc * p.qpb, nq = min(p.qpb, p.NQ - q0);
   const int NS = p.NL * p.NP;
@@ -1626,7 +1639,8 @@ hipError_t launch_sorted(const MsdaBwdArgs &a, const BktLayout &L, char *ws, flo
   p.blocks_per_xcd = blocks / 8;
   p.qpb = kPlaceCap / (4 * a.f.num_levels * a.f.num_point);
   const int qchunks = (a.f.num_query + p.qpb - 1) / p.qpb;
-  const unsigned cblocks = (unsigned)((int64_t)a.f.batch * a.f.num_heads * qchunks);
+  p.cblk8 = (int)(((int64_t)a.f.batch * a.f.num_heads * qchunks + 7) / 8);
+  const unsigned cblocks = 8u * (unsigned)p.cblk8;
   hipLaunchKernelGGL(fill_zero_f32, dim3(stream_grid(L.nbk)), dim3(kBlock), 0, stream,
                      reinterpret_cast<float *>(p.count), (int64_t)L.nbk);
   hipError_t e = hipGetLastError();
