@@ -21,10 +21,14 @@
 // fp32 workspace that is cleared here, accumulated, and narrowed into grad_value at the
 // end (binding_musa.mu:456-510 does the same for fp16).
 //
-// D = 32 with fp32 accumulation (every BEVFormer and DETR shape) runs the same mapping in
-// msda_col2im_d32_kernel (32-bit offsets, branch-free corner loads, shorter reduction), and
-// the levels of at most kCoarseBins positions leave its atomics for msda_coarse_gv_kernel,
-// which sums each position's corner adds of 256 queries before one atomic per channel.
+// D = 32 with fp32 accumulation (every BEVFormer and DETR shape) and a workspace of
+// msda_backward_workspace_bytes takes the sorted path (the msda_bkt_* kernels and
+// msda_coord_kernel below): the corner adds are bucketed by position and each bucket is
+// summed by the workgroup that owns its grad_value rows, so no corner takes an atomic.
+// With a smaller workspace, D = 32 runs the per-unit mapping in msda_col2im_d32_kernel
+// (32-bit offsets, branch-free corner loads, shorter reduction), and the levels of at most
+// kCoarseBins positions leave its atomics for msda_coarse_gv_kernel, which sums each
+// position's corner adds of 256 queries before one atomic per channel.
 //
 // One-level maps whose queries are the grid cells (temporal self-attention) take two other
 // kernels below: msda_gv_owner_kernel adds each grad_value row once per position owner,
@@ -857,17 +861,19 @@ __global__ void __launch_bounds__(kBlock) msda_col2im_d32_kernel(
 // slice is summed by one workgroup that owns those grad_value rows:
 //   1. msda_bkt_count_kernel: the valid corners of every sample counted per bucket (LDS
 //      histogram per block, one global add per bucket and block);
-//   2. msda_bkt_scan_kernel: bucket offsets and placement cursors, and the non-empty
-//      buckets listed per XCD (slice % 8, or bucket % 8 with fewer than 8 slices);
+//   2. msda_bkt_scan_kernel: bucket offsets and placement cursors, and the chunks of the
+//      non-empty buckets listed per XCD (slice % 8, or bucket % 8 with fewer than 8
+//      slices) with 16-byte headers;
 //   3. msda_bkt_place_kernel: the corners again, staged in LDS in bucket order, each
 //      bucket's range reserved once per block, then written as contiguous runs of
 //      8-byte (weight, query << kBkShift | position in bucket) records;
 //   4. msda_bkt_acc_kernel: per chunk of at most kAccChunk corners of one bucket, a
-//      counting sort by position in LDS; each 8-lane group takes whole positions (about
-//      1/64 of the chunk's corners), sums weight x grad_output row in registers (4
-//      channels per lane) and adds the sums to an LDS accumulator, which is added to
-//      grad_value at the end: with plain stores when the bucket is one chunk (no other
-//      workgroup writes these rows), else with atomics.
+//      counting sort by position in LDS; each group of 16-byte lanes (8 for fp32, 4 for
+//      16-bit types: one grad_output row) takes whole positions (about 1/64 or 1/128 of
+//      the chunk's corners), sums weight x grad_output row in registers and stores each
+//      position's sum to an LDS accumulator once, which is added to grad_value at the end:
+//      with plain read-modify-writes when the bucket is one chunk (no other workgroup
+//      writes these rows), else with atomics.
 // grad_sampling_loc / grad_attn_weight come from msda_coord_kernel (no atomics).
 // Corner set and weights are those of the reference (ms_deform_attn_kernels.cuh:427-490):
 // the same in-window test and per-corner bounds, weight = bilinear weight x attention.
