@@ -295,18 +295,85 @@ def _valid_corners(loc, shapes):
     return n
 
 
+def _run_workspace(d, go, dtype, ws_bytes):
+    """bevk_msda_backward through the C ABI with a workspace of ws_bytes: below
+    bevk_msda_backward_workspace_bytes (the sorted path's buffers), D = 32 takes the atomic
+    kernels (msda_col2im_d32_kernel + msda_coarse_gv_kernel); fp32 needs no workspace,
+    16-bit types the fp32 grad_value accumulator."""
+    import _bevk as b
+    dd = _dev(d, dtype)
+    value, loc = dd["value"], dd["sampling_loc"]
+    B, S, NH, D = value.shape
+    Lq, L, P = loc.shape[1], loc.shape[3], loc.shape[4]
+    g4 = go.to(dtype).to(DEV).view(B, Lq, NH, D)
+    gv = torch.zeros_like(value)
+    gl = torch.empty_like(loc)
+    ga = torch.empty_like(dd["attn_weight"])
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=DEV)
+    b.call("bevk_msda_backward", b.dtype_code(value), b.ptr(value), b.ptr(dd["spatial_shapes"]),
+           b.ptr(dd["level_start_index"]), b.ptr(loc), b.ptr(dd["attn_weight"]), b.ptr(g4),
+           *g4.stride(), B, S, NH, D, L, Lq, P, 64, 0, b.ptr(gv), b.ptr(gl), b.ptr(ga),
+           b.ptr(ws), ws_bytes, b.stream_of(value))
+    torch.cuda.synchronize()
+    return gv.cpu(), gl.cpu(), ga.cpu()
+
+
+def _accumulator_bytes(d, dtype):
+    return 0 if dtype == torch.float32 else d["value"].numel() * 4
+
+
 @pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
 def test_coarse_levels_overflow(dtype):
-    """Small levels only (all of them "coarse": 96 positions), 8 points per level and D =
-    32: the first workgroup's COARSE_Q queries bring more valid corner pairs than its LDS
-    list holds (COARSE_CAP), so it adds them one by one; the result matches the oracle."""
+    """Atomic kernels (a workspace without the sorted path's buffers). Small levels only
+    (all of them "coarse": 96 positions), 8 points per level and D = 32: the first
+    workgroup's COARSE_Q queries bring more valid corner pairs than its LDS list holds
+    (COARSE_CAP), so it adds them one by one; the result matches the oracle. The sorted
+    path (full workspace) is checked on the same inputs."""
     d = inputs.msda_random(1, [(6, 7), (4, 5), (3, 3), (2, 2)], 300, 2, 32, 8, seed=21,
                            loc_lo=0.05, loc_hi=0.95)
     first = d["sampling_loc"][0, :COARSE_Q, 0]  # the first workgroup: batch 0, head 0
     pairs = _valid_corners(first, d["spatial_shapes"])
     assert pairs > COARSE_CAP, pairs
     go = _grad_output(d, seed=9)
-    _check3(_run(d, go, dtype), _ref(d, go, dtype), dtype, f"coarse overflow {dtype}")
+    ref = _ref(d, go, dtype)
+    _check3(_run_workspace(d, go, dtype, _accumulator_bytes(d, dtype)), ref, dtype,
+            f"coarse overflow, atomic kernels {dtype}")
+    _check3(_run(d, go, dtype), ref, dtype, f"coarse overflow, sorted path {dtype}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
+@pytest.mark.parametrize("cfg", ["msda_detr", "msda_sca"])
+def test_atomic_kernels_reduced(cfg, dtype):
+    """The D = 32 atomic kernels (workspace below the sorted path's size) on the reduced
+    BASELINE configurations, whole."""
+    d = inputs.msda_inputs(cfg, scale_q=0.02, batch=1)
+    go = _grad_output(d)
+    _check3(_run_workspace(d, go, dtype, _accumulator_bytes(d, dtype)), _ref(d, go, dtype),
+            dtype, f"{cfg} atomic kernels {dtype}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
+def test_sorted_concentrated(dtype):
+    """Sorted path with every sample near one point: each slice's corners fall in a few
+    positions of one 256-position bucket per level (24 K corners: six accumulate chunks
+    that add with atomics), and single positions take thousands of corners (one lane group
+    walks them all)."""
+    g = torch.Generator().manual_seed(31)
+    d = inputs.msda_random(1, [(16, 16), (8, 8)], 1500, 2, 32, 4, seed=31)
+    d["sampling_loc"] = 0.5 + 0.02 * torch.randn(d["sampling_loc"].shape, generator=g)
+    go = _grad_output(d, seed=5)
+    _check3(_run(d, go, dtype), _ref(d, go, dtype), dtype, f"concentrated {dtype}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
+def test_sorted_ragged(dtype):
+    """Sorted path with 12 (batch, head) slices (not a multiple of the 8 XCD lists), a
+    spatial size of 790 (the last 256-position bucket partial), 333 queries (not a
+    multiple of a place block's 85) and samples outside the window."""
+    d = inputs.msda_random(3, [(20, 30), (10, 15), (5, 8)], 333, 4, 32, 4, seed=17,
+                           loc_lo=-0.2, loc_hi=1.2)
+    go = _grad_output(d, seed=8)
+    _check3(_run(d, go, dtype), _ref(d, go, dtype), dtype, f"ragged {dtype}")
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["fp32", "fp16"])
