@@ -39,6 +39,7 @@
 
 #include <hip/amd_detail/amd_hip_unsafe_atomics.h>
 
+#include <algorithm>
 #include <type_traits>
 
 namespace bevk {
@@ -903,7 +904,8 @@ struct BktParams {
   int B, NH, NQ, NL, NP, S, NBS, nbk, item_cap, qpb;
   int by_bucket;    // fewer than 8 slices: buckets go to XCD bucket % 8, else slice % 8
   int blocks_per_xcd;
-  int cblk8;        // count / place blocks per XCD
+  int cblk8;        // count / place chunks per XCD
+  int pblk;         // count / place blocks per XCD (persistent)
 };
 
 // a / d for 0 <= a < 2^24 and 0 < d: a reciprocal estimate and one correction step
@@ -913,17 +915,61 @@ __device__ __forceinline__ int fast_div(int a, int d) {
   return q + (r >= d) - (r < 0);
 }
 
-// The four corners of sample (unit, l, pt) of the slice's value map: position (-1 for an
-// invalid corner or a sample outside the window) and weight. Positions outside [0, S)
-// (inconsistent metadata) count as invalid.
+// Count and place work in chunks of qpb queries of one (batch, head) slice (at most
+// kPlaceCap / 4 samples). The chunks are numbered slice by slice and XCD x (block index
+// % 8) takes the x-th eighth of them, so the blocks of one XCD work on one or two slices at
+// a time and a bucket's records are written through one L2. The blocks are persistent:
+// block r of an XCD takes its chunks r, r + pblk, ..., and the next chunk's locations and
+// attention weights are loaded while the current one is processed.
+constexpr int kBkSPT = kPlaceCap / 4 / kBkThreads;  // samples of a chunk per thread
+
 template <typename T>
-__device__ __forceinline__ void sample_corners(const BktParams &p, int64_t unit, int l, int pt,
-                                               int (&pos)[4], float (&wt)[4]) {
+struct ChunkSamples {
+  Vec<T, 2> xy[kBkSPT];
+  T a[kBkSPT];
+};
+
+__device__ __forceinline__ void bkt_chunk(const BktParams &p, int lb, int &slice, int &q0,
+                                          int &nq) {
+  const int qchunks = (p.NQ + p.qpb - 1) / p.qpb;
+  slice = lb / qchunks;
+  q0 = (lb - slice * qchunks) * p.qpb;
+  nq = min(p.qpb, p.NQ - q0);
+}
+
+// This XCD's chunk range [lb0, lb1).
+__device__ __forceinline__ void bkt_range(const BktParams &p, int &lb0, int &lb1) {
+  const int total = p.B * p.NH * ((p.NQ + p.qpb - 1) / p.qpb);
+  lb0 = min((int)(blockIdx.x & 7) * p.cblk8, total);
+  lb1 = min(lb0 + p.cblk8, total);
+}
+
+// Sample i = threadIdx.x + j * kBkThreads of chunk lb (a thread past the chunk's samples
+// reads the last one again).
+template <typename T>
+__device__ __forceinline__ void load_chunk(const BktParams &p, int lb, ChunkSamples<T> &cs) {
+  int slice, q0, nq;
+  bkt_chunk(p, lb, slice, q0, nq);
+  const int b = slice / p.NH, h = slice - b * p.NH, NS = p.NL * p.NP;
   const T *loc = static_cast<const T *>(p.loc);
   const T *attn = static_cast<const T *>(p.attn);
-  const int64_t si = (unit * p.NL + l) * p.NP + pt;
-  const Vec<T, 2> xy = *reinterpret_cast<const Vec<T, 2> *>(loc + si * 2);
-  const float lx = (float)xy.v[0], ly = (float)xy.v[1], a = (float)attn[si];
+#pragma unroll
+  for (int j = 0; j < kBkSPT; ++j) {
+    const int i = min((int)threadIdx.x + j * kBkThreads, nq * NS - 1);
+    const int u = fast_div(i, NS), r = i - u * NS;
+    const int64_t si = (((int64_t)b * p.NQ + q0 + u) * p.NH + h) * NS + r;
+    cs.xy[j] = *reinterpret_cast<const Vec<T, 2> *>(loc + si * 2);
+    cs.a[j] = attn[si];
+  }
+}
+
+// The four corners of a sample of level l at location xy with attention weight a:
+// position (-1 for an invalid corner or a sample outside the window) and weight.
+// Positions outside [0, S) (inconsistent metadata) count as invalid.
+template <typename T>
+__device__ __forceinline__ void sample_corners(const BktParams &p, int l, const Vec<T, 2> &xy,
+                                               T at, int (&pos)[4], float (&wt)[4]) {
+  const float lx = (float)xy.v[0], ly = (float)xy.v[1], a = (float)at;
   const int Hl = (int)p.shapes[2 * l], Wl = (int)p.shapes[2 * l + 1];
   float him, wim;
   sample_coords<float>(lx, ly, Hl, Wl, him, wim);
@@ -942,42 +988,43 @@ __device__ __forceinline__ void sample_corners(const BktParams &p, int64_t unit,
   }
 }
 
-// Count / place block -> (slice, chunk of qpb queries). The chunks are numbered slice by
-// slice and XCD x (block index % 8) takes the x-th eighth of them, so the blocks of one XCD
-// work on one or two slices at a time and a bucket's records are written through one L2.
-__device__ __forceinline__ bool bkt_block(const BktParams &p, int &slice, int &qc) {
-  const int qchunks = (p.NQ + p.qpb - 1) / p.qpb;
-  const int r = blockIdx.x >> 3, lb = (int)(blockIdx.x & 7) * p.cblk8 + r;
-  if (r >= p.cblk8 || lb >= p.B * p.NH * qchunks) return false;
-  slice = lb / qchunks;
-  qc = lb - slice * qchunks;
-  return true;
-}
-
-// Block -> (slice, chunk of qpb queries); samples i = (query in chunk, level, point).
 template <typename T>
 __global__ void __launch_bounds__(kBkThreads) msda_bkt_count_kernel(const BktParams p) {
   __shared__ int lcnt[kBkMaxPerSlice];
-  int slice, qc;
-  if (!bkt_block(p, slice, qc)) return;
-  const int b = slice / p.NH, h = slice - b * p.NH;
-  const int q0 = qc * p.qpb, nq = min(p.qpb, p.NQ - q0);
   const int NS = p.NL * p.NP;
-  for (int k = threadIdx.x; k < p.NBS; k += kBkThreads) lcnt[k] = 0;
-  __syncthreads();
-  for (int i = threadIdx.x; i < nq * NS; i += kBkThreads) {
-    const int u = fast_div(i, NS), r = i - u * NS, l = fast_div(r, p.NP), pt = r - l * p.NP;
-    const int64_t unit = ((int64_t)b * p.NQ + q0 + u) * p.NH + h;
-    int pos[4];
-    float wt[4];
-    sample_corners<T>(p, unit, l, pt, pos, wt);
+  int lb0, lb1;
+  bkt_range(p, lb0, lb1);
+  ChunkSamples<T> cs;
+  int lb = lb0 + (int)(blockIdx.x >> 3);
+  if (lb < lb1) load_chunk<T>(p, lb, cs);
+  for (; lb < lb1; lb += p.pblk) {
+    int slice, q0, nq;
+    bkt_chunk(p, lb, slice, q0, nq);
+    int pos[kBkSPT][4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
-      if (pos[c] >= 0) atomicAdd(&lcnt[pos[c] >> kBkShift], 1);
+    for (int j = 0; j < kBkSPT; ++j) {
+      const int i = threadIdx.x + j * kBkThreads;
+      const int l = fast_div(i - fast_div(i, NS) * NS, p.NP);
+      float wt[4];
+      sample_corners<T>(p, i < nq * NS ? l : 0, cs.xy[j], cs.a[j], pos[j], wt);
+      if (i >= nq * NS) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) pos[j][c] = -1;
+      }
+    }
+    if (lb + p.pblk < lb1) load_chunk<T>(p, lb + p.pblk, cs);  // in flight during this chunk
+    __syncthreads();  // the previous chunk's flush is done
+    for (int k = threadIdx.x; k < p.NBS; k += kBkThreads) lcnt[k] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kBkSPT; ++j)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (pos[j][c] >= 0) atomicAdd(&lcnt[pos[j][c] >> kBkShift], 1);
+    __syncthreads();
+    for (int k = threadIdx.x; k < p.NBS; k += kBkThreads)
+      if (lcnt[k] > 0) atomicAdd(&p.count[slice * p.NBS + k], lcnt[k]);
   }
-  __syncthreads();
-  for (int k = threadIdx.x; k < p.NBS; k += kBkThreads)
-    if (lcnt[k] > 0) atomicAdd(&p.count[slice * p.NBS + k], lcnt[k]);
 }
 
 // Block x (of 8): exclusive scan of the bucket counts (block 0 stores offset and cursor),
@@ -1037,12 +1084,12 @@ __global__ void __launch_bounds__(1024) msda_bkt_scan_kernel(const BktParams p) 
   }
 }
 
-// Same blocks as the count kernel (qpb * L * P * 4 <= kPlaceCap): the corners of the
-// thread's samples (kept in registers), counted per bucket, staged in LDS in bucket order,
-// each bucket's range reserved once, then written as contiguous runs.
+// Same chunks as the count kernel (qpb * L * P * 4 <= kPlaceCap corners): per chunk, the
+// corners of the thread's samples (kept in registers), counted per bucket, staged in LDS in
+// bucket order, each bucket's range reserved once, then written as contiguous runs.
 template <typename T>
 __global__ void __launch_bounds__(kBkThreads) msda_bkt_place_kernel(const BktParams p) {
-  constexpr int SPT = kPlaceCap / 4 / kBkThreads;  // samples per thread
+  constexpr int SPT = kBkSPT;
   __shared__ int lcnt[kBkMaxPerSlice];   // counts, then staging cursors
   __shared__ int lst[kBkMaxPerSlice];    // first staged corner of each bucket
   __shared__ int gbase[kBkMaxPerSlice];  // first global slot of each bucket
@@ -1050,77 +1097,82 @@ __global__ void __launch_bounds__(kBkThreads) msda_bkt_place_kernel(const BktPar
   __shared__ uint32_t sq[kPlaceCap];
   __shared__ unsigned short sb[kPlaceCap];
   __shared__ int wsum[kBkThreads / kWave];
-  int slice, qc;
-  if (!bkt_block(p, slice, qc)) return;
-  const int b = slice / p.NH, h = slice - b * p.NH;
-  const int q0 = qc * p.qpb, nq = min(p.qpb, p.NQ - q0);
   const int NS = p.NL * p.NP;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-  for (int k = tid; k < p.NBS; k += kBkThreads) lcnt[k] = 0;
-  __syncthreads();
-  int rpos[SPT][4];
-  float rwt[SPT][4];
-  uint32_t rq[SPT];
+  int lb0, lb1;
+  bkt_range(p, lb0, lb1);
+  ChunkSamples<T> cs;
+  int lb = lb0 + (int)(blockIdx.x >> 3);
+  if (lb < lb1) load_chunk<T>(p, lb, cs);
+  for (; lb < lb1; lb += p.pblk) {
+    int slice, q0, nq;
+    bkt_chunk(p, lb, slice, q0, nq);
+    int rpos[SPT][4];
+    float rwt[SPT][4];
+    uint32_t rq[SPT];
 #pragma unroll
-  for (int j = 0; j < SPT; ++j) {
-    const int i = tid + j * kBkThreads;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) rpos[j][c] = -1;
-    rq[j] = 0;
-    if (i < nq * NS) {
-      const int u = fast_div(i, NS), r = i - u * NS, l = fast_div(r, p.NP), pt = r - l * p.NP;
-      const int64_t unit = ((int64_t)b * p.NQ + q0 + u) * p.NH + h;
-      sample_corners<T>(p, unit, l, pt, rpos[j], rwt[j]);
+    for (int j = 0; j < SPT; ++j) {
+      const int i = tid + j * kBkThreads;
+      const int u = fast_div(i, NS), l = fast_div(i - u * NS, p.NP);
+      sample_corners<T>(p, i < nq * NS ? l : 0, cs.xy[j], cs.a[j], rpos[j], rwt[j]);
       rq[j] = (uint32_t)(q0 + u) << kBkShift;
-    }
-  }
+      if (i >= nq * NS) {
 #pragma unroll
-  for (int j = 0; j < SPT; ++j)
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-      if (rpos[j][c] >= 0) atomicAdd(&lcnt[rpos[j][c] >> kBkShift], 1);
-  __syncthreads();
-  {  // exclusive scan of the NBS counts: thread tid owns [tid*E, tid*E + E)
-    const int E = (p.NBS + kBkThreads - 1) / kBkThreads;
-    const int e0 = min(tid * E, p.NBS), e1 = min(e0 + E, p.NBS);
-    int local = 0;
-    for (int e = e0; e < e1; ++e) local += lcnt[e];
-    int incl = local;
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-      const int v = __shfl_up(incl, d, kWave);
-      if (lane >= d) incl += v;
-    }
-    if (lane == kWave - 1) wsum[wave] = incl;
-    __syncthreads();
-    int run = incl - local;
-    for (int w2 = 0; w2 < wave; ++w2) run += wsum[w2];
-    for (int e = e0; e < e1; ++e) {
-      const int c = lcnt[e];
-      lst[e] = run;
-      gbase[e] = c > 0 ? atomicAdd(&p.cursor[slice * p.NBS + e], c) : 0;
-      lcnt[e] = run;
-      run += c;
-    }
-  }
-  __syncthreads();
-#pragma unroll
-  for (int j = 0; j < SPT; ++j)
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-      if (rpos[j][c] >= 0) {
-        const int k = rpos[j][c] >> kBkShift;
-        const int slot = atomicAdd(&lcnt[k], 1);
-        sw[slot] = rwt[j][c];
-        sq[slot] = rq[j] | (uint32_t)(rpos[j][c] & (kBkPos - 1));
-        sb[slot] = (unsigned short)k;
+        for (int c = 0; c < 4; ++c) rpos[j][c] = -1;
       }
-  __syncthreads();
-  const int total = lcnt[p.NBS - 1];  // the last bucket's cursor ends at the staged total
-  for (int i = tid; i < total; i += kBkThreads) {
-    const int k = sb[i];
-    const int dst = gbase[k] + (i - lst[k]);
-    p.pc[dst] = make_int2(__builtin_bit_cast(int, sw[i]), (int)sq[i]);
+    }
+    if (lb + p.pblk < lb1) load_chunk<T>(p, lb + p.pblk, cs);  // in flight during this chunk
+    __syncthreads();  // the previous chunk's writers are done with the LDS
+    for (int k = tid; k < p.NBS; k += kBkThreads) lcnt[k] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < SPT; ++j)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (rpos[j][c] >= 0) atomicAdd(&lcnt[rpos[j][c] >> kBkShift], 1);
+    __syncthreads();
+    {  // exclusive scan of the NBS counts: thread tid owns [tid*E, tid*E + E)
+      const int E = (p.NBS + kBkThreads - 1) / kBkThreads;
+      const int e0 = min(tid * E, p.NBS), e1 = min(e0 + E, p.NBS);
+      int local = 0;
+      for (int e = e0; e < e1; ++e) local += lcnt[e];
+      int incl = local;
+#pragma unroll
+      for (int d = 1; d < kWave; d <<= 1) {
+        const int v = __shfl_up(incl, d, kWave);
+        if (lane >= d) incl += v;
+      }
+      if (lane == kWave - 1) wsum[wave] = incl;
+      __syncthreads();
+      int run = incl - local;
+      for (int w2 = 0; w2 < wave; ++w2) run += wsum[w2];
+      for (int e = e0; e < e1; ++e) {
+        const int c = lcnt[e];
+        lst[e] = run;
+        gbase[e] = c > 0 ? atomicAdd(&p.cursor[slice * p.NBS + e], c) : 0;
+        lcnt[e] = run;
+        run += c;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < SPT; ++j)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (rpos[j][c] >= 0) {
+          const int k = rpos[j][c] >> kBkShift;
+          const int slot = atomicAdd(&lcnt[k], 1);
+          sw[slot] = rwt[j][c];
+          sq[slot] = rq[j] | (uint32_t)(rpos[j][c] & (kBkPos - 1));
+          sb[slot] = (unsigned short)k;
+        }
+    __syncthreads();
+    const int total = lcnt[p.NBS - 1];  // the last bucket's cursor ends at the staged total
+    for (int i = tid; i < total; i += kBkThreads) {
+      const int k = sb[i];
+      const int dst = gbase[k] + (i - lst[k]);
+      p.pc[dst] = make_int2(__builtin_bit_cast(int, sw[i]), (int)sq[i]);
+    }
   }
 }
 
@@ -1646,16 +1698,23 @@ hipError_t launch_sorted(const MsdaBwdArgs &a, const BktLayout &L, char *ws, flo
   p.qpb = kPlaceCap / (4 * a.f.num_levels * a.f.num_point);
   const int qchunks = (a.f.num_query + p.qpb - 1) / p.qpb;
   p.cblk8 = (int)(((int64_t)a.f.batch * a.f.num_heads * qchunks + 7) / 8);
-  const unsigned cblocks = 8u * (unsigned)p.cblk8;
+  // persistent count blocks: 8 per CU (4 KB LDS each); place blocks: 3 per CU (52 KB)
+  const int cus8 = device_cus() / 8;
+  const int count_pblk = std::max(1, std::min(p.cblk8, cus8 * 8));
+  const int place_pblk = std::max(1, std::min(p.cblk8, cus8 * 3));
   hipLaunchKernelGGL(fill_zero_f32, dim3(stream_grid(L.nbk)), dim3(kBlock), 0, stream,
                      reinterpret_cast<float *>(p.count), (int64_t)L.nbk);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((msda_bkt_count_kernel<T>), dim3(cblocks), dim3(kBkThreads), 0, stream, p);
+  p.pblk = count_pblk;
+  hipLaunchKernelGGL((msda_bkt_count_kernel<T>), dim3(8u * (unsigned)count_pblk), dim3(kBkThreads), 0,
+                     stream, p);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   hipLaunchKernelGGL(msda_bkt_scan_kernel, dim3(8), dim3(1024), 0, stream, p);
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  hipLaunchKernelGGL((msda_bkt_place_kernel<T>), dim3(cblocks), dim3(kBkThreads), 0, stream, p);
+  p.pblk = place_pblk;
+  hipLaunchKernelGGL((msda_bkt_place_kernel<T>), dim3(8u * (unsigned)place_pblk), dim3(kBkThreads), 0,
+                     stream, p);
   if ((e = hipGetLastError()) != hipSuccess) return e;
   hipLaunchKernelGGL((msda_bkt_acc_kernel<T>), dim3(blocks), dim3(kAccThreads), 0, stream, p);
   if ((e = hipGetLastError()) != hipSuccess) return e;
