@@ -31,9 +31,10 @@
 // position's corner adds of 256 queries before one atomic per channel.
 //
 // One-level maps whose queries are the grid cells (temporal self-attention) take two other
-// kernels below: msda_gv_owner_kernel adds each grad_value row once per position owner,
-// without atomics, and msda_grid_coord_kernel computes grad_sampling_loc /
-// grad_attn_weight and adds the samples far from their query with atomics.
+// kernels below when the sorted path's workspace is not given: msda_gv_owner_kernel adds
+// each grad_value row once per position owner, without atomics, and
+// msda_grid_coord_kernel computes grad_sampling_loc / grad_attn_weight and adds the
+// samples far from their query with atomics.
 #include "bevk_common.h"
 #include "bevk_launch.h"
 
@@ -1879,7 +1880,7 @@ template <typename T>
 hipError_t launch_f32(const MsdaBwdArgs &a, bool generic, hipStream_t stream) {
   float *gv = static_cast<float *>(a.grad_value);
   BktLayout L;
-  if (!generic && !owner_path<T>(a) && sorted_path<T>(a, 0, L))
+  if (!generic && sorted_path<T>(a, 0, L))
     return launch_sorted<T>(a, L, static_cast<char *>(a.workspace), gv, stream);
   if (generic || !owner_path<T>(a)) return launch_t<T, float>(a, gv, generic, stream);
   hipError_t e = launch_owner<T>(a, gv, true, stream);
@@ -1894,7 +1895,7 @@ hipError_t launch_half(const MsdaBwdArgs &a, bool generic, hipStream_t stream) {
   hipError_t e;
   BktLayout L;
   const int dtype = std::is_same<T, f16>::value ? 1 : 2;
-  if (!generic && !owner_path<T>(a) && sorted_path<T>(a, dtype, L)) {
+  if (!generic && sorted_path<T>(a, dtype, L)) {
     hipLaunchKernelGGL(fill_zero_f32, dim3(stream_grid(n)), dim3(kBlock), 0, stream, acc, n);
     e = hipGetLastError();
     if (e != hipSuccess) return e;

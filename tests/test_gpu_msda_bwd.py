@@ -71,6 +71,34 @@ def _check3(got, ref, dtype, what):
         check(x, r, dtype, f"{what} {name}")
 
 
+def _run_workspace(d, go, dtype, ws_bytes, gv_init=0.0):
+    """bevk_msda_backward through the C ABI with a workspace of ws_bytes: below
+    bevk_msda_backward_workspace_bytes (the sorted path's buffers), D = 32 takes the owner
+    kernels for grid queries and the atomic kernels (msda_col2im_d32_kernel +
+    msda_coarse_gv_kernel) otherwise; fp32 needs no workspace, 16-bit types the fp32
+    grad_value accumulator. grad_value starts at gv_init (fp32 adds to it)."""
+    import _bevk as b
+    dd = _dev(d, dtype)
+    value, loc = dd["value"], dd["sampling_loc"]
+    B, S, NH, D = value.shape
+    Lq, L, P = loc.shape[1], loc.shape[3], loc.shape[4]
+    g4 = go.to(dtype).to(DEV).view(B, Lq, NH, D)
+    gv = torch.full_like(value, gv_init)
+    gl = torch.empty_like(loc)
+    ga = torch.empty_like(dd["attn_weight"])
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=DEV)
+    b.call("bevk_msda_backward", b.dtype_code(value), b.ptr(value), b.ptr(dd["spatial_shapes"]),
+           b.ptr(dd["level_start_index"]), b.ptr(loc), b.ptr(dd["attn_weight"]), b.ptr(g4),
+           *g4.stride(), B, S, NH, D, L, Lq, P, 64, 0, b.ptr(gv), b.ptr(gl), b.ptr(ga),
+           b.ptr(ws), ws_bytes, b.stream_of(value))
+    torch.cuda.synchronize()
+    return gv.cpu(), gl.cpu(), ga.cpu()
+
+
+def _accumulator_bytes(d, dtype):
+    return 0 if dtype == torch.float32 else d["value"].numel() * 4
+
+
 @pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
 @pytest.mark.parametrize("cfg", ["msda_detr", "msda_tsa", "msda_sca"])
 def test_configs_reduced(cfg, dtype):
@@ -203,12 +231,17 @@ def _grid_queries(batch, H, W, heads, points, jitter_px, far_frac, seed):
 ])
 @pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
 def test_grid_queries(geom, dtype):
-    """Queries on the grid cells of a one-level map (the temporal self-attention form):
-    grad_value comes from the per-position owner pass plus atomics for the samples far
-    from their query; all three gradients are compared whole with the oracle."""
+    """Queries on the grid cells of a one-level map (the temporal self-attention form),
+    through the sorted path (the API's workspace) and through the owner kernels (a
+    workspace without the sorted path's buffers: grad_value from the per-position owner
+    pass plus atomics for the samples far from their query); all three gradients are
+    compared whole with the oracle."""
     d = _grid_queries(*geom, seed=sum(geom[:5]))
     go = _grad_output(d, seed=5)
-    _check3(_run(d, go, dtype), _ref(d, go, dtype), dtype, f"grid {geom} {dtype}")
+    ref = _ref(d, go, dtype)
+    _check3(_run(d, go, dtype), ref, dtype, f"grid {geom} {dtype} sorted path")
+    _check3(_run_workspace(d, go, dtype, _accumulator_bytes(d, dtype)), ref, dtype,
+            f"grid {geom} {dtype} owner kernels")
 
 
 def _crowded_grid(H, W, heads, cy, cx, seed):
@@ -245,8 +278,9 @@ def _crowded_grid(H, W, heads, cy, cx, seed):
 
 
 def test_grid_queries_accumulate_fp32():
-    """Grid queries take the owner pass; fp32 grad_value is still added to what the caller
-    holds (here 3.0 everywhere), including in a crowded tile."""
+    """Grid queries, fp32: grad_value is added to what the caller holds (here 3.0
+    everywhere), including in a crowded tile, by the sorted path (API) and by the owner
+    kernels (no workspace)."""
     import _modulated_deform_conv_ext as ext
     for d in (_grid_queries(1, 19, 21, 2, 4, 2.0, 0.05, seed=8), _crowded_grid(30, 28, 2, 12, 13, seed=4)[0]):
         go = _grad_output(d, seed=7)
@@ -258,19 +292,25 @@ def test_grid_queries_accumulate_fp32():
                      dd["sampling_loc"], dd["attn_weight"], go.to(DEV), gv, gl, ga)
         torch.cuda.synchronize()
         rv, rl, ra = _ref(d, go, torch.float32)
-        check(gv.cpu(), rv + 3.0, torch.float32, "grid grad_value accumulated")
-        check(gl.cpu(), rl, torch.float32, "grid grad_sampling_loc")
-        check(ga.cpu(), ra, torch.float32, "grid grad_attn_weight")
+        for what, got in (("sorted path", (gv.cpu(), gl.cpu(), ga.cpu())),
+                          ("owner kernels", _run_workspace(d, go, torch.float32, 0, gv_init=3.0))):
+            check(got[0], rv + 3.0, torch.float32, f"grid grad_value accumulated, {what}")
+            check(got[1], rl, torch.float32, f"grid grad_sampling_loc, {what}")
+            check(got[2], ra, torch.float32, f"grid grad_attn_weight, {what}")
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["fp32", "fp16"])
 def test_grid_queries_crowded_tile(dtype):
-    """A tile with more corner pairs than the owner pass keeps in LDS (2560) takes the
-    atomic branch; the result still matches the oracle."""
+    """Owner kernels (a workspace without the sorted path's buffers): a tile with more
+    corner pairs than the owner pass keeps in LDS (2560) takes the atomic branch; the
+    result still matches the oracle. The sorted path is checked on the same inputs."""
     d, pairs = _crowded_grid(30, 28, 2, 12, 13, seed=4)
     assert pairs > 2560, pairs
     go = _grad_output(d, seed=6)
-    _check3(_run(d, go, dtype), _ref(d, go, dtype), dtype, f"crowded {dtype}")
+    ref = _ref(d, go, dtype)
+    _check3(_run_workspace(d, go, dtype, _accumulator_bytes(d, dtype)), ref, dtype,
+            f"crowded {dtype} owner kernels")
+    _check3(_run(d, go, dtype), ref, dtype, f"crowded {dtype} sorted path")
 
 
 # Coarse-level backward constants (msda_bwd.hip): a workgroup takes COARSE_Q queries of
@@ -293,33 +333,6 @@ def _valid_corners(loc, shapes):
             y, x = hl + dy, wl + dx
             n += int((inside & (y >= 0) & (y < Hs) & (x >= 0) & (x < Ws)).sum())
     return n
-
-
-def _run_workspace(d, go, dtype, ws_bytes):
-    """bevk_msda_backward through the C ABI with a workspace of ws_bytes: below
-    bevk_msda_backward_workspace_bytes (the sorted path's buffers), D = 32 takes the atomic
-    kernels (msda_col2im_d32_kernel + msda_coarse_gv_kernel); fp32 needs no workspace,
-    16-bit types the fp32 grad_value accumulator."""
-    import _bevk as b
-    dd = _dev(d, dtype)
-    value, loc = dd["value"], dd["sampling_loc"]
-    B, S, NH, D = value.shape
-    Lq, L, P = loc.shape[1], loc.shape[3], loc.shape[4]
-    g4 = go.to(dtype).to(DEV).view(B, Lq, NH, D)
-    gv = torch.zeros_like(value)
-    gl = torch.empty_like(loc)
-    ga = torch.empty_like(dd["attn_weight"])
-    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=DEV)
-    b.call("bevk_msda_backward", b.dtype_code(value), b.ptr(value), b.ptr(dd["spatial_shapes"]),
-           b.ptr(dd["level_start_index"]), b.ptr(loc), b.ptr(dd["attn_weight"]), b.ptr(g4),
-           *g4.stride(), B, S, NH, D, L, Lq, P, 64, 0, b.ptr(gv), b.ptr(gl), b.ptr(ga),
-           b.ptr(ws), ws_bytes, b.stream_of(value))
-    torch.cuda.synchronize()
-    return gv.cpu(), gl.cpu(), ga.cpu()
-
-
-def _accumulator_bytes(d, dtype):
-    return 0 if dtype == torch.float32 else d["value"].numel() * 4
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
@@ -381,9 +394,10 @@ def test_sorted_ragged(dtype):
 def test_one_level_not_a_grid(case, dtype):
     """One level with num_query == spatial_size whose shapes do not make the queries its
     cells: H*W < S (the positions past H*W are never sampled), or the level starting at
-    position 16. The grid-query owner pass must not take them (both kernels read the
-    device metadata and fall back to atomics for every sample); every gradient matches
-    the oracle and the unsampled positions of grad_value are zero."""
+    position 16. The grid-query owner pass must not take them (both owner kernels read
+    the device metadata and fall back to atomics for every sample); through the owner
+    kernels and the sorted path every gradient matches the oracle and the unsampled
+    positions of grad_value are zero."""
     H, W, S = 9, 11, 120
     lsi0 = 0 if case == "hw_below_s" else 16
     g = torch.Generator().manual_seed(5)
@@ -393,12 +407,13 @@ def test_one_level_not_a_grid(case, dtype):
              sampling_loc=-0.1 + 1.2 * torch.rand(2, S, 2, 1, 4, 2, generator=g),
              attn_weight=torch.softmax(torch.randn(2, S, 2, 4, generator=g), -1).view(2, S, 2, 1, 4))
     go = _grad_output(d, seed=8)
-    got = _run(d, go, dtype)
     ref = _ref(d, go, dtype)
-    _check3(got, ref, dtype, f"one level {case} {dtype}")
     unsampled = torch.ones(S, dtype=torch.bool)
     unsampled[lsi0:lsi0 + H * W] = False
-    assert got[0][:, unsampled].abs().max().item() == 0.0
+    for what, got in (("owner kernels", _run_workspace(d, go, dtype, _accumulator_bytes(d, dtype))),
+                      ("sorted path", _run(d, go, dtype))):
+        _check3(got, ref, dtype, f"one level {case} {dtype} {what}")
+        assert got[0][:, unsampled].abs().max().item() == 0.0, what
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["fp32", "fp16"])
