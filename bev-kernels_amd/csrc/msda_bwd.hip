@@ -888,6 +888,7 @@ constexpr int kPlaceCap = 4096;            // corners a place block stages (2 bl
 constexpr int kAccThreads = 512;
 constexpr int kAccChunk = 4096;            // corners per accumulate item (LDS; 2 blocks per CU)
 constexpr int kAccPerThread = kAccChunk / kAccThreads;
+constexpr int kAccPiece = 4;               // chunks of one bucket a workgroup sums in turn
 constexpr int kAccBatch = 16;              // grad_output rows in flight per half-wave
 
 struct BktParams {
@@ -897,8 +898,8 @@ struct BktParams {
   int *count;       // [nbk] corners per bucket
   int *cursor;      // [nbk] next free slot (offsets after the scan)
   int *offset;      // [nbk + 1]
-  int *nitems;      // [8] buckets per XCD list
-  int4 *items;      // [8][item_cap] (bucket, first corner, corners, 1 if the bucket is one chunk)
+  int *nitems;      // [8] pieces per XCD list, then [8] work-queue counters
+  int4 *items;      // [8][item_cap] (bucket, first corner, corners, 1 if the bucket is one piece)
   int2 *pc;         // [capacity] corners: (weight bits, query << kBkShift | position in bucket)
   int64_t go_sb, go_sq, go_sh, go_sc;
   uint32_t go_rows_bytes;  // bytes from row (b, 0, h, 0) past row (b, NQ - 1, h, 31)
@@ -1029,11 +1030,13 @@ __global__ void __launch_bounds__(kBkThreads) msda_bkt_count_kernel(const BktPar
 }
 
 // Block x (of 8): exclusive scan of the bucket counts (block 0 stores offset and cursor),
-// then the chunks of at most kAccChunk corners of the buckets of XCD x in list x. Thread t
-// owns a contiguous run of buckets: one pass to sum them, one block scan of the run sums,
-// one pass to write.
+// then list x: the buckets of XCD x cut into pieces of at most kAccPiece chunks of
+// kAccChunk corners, pieces of several chunks first (the accumulate workgroups take them
+// from a queue, so the long ones start early). Thread t owns a contiguous run of buckets:
+// one pass to count, one block scan of the run totals, one pass to write.
 __global__ void __launch_bounds__(1024) msda_bkt_scan_kernel(const BktParams p) {
-  __shared__ int wsum[16], wsum2[16];
+  constexpr int kPieceCorners = kAccPiece * kAccChunk;
+  __shared__ int wsum[3][16];
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   const int x = blockIdx.x;
   const int E = (p.nbk + 1023) / 1024;
@@ -1041,47 +1044,76 @@ __global__ void __launch_bounds__(1024) msda_bkt_scan_kernel(const BktParams p) 
   auto mine = [&](int k) __attribute__((always_inline)) {
     return ((p.by_bucket ? k : k / p.NBS) & 7) == x;
   };
-  int sum = 0, nch = 0;
+  // pieces of a bucket of c corners: full pieces, then the rest; "long" = several chunks
+  auto pieces = [&](int c, int &nlong, int &nshort) __attribute__((always_inline)) {
+    const int full = c / kPieceCorners, rest = c - full * kPieceCorners;
+    nlong = full + (rest > kAccChunk);
+    nshort = rest > 0 && rest <= kAccChunk;
+  };
+  int v[3] = {0, 0, 0};  // corners, long pieces, short pieces
   for (int k = k0; k < k1; k += 4) {
     int c[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) c[j] = k + j < k1 ? p.count[k + j] : 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      sum += c[j];
-      if (k + j < k1 && mine(k + j)) nch += (c[j] + kAccChunk - 1) / kAccChunk;
+      v[0] += c[j];
+      if (k + j < k1 && mine(k + j)) {
+        int nl, ns;
+        pieces(c[j], nl, ns);
+        v[1] += nl;
+        v[2] += ns;
+      }
     }
   }
-  int incl = sum, incl2 = nch;
+  int incl[3] = {v[0], v[1], v[2]};
 #pragma unroll
   for (int d = 1; d < kWave; d <<= 1) {
-    const int t = __shfl_up(incl, d, kWave), t2 = __shfl_up(incl2, d, kWave);
-    if (lane >= d) { incl += t; incl2 += t2; }
+#pragma unroll
+    for (int r = 0; r < 3; ++r) {
+      const int t = __shfl_up(incl[r], d, kWave);
+      if (lane >= d) incl[r] += t;
+    }
   }
-  if (lane == kWave - 1) { wsum[wave] = incl; wsum2[wave] = incl2; }
+  if (lane == kWave - 1) {
+#pragma unroll
+    for (int r = 0; r < 3; ++r) wsum[r][wave] = incl[r];
+  }
   __syncthreads();
-  int run = incl - sum, run2 = incl2 - nch, total = 0, total2 = 0;
-  for (int w = 0; w < 16; ++w) {
-    if (w < wave) { run += wsum[w]; run2 += wsum2[w]; }
-    total += wsum[w];
-    total2 += wsum2[w];
+  int run[3], total[3];
+#pragma unroll
+  for (int r = 0; r < 3; ++r) {
+    run[r] = incl[r] - v[r];
+    total[r] = 0;
+    for (int w = 0; w < 16; ++w) {
+      if (w < wave) run[r] += wsum[r][w];
+      total[r] += wsum[r][w];
+    }
   }
+  int rl = run[1], rs = total[1] + run[2];  // list slots of this run's long / short pieces
+  int4 *list = p.items + (int64_t)x * p.item_cap;
+  int off = run[0];
   for (int k = k0; k < k1; ++k) {
     const int c = p.count[k];
     if (x == 0) {
-      p.offset[k] = run;
-      p.cursor[k] = run;
+      p.offset[k] = off;
+      p.cursor[k] = off;
     }
-    if (mine(k))
-      for (int j = 0; j * kAccChunk < c; ++j, ++run2)
-        if (run2 < p.item_cap)
-          p.items[x * p.item_cap + run2] =
-              make_int4(k, run + j * kAccChunk, min(kAccChunk, c - j * kAccChunk), c <= kAccChunk);
-    run += c;
+    if (mine(k)) {
+      const int whole = c <= kPieceCorners;
+      for (int f = 0; f < c; f += kPieceCorners) {
+        const int n = min(kPieceCorners, c - f);
+        int &slot = n > kAccChunk ? rl : rs;
+        if (slot < p.item_cap) list[slot] = make_int4(k, off + f, n, whole);
+        ++slot;
+      }
+    }
+    off += c;
   }
   if (tid == 0) {
-    if (x == 0) p.offset[p.nbk] = total;
-    p.nitems[x] = min(total2, p.item_cap);
+    if (x == 0) p.offset[p.nbk] = total[0];
+    p.nitems[x] = min(total[1] + total[2], p.item_cap);
+    p.nitems[8 + x] = 0;  // the accumulate kernel's queue
   }
 }
 
@@ -1177,9 +1209,11 @@ __global__ void __launch_bounds__(kBkThreads) msda_bkt_place_kernel(const BktPar
   }
 }
 
-// Persistent: block j of XCD x takes chunks j, j + blocks_per_xcd, ... of list x. A bucket
-// of one chunk adds its sums to grad_value with plain stores (no other workgroup writes
-// those rows); the chunks of a larger bucket add theirs with atomics.
+// Persistent: the workgroups of XCD x take the pieces of list x from a queue (one atomic
+// per piece, fetched one piece ahead). A piece is up to kAccPiece chunks of one bucket,
+// summed one after the other into the LDS accumulator; its rows are added to grad_value
+// once: with plain read-modify-writes when the piece is the whole bucket (no other
+// workgroup writes those rows), else with atomics.
 template <typename T>
 __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktParams p) {
   // a group of LPC lanes reads one 128-byte (fp32) or 64-byte (16-bit) grad_output row,
@@ -1187,38 +1221,48 @@ __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktP
   constexpr int D = 32, VEC = 16 / (int)sizeof(T), LPC = D / VEC;
   constexpr int NGR = kAccThreads / LPC;
   constexpr int BT = 4;                     // corners per batch of a group (no spills)
-  __shared__ float accs[kBkPos * D];        // the chunk's sums per position
+  __shared__ float accs[kBkPos * D];        // the piece's sums per position
   __shared__ int cnt[kBkPos + 1];           // counts, then each position's first corner
   __shared__ int cur[kBkPos];
   __shared__ float lw[kAccChunk];
   __shared__ uint32_t lq[kAccChunk];
   __shared__ int pcut[NGR + 1];             // first position of each group
   __shared__ int wsum[kAccThreads / kWave];
+  __shared__ unsigned char touched[kBkPos];  // positions with corners in the piece so far
+  __shared__ int s_next;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   const int cl = tid % LPC, gi = tid / LPC;
   const int xcd = blockIdx.x & 7;
   const int n_items = p.nitems[xcd];
+  int *queue = p.nitems + 8 + xcd;
   const int4 *items = p.items + (int64_t)xcd * p.item_cap;
   const T *gout = static_cast<const T *>(p.grad_out);
   // the corner records of a chunk, 8 per thread (streamed once: non-temporal loads keep the
   // grad_output rows in L2)
   float rw[kAccPerThread];
   uint32_t rq[kAccPerThread];
-  auto load_records = [&](const int4 &h) __attribute__((always_inline)) {
+  auto load_records = [&](int from, int n) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < kAccPerThread; ++j) {
-      const int i = min(tid + j * kAccThreads, h.z - 1);
+      const int i = min(tid + j * kAccThreads, n - 1);
       typedef int i2v __attribute__((ext_vector_type(2)));
-      const i2v c = __builtin_nontemporal_load(reinterpret_cast<const i2v *>(p.pc + h.y + i));
+      const i2v c = __builtin_nontemporal_load(reinterpret_cast<const i2v *>(p.pc + from + i));
       rw[j] = __builtin_bit_cast(float, c.x);
       rq[j] = (uint32_t)c.y;
     }
   };
-  for (int m = blockIdx.x >> 3; m < n_items; m += p.blocks_per_xcd) {
-    const int4 it = items[m];  // (bucket, first corner, corners, whole)
-    load_records(it);
-    const int k = it.x, n = it.z;
-    const bool whole = it.w != 0;  // the bucket is this one chunk
+  if (tid == 0) s_next = atomicAdd(queue, 1);
+  __syncthreads();
+  // the piece index is uniform: kept in a scalar register, so the piece header and every
+  // address and buffer descriptor derived from it are scalar too
+  int m = __builtin_amdgcn_readfirstlane(s_next);
+  while (m < n_items) {
+    const int4 it = items[m];  // (bucket, first corner, corners, whole bucket)
+    __syncthreads();  // s_next is read; the previous piece's readers of the LDS are done
+    if (tid == 0) s_next = atomicAdd(queue, 1);  // the next piece, fetched during this one
+    const int k = it.x, first = it.y, np_ = it.z;
+    const bool whole = it.w != 0;
+    const bool multi = np_ > kAccChunk;  // several chunks: sums added up in LDS
     const int slice = k / p.NBS, kb = k - slice * p.NBS;
     const int b = slice / p.NH, h = slice - b * p.NH;
     // grad_output rows of (b, ., h) through a buffer over the batch's rows (32-bit offsets)
@@ -1226,125 +1270,148 @@ __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktP
     const __amdgpu_buffer_rsrc_t gr = make_rsrc(gob, p.go_rows_bytes);
     const uint32_t go_q_bytes = (uint32_t)(p.go_sq * (int64_t)sizeof(T));
     const uint32_t ch_bytes = (uint32_t)(cl * VEC * sizeof(T));  // channels are contiguous
-    __syncthreads();  // the previous chunk's readers are done
-    for (int i = tid; i <= kBkPos; i += kAccThreads) cnt[i] = 0;
-    __syncthreads();
+    if (multi) {
+      for (int i = tid; i < kBkPos * D / 4; i += kAccThreads)
+        reinterpret_cast<float4 *>(accs)[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int i = tid; i < kBkPos; i += kAccThreads) touched[i] = 0;
+    }
+    for (int c0 = 0; c0 < np_; c0 += kAccChunk) {
+      const int n = min(kAccChunk, np_ - c0);
+      load_records(first + c0, n);
+      if (c0 > 0) __syncthreads();  // the previous chunk's walk and position flags are done
+      for (int i = tid; i <= kBkPos; i += kAccThreads) cnt[i] = 0;
+      __syncthreads();
 #pragma unroll
-    for (int j = 0; j < kAccPerThread; ++j)
-      if (tid + j * kAccThreads < n) atomicAdd(&cnt[rq[j] & (kBkPos - 1)], 1);
-    __syncthreads();
-    {  // exclusive scan of the kBkPos counts, one per thread of waves 0-3
-      int v = 0, incl = 0;
-      if (tid < kBkPos) {
-        v = cnt[tid];
-        incl = v;
+      for (int j = 0; j < kAccPerThread; ++j)
+        if (tid + j * kAccThreads < n) atomicAdd(&cnt[rq[j] & (kBkPos - 1)], 1);
+      __syncthreads();
+      {  // exclusive scan of the kBkPos counts, one per thread of waves 0-3
+        int v = 0, incl = 0;
+        if (tid < kBkPos) {
+          v = cnt[tid];
+          incl = v;
 #pragma unroll
-        for (int d = 1; d < kWave; d <<= 1) {
-          const int t = __shfl_up(incl, d, kWave);
-          if (lane >= d) incl += t;
+          for (int d = 1; d < kWave; d <<= 1) {
+            const int t = __shfl_up(incl, d, kWave);
+            if (lane >= d) incl += t;
+          }
+          if (lane == kWave - 1) wsum[wave] = incl;
         }
-        if (lane == kWave - 1) wsum[wave] = incl;
+        __syncthreads();
+        if (tid < kBkPos) {
+          for (int w2 = 0; w2 < wave; ++w2) incl += wsum[w2];
+          cur[tid] = incl - v;
+        }
       }
       __syncthreads();
-      if (tid < kBkPos) {
-        for (int w2 = 0; w2 < wave; ++w2) incl += wsum[w2];
-        cur[tid] = incl - v;
-      }
-    }
-    __syncthreads();
-    if (tid < kBkPos) cnt[tid] = cur[tid];
-    if (tid == 0) cnt[kBkPos] = n;
-    __syncthreads();
+      if (tid < kBkPos) cnt[tid] = cur[tid];
+      if (tid == 0) cnt[kBkPos] = n;
+      __syncthreads();
 #pragma unroll
-    for (int j = 0; j < kAccPerThread; ++j)
-      if (tid + j * kAccThreads < n) {
-        const int slot = atomicAdd(&cur[rq[j] & (kBkPos - 1)], 1);
-        lw[slot] = rw[j];
-        lq[slot] = rq[j] >> kBkShift;
-      }
-    // group cut points: pcut[g] = first position whose corners start at or after n * g /
-    // NGR (whole positions per group; a chunk holds ~16 corners per position)
-    if (tid <= NGR) {
-      const int target = n * tid / NGR;
-      int lo = 0, hi = kBkPos;  // smallest pos with cnt[pos] >= target (cnt[kBkPos] = n)
-      while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if (cnt[mid] >= target) hi = mid; else lo = mid + 1;
-      }
-      pcut[tid] = tid == NGR ? kBkPos : lo;
-    }
-    __syncthreads();
-    const int p0 = pcut[gi], p1 = pcut[gi + 1];
-    if (p0 < p1) {
-      // corners [k0, k1) of the group's positions, BT at a time (one 4-channel piece of
-      // each corner's grad_output row per lane), the next batch loaded while this one is
-      // summed
-      const int k0 = cnt[p0], k1 = cnt[p1];
-      int pos = p0, next = cnt[p0 + 1];
-      float acc[VEC];
-#pragma unroll
-      for (int c = 0; c < VEC; ++c) acc[c] = 0.f;
-      float wa[BT], wb[BT];
-      Vec<T, VEC> va[BT], vb[BT];
-      auto fetch = [&](int kk0, float (&w)[BT], Vec<T, VEC> (&v)[BT]) __attribute__((always_inline)) {
-        uint32_t qv[BT];
-#pragma unroll
-        for (int u = 0; u < BT; ++u) {
-          const int kk = min(kk0 + u, k1 - 1);
-          w[u] = lw[kk];
-          qv[u] = lq[kk];
+      for (int j = 0; j < kAccPerThread; ++j)
+        if (tid + j * kAccThreads < n) {
+          const int slot = atomicAdd(&cur[rq[j] & (kBkPos - 1)], 1);
+          lw[slot] = rw[j];
+          lq[slot] = rq[j] >> kBkShift;
         }
-#pragma unroll
-        for (int u = 0; u < BT; ++u) v[u] = buffer_load_vec<T, VEC>(gr, qv[u] * go_q_bytes + ch_bytes);
-      };
-      // each position is flushed once, by the group that owns it: a plain store (the
-      // rows of positions without corners are never read)
-      auto flush = [&]() __attribute__((always_inline)) {
-#pragma unroll
-        for (int c = 0; c < VEC; c += 4)
-          *reinterpret_cast<float4 *>(&accs[pos * D + cl * VEC + c]) =
-              make_float4(acc[c], acc[c + 1], acc[c + 2], acc[c + 3]);
+      // group cut points: pcut[g] = first position whose corners start at or after n * g /
+      // NGR (whole positions per group; a chunk holds ~16 corners per position)
+      if (tid <= NGR) {
+        const int target = n * tid / NGR;
+        int lo = 0, hi = kBkPos;  // smallest pos with cnt[pos] >= target (cnt[kBkPos] = n)
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (cnt[mid] >= target) hi = mid; else lo = mid + 1;
+        }
+        pcut[tid] = tid == NGR ? kBkPos : lo;
+      }
+      __syncthreads();
+      const int p0 = pcut[gi], p1 = pcut[gi + 1];
+      if (p0 < p1) {
+        // corners [k0, k1) of the group's positions, BT at a time (one 16-byte piece of
+        // each corner's grad_output row per lane), the next batch loaded while this one is
+        // summed
+        const int k0 = cnt[p0], k1 = cnt[p1];
+        int pos = p0, next = cnt[p0 + 1];
+        float acc[VEC];
 #pragma unroll
         for (int c = 0; c < VEC; ++c) acc[c] = 0.f;
-      };
-      auto consume = [&](int kk0, const float (&w)[BT], const Vec<T, VEC> (&v)[BT]) __attribute__((always_inline)) {
+        float wa[BT], wb[BT];
+        Vec<T, VEC> va[BT], vb[BT];
+        auto fetch = [&](int kk0, float (&w)[BT], Vec<T, VEC> (&v)[BT]) __attribute__((always_inline)) {
+          uint32_t qv[BT];
 #pragma unroll
-        for (int u = 0; u < BT; ++u) {
-          const int kk = kk0 + u;
-          if (kk < k1) {
-            if (kk >= next) {  // corner kk starts a later position of this group
-              flush();
-              do {
-                ++pos;
-                next = cnt[pos + 1];
-              } while (next <= kk);
-            }
-#pragma unroll
-            for (int c = 0; c < VEC; ++c) acc[c] += w[u] * (float)v[u].v[c];
+          for (int u = 0; u < BT; ++u) {
+            const int kk = min(kk0 + u, k1 - 1);
+            w[u] = lw[kk];
+            qv[u] = lq[kk];
           }
+#pragma unroll
+          for (int u = 0; u < BT; ++u) v[u] = buffer_load_vec<T, VEC>(gr, qv[u] * go_q_bytes + ch_bytes);
+        };
+        // each position of the chunk is flushed once, by the group that owns it: a plain
+        // store for a one-chunk piece, an add to the earlier chunks' sums otherwise (rows
+        // of positions without corners are never read)
+        auto flush = [&]() __attribute__((always_inline)) {
+#pragma unroll
+          for (int c = 0; c < VEC; c += 4) {
+            float4 *dst = reinterpret_cast<float4 *>(&accs[pos * D + cl * VEC + c]);
+            float4 v = make_float4(acc[c], acc[c + 1], acc[c + 2], acc[c + 3]);
+            if (multi) {
+              const float4 o = *dst;
+              v.x += o.x; v.y += o.y; v.z += o.z; v.w += o.w;
+            }
+            *dst = v;
+          }
+#pragma unroll
+          for (int c = 0; c < VEC; ++c) acc[c] = 0.f;
+        };
+        auto consume = [&](int kk0, const float (&w)[BT], const Vec<T, VEC> (&v)[BT]) __attribute__((always_inline)) {
+#pragma unroll
+          for (int u = 0; u < BT; ++u) {
+            const int kk = kk0 + u;
+            if (kk < k1) {
+              if (kk >= next) {  // corner kk starts a later position of this group
+                flush();
+                do {
+                  ++pos;
+                  next = cnt[pos + 1];
+                } while (next <= kk);
+              }
+#pragma unroll
+              for (int c = 0; c < VEC; ++c) acc[c] += w[u] * (float)v[u].v[c];
+            }
+          }
+        };
+        fetch(k0, wa, va);
+        int kk0 = k0;
+        for (; kk0 + BT < k1; kk0 += 2 * BT) {
+          fetch(kk0 + BT, wb, vb);
+          consume(kk0, wa, va);
+          if (kk0 + 2 * BT < k1) fetch(kk0 + 2 * BT, wa, va);
+          consume(kk0 + BT, wb, vb);
         }
-      };
-      fetch(k0, wa, va);
-      int kk0 = k0;
-      for (; kk0 + BT < k1; kk0 += 2 * BT) {
-        fetch(kk0 + BT, wb, vb);
-        consume(kk0, wa, va);
-        if (kk0 + 2 * BT < k1) fetch(kk0 + 2 * BT, wa, va);
-        consume(kk0 + BT, wb, vb);
+        if (kk0 < k1) consume(kk0, wa, va);
+        flush();
       }
-      if (kk0 < k1) consume(kk0, wa, va);
-      flush();
+      if (multi) {
+        __syncthreads();  // the chunk's counts are final until the next chunk clears them
+        if (tid < kBkPos && cnt[tid + 1] > cnt[tid]) touched[tid] = 1;
+      }
     }
-    // the chunk's rows (positions past S do not exist; positions without corners skipped):
+    // the piece's rows (positions past S do not exist; positions without corners skipped):
     // 4 channels per thread for the plain read-modify-write; atomics on consecutive floats
     // across the lanes (the L2 works per line of each atomic instruction)
     float *gvb = p.gv + ((int64_t)b * p.S + (int64_t)kb * kBkPos) * (p.NH * D) + h * D;
     const int npos = min(kBkPos, p.S - kb * kBkPos);
     __syncthreads();
+    auto used = [&](int pp) __attribute__((always_inline)) {
+      return multi ? touched[pp] != 0 : cnt[pp + 1] > cnt[pp];
+    };
     if (whole) {
       for (int i = tid; i < npos * (D / 4); i += kAccThreads) {
         const int pp = i / (D / 4), c = (i - pp * (D / 4)) * 4;
-        if (cnt[pp + 1] > cnt[pp]) {
+        if (used(pp)) {
           const float4 v = *reinterpret_cast<const float4 *>(&accs[pp * D + c]);
           float *dst = gvb + (int64_t)pp * (p.NH * D) + c;
           float4 o = *reinterpret_cast<const float4 *>(dst);
@@ -1355,9 +1422,10 @@ __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktP
     } else {
       for (int i = tid; i < npos * D; i += kAccThreads) {
         const int pp = i / D, c = i - pp * D;
-        if (cnt[pp + 1] > cnt[pp]) unsafeAtomicAdd(gvb + (int64_t)pp * (p.NH * D) + c, accs[i]);
+        if (used(pp)) unsafeAtomicAdd(gvb + (int64_t)pp * (p.NH * D) + c, accs[i]);
       }
     }
+    m = __builtin_amdgcn_readfirstlane(s_next);
   }
 }
 
