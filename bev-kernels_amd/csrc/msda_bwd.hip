@@ -888,7 +888,7 @@ constexpr int kPlaceCap = 4096;            // corners a place block stages (2 bl
 constexpr int kAccThreads = 512;
 constexpr int kAccChunk = 4096;            // corners per accumulate item (LDS; 2 blocks per CU)
 constexpr int kAccPerThread = kAccChunk / kAccThreads;
-constexpr int kAccPiece = 4;               // chunks of one bucket a workgroup sums in turn
+constexpr int kAccPiece = 3;               // chunks of one bucket a workgroup sums in turn
 constexpr int kAccBatch = 16;              // grad_output rows in flight per half-wave
 
 struct BktParams {
