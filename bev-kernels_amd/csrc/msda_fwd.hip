@@ -19,9 +19,11 @@
 //     shares it with the sample's lane group through LDS; the plain variant (few
 //     samples, or L/P known only at run time) lets every lane of the group compute it.
 //   * Work order: units are enumerated per (batch, head-group) slice, queries in order,
-//     slices one after the other. All 8 XCDs then work on the same slice at the same
-//     time: each XCD's L2 holds one slice (3.95 MB for fp32 SCA) and a line one XCD
-//     pulls from HBM is a MALL hit for the others.
+//     slices one after the other. The _lds variant lets XCD x take the x-th contiguous
+//     eighth of that order: each XCD works through its own slices (a whole slice at a
+//     time when there are at least 8), so its L2 holds one slice (3.95 MB for fp32 SCA)
+//     and every value line is pulled into one L2 only. The plain variant keeps all XCDs
+//     on one slice, each on an eighth of its queries (see xcd_chunk).
 //   * msda_generic_kernel: one thread per output element, any shape and dtype.
 #include "bevk_common.h"
 #include "bevk_launch.h"
@@ -54,15 +56,24 @@ struct WaveParams {
   int heads_per_slice;    // heads sharing one slice (2 when two heads fill a 128 B line)
   int slices_per_batch;   // NH / heads_per_slice
   int blocks_per_slice;   // ceil(NQ * heads_per_slice / units_per_block), a multiple of 8
+                          // (so the grid is a multiple of 8 blocks)
   uint32_t batch_bytes;   // bytes of value per batch (buffer range; < 2^31)
 };
 
-// Block r of a slice (blocks_per_slice a multiple of 8, the slice's first block index a
-// multiple of 8) runs on XCD r % 8; it takes chunk (r % 8) * (bps / 8) + r / 8, so each
-// XCD works through one contiguous eighth of the slice's queries. Where sampling
-// locations follow the queries (temporal self-attention over a BEV grid), the value rows
-// an XCD needs then stay in its own L2 instead of every XCD fetching every row.
+// Two block orders, both running block i on XCD i % 8 (blocks_per_slice and the grid are
+// multiples of 8):
+// * xcd_chunk (msda_wave_kernel): block r of a slice takes chunk (r % 8) * (bps / 8) + r / 8,
+//   so all XCDs work on the same slice, XCD x on one contiguous eighth of its queries.
+//   Where sampling locations follow the queries (temporal self-attention over a BEV
+//   grid), the value rows an XCD needs stay in its own L2 instead of every XCD fetching
+//   every row.
+// * xcd_block (msda_wave_lds_kernel): block i takes logical block (i % 8) * (grid / 8) +
+//   i / 8 of the slice-major order, so each XCD works through its own slices and every
+//   value line of a slice is pulled into one L2 only (random locations: fp32 SCA).
 __device__ __forceinline__ int xcd_chunk(int r, int bps) { return (r & 7) * (bps >> 3) + (r >> 3); }
+__device__ __forceinline__ int xcd_block() {
+  return (int)(blockIdx.x & 7) * (int)(gridDim.x >> 3) + (int)(blockIdx.x >> 3);
+}
 
 // NL/NP > 0: compile-time level/point counts; 0: read from params.
 template <typename T, int D, int VEC, int NL, int NP, int UPW>
@@ -247,8 +258,9 @@ __global__ void __launch_bounds__(kBlock) msda_wave_lds_kernel(const WaveParams 
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const int slice = blockIdx.x / p.blocks_per_slice;
-  const int chunk = xcd_chunk(blockIdx.x - slice * p.blocks_per_slice, p.blocks_per_slice);
+  const int lblk = xcd_block();  // the slice-major order, XCD x taking its x-th eighth
+  const int slice = lblk / p.blocks_per_slice;
+  const int chunk = lblk - slice * p.blocks_per_slice;
   const int b = slice / p.slices_per_batch;
   const int hg = slice - b * p.slices_per_batch;
   const int pos_stride = p.NH * D;
