@@ -437,10 +437,8 @@ __device__ __forceinline__ Vec<T, N> buffer_load_vec_s(__amdgpu_buffer_rsrc_t r,
                                                        uint32_t soff) {
   constexpr int bytes = sizeof(T) * N;
   if constexpr (bytes == 16) {
-    typedef int i4 __attribute__((ext_vector_type(4)));
     return __builtin_bit_cast(Vec<T, N>, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
   } else if constexpr (bytes == 8) {
-    typedef int i2 __attribute__((ext_vector_type(2)));
     return __builtin_bit_cast(Vec<T, N>, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
   } else if constexpr (bytes == 4) {
     return __builtin_bit_cast(Vec<T, N>, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));

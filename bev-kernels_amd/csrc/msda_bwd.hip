@@ -889,7 +889,6 @@ constexpr int kAccThreads = 512;
 constexpr int kAccChunk = 4096;            // corners per accumulate item (LDS; 2 blocks per CU)
 constexpr int kAccPerThread = kAccChunk / kAccThreads;
 constexpr int kAccPiece = 3;               // chunks of one bucket a workgroup sums in turn
-constexpr int kAccBatch = 16;              // grad_output rows in flight per half-wave
 
 struct BktParams {
   const void *loc, *attn, *grad_out;
