@@ -308,9 +308,9 @@ int64_t bevk_msda_backward_workspace_bytes(int dtype, int batch, int spatial_siz
  *   workspace          bevk_msda_backward_workspace_bytes(...) bytes, device memory.
  * im2col_step keeps the reference's contract. force_generic_col2im != 0 runs the
  * per-(batch, query, head) kernel alone, adding every level's grad_value with atomics
- * (the reference's generic col2im, binding_musa.mu:459); otherwise the grid-query owner
- * pass, the sorted grad_value path (D = 32, full workspace) or the D = 32 kernel with the
- * coarse-level sort are used where they apply.
+ * (the reference's generic col2im, binding_musa.mu:459); otherwise the sorted grad_value
+ * path (D = 32, full workspace), then the grid-query owner pass or the D = 32 kernel with
+ * the coarse-level sort (smaller workspaces) are used where they apply.
  * spatial_shapes / level_start_index must describe value (lsi[l] + H_l * W_l <=
  * spatial_size), as in the reference; they are read on the device only.
  * Replaces _msda_opt2_musa.backward (binding_musa.mu:414-543, :550-556).
