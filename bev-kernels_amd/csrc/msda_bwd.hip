@@ -860,22 +860,30 @@ __global__ void __launch_bounds__(kBlock) msda_col2im_d32_kernel(
 // msda_col2im_d32_kernel add one 128-byte row per valid corner (30.7 M rows for the fine
 // levels of SCA), at the L2's atomic line rate. Here the corner adds are bucketed by
 // position instead, and every bucket of kBkPos consecutive positions of a (batch, head)
-// slice is summed by one workgroup that owns those grad_value rows:
-//   1. msda_bkt_count_kernel: the valid corners of every sample counted per bucket (LDS
+// slice is summed by one workgroup that owns those grad_value rows. The unit of the sort
+// is a record: the two corners of one image row of a sample (x0 and x0 + 1, positions p
+// and p + 1) share the sample's grad_output row, so a record carries the first valid
+// position of the pair and two weights, for that position and for the next one (0 when
+// only one corner of the pair is valid); a sample gives at most two records.
+//   1. msda_bkt_count_kernel: the records of every sample counted per bucket (LDS
 //      histogram per block, one global add per bucket and block);
 //   2. msda_bkt_scan_kernel: bucket offsets and placement cursors, and the chunks of the
 //      non-empty buckets listed per XCD (slice % 8, or bucket % 8 with fewer than 8
 //      slices) with 16-byte headers;
-//   3. msda_bkt_place_kernel: the corners again, staged in LDS in bucket order, each
+//   3. msda_bkt_place_kernel: the records again, staged in LDS in bucket order, each
 //      bucket's range reserved once per block, then written as contiguous runs of
-//      8-byte (weight, query << kBkShift | position in bucket) records;
-//   4. msda_bkt_acc_kernel: per chunk of at most kAccChunk corners of one bucket, a
+//      (weight, next weight) pairs and (query << kBkShift | position in bucket) words;
+//   4. msda_bkt_acc_kernel: per chunk of at most kAccChunk records of one bucket, a
 //      counting sort by position in LDS; each group of 16-byte lanes (8 for fp32, 4 for
 //      16-bit types: one grad_output row) takes whole positions (about 1/64 or 1/128 of
-//      the chunk's corners), sums weight x grad_output row in registers and stores each
-//      position's sum to an LDS accumulator once, which is added to grad_value at the end:
-//      with plain read-modify-writes when the bucket is one chunk (no other workgroup
-//      writes these rows), else with atomics.
+//      the chunk's records), sums weight x grad_output row into two register sums
+//      (position, next position) and stores each position's sum to an LDS accumulator
+//      once; the next-position sum of a group's last position is added after a barrier.
+//      The accumulator has one row more than the bucket (the next bucket's first position,
+//      reached by records at the bucket's last position). It is added to grad_value at the
+//      end: with plain read-modify-writes when the bucket is one chunk (no other workgroup
+//      writes these rows), else with atomics; the first row and the extra row, which the
+//      neighbouring buckets also reach, always with atomics.
 // grad_sampling_loc / grad_attn_weight come from msda_coord_kernel (no atomics).
 // Corner set and weights are those of the reference (ms_deform_attn_kernels.cuh:427-490):
 // the same in-window test and per-corner bounds, weight = bilinear weight x attention.
@@ -884,9 +892,10 @@ constexpr int kBkShift = 8;
 constexpr int kBkPos = 1 << kBkShift;      // positions per bucket
 constexpr int kBkMaxPerSlice = 1024;       // buckets per slice (spatial_size <= 256 Ki)
 constexpr int kBkThreads = 256;
-constexpr int kPlaceCap = 4096;            // corners a place block stages (2 blocks per CU)
+constexpr int kChunkSamples = 1024;        // samples per count / place chunk
+constexpr int kChunkRecs = 2 * kChunkSamples;  // records a place block stages
 constexpr int kAccThreads = 512;
-constexpr int kAccChunk = 4096;            // corners per accumulate item (LDS; 2 blocks per CU)
+constexpr int kAccChunk = 2048;            // records per accumulate chunk (LDS; 2 blocks per CU)
 constexpr int kAccPerThread = kAccChunk / kAccThreads;
 constexpr int kAccPiece = 3;               // chunks of one bucket a workgroup sums in turn
 
@@ -894,12 +903,13 @@ struct BktParams {
   const void *loc, *attn, *grad_out;
   const int64_t *shapes, *lsi;
   float *gv;
-  int *count;       // [nbk] corners per bucket
+  int *count;       // [nbk] records per bucket
   int *cursor;      // [nbk] next free slot (offsets after the scan)
   int *offset;      // [nbk + 1]
   int *nitems;      // [8] pieces per XCD list, then [8] work-queue counters
-  int4 *items;      // [8][item_cap] (bucket, first corner, corners, 1 if the bucket is one piece)
-  int2 *pc;         // [capacity] corners: (weight bits, query << kBkShift | position in bucket)
+  int4 *items;      // [8][item_cap] (bucket, first record, records, 1 if the bucket is one piece)
+  float2 *rw;       // [capacity] record weights: (position, next position)
+  uint32_t *rq;     // [capacity] query << kBkShift | position in bucket
   int64_t go_sb, go_sq, go_sh, go_sc;
   uint32_t go_rows_bytes;  // bytes from row (b, 0, h, 0) past row (b, NQ - 1, h, 31)
   int B, NH, NQ, NL, NP, S, NBS, nbk, item_cap, qpb;
@@ -917,12 +927,12 @@ __device__ __forceinline__ int fast_div(int a, int d) {
 }
 
 // Count and place work in chunks of qpb queries of one (batch, head) slice (at most
-// kPlaceCap / 4 samples). The chunks are numbered slice by slice and XCD x (block index
+// kChunkSamples samples). The chunks are numbered slice by slice and XCD x (block index
 // % 8) takes the x-th eighth of them, so the blocks of one XCD work on one or two slices at
 // a time and a bucket's records are written through one L2. The blocks are persistent:
 // block r of an XCD takes its chunks r, r + pblk, ..., and the next chunk's locations and
 // attention weights are loaded while the current one is processed.
-constexpr int kBkSPT = kPlaceCap / 4 / kBkThreads;  // samples of a chunk per thread
+constexpr int kBkSPT = kChunkSamples / kBkThreads;  // samples of a chunk per thread
 
 template <typename T>
 struct ChunkSamples {
@@ -989,6 +999,25 @@ __device__ __forceinline__ void sample_corners(const BktParams &p, int l, const 
   }
 }
 
+// The two records of a sample (r = 0: corners 0 and 1, image row y0; r = 1: corners 2 and
+// 3, row y0 + 1). Both corners valid: position of the left one, weights (left, right);
+// one valid: its position, weights (its weight, 0); none: position -1. The right corner of
+// a row is the position after the left one.
+template <typename T>
+__device__ __forceinline__ void sample_records(const BktParams &p, int l, const Vec<T, 2> &xy,
+                                               T at, int (&rp)[2], float2 (&rw)[2]) {
+  int pos[4];
+  float wt[4];
+  sample_corners<T>(p, l, xy, at, pos, wt);
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int a = pos[2 * r], b = pos[2 * r + 1];
+    rp[r] = a >= 0 ? a : b;
+    rw[r] = a >= 0 ? make_float2(wt[2 * r], b >= 0 ? wt[2 * r + 1] : 0.f)
+                   : make_float2(wt[2 * r + 1], 0.f);
+  }
+}
+
 template <typename T>
 __global__ void __launch_bounds__(kBkThreads) msda_bkt_count_kernel(const BktParams p) {
   __shared__ int lcnt[kBkMaxPerSlice];
@@ -1001,17 +1030,14 @@ __global__ void __launch_bounds__(kBkThreads) msda_bkt_count_kernel(const BktPar
   for (; lb < lb1; lb += p.pblk) {
     int slice, q0, nq;
     bkt_chunk(p, lb, slice, q0, nq);
-    int pos[kBkSPT][4];
+    int pos[kBkSPT][2];
 #pragma unroll
     for (int j = 0; j < kBkSPT; ++j) {
       const int i = threadIdx.x + j * kBkThreads;
       const int l = fast_div(i - fast_div(i, NS) * NS, p.NP);
-      float wt[4];
-      sample_corners<T>(p, i < nq * NS ? l : 0, cs.xy[j], cs.a[j], pos[j], wt);
-      if (i >= nq * NS) {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) pos[j][c] = -1;
-      }
+      float2 wt[2];
+      sample_records<T>(p, i < nq * NS ? l : 0, cs.xy[j], cs.a[j], pos[j], wt);
+      if (i >= nq * NS) pos[j][0] = pos[j][1] = -1;
     }
     if (lb + p.pblk < lb1) load_chunk<T>(p, lb + p.pblk, cs);  // in flight during this chunk
     __syncthreads();  // the previous chunk's flush is done
@@ -1020,8 +1046,8 @@ __global__ void __launch_bounds__(kBkThreads) msda_bkt_count_kernel(const BktPar
 #pragma unroll
     for (int j = 0; j < kBkSPT; ++j)
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
-        if (pos[j][c] >= 0) atomicAdd(&lcnt[pos[j][c] >> kBkShift], 1);
+      for (int r = 0; r < 2; ++r)
+        if (pos[j][r] >= 0) atomicAdd(&lcnt[pos[j][r] >> kBkShift], 1);
     __syncthreads();
     for (int k = threadIdx.x; k < p.NBS; k += kBkThreads)
       if (lcnt[k] > 0) atomicAdd(&p.count[slice * p.NBS + k], lcnt[k]);
@@ -1030,11 +1056,11 @@ __global__ void __launch_bounds__(kBkThreads) msda_bkt_count_kernel(const BktPar
 
 // Block x (of 8): exclusive scan of the bucket counts (block 0 stores offset and cursor),
 // then list x: the buckets of XCD x cut into pieces of at most kAccPiece chunks of
-// kAccChunk corners, pieces of several chunks first (the accumulate workgroups take them
+// kAccChunk records, pieces of several chunks first (the accumulate workgroups take them
 // from a queue, so the long ones start early). Thread t owns a contiguous run of buckets:
 // one pass to count, one block scan of the run totals, one pass to write.
 __global__ void __launch_bounds__(1024) msda_bkt_scan_kernel(const BktParams p) {
-  constexpr int kPieceCorners = kAccPiece * kAccChunk;
+  constexpr int kPieceRecs = kAccPiece * kAccChunk;
   __shared__ int wsum[3][16];
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   const int x = blockIdx.x;
@@ -1043,13 +1069,13 @@ __global__ void __launch_bounds__(1024) msda_bkt_scan_kernel(const BktParams p) 
   auto mine = [&](int k) __attribute__((always_inline)) {
     return ((p.by_bucket ? k : k / p.NBS) & 7) == x;
   };
-  // pieces of a bucket of c corners: full pieces, then the rest; "long" = several chunks
+  // pieces of a bucket of c records: full pieces, then the rest; "long" = several chunks
   auto pieces = [&](int c, int &nlong, int &nshort) __attribute__((always_inline)) {
-    const int full = c / kPieceCorners, rest = c - full * kPieceCorners;
+    const int full = c / kPieceRecs, rest = c - full * kPieceRecs;
     nlong = full + (rest > kAccChunk);
     nshort = rest > 0 && rest <= kAccChunk;
   };
-  int v[3] = {0, 0, 0};  // corners, long pieces, short pieces
+  int v[3] = {0, 0, 0};  // records, long pieces, short pieces
   for (int k = k0; k < k1; k += 4) {
     int c[4];
 #pragma unroll
@@ -1099,9 +1125,9 @@ __global__ void __launch_bounds__(1024) msda_bkt_scan_kernel(const BktParams p) 
       p.cursor[k] = off;
     }
     if (mine(k)) {
-      const int whole = c <= kPieceCorners;
-      for (int f = 0; f < c; f += kPieceCorners) {
-        const int n = min(kPieceCorners, c - f);
+      const int whole = c <= kPieceRecs;
+      for (int f = 0; f < c; f += kPieceRecs) {
+        const int n = min(kPieceRecs, c - f);
         int &slot = n > kAccChunk ? rl : rs;
         if (slot < p.item_cap) list[slot] = make_int4(k, off + f, n, whole);
         ++slot;
@@ -1116,18 +1142,17 @@ __global__ void __launch_bounds__(1024) msda_bkt_scan_kernel(const BktParams p) 
   }
 }
 
-// Same chunks as the count kernel (qpb * L * P * 4 <= kPlaceCap corners): per chunk, the
-// corners of the thread's samples (kept in registers), counted per bucket, staged in LDS in
+// Same chunks as the count kernel (qpb * L * P <= kChunkSamples samples): per chunk, the
+// records of the thread's samples (kept in registers), counted per bucket, staged in LDS in
 // bucket order, each bucket's range reserved once, then written as contiguous runs.
 template <typename T>
 __global__ void __launch_bounds__(kBkThreads) msda_bkt_place_kernel(const BktParams p) {
   constexpr int SPT = kBkSPT;
   __shared__ int lcnt[kBkMaxPerSlice];   // counts, then staging cursors
-  __shared__ int lst[kBkMaxPerSlice];    // first staged corner of each bucket
-  __shared__ int gbase[kBkMaxPerSlice];  // first global slot of each bucket
-  __shared__ float sw[kPlaceCap];
-  __shared__ uint32_t sq[kPlaceCap];
-  __shared__ unsigned short sb[kPlaceCap];
+  __shared__ int gofs[kBkMaxPerSlice];   // global slot - staged index of each bucket's records
+  __shared__ float2 sw[kChunkRecs];
+  __shared__ uint32_t sq[kChunkRecs];
+  __shared__ unsigned short sb[kChunkRecs];
   __shared__ int wsum[kBkThreads / kWave];
   const int NS = p.NL * p.NP;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
@@ -1139,19 +1164,16 @@ __global__ void __launch_bounds__(kBkThreads) msda_bkt_place_kernel(const BktPar
   for (; lb < lb1; lb += p.pblk) {
     int slice, q0, nq;
     bkt_chunk(p, lb, slice, q0, nq);
-    int rpos[SPT][4];
-    float rwt[SPT][4];
+    int rpos[SPT][2];
+    float2 rwt[SPT][2];
     uint32_t rq[SPT];
 #pragma unroll
     for (int j = 0; j < SPT; ++j) {
       const int i = tid + j * kBkThreads;
       const int u = fast_div(i, NS), l = fast_div(i - u * NS, p.NP);
-      sample_corners<T>(p, i < nq * NS ? l : 0, cs.xy[j], cs.a[j], rpos[j], rwt[j]);
+      sample_records<T>(p, i < nq * NS ? l : 0, cs.xy[j], cs.a[j], rpos[j], rwt[j]);
       rq[j] = (uint32_t)(q0 + u) << kBkShift;
-      if (i >= nq * NS) {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) rpos[j][c] = -1;
-      }
+      if (i >= nq * NS) rpos[j][0] = rpos[j][1] = -1;
     }
     if (lb + p.pblk < lb1) load_chunk<T>(p, lb + p.pblk, cs);  // in flight during this chunk
     __syncthreads();  // the previous chunk's writers are done with the LDS
@@ -1160,8 +1182,8 @@ __global__ void __launch_bounds__(kBkThreads) msda_bkt_place_kernel(const BktPar
 #pragma unroll
     for (int j = 0; j < SPT; ++j)
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
-        if (rpos[j][c] >= 0) atomicAdd(&lcnt[rpos[j][c] >> kBkShift], 1);
+      for (int r = 0; r < 2; ++r)
+        if (rpos[j][r] >= 0) atomicAdd(&lcnt[rpos[j][r] >> kBkShift], 1);
     __syncthreads();
     {  // exclusive scan of the NBS counts: thread tid owns [tid*E, tid*E + E)
       const int E = (p.NBS + kBkThreads - 1) / kBkThreads;
@@ -1180,8 +1202,7 @@ __global__ void __launch_bounds__(kBkThreads) msda_bkt_place_kernel(const BktPar
       for (int w2 = 0; w2 < wave; ++w2) run += wsum[w2];
       for (int e = e0; e < e1; ++e) {
         const int c = lcnt[e];
-        lst[e] = run;
-        gbase[e] = c > 0 ? atomicAdd(&p.cursor[slice * p.NBS + e], c) : 0;
+        gofs[e] = (c > 0 ? atomicAdd(&p.cursor[slice * p.NBS + e], c) : 0) - run;
         lcnt[e] = run;
         run += c;
       }
@@ -1190,20 +1211,20 @@ __global__ void __launch_bounds__(kBkThreads) msda_bkt_place_kernel(const BktPar
 #pragma unroll
     for (int j = 0; j < SPT; ++j)
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
-        if (rpos[j][c] >= 0) {
-          const int k = rpos[j][c] >> kBkShift;
+      for (int r = 0; r < 2; ++r)
+        if (rpos[j][r] >= 0) {
+          const int k = rpos[j][r] >> kBkShift;
           const int slot = atomicAdd(&lcnt[k], 1);
-          sw[slot] = rwt[j][c];
-          sq[slot] = rq[j] | (uint32_t)(rpos[j][c] & (kBkPos - 1));
+          sw[slot] = rwt[j][r];
+          sq[slot] = rq[j] | (uint32_t)(rpos[j][r] & (kBkPos - 1));
           sb[slot] = (unsigned short)k;
         }
     __syncthreads();
     const int total = lcnt[p.NBS - 1];  // the last bucket's cursor ends at the staged total
     for (int i = tid; i < total; i += kBkThreads) {
-      const int k = sb[i];
-      const int dst = gbase[k] + (i - lst[k]);
-      p.pc[dst] = make_int2(__builtin_bit_cast(int, sw[i]), (int)sq[i]);
+      const int dst = gofs[sb[i]] + i;
+      p.rw[dst] = sw[i];
+      p.rq[dst] = sq[i];
     }
   }
 }
@@ -1212,22 +1233,24 @@ __global__ void __launch_bounds__(kBkThreads) msda_bkt_place_kernel(const BktPar
 // per piece, fetched one piece ahead). A piece is up to kAccPiece chunks of one bucket,
 // summed one after the other into the LDS accumulator; its rows are added to grad_value
 // once: with plain read-modify-writes when the piece is the whole bucket (no other
-// workgroup writes those rows), else with atomics.
+// workgroup writes those rows), else with atomics. The bucket's first row and the row
+// after the bucket are also reached by the neighbouring buckets' records (and the pieces
+// that sum them), so they always take atomics.
 template <typename T>
 __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktParams p) {
   // a group of LPC lanes reads one 128-byte (fp32) or 64-byte (16-bit) grad_output row,
   // 16 bytes per lane
   constexpr int D = 32, VEC = 16 / (int)sizeof(T), LPC = D / VEC;
   constexpr int NGR = kAccThreads / LPC;
-  constexpr int BT = 4;                     // corners per batch of a group (no spills)
-  __shared__ float accs[kBkPos * D];        // the piece's sums per position
-  __shared__ int cnt[kBkPos + 1];           // counts, then each position's first corner
+  constexpr int BT = VEC == 4 ? 4 : 3;      // records per batch of a group (no spills)
+  __shared__ float accs[(kBkPos + 1) * D];  // the piece's sums per position (+ the next bucket's first)
+  __shared__ int cnt[kBkPos + 1];           // counts, then each position's first record
   __shared__ int cur[kBkPos];
-  __shared__ float lw[kAccChunk];
+  __shared__ float2 lw[kAccChunk];
   __shared__ uint32_t lq[kAccChunk];
   __shared__ int pcut[NGR + 1];             // first position of each group
   __shared__ int wsum[kAccThreads / kWave];
-  __shared__ unsigned char touched[kBkPos];  // positions with corners in the piece so far
+  __shared__ unsigned char touched[kBkPos + 1];  // rows the piece has added to so far
   __shared__ int s_next;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   const int cl = tid % LPC, gi = tid / LPC;
@@ -1236,19 +1259,23 @@ __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktP
   int *queue = p.nitems + 8 + xcd;
   const int4 *items = p.items + (int64_t)xcd * p.item_cap;
   const T *gout = static_cast<const T *>(p.grad_out);
-  // the corner records of a chunk, 8 per thread (streamed once: non-temporal loads keep the
-  // grad_output rows in L2)
-  float rw[kAccPerThread];
+  // the records of a chunk, kAccPerThread per thread (streamed once: non-temporal loads
+  // keep the grad_output rows in L2)
+  float2 rw[kAccPerThread];
   uint32_t rq[kAccPerThread];
   auto load_records = [&](int from, int n) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < kAccPerThread; ++j) {
       const int i = min(tid + j * kAccThreads, n - 1);
-      typedef int i2v __attribute__((ext_vector_type(2)));
-      const i2v c = __builtin_nontemporal_load(reinterpret_cast<const i2v *>(p.pc + from + i));
-      rw[j] = __builtin_bit_cast(float, c.x);
-      rq[j] = (uint32_t)c.y;
+      typedef float f2v __attribute__((ext_vector_type(2)));
+      const f2v w = __builtin_nontemporal_load(reinterpret_cast<const f2v *>(p.rw + from + i));
+      rw[j] = make_float2(w.x, w.y);
+      rq[j] = __builtin_nontemporal_load(p.rq + from + i);
     }
+  };
+  // records at position pp of the current chunk (pp <= kBkPos; the extra row has none)
+  auto has = [&](int pp) __attribute__((always_inline)) {
+    return pp < kBkPos && cnt[pp + 1] > cnt[pp];
   };
   if (tid == 0) s_next = atomicAdd(queue, 1);
   __syncthreads();
@@ -1256,7 +1283,7 @@ __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktP
   // address and buffer descriptor derived from it are scalar too
   int m = __builtin_amdgcn_readfirstlane(s_next);
   while (m < n_items) {
-    const int4 it = items[m];  // (bucket, first corner, corners, whole bucket)
+    const int4 it = items[m];  // (bucket, first record, records, whole bucket)
     __syncthreads();  // s_next is read; the previous piece's readers of the LDS are done
     if (tid == 0) s_next = atomicAdd(queue, 1);  // the next piece, fetched during this one
     const int k = it.x, first = it.y, np_ = it.z;
@@ -1270,14 +1297,14 @@ __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktP
     const uint32_t go_q_bytes = (uint32_t)(p.go_sq * (int64_t)sizeof(T));
     const uint32_t ch_bytes = (uint32_t)(cl * VEC * sizeof(T));  // channels are contiguous
     if (multi) {
-      for (int i = tid; i < kBkPos * D / 4; i += kAccThreads)
+      for (int i = tid; i < (kBkPos + 1) * D / 4; i += kAccThreads)
         reinterpret_cast<float4 *>(accs)[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-      for (int i = tid; i < kBkPos; i += kAccThreads) touched[i] = 0;
+      for (int i = tid; i <= kBkPos; i += kAccThreads) touched[i] = 0;
     }
     for (int c0 = 0; c0 < np_; c0 += kAccChunk) {
       const int n = min(kAccChunk, np_ - c0);
       load_records(first + c0, n);
-      if (c0 > 0) __syncthreads();  // the previous chunk's walk and position flags are done
+      if (c0 > 0) __syncthreads();  // the previous chunk's carries and row flags are done
       for (int i = tid; i <= kBkPos; i += kAccThreads) cnt[i] = 0;
       __syncthreads();
 #pragma unroll
@@ -1313,8 +1340,8 @@ __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktP
           lw[slot] = rw[j];
           lq[slot] = rq[j] >> kBkShift;
         }
-      // group cut points: pcut[g] = first position whose corners start at or after n * g /
-      // NGR (whole positions per group; a chunk holds ~16 corners per position)
+      // group cut points: pcut[g] = first position whose records start at or after n * g /
+      // NGR (whole positions per group; a chunk holds ~8 records per position)
       if (tid <= NGR) {
         const int target = n * tid / NGR;
         int lo = 0, hi = kBkPos;  // smallest pos with cnt[pos] >= target (cnt[kBkPos] = n)
@@ -1326,18 +1353,37 @@ __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktP
       }
       __syncthreads();
       const int p0 = pcut[gi], p1 = pcut[gi + 1];
+      // sums of the group's current position and of the position after it
+      float accl[VEC], accr[VEC];
+#pragma unroll
+      for (int c = 0; c < VEC; ++c) accl[c] = accr[c] = 0.f;
+      bool carry = false;  // accr belongs to p1, the next group's first position
+      // each row is written by one group during the walk: a plain store for a one-chunk
+      // piece, an add to the earlier chunks' sums otherwise (rows that no record of the
+      // piece reaches are never read)
+      auto flush = [&](int at, float (&a)[VEC]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int c = 0; c < VEC; c += 4) {
+          float4 *dst = reinterpret_cast<float4 *>(&accs[at * D + cl * VEC + c]);
+          float4 v = make_float4(a[c], a[c + 1], a[c + 2], a[c + 3]);
+          if (multi) {
+            const float4 o = *dst;
+            v.x += o.x; v.y += o.y; v.z += o.z; v.w += o.w;
+          }
+          *dst = v;
+        }
+#pragma unroll
+        for (int c = 0; c < VEC; ++c) a[c] = 0.f;
+      };
       if (p0 < p1) {
-        // corners [k0, k1) of the group's positions, BT at a time (one 16-byte piece of
-        // each corner's grad_output row per lane), the next batch loaded while this one is
+        // records [k0, k1) of the group's positions, BT at a time (one 16-byte piece of
+        // each record's grad_output row per lane), the next batch loaded while this one is
         // summed
         const int k0 = cnt[p0], k1 = cnt[p1];
         int pos = p0, next = cnt[p0 + 1];
-        float acc[VEC];
-#pragma unroll
-        for (int c = 0; c < VEC; ++c) acc[c] = 0.f;
-        float wa[BT], wb[BT];
+        float2 wa[BT], wb[BT];
         Vec<T, VEC> va[BT], vb[BT];
-        auto fetch = [&](int kk0, float (&w)[BT], Vec<T, VEC> (&v)[BT]) __attribute__((always_inline)) {
+        auto fetch = [&](int kk0, float2 (&w)[BT], Vec<T, VEC> (&v)[BT]) __attribute__((always_inline)) {
           uint32_t qv[BT];
 #pragma unroll
           for (int u = 0; u < BT; ++u) {
@@ -1348,37 +1394,35 @@ __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktP
 #pragma unroll
           for (int u = 0; u < BT; ++u) v[u] = buffer_load_vec<T, VEC>(gr, qv[u] * go_q_bytes + ch_bytes);
         };
-        // each position of the chunk is flushed once, by the group that owns it: a plain
-        // store for a one-chunk piece, an add to the earlier chunks' sums otherwise (rows
-        // of positions without corners are never read)
-        auto flush = [&]() __attribute__((always_inline)) {
-#pragma unroll
-          for (int c = 0; c < VEC; c += 4) {
-            float4 *dst = reinterpret_cast<float4 *>(&accs[pos * D + cl * VEC + c]);
-            float4 v = make_float4(acc[c], acc[c + 1], acc[c + 2], acc[c + 3]);
-            if (multi) {
-              const float4 o = *dst;
-              v.x += o.x; v.y += o.y; v.z += o.z; v.w += o.w;
-            }
-            *dst = v;
-          }
-#pragma unroll
-          for (int c = 0; c < VEC; ++c) acc[c] = 0.f;
-        };
-        auto consume = [&](int kk0, const float (&w)[BT], const Vec<T, VEC> (&v)[BT]) __attribute__((always_inline)) {
+        auto consume = [&](int kk0, const float2 (&w)[BT], const Vec<T, VEC> (&v)[BT]) __attribute__((always_inline)) {
 #pragma unroll
           for (int u = 0; u < BT; ++u) {
             const int kk = kk0 + u;
             if (kk < k1) {
-              if (kk >= next) {  // corner kk starts a later position of this group
-                flush();
+              if (kk >= next) {  // record kk starts a later position of this group
+                flush(pos, accl);
+                int np = pos;
                 do {
-                  ++pos;
-                  next = cnt[pos + 1];
+                  ++np;
+                  next = cnt[np + 1];
                 } while (next <= kk);
+                if (np == pos + 1) {
+#pragma unroll
+                  for (int c = 0; c < VEC; ++c) {
+                    accl[c] = accr[c];
+                    accr[c] = 0.f;
+                  }
+                } else {
+                  flush(pos + 1, accr);  // no records there: this group's row
+                }
+                pos = np;
               }
 #pragma unroll
-              for (int c = 0; c < VEC; ++c) acc[c] += w[u] * (float)v[u].v[c];
+              for (int c = 0; c < VEC; ++c) {
+                const float g = (float)v[u].v[c];
+                accl[c] += w[u].x * g;
+                accr[c] += w[u].y * g;
+              }
             }
           }
         };
@@ -1391,21 +1435,35 @@ __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktP
           consume(kk0 + BT, wb, vb);
         }
         if (kk0 < k1) consume(kk0, wa, va);
-        flush();
+        flush(pos, accl);
+        if (pos + 1 < p1) flush(pos + 1, accr);
+        else carry = true;
       }
-      if (multi) {
-        __syncthreads();  // the chunk's counts are final until the next chunk clears them
-        if (tid < kBkPos && cnt[tid + 1] > cnt[tid]) touched[tid] = 1;
+      __syncthreads();  // every row of the walk is written
+      if (carry) {  // p1: stored by its group this chunk if it has records, else not yet
+        const bool keep = multi || has(p1);
+#pragma unroll
+        for (int c = 0; c < VEC; c += 4) {
+          float4 *dst = reinterpret_cast<float4 *>(&accs[p1 * D + cl * VEC + c]);
+          float4 v = make_float4(accr[c], accr[c + 1], accr[c + 2], accr[c + 3]);
+          if (keep) {
+            const float4 o = *dst;
+            v.x += o.x; v.y += o.y; v.z += o.z; v.w += o.w;
+          }
+          *dst = v;
+        }
       }
+      if (multi && tid <= kBkPos && (has(tid) || (tid > 0 && has(tid - 1)))) touched[tid] = 1;
     }
-    // the piece's rows (positions past S do not exist; positions without corners skipped):
-    // 4 channels per thread for the plain read-modify-write; atomics on consecutive floats
-    // across the lanes (the L2 works per line of each atomic instruction)
+    // the piece's rows, the next bucket's first included (positions past S do not exist;
+    // rows no record reached are skipped): 4 channels per thread for the plain
+    // read-modify-write; atomics on consecutive floats across the lanes (the L2 works per
+    // line of each atomic instruction)
     float *gvb = p.gv + ((int64_t)b * p.S + (int64_t)kb * kBkPos) * (p.NH * D) + h * D;
-    const int npos = min(kBkPos, p.S - kb * kBkPos);
+    const int npos = min(kBkPos + 1, p.S - kb * kBkPos);
     __syncthreads();
     auto used = [&](int pp) __attribute__((always_inline)) {
-      return multi ? touched[pp] != 0 : cnt[pp + 1] > cnt[pp];
+      return multi ? touched[pp] != 0 : (has(pp) || (pp > 0 && has(pp - 1)));
     };
     if (whole) {
       for (int i = tid; i < npos * (D / 4); i += kAccThreads) {
@@ -1413,9 +1471,16 @@ __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktP
         if (used(pp)) {
           const float4 v = *reinterpret_cast<const float4 *>(&accs[pp * D + c]);
           float *dst = gvb + (int64_t)pp * (p.NH * D) + c;
-          float4 o = *reinterpret_cast<const float4 *>(dst);
-          o.x += v.x; o.y += v.y; o.z += v.z; o.w += v.w;
-          *reinterpret_cast<float4 *>(dst) = o;
+          if (pp == 0 || pp == kBkPos) {
+            unsafeAtomicAdd(dst, v.x);
+            unsafeAtomicAdd(dst + 1, v.y);
+            unsafeAtomicAdd(dst + 2, v.z);
+            unsafeAtomicAdd(dst + 3, v.w);
+          } else {
+            float4 o = *reinterpret_cast<const float4 *>(dst);
+            o.x += v.x; o.y += v.y; o.z += v.z; o.w += v.w;
+            *reinterpret_cast<float4 *>(dst) = o;
+          }
         }
       }
     } else {
@@ -1666,21 +1731,21 @@ unsigned stream_grid(int64_t n) {
 // Workspace of the sorted grad_value path (bytes, after the 16-bit accumulator).
 struct BktLayout {
   int NBS = 0, nbk = 0, item_cap = 0;
-  int64_t cap = 0;  // corner slots
+  int64_t cap = 0;  // record slots (two per sample)
   int64_t off_count = 0, off_cursor = 0, off_offset = 0, off_nitems = 0, off_items = 0,
-          off_pc = 0, bytes = 0;
+          off_rw = 0, off_rq = 0, bytes = 0;
 };
 
 BktLayout bkt_layout(int64_t B, int64_t S, int64_t NH, int64_t NL, int64_t NQ, int64_t NP) {
   BktLayout L;
   auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
   const int64_t nbs = (S + kBkPos - 1) / kBkPos;
-  const int64_t cap = B * NQ * NH * NL * NP * 4;
+  const int64_t cap = B * NQ * NH * NL * NP * 2;
   const int64_t nbk = B * NH * nbs;
   const int64_t item_cap = (cap + kAccChunk - 1) / kAccChunk + nbk;  // chunks of one list
   if (nbs <= 0 || nbs > kBkMaxPerSlice || cap <= 0 || cap >= ((int64_t)1 << 31) ||
       nbk >= ((int64_t)1 << 26) || item_cap >= ((int64_t)1 << 26) || NQ >= ((int64_t)1 << 22) ||
-      NL * NP * 4 > kPlaceCap)
+      NL * NP > kChunkSamples)
     return L;  // bytes == 0: not applicable
   L.NBS = (int)nbs; L.nbk = (int)nbk; L.item_cap = (int)item_cap; L.cap = cap;
   int64_t o = 0;
@@ -1689,7 +1754,8 @@ BktLayout bkt_layout(int64_t B, int64_t S, int64_t NH, int64_t NL, int64_t NQ, i
   L.off_offset = o; o += up((nbk + 1) * 4);
   L.off_nitems = o; o += up(8 * 4);
   L.off_items = o;  o += up(8 * item_cap * 16);
-  L.off_pc = o;     o += up(cap * 8);
+  L.off_rw = o;     o += up(cap * 8);
+  L.off_rq = o;     o += up(cap * 4);
   L.bytes = o;
   return L;
 }
@@ -1752,7 +1818,8 @@ hipError_t launch_sorted(const MsdaBwdArgs &a, const BktLayout &L, char *ws, flo
   p.offset = reinterpret_cast<int *>(ws + L.off_offset);
   p.nitems = reinterpret_cast<int *>(ws + L.off_nitems);
   p.items = reinterpret_cast<int4 *>(ws + L.off_items);
-  p.pc = reinterpret_cast<int2 *>(ws + L.off_pc);
+  p.rw = reinterpret_cast<float2 *>(ws + L.off_rw);
+  p.rq = reinterpret_cast<uint32_t *>(ws + L.off_rq);
   p.go_sb = a.go_stride[0]; p.go_sq = a.go_stride[1];
   p.go_sh = a.go_stride[2]; p.go_sc = a.go_stride[3];
   p.B = a.f.batch; p.NH = a.f.num_heads; p.NQ = a.f.num_query; p.NL = a.f.num_levels;
@@ -1763,13 +1830,13 @@ hipError_t launch_sorted(const MsdaBwdArgs &a, const BktLayout &L, char *ws, flo
   p.by_bucket = (int64_t)a.f.batch * a.f.num_heads < 8 ? 1 : 0;
   const int blocks = (device_cus() / 8) * 8 * 2;  // two 8-wave workgroups per CU (LDS)
   p.blocks_per_xcd = blocks / 8;
-  p.qpb = kPlaceCap / (4 * a.f.num_levels * a.f.num_point);
+  p.qpb = kChunkSamples / (a.f.num_levels * a.f.num_point);
   const int qchunks = (a.f.num_query + p.qpb - 1) / p.qpb;
   p.cblk8 = (int)(((int64_t)a.f.batch * a.f.num_heads * qchunks + 7) / 8);
-  // persistent count blocks: 8 per CU (4 KB LDS each); place blocks: 3 per CU (52 KB)
+  // persistent count blocks: 8 per CU (4 KB LDS each); place blocks: 4 per CU (36 KB)
   const int cus8 = device_cus() / 8;
   const int count_pblk = std::max(1, std::min(p.cblk8, cus8 * 8));
-  const int place_pblk = std::max(1, std::min(p.cblk8, cus8 * 3));
+  const int place_pblk = std::max(1, std::min(p.cblk8, cus8 * 4));
   hipLaunchKernelGGL(fill_zero_f32, dim3(stream_grid(L.nbk)), dim3(kBlock), 0, stream,
                      reinterpret_cast<float *>(p.count), (int64_t)L.nbk);
   hipError_t e = hipGetLastError();

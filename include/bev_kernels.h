@@ -285,8 +285,9 @@ int bevk_msda_forward(
  * F16/BF16 need at least an fp32 accumulator of batch*spatial_size*num_heads*channels
  * elements (the reference allocates it inside its fp16 backward, binding_musa.mu:456-463;
  * here the caller owns it); F32/F64 need none. With channels == 32 the value returned
- * also holds the buffers of the sorted grad_value path (every valid corner of every
- * sample, 8 bytes each, bucketed by position), which bevk_msda_backward takes whenever
+ * also holds the buffers of the sorted grad_value path (for every sample, up to two
+ * 12-byte records, one per image row of its valid corners, bucketed by position), which
+ * bevk_msda_backward takes whenever
  * the workspace it is given is at least this large; a smaller workspace (at least the
  * accumulator) runs the atomic kernels instead. */
 int64_t bevk_msda_backward_workspace_bytes(int dtype, int batch, int spatial_size,

@@ -389,6 +389,43 @@ def test_sorted_ragged(dtype):
     _check3(_run(d, go, dtype), _ref(d, go, dtype), dtype, f"ragged {dtype}")
 
 
+@pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
+@pytest.mark.parametrize("num_query", [60, 2500], ids=["one_chunk", "pieces"])
+def test_sorted_bucket_edges(num_query, dtype):
+    """Sorted path, records at the edges of the 256-position buckets of a 6 x 100 map
+    (S = 600: buckets 0-255, 256-511 and a partial 512-599). The five points of every
+    query sit (with 0.04 px of jitter) in five cells:
+      A (2.4, 55.3): the top pair at positions 255 / 256 crosses from bucket 0 into 1;
+      B (4.6, 11.7): the bottom pair at 511 / 512 crosses into the partial bucket;
+      C (1.5, -0.4): the left corners outside the map (right-only records at 100, 200);
+      D (0.2, 99.3): the right corners outside (left-only records at 99, 199, next to C's);
+      E (5.5, 30.5): the bottom row outside (one record, in the partial bucket).
+    60 queries: every bucket is one accumulate chunk (read-modify-write, the first and the
+    extra row with atomics); 2,500: buckets of several chunks and pieces (atomics)."""
+    H, W, P = 6, 100, 5
+    cells = torch.tensor([[2.4, 55.3], [4.6, 11.7], [1.5, -0.4], [0.2, 99.3], [5.5, 30.5]],
+                         dtype=torch.float64)
+    g = torch.Generator().manual_seed(41)
+    B, NH = 1, 2
+    him = cells[:, 0] + 0.04 * (2 * torch.rand(B, num_query, NH, 1, P, generator=g) - 1)
+    wim = cells[:, 1] + 0.04 * (2 * torch.rand(B, num_query, NH, 1, P, generator=g) - 1)
+    loc = torch.stack([(wim + 0.5) / W, (him + 0.5) / H], -1).float()
+    # the corner cells the kernels see (h_im = loc * H - 0.5 in fp32)
+    for t in (torch.float32, torch.float16, torch.bfloat16):
+        lt = loc.to(t).float()
+        hh, ww = lt[..., 1] * H - 0.5, lt[..., 0] * W - 0.5
+        assert torch.equal(hh.floor()[0, :, :, 0], cells[:, 0].floor().float().expand(num_query, NH, P))
+        assert torch.equal(ww.floor()[0, :, :, 0], cells[:, 1].floor().float().expand(num_query, NH, P))
+    d = dict(value=torch.randn(B, H * W, NH, 32, generator=g),
+             spatial_shapes=torch.tensor([[H, W]], dtype=torch.int64),
+             level_start_index=torch.tensor([0], dtype=torch.int64),
+             sampling_loc=loc.contiguous(),
+             attn_weight=torch.softmax(torch.randn(B, num_query, NH, P, generator=g), -1)
+             .view(B, num_query, NH, 1, P).contiguous())
+    go = _grad_output(d, seed=12)
+    _check3(_run(d, go, dtype), _ref(d, go, dtype), dtype, f"bucket edges {num_query} {dtype}")
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["fp32", "fp16"])
 @pytest.mark.parametrize("case", ["hw_below_s", "level_offset"])
 def test_one_level_not_a_grid(case, dtype):
