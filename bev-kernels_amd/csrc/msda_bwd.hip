@@ -1338,7 +1338,7 @@ __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktP
         if (tid + j * kAccThreads < n) {
           const int slot = atomicAdd(&cur[rq[j] & (kBkPos - 1)], 1);
           lw[slot] = rw[j];
-          lq[slot] = rq[j] >> kBkShift;
+          lq[slot] = rq[j];
         }
       // group cut points: pcut[g] = first position whose records start at or after n * g /
       // NGR (whole positions per group; a chunk holds ~8 records per position)
@@ -1375,15 +1375,17 @@ __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktP
 #pragma unroll
         for (int c = 0; c < VEC; ++c) a[c] = 0.f;
       };
-      if (p0 < p1) {
+      const int k0 = cnt[p0], k1 = cnt[p1];
+      if (k0 < k1) {
         // records [k0, k1) of the group's positions, BT at a time (one 16-byte piece of
         // each record's grad_output row per lane), the next batch loaded while this one is
-        // summed
-        const int k0 = cnt[p0], k1 = cnt[p1];
-        int pos = p0, next = cnt[p0 + 1];
+        // summed; a position without records gets no row from the walk (its row is written
+        // by the carry of the group before it, or is never read)
+        int pos = (int)(lq[k0] & (kBkPos - 1));
         float2 wa[BT], wb[BT];
         Vec<T, VEC> va[BT], vb[BT];
-        auto fetch = [&](int kk0, float2 (&w)[BT], Vec<T, VEC> (&v)[BT]) __attribute__((always_inline)) {
+        int ra[BT], rb[BT];  // positions of the batch's records
+        auto fetch = [&](int kk0, float2 (&w)[BT], Vec<T, VEC> (&v)[BT], int (&rp)[BT]) __attribute__((always_inline)) {
           uint32_t qv[BT];
 #pragma unroll
           for (int u = 0; u < BT; ++u) {
@@ -1392,20 +1394,19 @@ __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktP
             qv[u] = lq[kk];
           }
 #pragma unroll
-          for (int u = 0; u < BT; ++u) v[u] = buffer_load_vec<T, VEC>(gr, qv[u] * go_q_bytes + ch_bytes);
+          for (int u = 0; u < BT; ++u) {
+            rp[u] = (int)(qv[u] & (kBkPos - 1));
+            v[u] = buffer_load_vec<T, VEC>(gr, (qv[u] >> kBkShift) * go_q_bytes + ch_bytes);
+          }
         };
-        auto consume = [&](int kk0, const float2 (&w)[BT], const Vec<T, VEC> (&v)[BT]) __attribute__((always_inline)) {
+        auto consume = [&](int kk0, const float2 (&w)[BT], const Vec<T, VEC> (&v)[BT], const int (&rp)[BT]) __attribute__((always_inline)) {
 #pragma unroll
           for (int u = 0; u < BT; ++u) {
             const int kk = kk0 + u;
             if (kk < k1) {
-              if (kk >= next) {  // record kk starts a later position of this group
+              if (rp[u] != pos) {  // record kk starts a later position of this group
                 flush(pos, accl);
-                int np = pos;
-                do {
-                  ++np;
-                  next = cnt[np + 1];
-                } while (next <= kk);
+                const int np = rp[u];
                 if (np == pos + 1) {
 #pragma unroll
                   for (int c = 0; c < VEC; ++c) {
@@ -1426,15 +1427,15 @@ __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktP
             }
           }
         };
-        fetch(k0, wa, va);
+        fetch(k0, wa, va, ra);
         int kk0 = k0;
         for (; kk0 + BT < k1; kk0 += 2 * BT) {
-          fetch(kk0 + BT, wb, vb);
-          consume(kk0, wa, va);
-          if (kk0 + 2 * BT < k1) fetch(kk0 + 2 * BT, wa, va);
-          consume(kk0 + BT, wb, vb);
+          fetch(kk0 + BT, wb, vb, rb);
+          consume(kk0, wa, va, ra);
+          if (kk0 + 2 * BT < k1) fetch(kk0 + 2 * BT, wa, va, ra);
+          consume(kk0 + BT, wb, vb, rb);
         }
-        if (kk0 < k1) consume(kk0, wa, va);
+        if (kk0 < k1) consume(kk0, wa, va, ra);
         flush(pos, accl);
         if (pos + 1 < p1) flush(pos + 1, accr);
         else carry = true;
