@@ -1340,16 +1340,31 @@ __global__ void __launch_bounds__(kAccThreads, 4) msda_bkt_acc_kernel(const BktP
           lw[slot] = rw[j];
           lq[slot] = rq[j];
         }
-      // group cut points: pcut[g] = first position whose records start at or after n * g /
-      // NGR (whole positions per group; a chunk holds ~8 records per position)
-      if (tid <= NGR) {
-        const int target = n * tid / NGR;
-        int lo = 0, hi = kBkPos;  // smallest pos with cnt[pos] >= target (cnt[kBkPos] = n)
-        while (lo < hi) {
-          const int mid = (lo + hi) >> 1;
-          if (cnt[mid] >= target) hi = mid; else lo = mid + 1;
+      // group cut points: pcut[g] = the smallest position pp with cnt[pp] >= t_g = n * g / NGR
+      // (whole positions per group; a chunk holds ~8 records per position)
+      if constexpr (VEC == 4) {
+        // fp32: position pp takes the groups with cnt[pp - 1] < t_g <= cnt[pp] (cnt[-1]
+        // read as -1; t_g <= c exactly when g <= ((c + 1) * NGR - 1) / n), no dependent
+        // LDS reads
+        if (tid <= kBkPos) {
+          const int hi = cnt[tid], lo = tid > 0 ? cnt[tid - 1] : -1;
+          const int g0 = fast_div((lo + 1) * NGR + n - 1, n);  // operands < 2^24
+          const int g1 = min(fast_div((hi + 1) * NGR - 1, n), NGR - 1);
+          for (int g = g0; g <= g1; ++g) pcut[g] = tid;
         }
-        pcut[tid] = tid == NGR ? kBkPos : lo;
+        if (tid == 0) pcut[NGR] = kBkPos;
+      } else {
+        // 16-bit types: a binary search per group (the form above measured slower here:
+        // its registers push the 16-bit kernel's allocation into more spills)
+        if (tid <= NGR) {
+          const int target = n * tid / NGR;
+          int lo = 0, hi = kBkPos;  // cnt[kBkPos] = n
+          while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (cnt[mid] >= target) hi = mid; else lo = mid + 1;
+          }
+          pcut[tid] = tid == NGR ? kBkPos : lo;
+        }
       }
       __syncthreads();
       const int p0 = pcut[gi], p1 = pcut[gi + 1];
