@@ -895,9 +895,9 @@ constexpr int kBkThreads = 256;
 constexpr int kChunkSamples = 1024;        // samples per count / place chunk
 constexpr int kChunkRecs = 2 * kChunkSamples;  // records a place block stages
 constexpr int kAccThreads = 512;
-constexpr int kAccChunk = 2048;            // records per accumulate chunk (LDS; 2 blocks per CU)
+constexpr int kAccChunk = 3584;            // records per accumulate chunk (79 KB LDS; 2 blocks per CU)
 constexpr int kAccPerThread = kAccChunk / kAccThreads;
-constexpr int kAccPiece = 3;               // chunks of one bucket a workgroup sums in turn
+constexpr int kAccPiece = 2;               // chunks of one bucket a workgroup sums in turn
 
 struct BktParams {
   const void *loc, *attn, *grad_out;

@@ -157,14 +157,14 @@ def _msda_bwd(dtype=0, step=64, b=2, nq=4, ws=0):
 def _sorted_bytes(b, s, h, nl, nq, np_):
     """Buffers of the sorted grad_value path: bucket counts, cursors and offsets (buckets of
     256 positions per (batch, head) slice), 8 per-XCD lists of 16-byte chunk headers (at
-    most 2048 records each), and for every possible record (one per image row of a
+    most 3584 records each), and for every possible record (one per image row of a
     sample's corners: 2 per sample) an 8-byte weight pair and a 4-byte query / position
     word; each region 256-byte aligned."""
     up = lambda x: -(-x // 256) * 256  # noqa: E731
     nbs = -(-s // 256)
     cap = b * nq * h * nl * np_ * 2
     nbk = b * h * nbs
-    items = -(-cap // 2048) + nbk
+    items = -(-cap // 3584) + nbk
     return (2 * up(nbk * 4) + up((nbk + 1) * 4) + up(32) + up(8 * items * 16) + up(cap * 8)
             + up(cap * 4))
 
