@@ -88,7 +88,7 @@ hipError_t launch_dcn_fused_h(int dtype, const DcnGeom &g, int channels_out, con
 // y[:, :2T], mask sigmoid(y[:, 2T:]), then the deformable implicit GEMM (+ bias, relu).
 // Returns false (and launches nothing) when the shape does not take the persistent
 // kernel; the caller then runs the offset conv and launch_dcn_fused_nhwc (kGeoYF32).
-bool dcn_mega_supported(int dtype, const DcnGeom &g, int channels_out);
+bool dcn_mega_supported(int dtype, const DcnGeom &g, int channels_out, const void *out);
 hipError_t launch_dcn_mega(int dtype, const DcnGeom &g, int channels_out, const void *x,
                            const void *w_off_packed, const float *b_off,
                            const void *w_packed, const void *bias, bool relu, float *y_out,

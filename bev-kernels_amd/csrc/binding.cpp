@@ -555,7 +555,7 @@ int bevk_dcn_mega_fwd_nhwc(int dtype, const void *data_im, const void *w_off_pac
   if (!data_im || !w_off_packed || !y || (channels_out > 0 && (!weight_packed || !out)))
     return fail(BEVK_ERR_INVALID, "%s: null tensor pointer", fn);
   const hipStream_t st = (hipStream_t)stream;
-  if (channels_out > 0 && bevk::dcn_mega_supported(dtype, g, channels_out))
+  if (channels_out > 0 && bevk::dcn_mega_supported(dtype, g, channels_out, out))
     return hip_status(bevk::launch_dcn_mega(dtype, g, channels_out, data_im, w_off_packed, b_off,
                                             weight_packed, bias, act_relu != 0, y, out, st),
                       fn);

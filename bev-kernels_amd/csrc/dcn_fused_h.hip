@@ -451,6 +451,7 @@ constexpr int kPKH = kPBK / 32;                 // 16x16x32 MFMA k-blocks per st
 constexpr int kPThreads = 512;                  // 4 consumer + 4 producer waves
 constexpr int kPProd = 256;                     // producer threads
 constexpr int kPCols = 256;                     // output columns per workgroup
+constexpr int kPStage = kPCols + 8;             // output staging row pitch (elements)
 
 // Workgroup shape for NRB 16-row blocks (at most; a workgroup stores NRB - 1 or NRB).
 template <int NRB>
@@ -494,13 +495,13 @@ __device__ __forceinline__ uint32_t b_frag_offset(int n, int kh, int lane, int n
 }
 
 // Consumer wave c: B(k+2) issued at step k, MFMA(k) from A buffer k % 2, one barrier per
-// step; then the epilogue (bias, relu, one rounding). Always NRB row blocks (compile-time,
-// so the MFMA loop and the accumulators carry no run-time conditions); nrb row blocks are
-// stored.
+// step; then the epilogue (bias, relu, one rounding) into the LDS output tile `stage`,
+// which the whole workgroup stores afterwards as full 16-byte pieces of output rows.
+// Always NRB row blocks (compile-time, so the MFMA loop and the accumulators carry no
+// run-time conditions).
 template <typename T, int NRB>
 __device__ __forceinline__ void dcn_p_consumer(const HParams &p, T (*As)[NRB * 16 * kPLDA],
-                                               int m0, int nrb, int n0, int nk, int lane,
-                                               int wave) {
+                                               T *stage, int n0, int nk, int lane, int wave) {
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, p.w_bytes);
   uint32_t bo[kPKH][4];
 #pragma unroll
@@ -557,21 +558,18 @@ __device__ __forceinline__ void dcn_p_consumer(const HParams &p, T (*As)[NRB * 1
   __builtin_amdgcn_s_setprio(0);
 
   // Epilogue: lane holds column 64 wave + 16 cb + (lane & 15), rows 4 (lane >> 4) + e.
-  T *out = static_cast<T *>(p.out);
   const T *bias = static_cast<const T *>(p.bias);
 #pragma unroll
   for (int cb = 0; cb < 4; ++cb) {
-    const int n = n0 + wave * 64 + cb * 16 + (lane & 15);
-    const float bv = (bias != nullptr && n < p.Cout) ? (float)bias[n] : 0.f;
+    const int c = wave * 64 + cb * 16 + (lane & 15);
+    const float bv = (bias != nullptr && n0 + c < p.Cout) ? (float)bias[n0 + c] : 0.f;
 #pragma unroll
     for (int rbi = 0; rbi < NRB; ++rbi)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int m = m0 + rbi * 16 + 4 * (lane >> 4) + e;
         float v = acc[rbi][cb][e] + bv;
         if (p.relu) v = v < 0.f ? 0.f : v;  // NaN stays NaN, as torch.relu
-        if (rbi < nrb && m < p.M && n < p.Cout)
-          out[(int64_t)m * p.Cout + n] = static_cast<T>(v);
+        stage[(rbi * 16 + 4 * (lane >> 4) + e) * kPStage + c] = static_cast<T>(v);
       }
   }
 }
@@ -743,6 +741,7 @@ __global__ void __launch_bounds__(kPThreads) dcn_fused_p_kernel(const PParams pp
   const HParams &p = pp.h;
   __shared__ __attribute__((aligned(16))) TapGeo geo[kPRows * kMaxTaps];
   __shared__ __attribute__((aligned(16))) T As[2][kPRows * kPLDA];
+  __shared__ __attribute__((aligned(16))) T stage[kPRows * kPStage];  // the output tile
   static_assert(!MEGA || sizeof(As) >= sizeof(float) * kPRows * 3 * kMaxTaps,
                 "the offset-conv output must fit in the A ring");
 
@@ -802,11 +801,22 @@ __global__ void __launch_bounds__(kPThreads) dcn_fused_p_kernel(const PParams pp
   // block (see above) and does not store it; the kernel's time is set by the full ranges.
   // Consumers and producers run the same number of barriers (one per step + prologue).
   if (wave < 4)
-    dcn_p_consumer<T, NRB>(p, As, m0, nrb, n0, nk, lane, wave);
+    dcn_p_consumer<T, NRB>(p, As, stage, n0, nk, lane, wave);
   else if (wave - 4 < SH::kLastWaves)
     dcn_p_producer<T, SH::kSPT, NRB, false>(p, geo, As, nk, tid - kPProd);
   else
     dcn_p_producer<T, SH::kSPT - 1, NRB, false>(p, geo, As, nk, tid - kPProd);
+  // The output tile: full 16-byte pieces of the workgroup's rows (Cout % 8 == 0 and a
+  // 16-byte aligned output, checked on the host: a piece is wholly inside or outside).
+  __syncthreads();
+  T *out = static_cast<T *>(p.out);
+  constexpr int kPieces = kPCols / 8;
+  for (int i = tid; i < nrows * kPieces; i += kPThreads) {
+    const int row = i / kPieces, c = (i - row * kPieces) * 8, m = m0 + row;
+    if (m < p.M && n0 + c < p.Cout)
+      *reinterpret_cast<int4 *>(out + (int64_t)m * p.Cout + n0 + c) =
+          *reinterpret_cast<const int4 *>(&stage[row * kPStage + c]);
+  }
 }
 
 // The persistent kernel runs one workgroup per CU over one 256-column half of Cout and
@@ -818,6 +828,8 @@ struct PConfig {
 PConfig p_config_for(const HParams &p, int geo) {
   PConfig c;
   if (geo == kGeoRegular || p.C % 64 != 0 || p.Cout <= 128 || p.Cout > 2 * kPCols) return c;
+  // the output tile leaves in 16-byte pieces of rows
+  if (p.Cout % 8 != 0 || reinterpret_cast<uintptr_t>(p.out) % 16 != 0) return c;
   const int cus = device_cus();
   const int nb = (cus / 8) * 8;
   const int halves = p.Cout > kPCols ? 2 : 1;
@@ -932,12 +944,12 @@ hipError_t launch_dcn_fused_h(int dtype, const DcnGeom &g, int channels_out, con
   }
 }
 
-bool dcn_mega_supported(int dtype, const DcnGeom &g, int channels_out) {
+bool dcn_mega_supported(int dtype, const DcnGeom &g, int channels_out, const void *out) {
   if ((dtype != 1 && dtype != 2) || g.deformable_group != 1 ||
       g.kernel_h * g.kernel_w > kMaxTaps)
     return false;
   const HParams p = make_hparams(dtype, g, channels_out, nullptr, nullptr, nullptr, nullptr,
-                                 nullptr, nullptr, nullptr, false);
+                                 nullptr, const_cast<void *>(out), nullptr, false);
   return p_config_for(p, kGeoYF32).nblocks != 0;
 }
 
@@ -945,7 +957,7 @@ hipError_t launch_dcn_mega(int dtype, const DcnGeom &g, int channels_out, const 
                            const void *w_off_packed, const float *b_off,
                            const void *w_packed, const void *bias, bool relu, float *y_out,
                            void *out, hipStream_t stream) {
-  if (!dcn_mega_supported(dtype, g, channels_out)) return hipErrorInvalidValue;
+  if (!dcn_mega_supported(dtype, g, channels_out, out)) return hipErrorInvalidValue;
   HParams p = make_hparams(dtype, g, channels_out, x, nullptr, nullptr, w_packed, bias, out,
                            nullptr, relu);
   p.w2 = w_off_packed;
