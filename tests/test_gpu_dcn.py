@@ -325,7 +325,8 @@ def test_fused_front_end_res4_fp16():
     (2, 64, 200, 130, 128),   # one column half, 8- and 9-block row ranges, column tail
     (1, 64, 320, 90, 100),    # two column halves (the second 64 wide), 4- and 5-block ranges
     (1, 128, 512, 80, 110),   # two full halves, 4- and 5-block ranges
-], ids=["half1", "half2-tail", "half2"])
+    (2, 64, 202, 130, 128),   # Cout % 8 != 0: the tiled kernel (16-byte output pieces)
+], ids=["half1", "half2-tail", "half2", "cout202"])
 def test_fused_half_row_balanced(dtype, form, shape):
     """Shapes that take the row-balanced persistent kernel (on a 256-CU device: NRB - 1 or
     NRB row blocks per workgroup, a partial last row block, one or two 256-column halves
@@ -366,6 +367,35 @@ def test_fused_half_row_balanced(dtype, form, shape):
     flat_out, flat_ref = out.cpu().reshape(-1, cout), ref.reshape(-1, cout)
     for sl in (slice(0, 1500), slice(-1500, None)):
         check(flat_out[sl], flat_ref[sl], dtype, f"row-balanced {form} vs oracle")
+
+
+@pytest.mark.parametrize("dtype", HALF, ids=["fp16", "bf16"])
+def test_fused_unaligned_output(dtype):
+    """A persistent-kernel shape with an output that starts 2 bytes past a 16-byte boundary
+    (a contiguous view one element into a larger buffer): the 16-byte stores of the
+    persistent kernel's epilogue do not apply, the tiled kernel writes the rows, the result
+    matches the aligned call within the dtype's tolerance and the elements around the
+    output keep their values."""
+    ext = _ext()
+    b, cin, cout, h, w = 2, 64, 200, 130, 128
+    g = torch.Generator().manual_seed(33)
+    x = torch.randn(b, h, w, cin, generator=g).to(dtype).to(DEV)
+    off = (2.0 * torch.randn(b, h, w, 18, generator=g)).to(dtype).to(DEV)
+    mask = torch.rand(b, h, w, 9, generator=g).to(dtype).to(DEV)
+    weight = (0.1 * torch.randn(cout, cin, 3, 3, generator=g)).to(dtype).to(DEV)
+    bias = torch.randn(cout, generator=g).to(dtype).to(DEV)
+    packed = ext.dcn_pack_weight(weight)
+    n = b * h * w * cout
+    aligned = torch.empty(b, h, w, cout, dtype=dtype, device=DEV)
+    buf = torch.full((n + 16,), 7.0, dtype=dtype, device=DEV)
+    shifted = buf[1:1 + n].view(b, h, w, cout)
+    assert shifted.data_ptr() % 16 == 2
+    for out in (aligned, shifted):
+        ext.dcn_fused_fwd_nhwc(x, off, mask, packed, bias, b, cin, h, w, h, w, cout, 3, 3, 1,
+                               1, 1, 1, 1, 1, out)
+    torch.cuda.synchronize()
+    check(shifted.float().cpu(), aligned.float().cpu(), dtype, "unaligned output vs aligned")
+    assert buf[0].item() == 7.0 and bool((buf[n + 1:] == 7.0).all())
 
 
 def test_fused_matches_gather_plus_gemm():
