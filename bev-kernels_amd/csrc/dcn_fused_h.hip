@@ -446,7 +446,15 @@ hipError_t launch_tt(const HParams &p, int geo, hipStream_t stream) {
 // barrier per K step (64 channels of one tap) hands the A tile over. The row range is
 // XCD-contiguous (XCD x owns the x-th eighth of M), so the image rows its gathers touch
 // stay in that XCD's L2.
-constexpr int kPBK = 64, kPLDA = kPBK + 8;      // K step, A tile row pitch (elements)
+constexpr int kPBK = 64, kPLDA = kPBK;          // K step, A tile row pitch (elements)
+
+// A tile element offset of (row, 16-byte chunk of the K step): rows are 128 bytes and the
+// chunk index is XORed with (row / 2) % 8, so the producers' stores (two rows of eight
+// chunks per 16 lanes) and the consumers' fragment reads (16 rows, one chunk) each touch
+// 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int a_off(int row, int chunk) {
+  return row * kPLDA + ((chunk ^ ((row >> 1) & 7)) << 3);
+}
 constexpr int kPKH = kPBK / 32;                 // 16x16x32 MFMA k-blocks per step
 constexpr int kPThreads = 512;                  // 4 consumer + 4 producer waves
 constexpr int kPProd = 256;                     // producer threads
@@ -536,7 +544,7 @@ __device__ __forceinline__ void dcn_p_consumer(const HParams &p, T (*As)[NRB * 1
 #pragma unroll
       for (int rbi = 0; rbi < NRB; ++rbi)
         af[rbi] = *reinterpret_cast<const int4v *>(
-            &As[buf][(rbi * 16 + (lane & 15)) * kPLDA + kh * 32 + 8 * (lane >> 4)]);
+            &As[buf][a_off(rbi * 16 + (lane & 15), kh * 4 + (lane >> 4))]);
 #pragma unroll
       for (int rbi = 0; rbi < NRB; ++rbi)
 #pragma unroll
@@ -619,7 +627,7 @@ __device__ __forceinline__ void dcn_p_offset_consumer(const HParams &p,
       for (int i = 0; i < RB; ++i) {
         const int rb = min(wave + 4 * i, NRB - 1);
         af[i] = *reinterpret_cast<const int4v *>(
-            &As[buf][(rb * 16 + (lane & 15)) * kPLDA + kh * 32 + 8 * (lane >> 4)]);
+            &As[buf][a_off(rb * 16 + (lane & 15), kh * 4 + (lane >> 4))]);
       }
 #pragma unroll
       for (int i = 0; i < RB; ++i)
@@ -707,7 +715,7 @@ __device__ __forceinline__ void dcn_p_producer(const HParams &p, const TapGeo *g
         const float4 w = *reinterpret_cast<const float4 *>(geo[row * TT + t].w);
         o = blend4<T>(ra[i], w.x, w.y, w.z, w.w);
       }
-      store_vec<T, 8>(&As[buf][row * kPLDA + kv * 8], o);
+      store_vec<T, 8>(&As[buf][a_off(row, kv)], o);
     }
   };
   V ra0[NS][NQ], ra1[NS][NQ];
