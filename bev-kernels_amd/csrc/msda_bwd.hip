@@ -1185,9 +1185,15 @@ __global__ void __launch_bounds__(kBkThreads) msda_bkt_place_kernel(const BktPar
       for (int r = 0; r < 2; ++r)
         if (rpos[j][r] >= 0) atomicAdd(&lcnt[rpos[j][r] >> kBkShift], 1);
     __syncthreads();
-    {  // exclusive scan of the NBS counts: thread tid owns [tid*E, tid*E + E)
-      const int E = (p.NBS + kBkThreads - 1) / kBkThreads;
-      const int e0 = min(tid * E, p.NBS), e1 = min(e0 + E, p.NBS);
+    // exclusive scan of the NBS counts: thread tid owns [tid*E, tid*E + E), E <= 4; each
+    // bucket's global range is reserved here, and the atomics' results are first used
+    // after the staging below, which runs while they return
+    constexpr int kMaxE = kBkMaxPerSlice / kBkThreads;
+    static_assert(kMaxE * kBkThreads == kBkMaxPerSlice, "bucket runs per thread");
+    const int E = (p.NBS + kBkThreads - 1) / kBkThreads;
+    const int e0 = min(tid * E, p.NBS), e1 = min(e0 + E, p.NBS);
+    int gres[kMaxE], gstart[kMaxE];
+    {
       int local = 0;
       for (int e = e0; e < e1; ++e) local += lcnt[e];
       int incl = local;
@@ -1200,11 +1206,17 @@ __global__ void __launch_bounds__(kBkThreads) msda_bkt_place_kernel(const BktPar
       __syncthreads();
       int run = incl - local;
       for (int w2 = 0; w2 < wave; ++w2) run += wsum[w2];
-      for (int e = e0; e < e1; ++e) {
-        const int c = lcnt[e];
-        gofs[e] = (c > 0 ? atomicAdd(&p.cursor[slice * p.NBS + e], c) : 0) - run;
-        lcnt[e] = run;
-        run += c;
+#pragma unroll
+      for (int j = 0; j < kMaxE; ++j) {
+        const int e = e0 + j;
+        gres[j] = 0;
+        gstart[j] = run;
+        if (e < e1) {
+          const int c = lcnt[e];
+          if (c > 0) gres[j] = atomicAdd(&p.cursor[slice * p.NBS + e], c);
+          lcnt[e] = run;
+          run += c;
+        }
       }
     }
     __syncthreads();
@@ -1219,6 +1231,9 @@ __global__ void __launch_bounds__(kBkThreads) msda_bkt_place_kernel(const BktPar
           sq[slot] = rq[j] | (uint32_t)(rpos[j][r] & (kBkPos - 1));
           sb[slot] = (unsigned short)k;
         }
+#pragma unroll
+    for (int j = 0; j < kMaxE; ++j)
+      if (e0 + j < e1) gofs[e0 + j] = gres[j] - gstart[j];
     __syncthreads();
     const int total = lcnt[p.NBS - 1];  // the last bucket's cursor ends at the staged total
     for (int i = tid; i < total; i += kBkThreads) {
