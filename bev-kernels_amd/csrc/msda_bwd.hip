@@ -1741,17 +1741,33 @@ __global__ void __launch_bounds__(kCoWaves * kWave) msda_coord_kernel(const Coor
   }
 }
 
+// Streaming passes over the fp32 grad_value workspace: 16-byte accesses when the
+// pointers allow them, element by element for the rest.
 __global__ void __launch_bounds__(kBlock) fill_zero_f32(float *__restrict__ p, int64_t n) {
   const int64_t stride = (int64_t)gridDim.x * kBlock;
-  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) p[i] = 0.f;
+  const int64_t i0 = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int64_t nv = reinterpret_cast<uintptr_t>(p) % 16 == 0 ? n / 4 : 0;
+  for (int64_t i = i0; i < nv; i += stride)
+    reinterpret_cast<float4 *>(p)[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int64_t i = nv * 4 + i0; i < n; i += stride) p[i] = 0.f;
 }
 
 template <typename T>
 __global__ void __launch_bounds__(kBlock) narrow_f32(const float *__restrict__ src,
                                                      T *__restrict__ dst, int64_t n) {
   const int64_t stride = (int64_t)gridDim.x * kBlock;
-  for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride)
-    dst[i] = (T)src[i];
+  const int64_t i0 = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const bool vec = reinterpret_cast<uintptr_t>(src) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(dst) % (4 * sizeof(T)) == 0;
+  const int64_t nv = vec ? n / 4 : 0;
+  for (int64_t i = i0; i < nv; i += stride) {
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    const f4v v = __builtin_nontemporal_load(reinterpret_cast<const f4v *>(src) + i);
+    Vec<T, 4> o;
+    o.v[0] = (T)v.x; o.v[1] = (T)v.y; o.v[2] = (T)v.z; o.v[3] = (T)v.w;
+    store_vec_nt<T, 4>(dst + 4 * i, o);
+  }
+  for (int64_t i = nv * 4 + i0; i < n; i += stride) dst[i] = (T)src[i];
 }
 
 unsigned stream_grid(int64_t n) {
