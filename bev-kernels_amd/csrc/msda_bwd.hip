@@ -917,6 +917,8 @@ struct BktParams {
   int blocks_per_xcd;
   int cblk8;        // count / place chunks per XCD
   int pblk;         // count / place blocks per XCD (persistent)
+  float *zero;      // 16-bit types: the fp32 grad_value workspace, cleared by the count
+  int64_t nzero4;   //   kernel (float4 groups; 0: nothing to clear)
 };
 
 // a / d for 0 <= a < 2^24 and 0 < d: a reciprocal estimate and one correction step
@@ -1027,7 +1029,21 @@ __global__ void __launch_bounds__(kBkThreads) msda_bkt_count_kernel(const BktPar
   ChunkSamples<T> cs;
   int lb = lb0 + (int)(blockIdx.x >> 3);
   if (lb < lb1) load_chunk<T>(p, lb, cs);
+  // the fp32 workspace of 16-bit types, cleared here (the accumulate kernel adds to it
+  // after this kernel): the block's share in 16-byte stores, a few per thread and chunk
+  // so that they stream out while the blocks compute, the rest after the last chunk
+  const int64_t zper = (p.nzero4 + gridDim.x - 1) / gridDim.x;
+  const int64_t z0 = (int64_t)blockIdx.x * zper, z1 = min(z0 + zper, p.nzero4);
+  const int nit = lb < lb1 ? (lb1 - 1 - lb) / p.pblk + 1 : 1;  // this block's chunks
+  const int64_t zstep = ((z1 - z0 + kBkThreads - 1) / kBkThreads + nit - 1) / nit * kBkThreads;
+  int64_t zi = z0;
+  auto clear_some = [&](int64_t upto) __attribute__((always_inline)) {
+    for (int64_t i = zi + threadIdx.x; i < upto; i += kBkThreads)
+      reinterpret_cast<float4 *>(p.zero)[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    zi = upto;
+  };
   for (; lb < lb1; lb += p.pblk) {
+    if (zi < z1) clear_some(min(zi + zstep, z1));
     int slice, q0, nq;
     bkt_chunk(p, lb, slice, q0, nq);
     int pos[kBkSPT][2];
@@ -1052,6 +1068,7 @@ __global__ void __launch_bounds__(kBkThreads) msda_bkt_count_kernel(const BktPar
     for (int k = threadIdx.x; k < p.NBS; k += kBkThreads)
       if (lcnt[k] > 0) atomicAdd(&p.count[slice * p.NBS + k], lcnt[k]);
   }
+  if (zi < z1) clear_some(z1);
 }
 
 // Block x (of 8): exclusive scan of the bucket counts (block 0 stores offset and cursor),
@@ -1551,6 +1568,9 @@ struct CoordParams {
   int tps;     // tiles per slice
   int nt8;     // tiles per XCD
   int ntiles;
+  const float *nsrc;  // 16-bit types: the fp32 grad_value workspace, narrowed into ndst
+  void *ndst;         //   by the waves after their tiles (float4 groups; 0: none)
+  int64_t nn4;
 };
 
 // Sum over each LPS-lane group (4 or 8) with DPP moves, no LDS traffic: xor 1 and xor 2
@@ -1615,7 +1635,34 @@ __global__ void __launch_bounds__(kCoWaves * kWave) msda_coord_kernel(const Coor
   // the wave's tile is uniform: kept in scalar registers
   const int tloc = __builtin_amdgcn_readfirstlane(r * kCoWaves + wave);
   const int tile = xcd * p.nt8 + tloc;
-  if (tloc >= p.nt8 || tile >= p.ntiles) return;
+  // 16-bit types: this wave's contiguous share of the fp32 grad_value workspace, narrowed
+  // into grad_value after the wave's tile (the accumulate kernel ran before this kernel)
+  auto narrow_share = [&]() __attribute__((always_inline)) {
+    const int64_t nw = (int64_t)gridDim.x * kCoWaves;
+    const int64_t per = (p.nn4 + nw - 1) / nw;
+    const int64_t i0 = ((int64_t)blockIdx.x * kCoWaves + wave) * per;
+    const int64_t i1 = min(i0 + per, p.nn4);
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    constexpr int U = 4;  // loads in flight per lane: one memory latency per round
+    for (int64_t i = i0 + lane; i < i1; i += U * kWave) {
+      f4v v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (i + u * kWave < i1)
+          v[u] = __builtin_nontemporal_load(reinterpret_cast<const f4v *>(p.nsrc) + i + u * kWave);
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (i + u * kWave < i1) {
+          Vec<T, 4> o;
+          o.v[0] = (T)v[u].x; o.v[1] = (T)v[u].y; o.v[2] = (T)v[u].z; o.v[3] = (T)v[u].w;
+          store_vec_nt<T, 4>(static_cast<T *>(p.ndst) + 4 * (i + u * kWave), o);
+        }
+    }
+  };
+  if (tloc >= p.nt8 || tile >= p.ntiles) {
+    if constexpr (sizeof(T) == 2) narrow_share();
+    return;
+  }
   const int slice = tile / p.tps;
   const int tq = tile - slice * p.tps;
   const int b = slice / p.NH, h = slice - b * p.NH;
@@ -1739,6 +1786,7 @@ __global__ void __launch_bounds__(kCoWaves * kWave) msda_coord_kernel(const Coor
       wave_lds_handover();
     }
   }
+  if constexpr (sizeof(T) == 2) narrow_share();
 }
 
 // Streaming passes over the fp32 grad_value workspace: 16-byte accesses when the
@@ -1850,9 +1898,13 @@ bool sorted_path(const MsdaBwdArgs &a, int dtype, BktLayout &L) {
 }
 
 // grad_value (fp32, added to gv) by the four bucket kernels, then the coordinate kernel.
+// fused_n: 16-bit types with a 16-byte aligned fp32 workspace gv and an 8-byte aligned
+// grad_value: the workspace's element count; the count kernel clears gv and the coordinate
+// kernel narrows it into grad_value. 0: gv is the caller's fp32 grad_value, or the
+// caller clears and narrows.
 template <typename T>
 hipError_t launch_sorted(const MsdaBwdArgs &a, const BktLayout &L, char *ws, float *gv,
-                         hipStream_t stream) {
+                         int64_t fused_n, hipStream_t stream) {
   BktParams p;
   p.loc = a.f.sampling_loc;
   p.attn = a.f.attn_weight;
@@ -1889,6 +1941,8 @@ hipError_t launch_sorted(const MsdaBwdArgs &a, const BktLayout &L, char *ws, flo
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   p.pblk = count_pblk;
+  p.zero = fused_n > 0 ? gv : nullptr;
+  p.nzero4 = fused_n / 4;
   hipLaunchKernelGGL((msda_bkt_count_kernel<T>), dim3(8u * (unsigned)count_pblk), dim3(kBkThreads), 0,
                      stream, p);
   if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -1918,6 +1972,9 @@ hipError_t launch_sorted(const MsdaBwdArgs &a, const BktLayout &L, char *ws, flo
   const int64_t ntiles = (int64_t)a.f.batch * a.f.num_heads * c.tps;
   c.ntiles = (int)ntiles;
   c.nt8 = (int)((ntiles + 7) / 8);
+  c.nsrc = gv;
+  c.ndst = a.grad_value;
+  c.nn4 = fused_n / 4;
   const unsigned cgrid = 8u * (unsigned)((c.nt8 + kCoWaves - 1) / kCoWaves);
   hipLaunchKernelGGL((msda_coord_kernel<T>), dim3(cgrid), dim3(kCoWaves * kWave), 0, stream, c);
   return hipGetLastError();
@@ -2062,7 +2119,7 @@ hipError_t launch_f32(const MsdaBwdArgs &a, bool generic, hipStream_t stream) {
   float *gv = static_cast<float *>(a.grad_value);
   BktLayout L;
   if (!generic && sorted_path<T>(a, 0, L))
-    return launch_sorted<T>(a, L, static_cast<char *>(a.workspace), gv, stream);
+    return launch_sorted<T>(a, L, static_cast<char *>(a.workspace), gv, 0, stream);
   if (generic || !owner_path<T>(a)) return launch_t<T, float>(a, gv, generic, stream);
   hipError_t e = launch_owner<T>(a, gv, true, stream);
   if (e != hipSuccess) return e;
@@ -2077,11 +2134,18 @@ hipError_t launch_half(const MsdaBwdArgs &a, bool generic, hipStream_t stream) {
   BktLayout L;
   const int dtype = std::is_same<T, f16>::value ? 1 : 2;
   if (!generic && sorted_path<T>(a, dtype, L)) {
-    hipLaunchKernelGGL(fill_zero_f32, dim3(stream_grid(n)), dim3(kBlock), 0, stream, acc, n);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    // the clear and the narrowing run inside the count and coordinate kernels when the
+    // pointers allow 16- and 8-byte accesses (n is a multiple of 32 here)
+    const bool fuse = reinterpret_cast<uintptr_t>(acc) % 16 == 0 &&
+                      reinterpret_cast<uintptr_t>(a.grad_value) % (4 * sizeof(T)) == 0;
+    if (!fuse) {
+      hipLaunchKernelGGL(fill_zero_f32, dim3(stream_grid(n)), dim3(kBlock), 0, stream, acc, n);
+      e = hipGetLastError();
+      if (e != hipSuccess) return e;
+    }
     e = launch_sorted<T>(a, L, static_cast<char *>(a.workspace) + half_acc_bytes(dtype, n), acc,
-                         stream);
+                         fuse ? n : 0, stream);
+    if (e != hipSuccess || fuse) return e;
   } else if (!generic && owner_path<T>(a)) {  // the owner pass writes every element of the workspace
     e = launch_owner<T>(a, acc, false, stream);
     if (e != hipSuccess) return e;

@@ -426,6 +426,46 @@ def test_sorted_bucket_edges(num_query, dtype):
     _check3(_run(d, go, dtype), _ref(d, go, dtype), dtype, f"bucket edges {num_query} {dtype}")
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+def test_sorted_unaligned_grad_value(dtype):
+    """16-bit sorted path with grad_value 2 bytes past an 8-byte boundary (a contiguous view
+    one element into a larger buffer): the workspace clear and the narrowing run as their
+    own passes instead of inside the count and coordinate kernels. Same gradients as the
+    aligned call, and the elements around grad_value keep their values."""
+    import _bevk as b
+    d = inputs.msda_random(2, [(20, 30), (10, 15)], 300, 4, 32, 4, seed=23)
+    go = _grad_output(d, seed=9)
+    dd = _dev(d, dtype)
+    value, loc = dd["value"], dd["sampling_loc"]
+    B, S, NH, D = value.shape
+    Lq, L, P = loc.shape[1], loc.shape[3], loc.shape[4]
+    g4 = go.to(dtype).to(DEV).view(B, Lq, NH, D)
+    ws_bytes = b.lib().bevk_msda_backward_workspace_bytes(b.dtype_code(value), B, S, NH, D, L,
+                                                          Lq, P)
+    n = value.numel()
+    outs = []
+    for shift in (0, 1):
+        buf = torch.full((n + 8,), 3.0, dtype=dtype, device=DEV)
+        gv = buf[shift:shift + n].view(value.shape)
+        assert gv.data_ptr() % 8 == 2 * shift
+        gl = torch.empty_like(loc)
+        ga = torch.empty_like(dd["attn_weight"])
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
+        b.call("bevk_msda_backward", b.dtype_code(value), b.ptr(value),
+               b.ptr(dd["spatial_shapes"]), b.ptr(dd["level_start_index"]), b.ptr(loc),
+               b.ptr(dd["attn_weight"]), b.ptr(g4), *g4.stride(), B, S, NH, D, L, Lq, P, 64, 0,
+               b.ptr(gv), b.ptr(gl), b.ptr(ga), b.ptr(ws), ws_bytes, b.stream_of(value))
+        torch.cuda.synchronize()
+        outs.append((gv.cpu().float(), gl.cpu().float(), ga.cpu().float(), buf.cpu()))
+    (gv0, gl0, ga0, _), (gv1, gl1, ga1, buf1) = outs
+    for name, x, r in (("grad_value", gv1, gv0), ("grad_sampling_loc", gl1, gl0),
+                       ("grad_attn_weight", ga1, ga0)):
+        check(x, r, dtype, f"unaligned grad_value run, {name} vs aligned")
+    assert buf1[0].item() == 3.0 and bool((buf1[n + 1:] == 3.0).all())
+    ref = _ref(d, go, dtype)
+    check(gv1, ref[0], dtype, "unaligned grad_value vs oracle")
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["fp32", "fp16"])
 @pytest.mark.parametrize("case", ["hw_below_s", "level_offset"])
 def test_one_level_not_a_grid(case, dtype):
