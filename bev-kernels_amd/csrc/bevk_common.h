@@ -52,6 +52,20 @@ __device__ __forceinline__ void store_vec_nt(T *p, const Vec<T, N> &v) {
 template <typename T> __device__ __forceinline__ T load_nt(const T *p) {
   return __builtin_nontemporal_load(p);
 }
+// Streaming load of a 4-, 8- or 16-byte vector (read once by the kernel).
+template <typename T, int N>
+__device__ __forceinline__ Vec<T, N> load_vec_nt(const T *p) {
+  if constexpr (sizeof(Vec<T, N>) == 16) {
+    typedef int i4 __attribute__((ext_vector_type(4)));
+    return __builtin_bit_cast(Vec<T, N>, __builtin_nontemporal_load(reinterpret_cast<const i4 *>(p)));
+  } else if constexpr (sizeof(Vec<T, N>) == 8) {
+    typedef int i2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(Vec<T, N>, __builtin_nontemporal_load(reinterpret_cast<const i2 *>(p)));
+  } else {
+    static_assert(sizeof(Vec<T, N>) == 4, "4-, 8- or 16-byte vectors");
+    return __builtin_bit_cast(Vec<T, N>, __builtin_nontemporal_load(reinterpret_cast<const int *>(p)));
+  }
+}
 template <> __device__ __forceinline__ f16 load_nt<f16>(const f16 *p) {
   unsigned short u = __builtin_nontemporal_load(reinterpret_cast<const unsigned short *>(p));
   return __builtin_bit_cast(f16, u);

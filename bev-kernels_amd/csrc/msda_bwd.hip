@@ -1710,8 +1710,15 @@ __global__ void __launch_bounds__(kCoWaves * kWave) msda_coord_kernel(const Coor
       const int si = si0 + min(q0 - q_begin, qlast) * dsi;
       xy_n = *reinterpret_cast<const Vec<T, 2> *>(loc + (int64_t)si * 2);
       a_n = attn[si];
+      // fp32: grad_output pieces are read once here; streaming loads, like the gradient
+      // stores below, keep the value lines in L2 (locations and weights stay ordinary
+      // loads: streaming them was faster at SCA but slower at TSA; the 16-bit forms keep
+      // ordinary accesses: streaming measured slower for TSA bf16)
       const int qg = min(q0 + ug, q_end - 1);
-      tv_n = *reinterpret_cast<const Vec<T, VEC> *>(gob + (int64_t)qg * p.go_sq + cl * VEC);
+      if constexpr (sizeof(T) == 4)
+        tv_n = load_vec_nt<T, VEC>(gob + (int64_t)qg * p.go_sq + cl * VEC);
+      else
+        tv_n = *reinterpret_cast<const Vec<T, VEC> *>(gob + (int64_t)qg * p.go_sq + cl * VEC);
     };
     fetch(q_begin);
     for (int q0 = q_begin; q0 < q_end; q0 += upi) {
@@ -1780,8 +1787,13 @@ __global__ void __launch_bounds__(kCoWaves * kWave) msda_coord_kernel(const Coor
         Vec<T, 2> gl;
         gl.v[0] = (T)rr.x;
         gl.v[1] = (T)rr.y;
-        *reinterpret_cast<Vec<T, 2> *>(gloc + (int64_t)si * 2) = gl;
-        gattn[si] = (T)rr.z;
+        if constexpr (sizeof(T) == 4) {
+          store_vec_nt<T, 2>(gloc + (int64_t)si * 2, gl);
+          __builtin_nontemporal_store((T)rr.z, gattn + si);
+        } else {
+          *reinterpret_cast<Vec<T, 2> *>(gloc + (int64_t)si * 2) = gl;
+          gattn[si] = (T)rr.z;
+        }
       }
       wave_lds_handover();
     }
