@@ -889,8 +889,12 @@ __global__ void __launch_bounds__(WPB * kWave, (WPB * BPC + 3) / 4) msda_tile_ke
       bool qv;
       const int q = query((wave + ps * WPB) * UPP + lane / NP, qv);
       const int64_t unit = ((int64_t)b * p.NQ + (qv ? q : 0)) * p.NH + h;
-      load_loc<T>(static_cast<const T *>(p.loc) + (unit * NP + lane % NP) * 2, lx[ps], ly[ps]);
-      la[ps] = static_cast<float>(load_nt(static_cast<const T *>(p.attn) + unit * NP + lane % NP));
+      // ordinary loads here (the other kernels stream these inputs): measured 98.4 ->
+      // 94.0 us for the temporal self-attention map, whose tiles' rows stay in L2
+      const T *lp = static_cast<const T *>(p.loc) + (unit * NP + lane % NP) * 2;
+      lx[ps] = static_cast<float>(lp[0]);
+      ly[ps] = static_cast<float>(lp[1]);
+      la[ps] = static_cast<float>(static_cast<const T *>(p.attn)[unit * NP + lane % NP]);
     }
 
     __syncthreads();  // the previous item's readers are done
