@@ -1063,11 +1063,10 @@ hipError_t launch_wave(const MsdaArgs &a, hipStream_t stream) {
         return launch_wave_t<T, 32, 4, 8>(a, stream);
       }
       if (L == 1 && P == 4) {  // BEVFormer TSA
-        // fp32: the tiled kernel (neighbourhood in LDS) measured 25% faster than the
-        // per-sample gather kernel; for 16-bit types the two are even.
-        if constexpr (sizeof(T) == 4)
-          if (a.num_query == a.spatial_size && device_cus() >= 8)
-            return launch_tile_t<T, 4, 16, 6, 8, 1>(a, stream);
+        // the tiled kernel (neighbourhood in LDS) measured faster than the per-sample
+        // gather kernel: fp32 by 25%, fp16 74.0 -> 69.1 us, bf16 75.4 -> 73.6 us
+        if (a.num_query == a.spatial_size && device_cus() >= 8)
+          return launch_tile_t<T, 4, 16, 6, 8, 1>(a, stream);
         return launch_wave_t<T, 32, 1, 4>(a, stream);
       }
       if (L == 4 && P == 4) {  // Deformable DETR
