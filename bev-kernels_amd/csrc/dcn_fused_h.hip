@@ -815,15 +815,16 @@ __global__ void __launch_bounds__(kPThreads) dcn_fused_p_kernel(const PParams pp
   else
     dcn_p_producer<T, SH::kSPT - 1, NRB, false>(p, geo, As, nk, tid - kPProd);
   // The output tile: full 16-byte pieces of the workgroup's rows (Cout % 8 == 0 and a
-  // 16-byte aligned output, checked on the host: a piece is wholly inside or outside).
+  // 16-byte aligned output, checked on the host: a piece is wholly inside or outside),
+  // streaming stores (written once; the input rows stay in L2).
   __syncthreads();
   T *out = static_cast<T *>(p.out);
   constexpr int kPieces = kPCols / 8;
   for (int i = tid; i < nrows * kPieces; i += kPThreads) {
     const int row = i / kPieces, c = (i - row * kPieces) * 8, m = m0 + row;
     if (m < p.M && n0 + c < p.Cout)
-      *reinterpret_cast<int4 *>(out + (int64_t)m * p.Cout + n0 + c) =
-          *reinterpret_cast<const int4 *>(&stage[row * kPStage + c]);
+      __builtin_nontemporal_store(*reinterpret_cast<const int4v *>(&stage[row * kPStage + c]),
+                                  reinterpret_cast<int4v *>(out + (int64_t)m * p.Cout + n0 + c));
   }
 }
 
