@@ -320,7 +320,7 @@ __global__ void __launch_bounds__(kBlock) col2im_coord_nhwc_vec_kernel(
   float s1 = 0.f, s2 = 0.f, s3 = 0.f, s4 = 0.f;
   if (live) {
     for (int c = li * VEC; c < C; c += LPP * VEC) {
-      const Vec<T, VEC> dv = load_vec<T, VEC>(drow + c);
+      const Vec<T, VEC> dv = load_vec_nt<T, VEC>(drow + c);  // read once: keep x in L2
       const uint32_t cb = (uint32_t)c * eb;
       const Vec<T, VEC> v1 = buffer_load_vec<T, VEC>(rim, o1 + cb);
       const Vec<T, VEC> v2 = buffer_load_vec<T, VEC>(rim, o2 + cb);
