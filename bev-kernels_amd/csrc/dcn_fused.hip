@@ -24,6 +24,8 @@
 #include "bevk_common.h"
 #include "bevk_launch.h"
 
+#include <hip/amd_detail/amd_hip_unsafe_atomics.h>
+
 namespace bevk {
 namespace {
 
@@ -45,6 +47,7 @@ struct FusedParams {
   int B, C, H, W, Ho, Wo, Cout, kh, kw, ph, pw, sh, sw, dh, dw;
   int M, K;
   int tiles_m;
+  int kz_steps;     // K steps per blockIdx.z part: two parts add into a cleared output
   uint32_t x_bytes, w_bytes;
 };
 
@@ -107,6 +110,9 @@ __global__ void __launch_bounds__(kThreads) dcn_fused_nhwc_kernel(const FusedPar
   }
   const int m0 = tile_m * BM;
   const int n0 = blockIdx.y * BN;
+  // K steps [ks0, ks1) of this workgroup (the whole K unless it is split over blockIdx.z)
+  const int nk = (p.K + BK - 1) / BK;
+  const int ks0 = (int)blockIdx.z * p.kz_steps, ks1 = min(nk, ks0 + p.kz_steps);
   const int HoWo = p.Ho * p.Wo;
   const int T_ = p.kh * p.kw;
 
@@ -138,7 +144,7 @@ __global__ void __launch_bounds__(kThreads) dcn_fused_nhwc_kernel(const FusedPar
     a_hb[i] = oh * p.sh - p.ph;
     a_wb[i] = ow * p.sw - p.pw;
     a_img[i] = b * p.H * p.W;
-    const int k = a_kv[i] * VEC;
+    const int k = ks0 * BK + a_kv[i] * VEC;
     a_t[i] = k / p.C;
     a_c[i] = k - a_t[i] * p.C;
     a_gt[i] = -1;  // tap whose geometry is cached: none yet
@@ -187,7 +193,7 @@ __global__ void __launch_bounds__(kThreads) dcn_fused_nhwc_kernel(const FusedPar
 #pragma unroll
     for (int i = 0; i < AV; ++i) {
       // Advance the slot's (t, c) to k = ks*BK + kv*VEC.
-      if (ks > 0) {
+      if (ks > ks0) {
         a_c[i] += BK;
         while (a_c[i] >= p.C) { a_c[i] -= p.C; ++a_t[i]; }
       }
@@ -250,16 +256,15 @@ __global__ void __launch_bounds__(kThreads) dcn_fused_nhwc_kernel(const FusedPar
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  const int nk = (p.K + BK - 1) / BK;
   const int lrow = lane & 31;
   const int lk = (lane >> 5) * lane_k<T>();
 
-  issue_loads(0);
-  for (int ks = 0; ks < nk; ++ks) {
-    const int buf = ks & 1;
+  issue_loads(ks0);
+  for (int ks = ks0; ks < ks1; ++ks) {
+    const int buf = (ks - ks0) & 1;
     store_lds(buf);
     __syncthreads();
-    if (ks + 1 < nk) issue_loads(ks + 1);
+    if (ks + 1 < ks1) issue_loads(ks + 1);
 #pragma unroll
     for (int kk = 0; kk < BK; kk += Mfma<T>::KSTEP) {
 #pragma unroll
@@ -276,12 +281,16 @@ __global__ void __launch_bounds__(kThreads) dcn_fused_nhwc_kernel(const FusedPar
 
   // ---- epilogue: D[row][col], lane holds col = lane%32,
   //      row = 8*(e/4) + 4*(lane/32) + e%4 for e in [0, 16).
+  //      Split K (fp32 only, no ReLU): each part adds its sum to the cleared output, the
+  //      bias with the first part; with two parts the result does not depend on their
+  //      order (0 + a + b == 0 + b + a).
   T *out = static_cast<T *>(p.out);
   const T *bias = static_cast<const T *>(p.bias);
+  const bool split = gridDim.z > 1;
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const int n = n0 + wn * WTN + j * 32 + lrow;
-    const float bv = (bias != nullptr && n < p.Cout) ? (float)bias[n] : 0.f;
+    const float bv = (bias != nullptr && n < p.Cout && blockIdx.z == 0) ? (float)bias[n] : 0.f;
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -290,7 +299,12 @@ __global__ void __launch_bounds__(kThreads) dcn_fused_nhwc_kernel(const FusedPar
         const int m = m0 + row;
         float v = acc[i][j][e] + bv;
         if (GEO != kGeoRegular && p.relu) v = v < 0.f ? 0.f : v;  // NaN stays NaN
-        if (m < p.M && n < p.Cout) out[(int64_t)m * p.Cout + n] = static_cast<T>(v);
+        if (m < p.M && n < p.Cout) {
+          if (sizeof(T) == 4 && split)
+            unsafeAtomicAdd(reinterpret_cast<float *>(out) + (int64_t)m * p.Cout + n, v);
+          else
+            out[(int64_t)m * p.Cout + n] = static_cast<T>(v);
+        }
       }
     }
   }
@@ -298,7 +312,8 @@ __global__ void __launch_bounds__(kThreads) dcn_fused_nhwc_kernel(const FusedPar
 
 template <typename T, int BM, int BN, int BK, int WM, int WN>
 hipError_t launch_cfg(const FusedParams &p, int geo, hipStream_t stream) {
-  dim3 grid(p.tiles_m, (p.Cout + BN - 1) / BN);
+  const int nk = (p.K + BK - 1) / BK;
+  dim3 grid(p.tiles_m, (p.Cout + BN - 1) / BN, (nk + p.kz_steps - 1) / p.kz_steps);
   if (geo == kGeoY)
     hipLaunchKernelGGL((dcn_fused_nhwc_kernel<T, BM, BN, BK, WM, WN, kGeoY>), grid,
                        dim3(kThreads), 0, stream, p);
@@ -316,11 +331,35 @@ hipError_t launch_cfg(const FusedParams &p, int geo, hipStream_t stream) {
   return hipGetLastError();
 }
 
+__global__ void __launch_bounds__(kThreads) fill_zero_f32x4(float *__restrict__ p, int64_t n4) {
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n4;
+       i += (int64_t)gridDim.x * kThreads)
+    reinterpret_cast<float4 *>(p)[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
 template <typename T>
 hipError_t launch_t(FusedParams p, int geo, hipStream_t stream) {
   constexpr int BK = sizeof(T) == 4 ? 16 : 32;
   constexpr int BM = 64;
   p.tiles_m = (p.M + BM - 1) / BM;
+  const int nk = (p.K + BK - 1) / BK;
+  p.kz_steps = nk;
+  // fp32 with fewer than three workgroups per CU (res4: 544 tiles, res5: 272) and no ReLU:
+  // K in two halves that add into the cleared output, twice the workgroups (res4 fp32
+  // 505 -> 465 us, res5 665 -> 517 us)
+  const int bn = p.Cout > 128 ? 256 : p.Cout > 64 ? 128 : 64;  // BN of the launch below
+  const int64_t tiles = (int64_t)p.tiles_m * ((p.Cout + bn - 1) / bn);
+  const int64_t n_out = (int64_t)p.M * p.Cout;
+  if (sizeof(T) == 4 && !p.relu && nk >= 64 && tiles < 3 * (int64_t)device_cus() &&
+      n_out % 4 == 0 && reinterpret_cast<uintptr_t>(p.out) % 16 == 0) {
+    p.kz_steps = (nk + 1) / 2;
+    const int64_t n4 = n_out / 4;
+    const unsigned g = (unsigned)std::min<int64_t>((n4 + kThreads - 1) / kThreads, 8192);
+    hipLaunchKernelGGL(fill_zero_f32x4, dim3(g), dim3(kThreads), 0, stream,
+                       static_cast<float *>(p.out), n4);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   if (p.Cout > 128) return launch_cfg<T, BM, 256, BK, 1, 4>(p, geo, stream);
   if (p.Cout > 64) return launch_cfg<T, BM, 128, BK, 1, 4>(p, geo, stream);
   return launch_cfg<T, BM, 64, BK, 2, 2>(p, geo, stream);
