@@ -21,6 +21,9 @@
 #include "bevk_common.h"
 #include "bevk_launch.h"
 
+#include <hip/amd_detail/amd_hip_unsafe_atomics.h>
+
+#include <algorithm>
 #include <type_traits>
 
 namespace bevk {
@@ -41,6 +44,8 @@ struct HParams {
   int C, H, W, Ho, Wo, Cout, kh, kw, ph, pw, sh, sw, dh, dw, M, K;
   int taps, nb_total, kb_total;  // packed weight blocks: [nb_total][kb_total][64][16 B]
   int mt, nt, tiles_per_xcd;     // output tiles (M x N) and tiles per XCD
+  int kz_steps;                  // K steps per blockIdx.y part (fp32 output: two parts add
+                                 // into the cleared output; else the whole K)
   uint32_t x_bytes, w_bytes;
   // offset conv of the one-launch forward: packed w_off (3T <= 32 columns, one 32-column
   // fragment block), its fp32 bias and the fp32 y [M][3T] written out (or null)
@@ -167,6 +172,9 @@ dcn_fused_h_kernel(const HParams p) {
   // XCD x (= blockIdx % 8) runs tiles [x * tiles_per_xcd, (x + 1) * tiles_per_xcd)
   const int tile = (int)(blockIdx.x & 7) * p.tiles_per_xcd + (int)(blockIdx.x >> 3);
   if ((int)(blockIdx.x >> 3) >= p.tiles_per_xcd || tile >= p.mt * p.nt) return;
+  // K steps [ks0, ks1) of this workgroup (whole taps in the TAPSTEP form)
+  const int nk = (p.K + BK - 1) / BK;
+  const int ks0 = (int)blockIdx.y * p.kz_steps, ks1 = min(nk, ks0 + p.kz_steps);
   const int mtile = tile / p.nt;
   const int m0 = mtile * BM, n0 = (tile - mtile * p.nt) * BN;
   const int TT = p.taps;
@@ -188,7 +196,7 @@ dcn_fused_h_kernel(const HParams p) {
     const int a = tid + i * NT;
     a_row[i] = a / KV;
     a_kv[i] = a - (a / KV) * KV;
-    const int k = a_kv[i] * VEC;
+    const int k = ks0 * BK + a_kv[i] * VEC;
     a_t[i] = k / p.C;
     a_c[i] = k - a_t[i] * p.C;
   }
@@ -230,7 +238,7 @@ dcn_fused_h_kernel(const HParams p) {
     } else {
 #pragma unroll
       for (int i = 0; i < AV; ++i) {
-        if (ks > 0) {
+        if (ks > ks0) {
           a_c[i] += BK;
           while (a_c[i] >= p.C) { a_c[i] -= p.C; ++a_t[i]; }
         }
@@ -314,39 +322,41 @@ dcn_fused_h_kernel(const HParams p) {
   // ---- K loop: A(k+1) is gathered and B(k+1) loaded while step k multiplies ---------
   // Pairs of steps with no exit in the middle of the body (an exit there makes the
   // compiler keep two copies of the accumulators), then an odd last step.
-  const int nk = (p.K + BK - 1) / BK;
-  issue_b(0, breg[0]);
-  issue_a(0);
+  issue_b(ks0, breg[0]);
+  issue_a(ks0);
   store_a(0);
-  if (nk > 1) issue_a(1);
-  int ks = 0;
-  for (; ks + 1 < nk; ks += 2) {
+  if (ks0 + 1 < ks1) issue_a(ks0 + 1);
+  int ks = ks0;
+  for (; ks + 1 < ks1; ks += 2) {
     __syncthreads();                       // A(ks) complete in buffer 0
     issue_b(ks + 1, breg[1]);
     compute(0, breg[0]);
     store_a(1);                            // A(ks+1) -> buffer 1
-    if (ks + 2 < nk) issue_a(ks + 2);
+    if (ks + 2 < ks1) issue_a(ks + 2);
     __syncthreads();
-    if (ks + 2 < nk) issue_b(ks + 2, breg[0]);
+    if (ks + 2 < ks1) issue_b(ks + 2, breg[0]);
     compute(1, breg[1]);
-    if (ks + 2 < nk) {
+    if (ks + 2 < ks1) {
       store_a(0);                          // A(ks+2) -> buffer 0
-      if (ks + 3 < nk) issue_a(ks + 3);
+      if (ks + 3 < ks1) issue_a(ks + 3);
     }
   }
-  if (ks < nk) {
+  if (ks < ks1) {
     __syncthreads();
     compute(0, breg[0]);
   }
 
   // ---- epilogue: lane holds col = lane % 32, rows 8*(e/4) + 4*(lane/32) + e%4 --------
+  //      K in two parts (fp32 output): each adds its sum to the cleared output, the bias
+  //      with the first; with two parts the result does not depend on their order.
   OutT *out = static_cast<OutT *>(p.out);
   using BiasT = typename std::conditional<GEO == kGeoRegular, float, T>::type;
   const BiasT *bias = static_cast<const BiasT *>(p.bias);
+  const bool split = gridDim.y > 1;
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const int n = n0 + (wn * TN + j) * 32 + lrow;
-    const float bv = (bias != nullptr && n < p.Cout) ? (float)bias[n] : 0.f;
+    const float bv = (bias != nullptr && n < p.Cout && blockIdx.y == 0) ? (float)bias[n] : 0.f;
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -354,7 +364,14 @@ dcn_fused_h_kernel(const HParams p) {
         const int m = m0 + wm * WTM + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
         float v = acc[i][j][e] + bv;
         if (GEO != kGeoRegular && p.relu) v = v < 0.f ? 0.f : v;  // NaN stays NaN
-        if (m < p.M && n < p.Cout) out[(int64_t)m * p.Cout + n] = static_cast<OutT>(v);
+        if (m < p.M && n < p.Cout) {
+          if constexpr (std::is_same<OutT, float>::value) {
+            if (split) unsafeAtomicAdd(out + (int64_t)m * p.Cout + n, v);
+            else out[(int64_t)m * p.Cout + n] = v;
+          } else {
+            out[(int64_t)m * p.Cout + n] = static_cast<OutT>(v);
+          }
+        }
       }
   }
 }
@@ -397,12 +414,38 @@ __global__ void __launch_bounds__(256) pack_weight_kc_kernel(const float *__rest
   packed[i] = src_tc ? w[i] : w[(n * C + c) * T + t];
 }
 
+__global__ void __launch_bounds__(256) zero_f32_kernel(float *__restrict__ p, int64_t n) {
+  const int64_t n4 = n >> 2;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (int64_t)gridDim.x * 256)
+    reinterpret_cast<float4 *>(p)[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+  const int64_t r = n4 * 4 + (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (r < n) p[r] = 0.f;
+}
+
 template <typename T, typename OutT, int BM, int BN, int BK, int WM, int WN, bool TAPSTEP>
 hipError_t launch_cfg(HParams p, int geo, hipStream_t stream) {
   p.mt = (p.M + BM - 1) / BM;
   p.nt = (p.Cout + BN - 1) / BN;
   p.tiles_per_xcd = (p.mt * p.nt + 7) / 8;
-  const dim3 grid(8 * p.tiles_per_xcd), block(64 * WM * WN);
+  const int nk = (p.K + BK - 1) / BK;
+  p.kz_steps = nk;
+  // fp32 output (the offset conv) with fewer than two tiles per CU: K in two parts that
+  // add into the cleared output, twice the K chains at once (res5 front end, 272 one-wave
+  // tiles: 70.9 -> 60.7 us; res4, 1088 tiles, slows down, 75.6 -> 86.7 us, and stays whole).
+  // The TAPSTEP form reads a tap's geometry at its first step, so a part is whole taps.
+  const int spt = TAPSTEP ? p.C / BK : 1;
+  const int units = TAPSTEP ? p.taps : nk;
+  if (std::is_same<OutT, float>::value && units >= 2 && nk >= 16 &&
+      (int64_t)p.mt * p.nt < 2 * (int64_t)device_cus() &&
+      reinterpret_cast<uintptr_t>(p.out) % 16 == 0) {
+    p.kz_steps = (units + 1) / 2 * spt;
+    const int64_t n = (int64_t)p.M * p.Cout;
+    const unsigned g = (unsigned)std::max<int64_t>(1, std::min<int64_t>((n / 4 + 255) / 256, 4096));
+    hipLaunchKernelGGL(zero_f32_kernel, dim3(g), dim3(256), 0, stream, static_cast<float *>(p.out), n);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  const dim3 grid(8 * p.tiles_per_xcd, (nk + p.kz_steps - 1) / p.kz_steps), block(64 * WM * WN);
   if (geo == kGeoY)
     hipLaunchKernelGGL((dcn_fused_h_kernel<T, OutT, BM, BN, BK, WM, WN, kGeoY, TAPSTEP>), grid,
                        block, 0, stream, p);
