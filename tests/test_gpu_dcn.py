@@ -598,6 +598,11 @@ def _mega_ref(x, w_off, b_off, weight, bias, dtype, s=1, p=1, dl=1, relu=False):
     (2, 64, 9, 11, 1, 1, 1),
     (1, 32, 12, 10, 2, 1, 1),
     (1, 16, 10, 9, 1, 2, 2),
+    # few tiles and a long K: K in two parts adding into y (half types), split by taps
+    # with 128-channel steps, by taps with 64-channel steps, and by steps (C % 64 != 0)
+    (1, 256, 12, 10, 1, 1, 1),
+    (1, 192, 9, 11, 1, 1, 1),
+    (1, 136, 10, 9, 1, 1, 1),
 ])
 def test_offset_conv_forward_nhwc(dtype, geom):
     """fused_tl.offset_conv_forward_nhwc: y accumulated and kept in fp32 on the matrix
