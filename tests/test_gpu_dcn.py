@@ -202,8 +202,10 @@ def _packed_layout_ref(weight, dtype):
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32],
                          ids=["fp16", "bf16", "fp32"])
 @pytest.mark.parametrize("shape", [(40, 24, 3, 3), (256, 256, 3, 3), (7, 8, 1, 1),
-                                   (33, 16, 5, 5)])
+                                   (33, 16, 5, 5), (70, 48, 3, 3), (32, 64, 7, 7)])
 def test_pack_weight_layout(dtype, shape):
+    """Packed layout, bit-exact: 16-bit C % 16 == 0 with <= 25 taps goes through LDS (row
+    and column tails: 33 x 16 x 5 x 5, 70 x 48), the rest element by element."""
     g = torch.Generator().manual_seed(sum(shape))
     w = torch.randn(*shape, generator=g).to(dtype)
     packed = _ext().dcn_pack_weight(w.to(DEV))
