@@ -510,19 +510,20 @@ hipError_t launch_cfg(HParams p, int geo, hipStream_t stream) {
     hipLaunchKernelGGL((dcn_fused_h_kernel<T, OutT, BM, BN, BK, WM, WN, kGeoRegular, TAPSTEP>),
                        grid, block, 0, stream, p);
     return hipGetLastError();
+  } else {  // input-dtype output: the deformable forms
+    if (geo == kGeoY)
+      hipLaunchKernelGGL((dcn_fused_h_kernel<T, OutT, BM, BN, BK, WM, WN, kGeoY, TAPSTEP>), grid,
+                         block, 0, stream, p);
+    else if (geo == kGeoYF32)
+      hipLaunchKernelGGL((dcn_fused_h_kernel<T, OutT, BM, BN, BK, WM, WN, kGeoYF32, TAPSTEP>),
+                         grid, block, 0, stream, p);
+    else if (geo == kGeoMask)
+      hipLaunchKernelGGL((dcn_fused_h_kernel<T, OutT, BM, BN, BK, WM, WN, kGeoMask, TAPSTEP>),
+                         grid, block, 0, stream, p);
+    else
+      return hipErrorInvalidValue;
+    return hipGetLastError();
   }
-  if (geo == kGeoY)
-    hipLaunchKernelGGL((dcn_fused_h_kernel<T, OutT, BM, BN, BK, WM, WN, kGeoY, TAPSTEP>), grid,
-                       block, 0, stream, p);
-  else if (geo == kGeoYF32)
-    hipLaunchKernelGGL((dcn_fused_h_kernel<T, OutT, BM, BN, BK, WM, WN, kGeoYF32, TAPSTEP>),
-                       grid, block, 0, stream, p);
-  else if (geo == kGeoMask)
-    hipLaunchKernelGGL((dcn_fused_h_kernel<T, OutT, BM, BN, BK, WM, WN, kGeoMask, TAPSTEP>),
-                       grid, block, 0, stream, p);
-  else
-    return hipErrorInvalidValue;
-  return hipGetLastError();
 }
 
 template <typename T, bool TAPSTEP>
