@@ -151,7 +151,8 @@ int64_t bevk_dcn_fused_im2col_nhwc_workspace_bytes(int dtype, int batch_size, in
  * y = conv(x, w_off) + b_off is accumulated in fp32 and kept in fp32 (matrix cores, with the
  * same stride / padding / dilation as the deformable taps); offsets = y[:, :2T] ((dy, dx) per
  * tap), mask = sigmoid(y[:, 2T:3T]); then the NHWC gather. `workspace` (device memory of at
- * least bevk_dcn_fused_im2col_nhwc_workspace_bytes) holds the packed w_off and y.
+ * least bevk_dcn_fused_im2col_nhwc_workspace_bytes) holds y and, for F16 / BF16, the packed
+ * w_off (F32 reads w_off as given; the size is the same for every dtype).
  * Replaces binding.cpp:72-78 modulated_deformable_fused_im2col_nhwc_cuda
  * (dcn_fused_nhwc_cuda.cu:92-126, kernel dcn_fused_nhwc_kernel.cuh:211-303). dg == 1.
  * dtypes F32 (any kernel size), F16 / BF16 (at most 9 taps); C a multiple of 16 bytes'
