@@ -921,6 +921,10 @@ __global__ void __launch_bounds__(kPThreads) dcn_fused_p_kernel(const PParams pp
   // Always the NRB-block body: a range of NRB - 1 blocks has zero geometry in its last
   // block (see above) and does not store it; the kernel's time is set by the full ranges.
   // Consumers and producers run the same number of barriers (one per step + prologue).
+  // Producer waves issue first when both roles are ready: the gathers of the next K step
+  // leave earlier and the matrix-core work waits less at the barrier (res4 fp16 71.0 ->
+  // 67.8 us; the consumers raised instead, 70.2 us).
+  if (wave >= 4) __builtin_amdgcn_s_setprio(2);
   if (wave < 4)
     dcn_p_consumer<T, NRB>(p, As, stage, n0, nk, lane, wave);
   else if (wave - 4 < SH::kLastWaves)
