@@ -25,6 +25,7 @@
 //     and every value line is pulled into one L2 only. The plain variant keeps all XCDs
 //     on one slice, each on an eighth of its queries (see xcd_chunk).
 //   * msda_generic_kernel: one thread per output element, any shape and dtype.
+#include <atomic>
 #include "bevk_common.h"
 #include "bevk_launch.h"
 
@@ -1131,17 +1132,20 @@ hipError_t launch_msda_forward(int dtype, const MsdaArgs &a, bool force_generic,
   }
 }
 
+// CU count of the current device, read once per device. Several host threads may launch
+// at once: each slot is an atomic, and two threads that both find it empty store the same
+// value.
 int device_cus() {
-  static int cus[64] = {0};
+  static std::atomic<int> cus[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cus[dev] == 0) {
-    int n = 0;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
       return 0;
-    cus[dev] = n;
+    cus[dev].store(n, std::memory_order_relaxed);
   }
-  return cus[dev];
+  return n;
 }
 
 }  // namespace bevk
