@@ -17,6 +17,8 @@ added to what the caller passes, everything else is written.
 """
 from __future__ import annotations
 
+import os
+
 import torch
 
 import _bevk as _b
@@ -558,13 +560,58 @@ def forward(value, spatial_shapes, level_start_index, sampling_loc, attn_weight,
     return output
 
 
+MSDA_BACKWARD_MAX_WORKSPACE_ENV = "BEVK_MSDA_BACKWARD_MAX_WORKSPACE"
+
+
+def _workspace_cap(max_workspace_bytes):
+    """The byte cap on the backward's scratch: the argument, else the environment variable
+    BEVK_MSDA_BACKWARD_MAX_WORKSPACE (bytes), else none."""
+    if max_workspace_bytes is not None:
+        return int(max_workspace_bytes)
+    env = os.environ.get(MSDA_BACKWARD_MAX_WORKSPACE_ENV)
+    if env is None or env.strip() == "":
+        return None
+    try:
+        return int(env)
+    except ValueError:
+        raise RuntimeError(f"{MSDA_BACKWARD_MAX_WORKSPACE_ENV}={env!r} is not a byte count")
+
+
+def backward_workspace_bytes(value, num_levels, num_query, num_point, max_workspace_bytes=None):
+    """(bytes the backward will ask for, the least it can run with) for value
+    [B, S, heads, D]: bevk_msda_backward_workspace_bytes, or the least when that is above
+    the cap (_workspace_cap). The least is the fp32 grad_value accumulator of 16-bit types
+    and nothing for fp32 / fp64."""
+    batch, spatial, heads, channels = value.shape
+    full = _b.lib().bevk_msda_backward_workspace_bytes(_b.dtype_code(value), batch, spatial,
+                                                        heads, channels, num_levels, num_query,
+                                                        num_point)
+    if full < 0:
+        raise RuntimeError("msda_backward: invalid sizes")
+    least = value.numel() * 4 if value.dtype in (torch.float16, torch.bfloat16) else 0
+    cap = _workspace_cap(max_workspace_bytes)
+    if cap is not None and full > max(cap, least):
+        return least, least
+    return full, least
+
+
 def backward(value, spatial_shapes, level_start_index, sampling_loc, attn_weight, grad_output,
              grad_value, grad_sampling_loc, grad_attn_weight, im2col_step=64,
-             force_generic_col2im=False):
+             force_generic_col2im=False, max_workspace_bytes=None):
     """MSDA backward (binding_musa.mu:414-543). Fills the caller's tensors:
     grad_value [B, S, heads, D] is ADDED to for fp32/fp64 and overwritten for fp16/bf16
     (accumulated in an fp32 buffer, then narrowed); grad_sampling_loc and
-    grad_attn_weight are written. grad_output [B, Lq, heads*D] may be strided."""
+    grad_attn_weight are written. grad_output [B, Lq, heads*D] may be strided.
+
+    Scratch: with head_dim 32 the fastest kernels (grad_value by a bucket sort of the
+    samples, no per-corner atomics) take bevk_msda_backward_workspace_bytes of device
+    memory, about 12 bytes per (sample, corner row) on top of the fp32 accumulator 16-bit
+    types need (SCA, 6 cameras: 370 MB fp32, 560 MB fp16). When that exceeds
+    max_workspace_bytes (default: the BEVK_MSDA_BACKWARD_MAX_WORKSPACE environment
+    variable; unset = no cap), or its allocation fails, the call passes only the least
+    workspace and the library runs the atomic kernels instead, as the reference does: no
+    scratch for fp32 / fp64, the fp32 grad_value accumulator for fp16 / bf16
+    (binding_musa.mu:456-467). The accumulator is needed whatever the cap."""
     fn = "msda_backward"
     batch, spatial, heads, channels, num_levels, num_query, num_point = _msda_check(
         fn, value, spatial_shapes, level_start_index, sampling_loc, attn_weight)
@@ -584,11 +631,15 @@ def backward(value, spatial_shapes, level_start_index, sampling_loc, attn_weight
     g4 = grad_output.view(batch, num_query, heads, channels)
     sb, sq, sh, sc = g4.stride()
     code = _b.dtype_code(value)
-    nbytes = _b.lib().bevk_msda_backward_workspace_bytes(code, batch, spatial, heads, channels,
-                                                          num_levels, num_query, num_point)
-    if nbytes < 0:
-        raise RuntimeError(f"{fn}: invalid sizes")
-    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=value.device)
+    nbytes, least = backward_workspace_bytes(value, num_levels, num_query, num_point,
+                                             max_workspace_bytes)
+    try:
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=value.device)
+    except torch.OutOfMemoryError:
+        if nbytes <= least:
+            raise
+        nbytes = least
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=value.device)
     _b.call("bevk_msda_backward", code, _b.ptr(value), _b.ptr(spatial_shapes),
             _b.ptr(level_start_index), _b.ptr(sampling_loc), _b.ptr(attn_weight), _b.ptr(g4),
             sb, sq, sh, sc, batch, spatial, heads, channels, num_levels, num_query, num_point,

@@ -3,7 +3,7 @@ naotic/bev-kernels msda_musa_opt2/msda_musa_opt2/dispatch.py:15-69, running on t
 gfx950 kernels of libbevk.so (registered in ``_modulated_deform_conv_ext``)."""
 from __future__ import annotations
 
-from typing import Tuple
+from typing import Optional, Tuple
 
 import torch
 
@@ -42,10 +42,14 @@ def ms_deform_attn_backward(
     *,
     im2col_step: int = 64,
     force_generic_col2im: bool = False,
+    max_workspace_bytes: Optional[int] = None,
 ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Gradients (value, sampling_loc, attn_weight) of ms_deform_attn_forward for
     grad_output [B, Lq, heads * D]. fp32 / fp64, and fp16 / bf16 with fp32 arithmetic and
-    an fp32 grad_value accumulator."""
+    an fp32 grad_value accumulator. max_workspace_bytes (keyword only, not in the
+    reference) caps the scratch: above it the atomic kernels run with the reference's
+    memory use (default: the BEVK_MSDA_BACKWARD_MAX_WORKSPACE environment variable,
+    unset = no cap)."""
     if not torch.cuda.is_available():
         raise RuntimeError("ms_deform_attn_backward requires a HIP device (torch.cuda)")
     grad_value = torch.zeros_like(value)
@@ -53,5 +57,6 @@ def ms_deform_attn_backward(
     grad_attn_weight = torch.zeros_like(attn_weight)
     _ext().backward(value, spatial_shapes, level_start_index, sampling_loc, attn_weight,
                     grad_output, grad_value, grad_sampling_loc, grad_attn_weight,
-                    im2col_step=im2col_step, force_generic_col2im=force_generic_col2im)
+                    im2col_step=im2col_step, force_generic_col2im=force_generic_col2im,
+                    max_workspace_bytes=max_workspace_bytes)
     return grad_value, grad_sampling_loc, grad_attn_weight

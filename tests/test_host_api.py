@@ -143,3 +143,33 @@ def test_baseline_input_generators():
     c = inputs.dcn_inputs("dcn_res4", batch=1)
     assert c["x"].shape == (1, 256, 58, 100) and c["offset"].shape == (1, 18, 58, 100)
     assert abs(c["weight"].std().item() - (2 / 2304) ** 0.5) < 2e-3
+
+
+def test_msda_backward_workspace_cap(monkeypatch):
+    """The backward's scratch choice (host logic, no launch): the sorted path's workspace
+    without a cap; above max_workspace_bytes or BEVK_MSDA_BACKWARD_MAX_WORKSPACE only the
+    least the library runs with (nothing for fp32, the fp32 grad_value accumulator for
+    16-bit types, as binding_musa.mu:456-467 allocates)."""
+    monkeypatch.delenv(ext.MSDA_BACKWARD_MAX_WORKSPACE_ENV, raising=False)
+    B, S, NH, D, L, Q, P = 6, 30825, 8, 32, 4, 10000, 8
+    for dtype, least in ((torch.float32, 0), (torch.float16, B * S * NH * D * 4),
+                         (torch.bfloat16, B * S * NH * D * 4)):
+        value = torch.empty(B, S, NH, D, dtype=dtype, device="meta")
+        full, lo = ext.backward_workspace_bytes(value, L, Q, P)
+        assert lo == least and full > least
+        assert ext.backward_workspace_bytes(value, L, Q, P, max_workspace_bytes=full) == (full, lo)
+        assert ext.backward_workspace_bytes(value, L, Q, P, max_workspace_bytes=full - 1) == (lo, lo)
+        assert ext.backward_workspace_bytes(value, L, Q, P, max_workspace_bytes=0) == (lo, lo)
+        monkeypatch.setenv(ext.MSDA_BACKWARD_MAX_WORKSPACE_ENV, str(full - 1))
+        assert ext.backward_workspace_bytes(value, L, Q, P) == (lo, lo)
+        # the argument wins over the environment
+        assert ext.backward_workspace_bytes(value, L, Q, P, max_workspace_bytes=full) == (full, lo)
+        monkeypatch.setenv(ext.MSDA_BACKWARD_MAX_WORKSPACE_ENV, "lots")
+        with pytest.raises(RuntimeError, match="byte count"):
+            ext.backward_workspace_bytes(value, L, Q, P)
+        monkeypatch.delenv(ext.MSDA_BACKWARD_MAX_WORKSPACE_ENV)
+    # SCA sizes the notes quote: about 370 MB fp32 and 560 MB fp16 for the sorted path
+    f32 = ext.backward_workspace_bytes(torch.empty(B, S, NH, D, device="meta"), L, Q, P)[0]
+    f16 = ext.backward_workspace_bytes(
+        torch.empty(B, S, NH, D, dtype=torch.float16, device="meta"), L, Q, P)[0]
+    assert 300e6 < f32 < 450e6 and 450e6 < f16 < 650e6
