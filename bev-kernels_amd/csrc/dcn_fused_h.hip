@@ -945,6 +945,269 @@ __global__ void __launch_bounds__(kPThreads) dcn_fused_p_kernel(const PParams pp
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// Symmetric persistent kernel (fp16 / bf16, 128 < Cout <= 512, C % 64 == 0): the work
+// split of dcn_fused_p_kernel (one workgroup per CU, NRB 16-row blocks x one 256-column
+// half of Cout, XCD-contiguous row ranges) with eight waves that each do both jobs:
+//   * MFMA: wave w computes columns [32 w, 32 w + 32) of every row block
+//     (v_mfma_f32_16x16x32) from the A tile in LDS, its A fragments read kSAhead
+//     fragments ahead in a fixed order, its B fragments loaded two steps ahead;
+//   * gather: thread t owns the A-tile slots (row t / 8 + 64 i, 16-byte k-vector t % 8)
+//     with one register set of corners per slot; at step k it blends the slot's corners
+//     of step k + 1 into the other A buffer and issues the slot's loads of step k + 2.
+// Why this split (measured on gfx950): one wave issues vector ALU instructions at about
+// one per 8 cycles while two waves on a SIMD reach one per 4, so the blend arithmetic
+// (about 250 instructions per SIMD and K step) runs twice as fast spread over both waves
+// of each SIMD as on one producer wave; and a wave with about one step of gathers in
+// flight (8-12 loads here) keeps the vector-memory path busier than one with two steps
+// (about 40 loads). The price is that every wave reads the whole A tile from LDS.
+// One barrier per K step (64 channels of one tap) hands the A tile over.
+constexpr int kSThreads = 512;
+constexpr int kSAhead = 3;  // A fragments read ahead of their MFMAs
+
+template <int NRB>
+struct SShape {
+  static constexpr int kRows = NRB * 16;
+  static constexpr int kSlots = kRows * (kPBK / 8);
+  static constexpr int kNS = (kSlots + kSThreads - 1) / kSThreads;           // slots per thread
+  static constexpr int kFullWaves = (kSlots - (kNS - 1) * kSThreads) / kWave;  // waves with kNS
+  static_assert(kFullWaves * kWave == kSlots - (kNS - 1) * kSThreads && kFullWaves >= 1,
+                "the last slot set must cover whole waves");
+};
+
+template <typename T, int NRB, int NS>
+__device__ __forceinline__ void dcn_s_body(const HParams &p, const TapGeo *geo,
+                                           T (*As)[NRB * 16 * kPLDA], T *stage, int n0, int nk,
+                                           int lane, int wave, int tid) {
+  using V = Vec<T, 8>;
+  constexpr int KV = kPBK / 8;
+  constexpr int NF = 2 * NRB;        // A fragments per step (k-half x row block)
+  constexpr int NP = NS * 8;         // blend pieces per step (slot x element)
+  const int TT = p.taps;
+  const int spt = p.C / kPBK;        // K steps per tap
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, p.x_bytes);
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, p.w_bytes);
+  const uint32_t xoob = p.x_bytes;
+  const int kv = tid % KV;
+
+  // B fragments of the wave's 32 columns (2 blocks of 16); the K step is the scalar offset.
+  uint32_t bo[kPKH][2];
+#pragma unroll
+  for (int kh = 0; kh < kPKH; ++kh)
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+      bo[kh][cb] = b_frag_offset(n0 + wave * 32 + cb * 16 + (lane & 15), kh, lane, p.nb_total,
+                                 p.kb_total, p.w_bytes);
+  auto issue_b = [&](int ks, int4v (&br)[kPKH][2]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int kh = 0; kh < kPKH; ++kh)
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb)
+        br[kh][cb] = __builtin_amdgcn_raw_buffer_load_b128(
+            wr, bo[kh][cb], (uint32_t)ks * (uint32_t)(kPBK / 16) * 1024u, 0);
+  };
+
+  // Gather slots.
+  uint32_t go[NS][4];   // corner offsets of the slot's current tap (+ k-vector)
+  V ra[NS][4];          // the slot's corners of the next step to blend
+  auto slot_row = [&](int i) __attribute__((always_inline)) { return (tid + i * kSThreads) / KV; };
+  auto issue_slot = [&](int i, int ks) __attribute__((always_inline)) {
+    const int t = ks / spt, cs = ks - t * spt;
+    if (cs == 0) {
+      if (t < TT) {
+        const int4v o = *reinterpret_cast<const int4v *>(geo[slot_row(i) * TT + t].o);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          go[i][q] = (uint32_t)o[q] == xoob ? xoob : (uint32_t)o[q] + (uint32_t)(kv * 8 * sizeof(T));
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) go[i][q] = xoob;
+      }
+    }
+    const uint32_t so = (uint32_t)(cs * kPBK * sizeof(T));
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      ra[i][q] = __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(xr, go[i][q], so, 0));
+  };
+
+  floatx4 acc[NRB][2];
+#pragma unroll
+  for (int i = 0; i < NRB; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  // Step ks: the MFMAs of A buffer ks % 2 (fragment f = kh * NRB + rb read kSAhead
+  // fragments before its MFMAs), with the blend of step ks + 1 into the other buffer
+  // spread over the fragments: piece p (slot p / 8, element p % 8: four fused
+  // multiply-adds in fp32) goes with fragment p * NF / NP; after a slot's eighth element
+  // its A-tile store and its loads of step ks + 2. The order is fixed with sched_barriers
+  // (and each element's sum is pinned where it is computed), so the vector ALU work issues
+  // between the matrix-core instructions. Then B(ks + 2) and the barrier.
+  auto step = [&](int ks, int4v (&br)[kPKH][2]) __attribute__((always_inline)) {
+    const T *tile = &As[ks & 1][0];
+    T *next = &As[(ks + 1) & 1][0];
+    const int tb = min((ks + 1) / spt, TT - 1);  // tap of the step being blended (clamped)
+    int4v af[NF];
+    auto read_frag = [&](int f) __attribute__((always_inline)) {
+      af[f] = *reinterpret_cast<const int4v *>(
+          &tile[a_off((f % NRB) * 16 + (lane & 15), (f / NRB) * 4 + (lane >> 4))]);
+    };
+    float4 w4[NS];
+#pragma unroll
+    for (int i = 0; i < NS; ++i)
+      w4[i] = *reinterpret_cast<const float4 *>(geo[slot_row(i) * TT + tb].w);
+#pragma unroll
+    for (int f = 0; f < kSAhead; ++f) read_frag(f);
+    float bl[8];
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      if (f + kSAhead < NF) read_frag(f + kSAhead);
+      const int kh = f / NRB, rbi = f % NRB;
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb) acc[rbi][cb] = mfma16x16<T>(af[f], br[kh][cb], acc[rbi][cb]);
+#pragma unroll
+      for (int pc = 0; pc < NP; ++pc) {
+        if (pc * NF / NP != f) continue;
+        const int i = pc / 8, e = pc % 8;
+        float sum = __builtin_fmaf(w4[i].x, (float)ra[i][0].v[e], 0.f);
+        sum = __builtin_fmaf(w4[i].y, (float)ra[i][1].v[e], sum);
+        sum = __builtin_fmaf(w4[i].z, (float)ra[i][2].v[e], sum);
+        bl[e] = __builtin_fmaf(w4[i].w, (float)ra[i][3].v[e], sum);
+        asm volatile("" : "+v"(bl[e]));  // computed here, not moved to its use
+        if (e == 7) {
+          V o;
+#pragma unroll
+          for (int u = 0; u < 8; ++u) o.v[u] = static_cast<T>(bl[u]);
+          store_vec<T, 8>(&next[a_off(slot_row(i), kv)], o);
+          issue_slot(i, ks + 2);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    issue_b(ks + 2, br);
+    __syncthreads();
+  };
+
+  int4v br0[kPKH][2], br1[kPKH][2];
+  issue_b(0, br0);
+  issue_b(1, br1);
+  // prologue: A(0) blended here; the loads of step 1 issued
+#pragma unroll
+  for (int i = 0; i < NS; ++i) issue_slot(i, 0);
+#pragma unroll
+  for (int i = 0; i < NS; ++i) {
+    const float4 w = *reinterpret_cast<const float4 *>(geo[slot_row(i) * TT].w);
+    store_vec<T, 8>(&As[0][a_off(slot_row(i), kv)], blend4<T>(ra[i], w.x, w.y, w.z, w.w));
+    issue_slot(i, 1);
+  }
+  __syncthreads();
+  int ks = 0;
+  for (; ks + 2 <= nk; ks += 2) {
+    step(ks, br0);
+    step(ks + 1, br1);
+  }
+  if (ks < nk) step(ks, br0);
+
+  // Epilogue: lane holds column 32 wave + 16 cb + (lane & 15), rows 4 (lane >> 4) + e.
+  const T *bias = static_cast<const T *>(p.bias);
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) {
+    const int c = wave * 32 + cb * 16 + (lane & 15);
+    const float bv = (bias != nullptr && n0 + c < p.Cout) ? (float)bias[n0 + c] : 0.f;
+#pragma unroll
+    for (int rbi = 0; rbi < NRB; ++rbi)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float v = acc[rbi][cb][e] + bv;
+        if (p.relu) v = v < 0.f ? 0.f : v;  // NaN stays NaN, as torch.relu
+        stage[(rbi * 16 + 4 * (lane >> 4) + e) * kPStage + c] = static_cast<T>(v);
+      }
+  }
+}
+
+// MEGA: the one-launch forward, as dcn_fused_p_kernel's: pass 1 (the offset conv of the
+// workgroup's rows, fp32 y with its bias in LDS and, when given, in p.y_out) runs with the
+// producer / consumer roles of dcn_fused_p_kernel, pass 2 with the symmetric body.
+template <typename T, int GEO, int NRB, bool MEGA>
+__global__ void __launch_bounds__(kSThreads) dcn_fused_s_kernel(const PParams pp) {
+  using SH = SShape<NRB>;
+  using PSH = PShape<NRB>;
+  constexpr int kRows = SH::kRows;
+  const HParams &p = pp.h;
+  __shared__ __attribute__((aligned(16))) TapGeo geo[kRows * kMaxTaps];
+  __shared__ __attribute__((aligned(16))) T As[2][kRows * kPLDA];
+  __shared__ __attribute__((aligned(16))) T stage[kRows * kPStage];  // the output tile
+  static_assert(!MEGA || sizeof(As) >= sizeof(float) * kRows * 3 * kMaxTaps,
+                "the offset-conv output must fit in the A ring");
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int bpx = pp.nblocks >> 3;
+  const int xcd = (int)(blockIdx.x & 7);
+  const int xph = 8 / pp.halves;
+  const int half = xcd / xph;
+  const int nbh = pp.nblocks / pp.halves;
+  const int r = (xcd - half * xph) * bpx + (int)(blockIdx.x >> 3);
+  const int rb0 = (int)((int64_t)pp.rb_total * r / nbh);
+  const int nrb = (int)((int64_t)pp.rb_total * (r + 1) / nbh) - rb0;
+  if (nrb < NRB - 1 || nrb > NRB) return;
+  const int n0 = half * kPCols;
+  const int m0 = rb0 * 16;
+  const int nrows = nrb * 16;
+  const int TT = p.taps;
+  const uint32_t xoob = p.x_bytes;
+  const int nk = TT * (p.C / kPBK);
+  float *ys = reinterpret_cast<float *>(&As[0][0]);
+
+  if constexpr (MEGA) {
+    for (int g = tid; g < kRows * TT; g += kSThreads) {
+      const int row = g / TT, t = g - row * TT, m = m0 + row;
+      geo[g] = (row < nrows && m < p.M) ? tap_geo<T, kGeoRegular>(p, nullptr, 0, m, t)
+                                        : empty_geo(xoob);
+    }
+    __syncthreads();
+    if (wave < 4)
+      dcn_p_offset_consumer<T, NRB>(p, As, ys, m0, nrb, nk, lane, wave);
+    else if (wave - 4 < PSH::kLastWaves)
+      dcn_p_producer<T, PSH::kSPT, NRB, true>(p, geo, As, nk, tid - kPProd);
+    else
+      dcn_p_producer<T, PSH::kSPT - 1, NRB, true>(p, geo, As, nk, tid - kPProd);
+    __syncthreads();  // y of every row in ys
+  }
+  for (int g = tid; g < kRows * TT; g += kSThreads) {
+    const int row = g / TT, t = g - row * TT, m = m0 + row;
+    TapGeo G = empty_geo(xoob);
+    if (row < nrows && m < p.M) {
+      if constexpr (MEGA)
+        G = tap_geo<T, kGeoYF32>(p, ys, row, m, t);   // bias already in ys
+      else
+        G = tap_geo<T, GEO>(p, p.off, m, m, t);
+    }
+    geo[g] = G;
+  }
+  __syncthreads();  // MEGA: ys is dead from here, the A ring is written again
+  if (wave < SH::kFullWaves)
+    dcn_s_body<T, NRB, SH::kNS>(p, geo, As, stage, n0, nk, lane, wave, tid);
+  else
+    dcn_s_body<T, NRB, SH::kNS - 1>(p, geo, As, stage, n0, nk, lane, wave, tid);
+  __syncthreads();
+  T *out = static_cast<T *>(p.out);
+  constexpr int kPieces = kPCols / 8;
+  for (int i = tid; i < nrows * kPieces; i += kSThreads) {
+    const int row = i / kPieces, c = (i - row * kPieces) * 8, m = m0 + row;
+    if (m < p.M && n0 + c < p.Cout)
+      __builtin_nontemporal_store(*reinterpret_cast<const int4v *>(&stage[row * kPStage + c]),
+                                  reinterpret_cast<int4v *>(out + (int64_t)m * p.Cout + n0 + c));
+  }
+}
+
+template <typename T, int GEO, bool MEGA>
+hipError_t launch_s_geo(const PParams &pp, hipStream_t stream) {
+  hipLaunchKernelGGL((dcn_fused_s_kernel<T, GEO, 9, MEGA>), dim3(pp.nblocks), dim3(kSThreads),
+                     0, stream, pp);
+  return hipGetLastError();
+}
+
 // The persistent kernel runs one workgroup per CU over one 256-column half of Cout and
 // NRB - 1 or NRB row blocks (NRB = 9: res4-like shapes; NRB = 5: res5-like, Cout 512).
 // The CU count is read once per device (device_cus).
@@ -975,12 +1238,9 @@ PConfig p_config_for(const HParams &p, int geo) {
 
 template <typename T, int GEO, bool MEGA>
 hipError_t launch_p_geo(const PParams &pp, int nrb, hipStream_t stream) {
-  if (nrb == 9)
-    hipLaunchKernelGGL((dcn_fused_p_kernel<T, GEO, 9, MEGA>), dim3(pp.nblocks), dim3(kPThreads),
-                       0, stream, pp);
-  else
-    hipLaunchKernelGGL((dcn_fused_p_kernel<T, GEO, 5, MEGA>), dim3(pp.nblocks), dim3(kPThreads),
-                       0, stream, pp);
+  if (nrb != 5) return hipErrorInvalidValue;  // 9-block ranges run dcn_fused_s_kernel
+  hipLaunchKernelGGL((dcn_fused_p_kernel<T, GEO, 5, MEGA>), dim3(pp.nblocks), dim3(kPThreads), 0,
+                     stream, pp);
   return hipGetLastError();
 }
 
@@ -992,6 +1252,16 @@ hipError_t launch_p(const HParams &h, int geo, const PConfig &c, bool mega,
   pp.rb_total = (h.M + 15) / 16;
   pp.nblocks = c.nblocks;
   pp.halves = c.halves;
+  // 144-row workgroups: the symmetric kernel (the blend arithmetic of 144 rows split over
+  // both waves of each SIMD: res4 fp16 69.2 -> 67.3 us, bf16 77.5 -> 71.5 us); 80-row
+  // workgroups keep the producer / consumer kernel (the symmetric one measured res5 fp16
+  // 76.4 -> 78.1 us, bf16 78.3 -> 83.4 us: less blend work per SIMD, twice the A-tile reads).
+  if (c.nrb == 9) {
+    if (mega) return launch_s_geo<T, kGeoYF32, true>(pp, stream);
+    if (geo == kGeoY) return launch_s_geo<T, kGeoY, false>(pp, stream);
+    if (geo == kGeoYF32) return launch_s_geo<T, kGeoYF32, false>(pp, stream);
+    return launch_s_geo<T, kGeoMask, false>(pp, stream);
+  }
   if (mega) return launch_p_geo<T, kGeoYF32, true>(pp, c.nrb, stream);
   if (geo == kGeoY) return launch_p_geo<T, kGeoY, false>(pp, c.nrb, stream);
   if (geo == kGeoYF32) return launch_p_geo<T, kGeoYF32, false>(pp, c.nrb, stream);

@@ -1,0 +1,100 @@
+"""The one-launch DCN forward and its callers at the benchmarked sizes, where the K loop
+is long and (res5) Cout spans two 256-column halves:
+
+  * res4: B = 6, C = Cout = 256, 58 x 100 (36 K steps of 64 channels per pass);
+  * res5: B = 6, C = Cout = 512, 29 x 50 (72 K steps; the two column halves each run the
+    offset-conv pass and write y).
+
+fused_dcn_mega_forward_nhwc (fused_tl.py:565-766), dcn_split_nhwc with the FrozenBN +
+ReLU epilogue (dcn_split_nhwc.py:178-204) and ModulatedDeformConv2dPack(backend='fuse_c')
+on a 256-channel layer are run on the whole batch; the first and the last image are
+compared element by element with the float64 oracle (offset conv in float64, deformable
+taps rounded to the input dtype as the kernel's A tile, sum in float64), and the fp32 y
+the kernel writes for the backward with the float64 offset conv of the whole batch."""
+import pytest
+import torch
+
+from _tol import check
+from oracle import dcn as od
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda")
+
+SHAPES = {"res4": (6, 256, 256, 58, 100), "res5": (6, 512, 512, 29, 50)}
+IMAGES = [0, 5]
+
+
+def _problem(b, cin, cout, h, w, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(b, h, w, cin, generator=g).to(dtype)
+    # a trained offset conv gives offsets of a few pixels and mask logits around 0
+    w_off = ((1.5 / (9 * cin) ** 0.5) * torch.randn(27, cin, 3, 3, generator=g)).to(dtype)
+    b_off = 0.5 * torch.randn(27, generator=g)
+    weight = ((1.0 / (9 * cin) ** 0.5) * torch.randn(cout, cin, 3, 3, generator=g)).to(dtype)
+    bias = (0.1 * torch.randn(cout, generator=g)).to(dtype)
+    return x, w_off, b_off, weight, bias
+
+
+def _ref(x, w_off, b_off, weight, bias, dtype, relu=False):
+    return od.mega_forward_nhwc(x[IMAGES].double(), w_off.double(), b_off.double(),
+                                weight.double(), None if bias is None else bias.double(),
+                                1, 1, 1, col_dtype=dtype, relu=relu)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+@pytest.mark.parametrize("cfg", ["res4", "res5"])
+def test_mega_forward_full_size(cfg, dtype):
+    from modulated_deform_conv import dcn_split_nhwc as dsn
+    from modulated_deform_conv import fused_tl
+    x, w_off, b_off, weight, bias = _problem(*SHAPES[cfg], dtype, seed=31)
+    dv = [t.to(DEV) for t in (x, w_off, b_off, weight, bias)]
+    out = fused_tl.fused_dcn_mega_forward_nhwc(*dv, 1, 1, 1)
+    out2, y = dsn.mega_forward(*dv, 1, 1, 1)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2)
+    y_ref = od.offset_conv_nhwc(x.double(), w_off.double(), b_off.double(), 1, 1, 1)
+    check(y.cpu(), y_ref, torch.float32, f"{cfg} {dtype} y")
+    check(out[IMAGES].cpu(), _ref(x, w_off, b_off, weight, bias, dtype), dtype,
+          f"{cfg} {dtype} one launch")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+@pytest.mark.parametrize("cfg", ["res4", "res5"])
+def test_split_bn_relu_full_size(cfg, dtype):
+    """dcn_split_nhwc: FrozenBN folded into the packed weight and bias, ReLU in the store."""
+    from modulated_deform_conv import dcn_split_nhwc as dsn
+    b, cin, cout, h, w = SHAPES[cfg]
+    x, w_off, b_off, weight, bias = _problem(b, cin, cout, h, w, dtype, seed=37)
+    g = torch.Generator().manual_seed(5)
+    scale = 0.5 + torch.rand(cout, generator=g)
+    shift = 0.2 * torch.randn(cout, generator=g)
+    out = dsn.dcn_split_nhwc(*(t.to(DEV) for t in (x, w_off, b_off, weight, bias)), 1, 1, 1,
+                             scale.to(DEV), shift.to(DEV), True)
+    torch.cuda.synchronize()
+    assert (out >= 0).all()
+    w_eff = (weight.double() * scale.to(dtype).double().view(-1, 1, 1, 1)).to(dtype)
+    b_eff = (shift + bias.float() * scale).to(dtype)
+    check(out[IMAGES].cpu(), _ref(x, w_off, b_off, w_eff, b_eff, dtype, relu=True), dtype,
+          f"{cfg} {dtype} bn relu")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+def test_pack_fuse_c_256_channels(dtype):
+    """ModulatedDeformConv2dPack(backend='fuse_c') on a res4 layer (NCHW in and out)."""
+    from modulated_deform_conv import ModulatedDeformConv2dPack
+    torch.manual_seed(41)
+    mod = ModulatedDeformConv2dPack(256, 256, 3, stride=1, padding=1, backend="fuse_c")
+    with torch.no_grad():
+        mod.conv_offset.weight.normal_(0, 1.5 / (9 * 256) ** 0.5)
+        mod.conv_offset.bias.normal_(0, 0.5)
+        mod.weight.normal_(0, 1.0 / (9 * 256) ** 0.5)
+        mod.bias.normal_(0, 0.1)
+    mod = mod.to(dtype).to(DEV)
+    x = torch.randn(6, 256, 58, 100).to(dtype)
+    with torch.no_grad():
+        out = mod(x.to(DEV))
+    torch.cuda.synchronize()
+    x_nhwc = x.permute(0, 2, 3, 1)
+    ref = _ref(x_nhwc, mod.conv_offset.weight.cpu(), mod.conv_offset.bias.float().cpu(),
+               mod.weight.cpu(), mod.bias.cpu(), dtype)
+    check(out[IMAGES].permute(0, 2, 3, 1).cpu(), ref, dtype, f"pack fuse_c {dtype}")
