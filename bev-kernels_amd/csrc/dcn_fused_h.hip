@@ -545,10 +545,11 @@ hipError_t launch_tt(const HParams &p, int geo, hipStream_t stream) {
 }
 
 // ---------------------------------------------------------------------------------------
-// Persistent, row-balanced variant (128 < Cout <= 256, C % 64 == 0). One workgroup of 8
-// waves per CU owns a contiguous range of 8-9 blocks of 16 output rows (all of M split
-// evenly over the CUs, so no CU runs a second round) and all BN = 256 output channels for
-// the whole K loop. The waves specialise: waves 0-3 ("consumers") run the MFMAs, wave c
+// Persistent, row-balanced variant (128 < Cout <= 512, C % 64 == 0), for row chunks of at
+// most 5 blocks (80-row tiles; larger chunks run dcn_fused_s_kernel). One workgroup of 8
+// waves per CU owns contiguous chunks of 16-row blocks of M (p_config_for) and all BN = 256
+// output channels of one column half for the whole K loop. The waves specialise: waves
+// 0-3 ("consumers") run the MFMAs, wave c
 // computing columns [64 c, 64 c + 64) of every row block with v_mfma_f32_16x16x32 and
 // loading its B fragments from the fragment-packed weight one step ahead; waves 4-7
 // ("producers") gather the four corners of every (row, 16-byte k-vector) slot two steps
@@ -600,8 +601,11 @@ template <> __device__ __forceinline__ floatx4 mfma16x16<bf16>(int4v a, int4v b,
 struct PParams {
   HParams h;
   int rb_total;  // 16-row blocks of M
-  int nblocks;   // workgroups (a multiple of 8)
+  int nblocks;   // workgroups resident at once, one per CU (a multiple of 8)
   int halves;    // 256-column halves of Cout (1 or 2): XCDs 0-3 take half 0, 4-7 half 1
+  int rounds;    // the grid is nblocks * rounds workgroups, one row chunk each: each
+                 // half's blocks are cut into rounds * nblocks / halves balanced chunks of
+                 // at most NRB blocks
 };
 
 // B fragment of v_mfma_f32_16x16x32 read from the 32x32x16 fragment packing: lane l takes
@@ -868,24 +872,25 @@ __global__ void __launch_bounds__(kPThreads) dcn_fused_p_kernel(const PParams pp
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  // XCD-contiguous row ranges: block b runs on XCD b % 8. With two column halves, XCDs
-  // 0-3 take half 0 and 4-7 half 1, so each XCD's L2 holds one half of the weight.
-  const int bpx = pp.nblocks >> 3;
+  // Workgroup b runs on XCD b % 8; XCD x takes a contiguous range of its half's chunks, so
+  // the image rows its gathers touch stay in its L2. With two column halves XCDs 0-3 take
+  // half 0 and 4-7 half 1, so each XCD's L2 holds one half of the weight.
+  const int bpx = (int)(gridDim.x >> 3);               // workgroups per XCD
   const int xcd = (int)(blockIdx.x & 7);
   const int xph = 8 / pp.halves;                       // XCDs per half
   const int half = xcd / xph;
-  const int nbh = pp.nblocks / pp.halves;              // workgroups per half
-  const int r = (xcd - half * xph) * bpx + (int)(blockIdx.x >> 3);
-  const int rb0 = (int)((int64_t)pp.rb_total * r / nbh);
-  const int nrb = (int)((int64_t)pp.rb_total * (r + 1) / nbh) - rb0;  // NRB - 1 or NRB
-  if (nrb < NRB - 1 || nrb > NRB) return;
+  const int nch = (int)gridDim.x / pp.halves;          // row chunks per half
+  const int j = (xcd - half * xph) * bpx + (int)(blockIdx.x >> 3);
   const int n0 = half * kPCols;
-  const int m0 = rb0 * 16;
-  const int nrows = nrb * 16;
   const int TT = p.taps;
   const uint32_t xoob = p.x_bytes;
   const int nk = TT * (p.C / kPBK);
   float *ys = reinterpret_cast<float *>(&As[0][0]);
+  const int rb0 = (int)((int64_t)pp.rb_total * j / nch);
+  const int nrb = (int)((int64_t)pp.rb_total * (j + 1) / nch) - rb0;  // at most NRB
+  if (nrb <= 0) return;
+  const int m0 = rb0 * 16;
+  const int nrows = nrb * 16;
 
   if constexpr (MEGA) {
     // Pass 1: the offset conv. Plain-convolution geometry (one pixel per row and tap).
@@ -899,7 +904,7 @@ __global__ void __launch_bounds__(kPThreads) dcn_fused_p_kernel(const PParams pp
       dcn_p_offset_consumer<T, NRB>(p, As, ys, m0, nrb, nk, lane, wave);
     else if (wave - 4 < SH::kLastWaves)
       dcn_p_producer<T, SH::kSPT, NRB, true>(p, geo, As, nk, tid - kPProd);
-    else
+    else if constexpr (SH::kLastWaves < 4)
       dcn_p_producer<T, SH::kSPT - 1, NRB, true>(p, geo, As, nk, tid - kPProd);
     __syncthreads();  // y of every row in ys
   }
@@ -929,7 +934,7 @@ __global__ void __launch_bounds__(kPThreads) dcn_fused_p_kernel(const PParams pp
     dcn_p_consumer<T, NRB>(p, As, stage, n0, nk, lane, wave);
   else if (wave - 4 < SH::kLastWaves)
     dcn_p_producer<T, SH::kSPT, NRB, false>(p, geo, As, nk, tid - kPProd);
-  else
+  else if constexpr (SH::kLastWaves < 4)
     dcn_p_producer<T, SH::kSPT - 1, NRB, false>(p, geo, As, nk, tid - kPProd);
   // The output tile: full 16-byte pieces of the workgroup's rows (Cout % 8 == 0 and a
   // 16-byte aligned output, checked on the host: a piece is wholly inside or outside),
@@ -1142,22 +1147,22 @@ __global__ void __launch_bounds__(kSThreads) dcn_fused_s_kernel(const PParams pp
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int bpx = pp.nblocks >> 3;
+  const int bpx = (int)(gridDim.x >> 3);  // workgroups per XCD (as dcn_fused_p_kernel)
   const int xcd = (int)(blockIdx.x & 7);
   const int xph = 8 / pp.halves;
   const int half = xcd / xph;
-  const int nbh = pp.nblocks / pp.halves;
-  const int r = (xcd - half * xph) * bpx + (int)(blockIdx.x >> 3);
-  const int rb0 = (int)((int64_t)pp.rb_total * r / nbh);
-  const int nrb = (int)((int64_t)pp.rb_total * (r + 1) / nbh) - rb0;
-  if (nrb < NRB - 1 || nrb > NRB) return;
+  const int nch = (int)gridDim.x / pp.halves;  // row chunks per half
+  const int j = (xcd - half * xph) * bpx + (int)(blockIdx.x >> 3);
   const int n0 = half * kPCols;
-  const int m0 = rb0 * 16;
-  const int nrows = nrb * 16;
   const int TT = p.taps;
   const uint32_t xoob = p.x_bytes;
   const int nk = TT * (p.C / kPBK);
   float *ys = reinterpret_cast<float *>(&As[0][0]);
+  const int rb0 = (int)((int64_t)pp.rb_total * j / nch);
+  const int nrb = (int)((int64_t)pp.rb_total * (j + 1) / nch) - rb0;  // at most NRB
+  if (nrb <= 0) return;
+  const int m0 = rb0 * 16;
+  const int nrows = nrb * 16;
 
   if constexpr (MEGA) {
     for (int g = tid; g < kRows * TT; g += kSThreads) {
@@ -1202,17 +1207,29 @@ __global__ void __launch_bounds__(kSThreads) dcn_fused_s_kernel(const PParams pp
 }
 
 template <typename T, int GEO, bool MEGA>
-hipError_t launch_s_geo(const PParams &pp, hipStream_t stream) {
-  hipLaunchKernelGGL((dcn_fused_s_kernel<T, GEO, 9, MEGA>), dim3(pp.nblocks), dim3(kSThreads),
-                     0, stream, pp);
+hipError_t launch_s_geo(const PParams &pp, int nrb, hipStream_t stream) {
+  const dim3 g(pp.nblocks * pp.rounds), b(kSThreads);
+  switch (nrb) {
+    case 6: hipLaunchKernelGGL((dcn_fused_s_kernel<T, GEO, 6, MEGA>), g, b, 0, stream, pp); break;
+    case 7: hipLaunchKernelGGL((dcn_fused_s_kernel<T, GEO, 7, MEGA>), g, b, 0, stream, pp); break;
+    case 8: hipLaunchKernelGGL((dcn_fused_s_kernel<T, GEO, 8, MEGA>), g, b, 0, stream, pp); break;
+    case 9: hipLaunchKernelGGL((dcn_fused_s_kernel<T, GEO, 9, MEGA>), g, b, 0, stream, pp); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
-// The persistent kernel runs one workgroup per CU over one 256-column half of Cout and
-// NRB - 1 or NRB row blocks (NRB = 9: res4-like shapes; NRB = 5: res5-like, Cout 512).
-// The CU count is read once per device (device_cus).
+// The persistent kernels run one workgroup per CU over one 256-column half of Cout. The
+// 16-row blocks of M are cut into `rounds` balanced chunks per CU (the grid has rounds
+// workgroups per CU, one chunk each), rounds chosen so a chunk has at most 9 blocks, and
+// the tile is sized to the largest chunk (NRB blocks,
+// so a chunk leaves at most one block of its tile with zero geometry): NRB 6-9 runs the
+// symmetric kernel (dcn_fused_s_kernel), NRB 2-5 the producer / consumer kernel
+// (dcn_fused_p_kernel). So any M runs on every CU (B = 6 res4: one round of 8-9 blocks;
+// res5, two column halves: one round of 4-5 blocks). The CU count is read once per device
+// (device_cus).
 struct PConfig {
-  int nblocks = 0, nrb = 0, halves = 0;
+  int nblocks = 0, nrb = 0, halves = 0, rounds = 0;
 };
 PConfig p_config_for(const HParams &p, int geo) {
   PConfig c;
@@ -1221,26 +1238,30 @@ PConfig p_config_for(const HParams &p, int geo) {
   if (p.Cout % 8 != 0 || reinterpret_cast<uintptr_t>(p.out) % 16 != 0) return c;
   const int cus = device_cus();
   const int nb = (cus / 8) * 8;
+  if (nb < 8) return c;
   const int halves = p.Cout > kPCols ? 2 : 1;
   const int64_t rb = (int64_t)((p.M + 15) / 16);
   const int64_t nbh = nb / halves;
-  if (nb < 8) return c;
-  for (int nrb : {9, 5}) {
-    if (rb >= nbh * (nrb - 1) && rb <= nbh * nrb) {
-      c.nblocks = nb;
-      c.nrb = nrb;
-      c.halves = halves;
-      return c;
-    }
-  }
+  const int64_t rounds = std::max<int64_t>(1, (rb + nbh * 9 - 1) / (nbh * 9));
+  const int64_t per = (rb + nbh * rounds - 1) / (nbh * rounds);  // largest chunk
+  if (rounds > (1 << 20)) return c;
+  c.nblocks = nb;
+  c.nrb = (int)std::max<int64_t>(2, per);
+  c.halves = halves;
+  c.rounds = (int)rounds;
   return c;
 }
 
 template <typename T, int GEO, bool MEGA>
 hipError_t launch_p_geo(const PParams &pp, int nrb, hipStream_t stream) {
-  if (nrb != 5) return hipErrorInvalidValue;  // 9-block ranges run dcn_fused_s_kernel
-  hipLaunchKernelGGL((dcn_fused_p_kernel<T, GEO, 5, MEGA>), dim3(pp.nblocks), dim3(kPThreads), 0,
-                     stream, pp);
+  const dim3 g(pp.nblocks * pp.rounds), b(kPThreads);
+  switch (nrb) {
+    case 2: hipLaunchKernelGGL((dcn_fused_p_kernel<T, GEO, 2, MEGA>), g, b, 0, stream, pp); break;
+    case 3: hipLaunchKernelGGL((dcn_fused_p_kernel<T, GEO, 3, MEGA>), g, b, 0, stream, pp); break;
+    case 4: hipLaunchKernelGGL((dcn_fused_p_kernel<T, GEO, 4, MEGA>), g, b, 0, stream, pp); break;
+    case 5: hipLaunchKernelGGL((dcn_fused_p_kernel<T, GEO, 5, MEGA>), g, b, 0, stream, pp); break;
+    default: return hipErrorInvalidValue;  // 6-9 blocks run dcn_fused_s_kernel
+  }
   return hipGetLastError();
 }
 
@@ -1252,15 +1273,16 @@ hipError_t launch_p(const HParams &h, int geo, const PConfig &c, bool mega,
   pp.rb_total = (h.M + 15) / 16;
   pp.nblocks = c.nblocks;
   pp.halves = c.halves;
-  // 144-row workgroups: the symmetric kernel (the blend arithmetic of 144 rows split over
-  // both waves of each SIMD: res4 fp16 69.2 -> 67.3 us, bf16 77.5 -> 71.5 us); 80-row
-  // workgroups keep the producer / consumer kernel (the symmetric one measured res5 fp16
-  // 76.4 -> 78.1 us, bf16 78.3 -> 83.4 us: less blend work per SIMD, twice the A-tile reads).
-  if (c.nrb == 9) {
-    if (mega) return launch_s_geo<T, kGeoYF32, true>(pp, stream);
-    if (geo == kGeoY) return launch_s_geo<T, kGeoY, false>(pp, stream);
-    if (geo == kGeoYF32) return launch_s_geo<T, kGeoYF32, false>(pp, stream);
-    return launch_s_geo<T, kGeoMask, false>(pp, stream);
+  pp.rounds = c.rounds;
+  // 6-9 blocks: the symmetric kernel (the blend arithmetic of 144 rows split over both
+  // waves of each SIMD: res4 fp16 69.2 -> 67.3 us, bf16 77.5 -> 71.5 us); up to 5 blocks
+  // the producer / consumer kernel (the symmetric one measured res5 fp16 76.4 -> 78.1 us,
+  // bf16 78.3 -> 83.4 us: less blend work per SIMD, twice the A-tile reads).
+  if (c.nrb >= 6) {
+    if (mega) return launch_s_geo<T, kGeoYF32, true>(pp, c.nrb, stream);
+    if (geo == kGeoY) return launch_s_geo<T, kGeoY, false>(pp, c.nrb, stream);
+    if (geo == kGeoYF32) return launch_s_geo<T, kGeoYF32, false>(pp, c.nrb, stream);
+    return launch_s_geo<T, kGeoMask, false>(pp, c.nrb, stream);
   }
   if (mega) return launch_p_geo<T, kGeoYF32, true>(pp, c.nrb, stream);
   if (geo == kGeoY) return launch_p_geo<T, kGeoY, false>(pp, c.nrb, stream);

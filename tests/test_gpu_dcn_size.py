@@ -98,3 +98,41 @@ def test_pack_fuse_c_256_channels(dtype):
     ref = _ref(x_nhwc, mod.conv_offset.weight.cpu(), mod.conv_offset.bias.float().cpu(),
                mod.weight.cpu(), mod.bias.cpu(), dtype)
     check(out[IMAGES].permute(0, 2, 3, 1).cpu(), ref, dtype, f"pack fuse_c {dtype}")
+
+
+# Shapes off the B = 6 benchmark: (batch, C, Cout, H, W). On a 256-CU device: B=1 res4
+# (363 row blocks, chunks of 1-2 blocks, 80-row tiles), B=4 res4 (1450 blocks, chunks of
+# 5-6, 144-row tiles), B=8 res4 (2900 blocks: two chunks per workgroup), B=1 res5 (two
+# column halves, 91 blocks: most chunks of one block, some workgroups idle), a 2 x 9 x 7
+# map (most chunks empty) and an odd width with Cout 320.
+GENERAL = [(1, 256, 256, 58, 100), (4, 256, 256, 58, 100), (8, 256, 256, 58, 100),
+           (1, 512, 512, 29, 50), (2, 64, 192, 9, 7), (3, 128, 320, 37, 61)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+@pytest.mark.parametrize("shape", GENERAL, ids=lambda s: "x".join(map(str, s)))
+def test_persistent_schedule_any_rows(shape, dtype):
+    """The chunked persistent schedule at row counts off the benchmark bands: the fused
+    forward (offsets and mask given) and the one-launch forward, every pixel against the
+    float64 oracle (images 0 and last for the large batches)."""
+    from modulated_deform_conv import fused_tl
+    b, cin, cout, h, w = shape
+    x, w_off, b_off, weight, bias = _problem(b, cin, cout, h, w, dtype, seed=sum(shape))
+    imgs = [0, b - 1] if b > 2 else list(range(b))
+    dv = [t.to(DEV) for t in (x, w_off, b_off, weight, bias)]
+    out = fused_tl.fused_dcn_mega_forward_nhwc(*dv, 1, 1, 1)
+    torch.cuda.synchronize()
+    ref = od.mega_forward_nhwc(x[imgs].double(), w_off.double(), b_off.double(),
+                               weight.double(), bias.double(), 1, 1, 1, col_dtype=dtype)
+    check(out[imgs].cpu(), ref, dtype, f"one launch {shape}")
+    # fused kernel with offsets and mask from the float64 offset conv, rounded to dtype
+    y = od.offset_conv_nhwc(x.double(), w_off.double(), b_off.double(), 1, 1, 1)
+    off, msk = od.split_y_nhwc(y, 9)
+    off, msk = off.to(dtype), msk.to(dtype)
+    out = fused_tl.fused_dcn_forward_nhwc(x.to(DEV), off.to(DEV), msk.to(DEV), weight.to(DEV),
+                                          bias.to(DEV), 1, 1, 1)
+    torch.cuda.synchronize()
+    ref = od.forward_nhwc(x[imgs].double(), off[imgs].double(), msk[imgs].double(),
+                          weight.double(), bias.double(), 1, 1, 1, col_dtype=dtype,
+                          coord_dtype=torch.float32)
+    check(out[imgs].cpu(), ref, dtype, f"fused {shape}")

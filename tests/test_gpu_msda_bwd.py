@@ -614,3 +614,41 @@ def test_gradcheck_fp64():
         lambda v, loc, a: fn(v, dd["spatial_shapes"], dd["level_start_index"], loc, a, 64),
         (dd["value"].requires_grad_(True), dd["sampling_loc"].requires_grad_(True),
          dd["attn_weight"].requires_grad_(True)), eps=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16], ids=["fp32", "fp16"])
+def test_backward_workspace_cap(dtype, monkeypatch):
+    """ms_deform_attn_backward with the sorted path's workspace (no cap) and with
+    max_workspace_bytes=0 (the atomic kernels with the reference's memory use: nothing for
+    fp32, the fp32 grad_value accumulator for fp16), and with the cap from
+    BEVK_MSDA_BACKWARD_MAX_WORKSPACE: all three against the oracle; the capped calls'
+    peak device memory is below the uncapped call's by about the sorted buffers."""
+    import _modulated_deform_conv_ext as ext
+    monkeypatch.delenv(ext.MSDA_BACKWARD_MAX_WORKSPACE_ENV, raising=False)
+    d = inputs.msda_inputs("msda_sca", scale_q=0.05)
+    go = _grad_output(d)
+    ref = _ref(d, go, dtype)
+    value = d["value"].to(dtype)
+    L, Q, P = d["sampling_loc"].shape[3], d["sampling_loc"].shape[1], d["sampling_loc"].shape[4]
+    full, least = ext.backward_workspace_bytes(value, L, Q, P)
+    assert full > least
+
+    def run_peak(**kw):
+        dd = _dev(d, dtype)
+        g = go.to(dtype).to(DEV)
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats()
+        base = torch.cuda.memory_allocated()
+        got = _api().ms_deform_attn_backward(**dd, grad_output=g, **kw)
+        torch.cuda.synchronize()
+        return [t.cpu() for t in got], torch.cuda.max_memory_allocated() - base
+
+    got, peak_full = run_peak()
+    _check3(got, ref, dtype, "sorted path")
+    got, peak_capped = run_peak(max_workspace_bytes=0)
+    _check3(got, ref, dtype, "capped")
+    monkeypatch.setenv(ext.MSDA_BACKWARD_MAX_WORKSPACE_ENV, str(full - 1))
+    got, peak_env = run_peak()
+    _check3(got, ref, dtype, "capped from the environment")
+    assert peak_full - peak_capped >= 0.9 * (full - least), (peak_full, peak_capped, full, least)
+    assert peak_env == peak_capped
