@@ -10,7 +10,8 @@ Len_q 10000, 8 heads x 32, 8 points), fp32, with inputs resident in HBM:
              read once, output written once: 435.15 MB) / mean kernel time
   roofline   the same figure against 8 TB/s, kernel time from HIP events on the stream
              the kernel runs on; `traffic` from the committed rocprofv3 counter summary
-  secondary  the fused NHWC DCNv2 res4 fp16 forward in MFMA TFLOP/s (2*M*K*Cout flops)
+  secondary  the fused NHWC DCNv2 res4 fp16 forward in MFMA TFLOP/s (2*M*K*Cout flops),
+             timed like a configs row (>= 100 launches; mean and median)
   configs    every BASELINE configuration x dtype: us, GB/s or TFLOP/s, roofline fraction;
              the backward kernels (MSDA backward, DCN NHWC column-to-image) in GB/s of
              compulsory bytes
@@ -112,15 +113,16 @@ def msda_case(name, dtype, cache):
     return (lambda: ext.forward(v, ss, lsi, loc, att, 64, False)), nbytes
 
 
-def dcn_fused_case(name, dtype, cache):
+def dcn_fused_case(name, dtype, cache, batch=None):
     """Fused NHWC kernel call of one DCN configuration (weight packed once, untimed, as a
-    module does on its first call)."""
+    module does on its first call); batch overrides the configuration's image count."""
     import torch
     import _modulated_deform_conv_ext as ext
     from oracle import inputs
-    if name not in cache:
-        cache[name] = inputs.nchw_to_nhwc(inputs.dcn_inputs(name))
-    d = cache[name]
+    key = name if batch is None else f"{name}_b{batch}"
+    if key not in cache:
+        cache[key] = inputs.nchw_to_nhwc(inputs.dcn_inputs(name, batch=batch))
+    d = cache[key]
     dev = torch.device("cuda")
     x = d["x"].to(dtype).to(dev)
     off = d["offset"].to(dtype).to(dev)
@@ -380,7 +382,8 @@ def main():
         if kind == "msda":
             fn, _ = msda_case(name, dtype_of(dt), cache)
         elif kind == "dcn":
-            fn, _ = dcn_fused_case(name, dtype_of(dt), cache)
+            dt, _, b = dt.partition(":")
+            fn, _ = dcn_fused_case(name, dtype_of(dt), cache, batch=int(b) if b else None)
         elif kind == "dcn_nchw":
             fn, _ = dcn_nchw_case(name, cache)
         elif kind == "dcn_mega":
@@ -412,9 +415,10 @@ def main():
     dcn_traffic = read_counters(DCN_COUNTER_FILE)
     warm_us = Timer(cold=False).run(fn, steps, warmup)[0]
 
-    # ---- secondary: DCN res4 fp16 fused -----------------------------------------------
+    # ---- secondary: DCN res4 fp16 fused, on the configs protocol (>= 100 launches) ------
+    reps, wu = max(100, steps), max(10, warmup)   # per row: >= 100 timed after >= 10
     dfn, flops = dcn_fused_case("dcn_res4", torch.float16, cache)
-    d_mean, d_med, _ = timer.run(dfn, steps, warmup)
+    d_mean, d_med, _ = timer.run(dfn, reps, wu)
     tflops = flops / (d_mean * 1e-6) / 1e12
 
     line = {
@@ -441,7 +445,8 @@ def main():
                      "traffic": None if traffic is None else round(traffic)},
         "secondary": {
             "metric": "DCNv2 NHWC fused forward, res4 (B=6, 256->256, 58x100), fp16",
-            "us": round(d_mean, 2), "value": round(tflops, 2), "unit": "TFLOP/s",
+            "us": round(d_mean, 2), "median_us": round(d_med, 2), "launches": reps,
+            "value": round(tflops, 2), "unit": "TFLOP/s",
             "roofline": {"bound": "mfma", "achieved": round(tflops, 2),
                          "peak": MFMA_PEAK_TFLOPS["fp16"], "unit": "TFLOP/s",
                          "frac": round(tflops / MFMA_PEAK_TFLOPS["fp16"], 4),
@@ -450,7 +455,6 @@ def main():
 
     if not args.no_configs:
         rows = []
-        reps, wu = max(100, steps), max(10, warmup)   # per row: >= 100 timed after >= 10
         for name in ("msda_sca", "msda_tsa", "msda_detr"):
             for dt in ("fp32", "fp16", "bf16"):
                 f, nb = msda_case(name, dtype_of(dt), cache)
@@ -479,6 +483,14 @@ def main():
                 rows.append({"config": name + "_mega_one_launch", "dtype": dt,
                              "us": round(m, 2), "TFLOP/s": round(tf, 2),
                              "frac_mfma": round(tf / MFMA_PEAK_TFLOPS[dt], 4)})
+            # the same layer at other batch sizes (the persistent schedule at any row count)
+            for b in ((1, 4) if name == "dcn_res4" else (1,)):
+                f, fl = dcn_fused_case(name, torch.float16, cache, batch=b)
+                m, _, _ = timer.run(f, reps, wu)
+                tf = fl / (m * 1e-6) / 1e12
+                rows.append({"config": f"{name}_nhwc_fused_b{b}", "dtype": "fp16",
+                             "us": round(m, 2), "TFLOP/s": round(tf, 2),
+                             "frac_mfma": round(tf / MFMA_PEAK_TFLOPS["fp16"], 4)})
             f, nb = dcn_front_case(name, dtype_of("fp16"), cache)
             m, _, _ = timer.run(f, reps, wu)
             g = nb / (m * 1e-6) / 1e9

@@ -1376,13 +1376,18 @@ hipError_t launch_dcn_fused_h(int dtype, const DcnGeom &g, int channels_out, con
   }
 }
 
+// The one-launch form runs where Cout fits one 256-column half. With two halves every
+// workgroup pair would compute the offset conv of the same rows, so the caller runs the
+// offset conv once into y and then the fused kernel reading y: res5 fp16 113 -> 104 us,
+// bf16 117 -> 106 us (res4, one half, stays in one launch: 88 us against about 94).
 bool dcn_mega_supported(int dtype, const DcnGeom &g, int channels_out, const void *out) {
   if ((dtype != 1 && dtype != 2) || g.deformable_group != 1 ||
       g.kernel_h * g.kernel_w > kMaxTaps)
     return false;
   const HParams p = make_hparams(dtype, g, channels_out, nullptr, nullptr, nullptr, nullptr,
                                  nullptr, const_cast<void *>(out), nullptr, false);
-  return p_config_for(p, kGeoYF32).nblocks != 0;
+  const PConfig c = p_config_for(p, kGeoYF32);
+  return c.nblocks != 0 && c.halves == 1;
 }
 
 hipError_t launch_dcn_mega(int dtype, const DcnGeom &g, int channels_out, const void *x,

@@ -250,10 +250,11 @@ int bevk_dcn_offset_conv_nhwc(int dtype, const void *data_im, const void *w_off_
  *   sigmoid(y[:, 2T:]), then out = deformable conv (+ bias) as bevk_dcn_fused_fwd_nhwc,
  *   with max(out, 0) when act_relu != 0.
  *   weight_packed / bias / out: as bevk_dcn_fused_fwd_nhwc (channels_out may be 0: y only).
- * F16 / BF16 shapes that take the persistent kernel (C % 64 == 0, 128 < Cout <= 512, the
- * row counts of the BEVFormer res4/res5 layers on a 256-CU device) run as ONE launch: y
- * stays in LDS for the gather and never returns from HBM. Other shapes run the offset conv
- * and then the fused kernel reading y. dtypes F32, F16, BF16; dg == 1. */
+ * F16 / BF16 shapes that take the persistent kernels with one column half (C % 64 == 0,
+ * 128 < Cout <= 256, Cout % 8 == 0, any row count) run as ONE launch: y stays in LDS for
+ * the gather and never returns from HBM. Other shapes (Cout > 256 among them, where one
+ * launch would compute the offset conv once per column half) run the offset conv and then
+ * the fused kernel reading y. dtypes F32, F16, BF16; dg == 1. */
 int bevk_dcn_mega_fwd_nhwc(int dtype, const void *data_im, const void *w_off_packed,
                            const float *b_off, const void *weight_packed, const void *bias,
                            int batch_size, int channels, int height_im, int width_im,
