@@ -643,8 +643,6 @@ __device__ __forceinline__ void dcn_p_consumer(const HParams &p, T (*As)[NRB * 1
         br[kh][cb] = __builtin_amdgcn_raw_buffer_load_b128(
             wr, bo[kh][cb], (uint32_t)ks * (uint32_t)(kPBK / 16) * 1024u, 0);
   };
-  // The matrix-core waves go first when both waves of a SIMD are ready to issue.
-  __builtin_amdgcn_s_setprio(1);
   floatx4 acc[NRB][4];
 #pragma unroll
   for (int i = 0; i < NRB; ++i)
@@ -680,7 +678,6 @@ __device__ __forceinline__ void dcn_p_consumer(const HParams &p, T (*As)[NRB * 1
     step(ks + 1, br1);
   }
   if (ks < nk) step(ks, br0);
-  __builtin_amdgcn_s_setprio(0);
 
   // Epilogue: lane holds column 64 wave + 16 cb + (lane & 15), rows 4 (lane >> 4) + e.
   const T *bias = static_cast<const T *>(p.bias);

@@ -1,8 +1,10 @@
 """The allocation-free fused front end (bevk_modulated_deformable_fused_im2col_nhwc_noalloc)
 against the workspace entry point it mirrors (bevk_modulated_deformable_fused_im2col_nhwc):
 same kernels, so the columns must be bit-identical; two calls in a row, the second with a
-smaller input (the library's static scratch keeps the first call's contents); a shape whose
-scratch need exceeds the static scratch is rejected before any device work."""
+smaller input (the library's static scratch keeps the first call's contents); the call
+captured in a HIP graph and replayed, with eager work between the replays, bit-identical
+to the eager call every time; a shape whose scratch need exceeds the static scratch is
+rejected before any device work."""
 import pytest
 import torch
 
@@ -36,7 +38,8 @@ def _run_workspace(x, w_off, b_off):
     return col
 
 
-@pytest.mark.parametrize("dtype", [torch.float16, torch.float32], ids=["fp16", "fp32"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32],
+                         ids=["fp16", "bf16", "fp32"])
 def test_noalloc_matches_workspace_entry(dtype):
     for (b, c, h, w), seed in (((2, 64, 30, 41), 1), ((1, 32, 13, 17), 2)):
         x, w_off, b_off = _problem(b, c, h, w, dtype, seed)
@@ -46,6 +49,38 @@ def test_noalloc_matches_workspace_entry(dtype):
         torch.cuda.synchronize()
         assert torch.isfinite(col.float()).all()
         assert torch.equal(col, ref), f"shape {(b, c, h, w)}: noalloc != workspace entry"
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32],
+                         ids=["fp16", "bf16", "fp32"])
+def test_noalloc_graph_capture(dtype):
+    """The entry point allocates nothing, so it can be captured: one eager warm-up call,
+    capture on a side stream, then replays (with other inputs copied into the captured
+    buffers and eager library calls in between), each compared with the eager result."""
+    b, c, h, w = 2, 64, 30, 41
+    x, w_off, b_off = _problem(b, c, h, w, dtype, 4)
+    col = torch.empty(b * h * w, 9 * c, dtype=dtype, device=DEV)
+    _run_noalloc(x, w_off, b_off, col)  # warm-up outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            _run_noalloc(x, w_off, b_off, col)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    for seed in (5, 6, 7):
+        x2, w2, bo2 = _problem(b, c, h, w, dtype, seed)
+        x.copy_(x2)
+        w_off.copy_(w2)
+        b_off.copy_(bo2)
+        col.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = _run_workspace(x2, w2, bo2)  # eager, between replays
+        torch.cuda.synchronize()
+        assert torch.equal(col, ref), f"replay with seed {seed} != eager"
 
 
 def test_noalloc_rejects_oversize():
