@@ -383,6 +383,9 @@ struct CachedParams {
   int parts;             // query ranges per slice
   int blocks_per_xcd;    // gridDim.x / 8
   int xcd_group;         // XCDs sharing one item (1, 2, 4 or 8)
+  int head_pairs;        // 1: an item is a (batch, head pair) slice, the two heads of which
+                         // share the 128-byte lines of value (D * sizeof(T) == 64); half of
+                         // the item's blocks take each head, so one L2 fill serves both
   uint32_t batch_bytes;  // bytes of value per batch (buffer range; < 2^31)
 };
 
@@ -452,14 +455,21 @@ __global__ void __launch_bounds__(WPB * kWave) msda_cached_kernel(const CachedPa
   const uint32_t cb = (uint32_t)((ul - pt * G) * VEC * sizeof(T));
 
   for (int item = gi; item < p.nitems; item += ngroups) {
-    const int slice = item / p.parts;
+    int slice = item / p.parts;
     const int part = item - slice * p.parts;
+    int kbi = kb, nkbi = nkb;  // this block's rank among the item's blocks for its head
+    if (p.head_pairs) {
+      const int nlo = nkb / 2, hi = kb >= nlo ? 1 : 0;
+      slice = 2 * slice + hi;
+      kbi = kb - hi * nlo;
+      nkbi = hi ? nkb - nlo : nlo;
+    }
     const int b = slice / p.NH;
     const int h = slice - b * p.NH;
     const int qa = (int)((int64_t)p.NQ * part / p.parts);
     const int nqp = (int)((int64_t)p.NQ * (part + 1) / p.parts) - qa;
-    const int q0 = qa + (int)((int64_t)nqp * kb / nkb);
-    const int q1 = qa + (int)((int64_t)nqp * (kb + 1) / nkb);
+    const int q0 = qa + (int)((int64_t)nqp * kbi / nkbi);
+    const int q1 = qa + (int)((int64_t)nqp * (kbi + 1) / nkbi);
     if (q0 >= q1) continue;  // uniform over the block
 
     const T *vbase = static_cast<const T *>(p.value) + (int64_t)b * p.S * pos_stride;
@@ -801,12 +811,16 @@ hipError_t launch_cached_t(const MsdaArgs &a, hipStream_t stream, int xcd_group 
   p.S = a.spatial_size;
   p.NH = a.num_heads;
   p.NQ = a.num_query;
-  const int slices = a.batch * a.num_heads;
-  p.parts = 8 / gcd_int(slices, 8);  // items = a multiple of the 8 XCDs
-  p.nitems = slices * p.parts;
   const int blocks = (device_cus() / 8) * 8;
   p.blocks_per_xcd = blocks / 8;
   p.xcd_group = xcd_group;
+  // 16-bit D = 32: two heads per 128-byte line; items are head pairs when every block of
+  // the item's XCD group has a partner for the other head
+  p.head_pairs = (D * (int)sizeof(T) == 64 && a.num_heads % 2 == 0 &&
+                  p.blocks_per_xcd * xcd_group >= 2) ? 1 : 0;
+  const int slices = a.batch * a.num_heads / (p.head_pairs ? 2 : 1);
+  p.parts = 8 / gcd_int(slices, 8);  // items = a multiple of the 8 XCDs
+  p.nitems = slices * p.parts;
   p.batch_bytes = (uint32_t)((int64_t)a.spatial_size * a.num_heads * D * sizeof(T));
   if (blocks == 0 || p.nitems == 0) return hipSuccess;
   hipLaunchKernelGGL((msda_cached_kernel<T, D, NL, NP, WPB, UPW, MIXL>), dim3(blocks),
