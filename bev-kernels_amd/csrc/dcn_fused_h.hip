@@ -65,6 +65,16 @@ template <> __device__ __forceinline__ floatx16 mfma16<bf16>(const bf16 *a, int4
                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
+// The same MFMA with the A fragment already in registers.
+template <typename T> __device__ __forceinline__ floatx16 mfma16r(int4v a, int4v b, floatx16 c) {
+  if constexpr (std::is_same<T, f16>::value)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, a),
+                                                  __builtin_bit_cast(half8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
 struct TapGeo {
   float w[4];
   uint32_t o[4];
@@ -481,6 +491,179 @@ __global__ void __launch_bounds__(256) zero_f32_kernel(float *__restrict__ p, in
   if (r < n) p[r] = 0.f;
 }
 
+// The offset conv of the usual DCN layer (3 x 3 taps, stride 1, dilation 1, C % 64 == 0,
+// Cout <= 32) by output row segments: a workgroup takes 32 * NSUB (NSUB = 1, 2)
+// consecutive pixels of one output row and loops over 64-channel chunks.
+//   * A operand: per chunk the segment's input window (3 rows x 32 * NSUB + 2 pixels) is
+//     staged in LDS once and every tap reads its fragments from it, so an input pixel
+//     leaves L2 3 times instead of 9 (the tiled form gathers each tap separately).
+//   * B operand: each wave loads its own weight fragments straight into registers; one
+//     fragment feeds the MFMAs of all NSUB subtiles. Through LDS they would double the LDS
+//     traffic, which (one 1 KB A fragment per 32 x 32 x 16 MFMA) already matches the
+//     matrix cores' rate.
+//   * Pipeline: chunk c + 1's window is written to the second LDS buffer while chunk c
+//     multiplies (one barrier per chunk), and the loads of chunk c + 2 are in flight.
+//   * The chunk's 36 (tap, 16-channel block) MFMA steps are split over the 8 waves (wave w:
+//     steps w, w + 8, ...); their partial sums meet in LDS and are added in wave order, so
+//     every run gives the same result, with no atomics and no cleared output.
+// Time is set by the latency of the chunk chain, not by bandwidth: B = 1 and B = 6 at the
+// res5 shape measure alike (13.0 and 14.3 us, against 26.6 us plus a 4.8 us clear for the
+// tiled form with K in two parts); at res4, 696 segments, one workgroup per CU, 27.4 us
+// against 28.3 us.
+constexpr int kBandWaves = 8, kBandPitch = 64 + 8;  // LDS window: halves per pixel
+template <int NSUB> struct BandShape {
+  static constexpr int SEG = 32 * NSUB, PW = SEG + 2;
+  static constexpr int NU = (36 + kBandWaves - 1) / kBandWaves;  // MFMA steps per wave
+  static constexpr int NV = 3 * PW * 8;                          // window vectors per chunk
+  static constexpr int VPT = (NV + 64 * kBandWaves - 1) / (64 * kBandWaves);
+  static constexpr int WIN_BYTES = 3 * PW * kBandPitch * 2;
+  static constexpr int RED_BYTES = kBandWaves * NSUB * 1024 * 4;
+  static constexpr int LDS = 2 * WIN_BYTES > RED_BYTES ? 2 * WIN_BYTES : RED_BYTES;
+};
+
+template <typename T, int NSUB>
+__global__ void __launch_bounds__(64 * kBandWaves) offset_conv_band_kernel(const HParams p) {
+  using S = BandShape<NSUB>;
+  constexpr int NT = 64 * kBandWaves, NU = S::NU;
+  static_assert(NSUB == 1 || NSUB == 2, "segment of one or two subtiles");
+  using V = Vec<T, 8>;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[S::LDS];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // XCD x (= blockIdx % 8) runs segments [x * tiles_per_xcd, (x + 1) * tiles_per_xcd):
+  // neighbouring output rows, whose windows overlap, share that XCD's L2
+  const int idx = (int)(blockIdx.x & 7) * p.tiles_per_xcd + (int)(blockIdx.x >> 3);
+  if ((int)(blockIdx.x >> 3) >= p.tiles_per_xcd || idx >= p.mt) return;
+  const int row = idx / p.nt, ow0 = (idx - row * p.nt) * S::SEG;  // row = b * Ho + oh
+  const int b = row / p.Ho, oh = row - b * p.Ho;
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, p.x_bytes);
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, p.w_bytes);
+
+  // window slots: vector q (16 bytes) of pixel px of window row r; byte offset in x
+  // (x_bytes outside the image: reads 0) and byte offset in an LDS buffer (-1: spare slot)
+  uint32_t xo[S::VPT];
+  int wl[S::VPT];
+#pragma unroll
+  for (int i = 0; i < S::VPT; ++i) {
+    const int v = tid + i * NT;
+    const int r = v / (S::PW * 8), rem = v - r * (S::PW * 8), px = rem >> 3, q = rem & 7;
+    const int h = oh - p.ph + r, w = ow0 - p.pw + px;
+    const bool in = v < S::NV && h >= 0 && h < p.H && w >= 0 && w < p.W;
+    xo[i] = in ? (uint32_t)((b * p.H + h) * p.W + w) * (uint32_t)p.C * (uint32_t)sizeof(T) +
+                     (uint32_t)q * 16u
+               : p.x_bytes;
+    wl[i] = v < S::NV ? ((r * S::PW + px) * kBandPitch + q * 8) * (int)sizeof(T) : -1;
+  }
+  // this wave's MFMA steps u = wave + 8 j (tap u / 4, 16-channel block u % 4; steps past
+  // 35 load step 35 and skip the MFMA) and the lane's 16 bytes of their weight fragments:
+  // block (tap * C + chunk * 64) / 16 + u % 4 of the packed weight
+  uint32_t bo[NU];
+#pragma unroll
+  for (int j = 0; j < NU; ++j) {
+    const int u = min(wave + j * kBandWaves, 35);
+    bo[j] = (uint32_t)((u >> 2) * (p.C / 16) + (u & 3)) * 1024u + (uint32_t)lane * 16u;
+  }
+
+  // Chunk c's window and weights are loaded into register stage c % 2 two chunks ahead;
+  // the window goes to LDS buffer c % 2. Every load is issued unconditionally (chunk
+  // indices past the end repeat the last chunk), so the vector-memory wait counts are exact.
+  const int nch = p.C / 64;
+  V xv[2][S::VPT];
+  int4v wb[2][NU];
+  auto load_x = [&](V (&x)[S::VPT], int cc) {
+    const uint32_t so = (uint32_t)min(cc, nch - 1) * 128u;
+#pragma unroll
+    for (int i = 0; i < S::VPT; ++i)
+      x[i] = __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(xr, xo[i], so, 0));
+  };
+  auto load_w = [&](int4v (&w)[NU], int cc) {
+    const uint32_t so = (uint32_t)min(cc, nch - 1) * 4096u;
+#pragma unroll
+    for (int j = 0; j < NU; ++j) w[j] = __builtin_amdgcn_raw_buffer_load_b128(wr, bo[j], so, 0);
+  };
+  auto store_x = [&](const V (&x)[S::VPT], int buf) {
+#pragma unroll
+    for (int i = 0; i < S::VPT; ++i)
+      if (wl[i] >= 0) *reinterpret_cast<V *>(smem + buf * S::WIN_BYTES + wl[i]) = x[i];
+  };
+
+  // lane's A fragment row: pixel 32 k + lane % 32 of subtile k, channels 8 (lane / 32) + ..
+  const T *abase = reinterpret_cast<const T *>(smem) + (lane & 31) * kBandPitch + (lane >> 5) * 8;
+  floatx16 acc[NSUB];
+#pragma unroll
+  for (int k = 0; k < NSUB; ++k)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[k][e] = 0.f;
+  // fragment f = (step j = f / NSUB, subtile k = f % NSUB), read RING fragments ahead of
+  // its MFMA (left to itself the scheduler moves each read next to its MFMA)
+  constexpr int NF = NU * NSUB, RING = 4;
+  auto frag = [&](int f, int buf) -> int4v {
+    const int j = f / NSUB, k = f - j * NSUB;
+    const int u = min(wave + j * kBandWaves, 35), t = u >> 2, ki = t / 3, kj = t - ki * 3;
+    return *reinterpret_cast<const int4v *>(abase + buf * (S::WIN_BYTES / (int)sizeof(T)) +
+                                            (ki * S::PW + kj + 32 * k) * kBandPitch +
+                                            (u & 3) * 16);
+  };
+  auto compute = [&](const int4v (&w)[NU], int buf) {
+    int4v fa[RING];
+#pragma unroll
+    for (int f = 0; f < RING && f < NF; ++f) fa[f] = frag(f, buf);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      const int j = f / NSUB, k = f - j * NSUB;
+      if (wave + j * kBandWaves < 36) acc[k] = mfma16r<T>(fa[f % RING], w[j], acc[k]);
+      if (f + RING < NF) fa[f % RING] = frag(f + RING, buf);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  load_w(wb[0], 0);
+  load_w(wb[1], 1);
+  load_x(xv[0], 0);
+  load_x(xv[1], 1);
+  store_x(xv[0], 0);
+  load_x(xv[0], 2);
+  __syncthreads();
+  // step cc: chunk cc + 1's window into the other buffer while chunk cc multiplies; steps
+  // past the last chunk skip the MFMAs (an exit inside the unrolled pair would make the
+  // compiler keep every stage twice)
+#pragma nounroll
+  for (int c0 = 0; c0 < nch; c0 += 2) {
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+      const int cc = c0 + d;
+      store_x(xv[d ^ 1], d ^ 1);
+      load_x(xv[d ^ 1], cc + 3);
+      if (cc < nch) compute(wb[d], d);
+      load_w(wb[d], cc + 2);
+      __syncthreads();  // window cc + 1 complete, every wave done with window cc
+    }
+  }
+
+  // partial sums: wave w's subtile k at red[(w * NSUB + k) * 1024 + e * 64 + lane], added
+  // in wave order
+  float *red = reinterpret_cast<float *>(smem);
+#pragma unroll
+  for (int k = 0; k < NSUB; ++k)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) red[(wave * NSUB + k) * 1024 + e * 64 + lane] = acc[k][e];
+  __syncthreads();
+  float *out = static_cast<float *>(p.out);
+  const float *bias = static_cast<const float *>(p.bias);
+  for (int o = tid; o < NSUB * 1024; o += NT) {
+    const int k = o >> 10, r = o & 1023;
+    float v = red[k * 1024 + r];
+#pragma unroll
+    for (int w = 1; w < kBandWaves; ++w) v += red[(w * NSUB + k) * 1024 + r];
+    const int e = r >> 6, l = r & 63, n = l & 31;
+    const int ow = ow0 + 32 * k + 8 * (e >> 2) + 4 * (l >> 5) + (e & 3);
+    if (ow < p.Wo && n < p.Cout) {
+      if (bias != nullptr) v += bias[n];
+      out[((int64_t)row * p.Wo + ow) * p.Cout + n] = v;
+    }
+  }
+}
+
 template <typename T, typename OutT, int BM, int BN, int BK, int WM, int WN, bool TAPSTEP>
 hipError_t launch_cfg(HParams p, int geo, hipStream_t stream) {
   p.mt = (p.M + BM - 1) / BM;
@@ -526,6 +709,23 @@ hipError_t launch_cfg(HParams p, int geo, hipStream_t stream) {
   }
 }
 
+template <typename T, int NSUB>
+hipError_t launch_band(HParams p, hipStream_t stream) {
+  using S = BandShape<NSUB>;
+  if (p.M == 0) return hipSuccess;
+  p.nt = (p.Wo + S::SEG - 1) / S::SEG;  // segments per output row
+  p.mt = (p.M / p.Wo) * p.nt;           // segments
+  p.tiles_per_xcd = (p.mt + 7) / 8;
+  hipLaunchKernelGGL((offset_conv_band_kernel<T, NSUB>), dim3(8 * p.tiles_per_xcd),
+                     dim3(64 * kBandWaves), 0, stream, p);
+  return hipGetLastError();
+}
+
+bool band_geometry(const HParams &p) {
+  return p.kh == 3 && p.kw == 3 && p.sh == 1 && p.sw == 1 && p.dh == 1 && p.dw == 1 &&
+         p.C % 64 == 0 && p.Cout <= 32;
+}
+
 template <typename T, bool TAPSTEP>
 hipError_t launch_tt(const HParams &p, int geo, hipStream_t stream) {
   // Offset conv: Cout = 3T <= 27, fp32 output. One-wave 32 x 32 tiles: no wave spends
@@ -535,6 +735,8 @@ hipError_t launch_tt(const HParams &p, int geo, hipStream_t stream) {
   // length (front end res4 75.6 -> 73.9 us, res5 60.9 -> 55.5 us; 256 channels, 254
   // registers and 42 KB of LDS, measured 86.7 and 57.6 us).
   if (geo == kGeoRegular) {
+    if (TAPSTEP && band_geometry(p))
+      return p.Wo > 32 ? launch_band<T, 2>(p, stream) : launch_band<T, 1>(p, stream);
     if (TAPSTEP && p.C % 128 == 0)
       return launch_cfg<T, float, 32, 32, 128, 1, 1, true>(p, geo, stream);
     return launch_cfg<T, float, 32, 32, 64, 1, 1, TAPSTEP>(p, geo, stream);
@@ -1375,8 +1577,9 @@ hipError_t launch_dcn_fused_h(int dtype, const DcnGeom &g, int channels_out, con
 
 // The one-launch form runs where Cout fits one 256-column half. With two halves every
 // workgroup pair would compute the offset conv of the same rows, so the caller runs the
-// offset conv once into y and then the fused kernel reading y: res5 fp16 113 -> 104 us,
-// bf16 117 -> 106 us (res4, one half, stays in one launch: 88 us against about 94).
+// offset conv once into y (the row-segment kernel) and then the fused kernel reading y:
+// res5 fp16 113 -> 88 us, bf16 117 -> 91 us (res4, one half, stays in one launch: 88-90 us
+// against 26 + 65 us in two).
 bool dcn_mega_supported(int dtype, const DcnGeom &g, int channels_out, const void *out) {
   if ((dtype != 1 && dtype != 2) || g.deformable_group != 1 ||
       g.kernel_h * g.kernel_w > kMaxTaps)

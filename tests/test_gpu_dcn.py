@@ -600,10 +600,16 @@ def _mega_ref(x, w_off, b_off, weight, bias, dtype, s=1, p=1, dl=1, relu=False):
     (2, 64, 9, 11, 1, 1, 1),
     (1, 32, 12, 10, 2, 1, 1),
     (1, 16, 10, 9, 1, 2, 2),
-    # few tiles and a long K: K in two parts adding into y (half types), split by taps
-    # with 128-channel steps, by taps with 64-channel steps, and by steps (C % 64 != 0)
+    # half types, 3 x 3 stride 1 with C % 64 == 0: output row segments of one or two
+    # subtiles (a 150-pixel row in three segments; no padding); other geometries with
+    # C % 64 == 0 take the tiled form (stride 2 with 128-channel steps, dilation 2 with K
+    # in two parts adding into y), and C % 64 != 0 with a long K splits by steps
     (1, 256, 12, 10, 1, 1, 1),
     (1, 192, 9, 11, 1, 1, 1),
+    (2, 64, 5, 150, 1, 1, 1),
+    (1, 128, 8, 40, 1, 0, 1),
+    (1, 128, 10, 12, 2, 1, 1),
+    (1, 192, 11, 9, 1, 2, 2),
     (1, 136, 10, 9, 1, 1, 1),
 ])
 def test_offset_conv_forward_nhwc(dtype, geom):
