@@ -786,6 +786,10 @@ struct PShape {
   static constexpr int kLastWaves = (kSlots - (kSPT - 1) * kPProd) / kWave;
   static_assert(kLastWaves * kWave == kSlots - (kSPT - 1) * kPProd && kLastWaves >= 1,
                 "the last slot set must cover whole producer waves");
+  // K steps in flight: gathers (producers) and weight fragments (consumers). Few rows
+  // leave a step little work to cover a gather's round trip, and registers to spare.
+  static constexpr int kPD = NRB <= 3 ? 6 : 2;
+  static constexpr int kCD = NRB <= 3 ? 4 : 2;
 };
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
@@ -826,7 +830,7 @@ __device__ __forceinline__ uint32_t b_frag_offset(int n, int kh, int lane, int n
 // which the whole workgroup stores afterwards as full 16-byte pieces of output rows.
 // Always NRB row blocks (compile-time, so the MFMA loop and the accumulators carry no
 // run-time conditions).
-template <typename T, int NRB>
+template <typename T, int NRB, int CD>
 __device__ __forceinline__ void dcn_p_consumer(const HParams &p, T (*As)[NRB * 16 * kPLDA],
                                                T *stage, int n0, int nk, int lane, int wave) {
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, p.w_bytes);
@@ -850,9 +854,9 @@ __device__ __forceinline__ void dcn_p_consumer(const HParams &p, T (*As)[NRB * 1
   for (int i = 0; i < NRB; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-  // Two B register sets: B(k+2) is loaded right after step k's MFMAs, so a weight load
-  // queued behind the producers' gathers has a whole step to arrive.
-  int4v br0[kPKH][4], br1[kPKH][4];
+  // CD B register sets: B(k+CD) is loaded right after step k's MFMAs, so a weight load
+  // queued behind the producers' gathers has CD - 1 steps to arrive.
+  int4v br[CD][kPKH][4];
   auto step = [&](int ks, int4v (&br)[kPKH][4]) __attribute__((always_inline)) {
     const int buf = ks & 1;
 #pragma unroll
@@ -868,18 +872,20 @@ __device__ __forceinline__ void dcn_p_consumer(const HParams &p, T (*As)[NRB * 1
         for (int cb = 0; cb < 4; ++cb)
           acc[rbi][cb] = mfma16x16<T>(af[rbi], br[kh][cb], acc[rbi][cb]);
     }
-    issue_b(ks + 2, br);
+    issue_b(ks + CD, br);
     __syncthreads();
   };
-  issue_b(0, br0);
-  issue_b(1, br1);
+#pragma unroll
+  for (int d = 0; d < CD; ++d) issue_b(d, br[d]);
   __syncthreads();  // A(0) written by the producers
   int ks = 0;
-  for (; ks + 2 <= nk; ks += 2) {
-    step(ks, br0);
-    step(ks + 1, br1);
+  for (; ks + CD <= nk; ks += CD) {
+#pragma unroll
+    for (int d = 0; d < CD; ++d) step(ks + d, br[d]);
   }
-  if (ks < nk) step(ks, br0);
+#pragma unroll
+  for (int d = 0; d + 1 < CD; ++d)
+    if (ks + d < nk) step(ks + d, br[d]);
 
   // Epilogue: lane holds column 64 wave + 16 cb + (lane & 15), rows 4 (lane >> 4) + e.
   const T *bias = static_cast<const T *>(p.bias);
@@ -976,12 +982,12 @@ __device__ __forceinline__ void dcn_p_offset_consumer(const HParams &p,
 }
 
 // Producer thread ptid (0..255) with NS gather slots: slot i is (row, k-vector) =
-// (s / KV, s % KV), s = ptid + 256 i. The gathers of step k + 2 are issued at step k into
-// register set k % 2 (blended at step k - 1); A(k+1) is blended at step k from set
-// (k+1) % 2 into buffer (k+1) % 2. Every load is issued unconditionally (steps past the end
-// read out of range), so the compiler's wait counts stay exact and the gathers of the next
-// steps stay in flight. REG: plain convolution taps (one pixel per slot, no blend).
-template <typename T, int NS, int NRB, bool REG>
+// (s / KV, s % KV), s = ptid + 256 i. The gathers of step k + PD are issued at step k into
+// register set k % PD (blended at step k - 1); A(k+1) is blended at step k from set
+// (k+1) % PD into buffer (k+1) % 2. Every load is issued unconditionally (steps past the
+// end read out of range), so the compiler's wait counts stay exact and the gathers of the
+// next steps stay in flight. REG: plain convolution taps (one pixel per slot, no blend).
+template <typename T, int NS, int NRB, bool REG, int PD>
 __device__ __forceinline__ void dcn_p_producer(const HParams &p, const TapGeo *geo,
                                                T (*As)[NRB * 16 * kPLDA], int nk, int ptid) {
   using V = Vec<T, 8>;
@@ -1034,23 +1040,25 @@ __device__ __forceinline__ void dcn_p_producer(const HParams &p, const TapGeo *g
       store_vec<T, 8>(&As[buf][a_off(row, kv)], o);
     }
   };
-  V ra0[NS][NQ], ra1[NS][NQ];
+  V ra[PD][NS][NQ];
   auto step = [&](int ks, V (&ra_issue)[NS][NQ], const V (&ra_blend)[NS][NQ])
       __attribute__((always_inline)) {
-    issue_gather(ks + 2, ra_issue);
+    issue_gather(ks + PD, ra_issue);
     blend(ks + 1, ra_blend, (ks + 1) & 1);
     __syncthreads();
   };
-  issue_gather(0, ra0);
-  issue_gather(1, ra1);
-  blend(0, ra0, 0);
+#pragma unroll
+  for (int d = 0; d < PD; ++d) issue_gather(d, ra[d]);
+  blend(0, ra[0], 0);
   __syncthreads();
   int k0 = 0;
-  for (; k0 + 2 <= nk; k0 += 2) {
-    step(k0, ra0, ra1);
-    step(k0 + 1, ra1, ra0);
+  for (; k0 + PD <= nk; k0 += PD) {
+#pragma unroll
+    for (int d = 0; d < PD; ++d) step(k0 + d, ra[d], ra[(d + 1) % PD]);
   }
-  if (k0 < nk) step(k0, ra0, ra1);
+#pragma unroll
+  for (int d = 0; d + 1 < PD; ++d)
+    if (k0 + d < nk) step(k0 + d, ra[d], ra[(d + 1) % PD]);
 }
 
 // GEO: kGeoMask, kGeoY or kGeoYF32 (read from global memory). MEGA: the one-launch
@@ -1102,9 +1110,9 @@ __global__ void __launch_bounds__(kPThreads) dcn_fused_p_kernel(const PParams pp
     if (wave < 4)
       dcn_p_offset_consumer<T, NRB>(p, As, ys, m0, nrb, nk, lane, wave);
     else if (wave - 4 < SH::kLastWaves)
-      dcn_p_producer<T, SH::kSPT, NRB, true>(p, geo, As, nk, tid - kPProd);
+      dcn_p_producer<T, SH::kSPT, NRB, true, 2>(p, geo, As, nk, tid - kPProd);
     else if constexpr (SH::kLastWaves < 4)
-      dcn_p_producer<T, SH::kSPT - 1, NRB, true>(p, geo, As, nk, tid - kPProd);
+      dcn_p_producer<T, SH::kSPT - 1, NRB, true, 2>(p, geo, As, nk, tid - kPProd);
     __syncthreads();  // y of every row in ys
   }
 
@@ -1130,11 +1138,11 @@ __global__ void __launch_bounds__(kPThreads) dcn_fused_p_kernel(const PParams pp
   // 67.8 us; the consumers raised instead, 70.2 us).
   if (wave >= 4) __builtin_amdgcn_s_setprio(2);
   if (wave < 4)
-    dcn_p_consumer<T, NRB>(p, As, stage, n0, nk, lane, wave);
+    dcn_p_consumer<T, NRB, SH::kCD>(p, As, stage, n0, nk, lane, wave);
   else if (wave - 4 < SH::kLastWaves)
-    dcn_p_producer<T, SH::kSPT, NRB, false>(p, geo, As, nk, tid - kPProd);
+    dcn_p_producer<T, SH::kSPT, NRB, false, SH::kPD>(p, geo, As, nk, tid - kPProd);
   else if constexpr (SH::kLastWaves < 4)
-    dcn_p_producer<T, SH::kSPT - 1, NRB, false>(p, geo, As, nk, tid - kPProd);
+    dcn_p_producer<T, SH::kSPT - 1, NRB, false, SH::kPD>(p, geo, As, nk, tid - kPProd);
   // The output tile: full 16-byte pieces of the workgroup's rows (Cout % 8 == 0 and a
   // 16-byte aligned output, checked on the host: a piece is wholly inside or outside),
   // streaming stores (written once; the input rows stay in L2).
@@ -1373,9 +1381,9 @@ __global__ void __launch_bounds__(kSThreads) dcn_fused_s_kernel(const PParams pp
     if (wave < 4)
       dcn_p_offset_consumer<T, NRB>(p, As, ys, m0, nrb, nk, lane, wave);
     else if (wave - 4 < PSH::kLastWaves)
-      dcn_p_producer<T, PSH::kSPT, NRB, true>(p, geo, As, nk, tid - kPProd);
+      dcn_p_producer<T, PSH::kSPT, NRB, true, 2>(p, geo, As, nk, tid - kPProd);
     else
-      dcn_p_producer<T, PSH::kSPT - 1, NRB, true>(p, geo, As, nk, tid - kPProd);
+      dcn_p_producer<T, PSH::kSPT - 1, NRB, true, 2>(p, geo, As, nk, tid - kPProd);
     __syncthreads();  // y of every row in ys
   }
   for (int g = tid; g < kRows * TT; g += kSThreads) {
