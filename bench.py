@@ -11,7 +11,8 @@ Len_q 10000, 8 heads x 32, 8 points), fp32, with inputs resident in HBM:
   roofline   the same figure against 8 TB/s, kernel time from HIP events on the stream
              the kernel runs on; `traffic` from the committed rocprofv3 counter summary
   secondary  the fused NHWC DCNv2 res4 fp16 forward in MFMA TFLOP/s (2*M*K*Cout flops),
-             timed like a configs row (>= 100 launches; mean and median)
+             timed like a configs row (>= 100 launches; mean and median); the configs
+             row of that kernel reports these same launches
   configs    every BASELINE configuration x dtype: us, GB/s or TFLOP/s, roofline fraction;
              the backward kernels (MSDA backward, DCN NHWC column-to-image) in GB/s of
              compulsory bytes
@@ -465,7 +466,10 @@ def main():
         for name in ("dcn_res4", "dcn_res5"):
             for dt in ("fp16", "bf16", "fp32"):
                 f, fl = dcn_fused_case(name, dtype_of(dt), cache)
-                m, _, _ = timer.run(f, reps, wu)
+                if name == "dcn_res4" and dt == "fp16":
+                    m = d_mean  # the secondary's launches: one figure for this kernel
+                else:
+                    m, _, _ = timer.run(f, reps, wu)
                 tf = fl / (m * 1e-6) / 1e12
                 rows.append({"config": name + "_nhwc_fused", "dtype": dt, "us": round(m, 2),
                              "TFLOP/s": round(tf, 2),
