@@ -222,10 +222,6 @@ int bevk_dcn_fused_fwd_nhwc(
     int channels_out, int kernel_h, int kernel_w, int pad_h, int pad_w, int stride_h,
     int stride_w, int dilation_h, int dilation_w, void *out, void *stream);
 
-/* ------------------------------------------------------------------------- */
-/* Multi-scale deformable attention                                            */
-/* ------------------------------------------------------------------------- */
-
 /* Offset conv of the NHWC front end on the matrix cores:
  *   data_im       [B, H, W, C]
  *   w_off_packed  bevk_dcn_pack_weight of the offset-conv weight [3T, C, kh, kw]
@@ -262,6 +258,10 @@ int bevk_dcn_mega_fwd_nhwc(int dtype, const void *data_im, const void *w_off_pac
                            int kernel_w, int pad_h, int pad_w, int stride_h, int stride_w,
                            int dilation_h, int dilation_w, int act_relu, float *y, void *out,
                            void *stream);
+
+/* ------------------------------------------------------------------------- */
+/* Multi-scale deformable attention                                            */
+/* ------------------------------------------------------------------------- */
 
 /* MSDA forward.
  *   value              [B, spatial_size, num_heads, channels]
