@@ -852,7 +852,9 @@ struct TileParams {
 };
 
 // BPC workgroups of WPB waves per CU: the second bound is waves per SIMD.
-template <typename T, int NP, int TS, int MG, int WPB, int BPC>
+// PF: the next item's locations, weights and neighbourhood are loaded into registers
+// while the current item's passes run (the registers must allow it: 16-bit types).
+template <typename T, int NP, int TS, int MG, int WPB, int BPC, bool PF>
 __global__ void __launch_bounds__(WPB * kWave, (WPB * BPC + 3) / 4) msda_tile_kernel(const TileParams p) {
   constexpr int D = 32;
   constexpr int VEC = 16 / (int)sizeof(T);
@@ -890,64 +892,118 @@ __global__ void __launch_bounds__(WPB * kWave, (WPB * BPC + 3) / 4) msda_tile_ke
   const int g = lane / G;
   const uint32_t cb = (uint32_t)(lane % G) * 16u;
 
-  for (int item = xcd * per + (blockIdx.x >> 3); item < i_end; item += p.blocks_per_xcd) {
+  typedef int i4 __attribute__((ext_vector_type(4)));
+  constexpr int P16 = ROW / 16;
+  constexpr int NPC = RS * RS * P16;              // 16-byte pieces of the neighbourhood
+  constexpr int NT = WPB * kWave;
+  constexpr int NLD = (NPC + NT - 1) / NT;        // pieces per thread
+  // Query of unit ul of tile `tile` = (ty, tx) (valid flag in qv).
+  auto query_of = [&](int tile, int ty, int tx, int ul, bool &qv)
+      __attribute__((always_inline)) -> int {
+    if (grid) {
+      const int qy = ty * TS + ul / TS, qx = tx * TS + ul % TS;
+      qv = ul < TS * TS && qy < H && qx < W;
+      return qy * W + qx;
+    }
+    const int q = tile * TS * TS + ul;
+    qv = ul < TS * TS && q < p.NQ;
+    return q;
+  };
+  // Loads of item `it`: this wave's locations and weights of the tile, and the thread's
+  // pieces of the head's value rows of the tile grown by MG cells on every side (out of
+  // range, i.e. no request, past the grid, past the last item or without a grid). Every
+  // load is unconditional, so the wait counts stay exact.
+  float lx[NPASS], ly[NPASS], la[NPASS];
+  i4 v[NLD];
+  auto fetch_loc = [&](int tile, int ty, int tx, int b, int h) __attribute__((always_inline)) {
+    // every pass's address first, then the loads: address arithmetic between the loads
+    // let the register allocator put a temporary on a pending load's register, which
+    // cost a wait for the first pass's loads before the second's were issued
+    const T *lp[NPASS];
+    const T *ap[NPASS];
+#pragma unroll
+    for (int ps = 0; ps < NPASS; ++ps) {
+      bool qv;
+      const int q = query_of(tile, ty, tx, (wave + ps * WPB) * UPP + lane / NP, qv);
+      const int64_t unit = ((int64_t)b * p.NQ + (qv ? q : 0)) * p.NH + h;
+      lp[ps] = static_cast<const T *>(p.loc) + (unit * NP + lane % NP) * 2;
+      ap[ps] = static_cast<const T *>(p.attn) + unit * NP + lane % NP;
+    }
+    // ordinary loads here (the other kernels stream these inputs): measured 98.4 ->
+    // 94.0 us for the temporal self-attention map, whose tiles' rows stay in L2
+#pragma unroll
+    for (int ps = 0; ps < NPASS; ++ps) {
+      lx[ps] = static_cast<float>(lp[ps][0]);
+      ly[ps] = static_cast<float>(lp[ps][1]);
+      la[ps] = static_cast<float>(*ap[ps]);
+    }
+  };
+  // neighbourhood with origin (ry0, rx0) of head offset hof in the batch slice rs
+  auto fetch_nb = [&](bool live, int ry0, int rx0, __amdgpu_buffer_rsrc_t rs, uint32_t hof)
+      __attribute__((always_inline)) {
+#pragma unroll
+    for (int k = 0; k < NLD; ++k) {
+      const int i = (int)threadIdx.x + k * NT;
+      const int pos = i / P16, piece = i - pos * P16;
+      const int y = ry0 + pos / RS, x = rx0 + pos % RS;
+      const bool in = live && i < NPC && (unsigned)y < (unsigned)H && (unsigned)x < (unsigned)W;
+      v[k] = __builtin_amdgcn_raw_buffer_load_b128(
+          rs, in ? (uint32_t)((S0 + y * W + x) * pos_stride) * sizeof(T) + hof + piece * 16
+                 : kOOB,
+          0, 0);
+    }
+  };
+
+  // PF: the loads of item it (past the last item: locations of the last, no neighbourhood)
+  auto fetch_item = [&](int it) __attribute__((always_inline)) {
+    const bool live = grid && it < i_end;
+    const int itc = it < i_end ? it : i_end - 1;  // a valid item for the location reads
+    const int tile = itc % ntile, bh = itc / ntile;
+    const int h = bh % p.NH, b = bh / p.NH;
+    const int ty = tile / tiles_x, tx = tile - ty * tiles_x;
+    fetch_loc(tile, ty, tx, b, h);
+    fetch_nb(live, ty * TS - MG, tx * TS - MG,
+             make_rsrc(static_cast<const T *>(p.value) + (int64_t)b * p.S * pos_stride,
+                       p.batch_bytes),
+             (uint32_t)(h * D * sizeof(T)));
+  };
+  int item = xcd * per + (blockIdx.x >> 3);
+  if constexpr (PF) {
+    if (item >= i_end) return;  // (fetch_item needs an item of this block)
+    fetch_item(item);
+  }
+  for (; item < i_end; item += p.blocks_per_xcd) {
+    // without PF (fp32, whose registers are taken): locations first, the neighbourhood
+    // after the barrier below, every load of the item in flight before the first store
     const int tile = item % ntile;
     const int bh = item / ntile;
     const int h = bh % p.NH, b = bh / p.NH;
     const int ty = tile / tiles_x, tx = tile - ty * tiles_x;
+    if constexpr (!PF) fetch_loc(tile, ty, tx, b, h);
     // Neighbourhood origin; a huge origin when there is no grid keeps every corner out.
     const int ry0 = grid ? ty * TS - MG : -(1 << 28), rx0 = grid ? tx * TS - MG : -(1 << 28);
     const T *vbase = static_cast<const T *>(p.value) + (int64_t)b * p.S * pos_stride;
     const __amdgpu_buffer_rsrc_t rsrc = make_rsrc(vbase, p.batch_bytes);
     const uint32_t hoff = (uint32_t)(h * D * sizeof(T));
-
-    // Query of unit ul of the tile (valid flag in qv).
     auto query = [&](int ul, bool &qv) __attribute__((always_inline)) -> int {
-      if (grid) {
-        const int qy = ty * TS + ul / TS, qx = tx * TS + ul % TS;
-        qv = ul < TS * TS && qy < H && qx < W;
-        return qy * W + qx;
-      }
-      const int q = tile * TS * TS + ul;
-      qv = ul < TS * TS && q < p.NQ;
-      return q;
+      return query_of(tile, ty, tx, ul, qv);
     };
-    // Locations and weights of all this wave's samples of the tile, loaded before the
-    // neighbourhood so that both are in flight together.
-    float lx[NPASS], ly[NPASS], la[NPASS];
+    // this item's locations and weights (PF: copied before the next item's loads reuse
+    // lx / ly / la; without PF they are read in place, so nothing waits for them before
+    // phase 1)
+    float cx[NPASS], cy[NPASS], ca[NPASS];
+    if constexpr (PF) {
 #pragma unroll
-    for (int ps = 0; ps < NPASS; ++ps) {
-      bool qv;
-      const int q = query((wave + ps * WPB) * UPP + lane / NP, qv);
-      const int64_t unit = ((int64_t)b * p.NQ + (qv ? q : 0)) * p.NH + h;
-      // ordinary loads here (the other kernels stream these inputs): measured 98.4 ->
-      // 94.0 us for the temporal self-attention map, whose tiles' rows stay in L2
-      const T *lp = static_cast<const T *>(p.loc) + (unit * NP + lane % NP) * 2;
-      lx[ps] = static_cast<float>(lp[0]);
-      ly[ps] = static_cast<float>(lp[1]);
-      la[ps] = static_cast<float>(static_cast<const T *>(p.attn)[unit * NP + lane % NP]);
+      for (int ps = 0; ps < NPASS; ++ps) {
+        cx[ps] = lx[ps];
+        cy[ps] = ly[ps];
+        ca[ps] = la[ps];
+      }
     }
 
     __syncthreads();  // the previous item's readers are done
-    if (grid) {
-      // All of a thread's loads are in flight before the first LDS write.
-      constexpr int P16 = ROW / 16;
-      constexpr int NPC = RS * RS * P16;
-      constexpr int NT = WPB * kWave;
-      constexpr int NLD = (NPC + NT - 1) / NT;
-      typedef int i4 __attribute__((ext_vector_type(4)));
-      i4 v[NLD];
-#pragma unroll
-      for (int k = 0; k < NLD; ++k) {
-        const int i = (int)threadIdx.x + k * NT;
-        const int pos = i / P16, piece = i - pos * P16;
-        const int y = ry0 + pos / RS, x = rx0 + pos % RS;
-        const bool in = i < NPC && (unsigned)y < (unsigned)H && (unsigned)x < (unsigned)W;
-        v[k] = __builtin_amdgcn_raw_buffer_load_b128(
-            rsrc, in ? (uint32_t)((S0 + y * W + x) * pos_stride) * sizeof(T) + hoff + piece * 16
-                     : kOOB,
-            0, 0);
-      }
+    if (PF || grid) {
+      if constexpr (!PF) fetch_nb(true, ry0, rx0, rsrc, hoff);
 #pragma unroll
       for (int k = 0; k < NLD; ++k) {
         const int i = (int)threadIdx.x + k * NT;
@@ -955,6 +1011,8 @@ __global__ void __launch_bounds__(WPB * kWave, (WPB * BPC + 3) / 4) msda_tile_ke
       }
     }
     __syncthreads();
+    // the next item's loads, in flight during this item's passes
+    if constexpr (PF) fetch_item(item + p.blocks_per_xcd);
 
 #pragma unroll
     for (int ps = 0; ps < NPASS; ++ps) {
@@ -965,7 +1023,7 @@ __global__ void __launch_bounds__(WPB * kWave, (WPB * BPC + 3) / 4) msda_tile_ke
       {
         bool qv;
         query(u0 + lane / NP, qv);
-        const float x = lx[ps], y = ly[ps], a = la[ps];
+        const float x = PF ? cx[ps] : lx[ps], y = PF ? cy[ps] : ly[ps], a = PF ? ca[ps] : la[ps];
         const float him = y * Hf - 0.5f, wim = x * Wf - 0.5f;
         // Corners inside the neighbourhood: their LDS address; outside it (or invalid):
         // the zero row, and for a valid one its value-buffer offset in far_off. Written
@@ -1061,7 +1119,7 @@ __global__ void __launch_bounds__(WPB * kWave, (WPB * BPC + 3) / 4) msda_tile_ke
 }
 
 // BPC: workgroups per CU (the LDS use must allow it).
-template <typename T, int NP, int TS, int MG, int WPB, int BPC>
+template <typename T, int NP, int TS, int MG, int WPB, int BPC, bool PF>
 hipError_t launch_tile_t(const MsdaArgs &a, hipStream_t stream) {
   TileParams p;
   p.value = a.value;
@@ -1078,8 +1136,8 @@ hipError_t launch_tile_t(const MsdaArgs &a, hipStream_t stream) {
   p.blocks_per_xcd = blocks / 8;
   p.batch_bytes = (uint32_t)((int64_t)a.spatial_size * a.num_heads * 32 * sizeof(T));
   if (blocks == 0 || a.batch == 0 || a.num_query == 0) return hipSuccess;
-  hipLaunchKernelGGL((msda_tile_kernel<T, NP, TS, MG, WPB, BPC>), dim3(blocks), dim3(WPB * kWave), 0,
-                     stream, p);
+  hipLaunchKernelGGL((msda_tile_kernel<T, NP, TS, MG, WPB, BPC, PF>), dim3(blocks),
+                     dim3(WPB * kWave), 0, stream, p);
   return hipGetLastError();
 }
 
@@ -1099,7 +1157,10 @@ hipError_t launch_wave(const MsdaArgs &a, hipStream_t stream) {
         // the tiled kernel (neighbourhood in LDS) measured faster than the per-sample
         // gather kernel: fp32 by 25%, fp16 74.0 -> 69.1 us, bf16 75.4 -> 73.6 us
         if (a.num_query == a.spatial_size && device_cus() >= 8)
-          return launch_tile_t<T, 4, 16, 6, 8, 1>(a, stream);
+          if constexpr (sizeof(T) == 2)
+            return launch_tile_t<T, 4, 16, 6, 8, 1, true>(a, stream);
+          else
+            return launch_tile_t<T, 4, 16, 6, 8, 1, false>(a, stream);
         return launch_wave_t<T, 32, 1, 4>(a, stream);
       }
       if (L == 4 && P == 4) {  // Deformable DETR
