@@ -501,8 +501,9 @@ __global__ void __launch_bounds__(256) zero_f32_kernel(float *__restrict__ p, in
 //     fragment feeds the MFMAs of all NSUB subtiles. Through LDS they would double the LDS
 //     traffic, which (one 1 KB A fragment per 32 x 32 x 16 MFMA) already matches the
 //     matrix cores' rate.
-//   * Pipeline: chunk c + 1's window is written to the second LDS buffer while chunk c
-//     multiplies (one barrier per chunk), and the loads of chunk c + 2 are in flight.
+//   * Pipeline: while chunk c multiplies, chunk c + 1's window is written to the second
+//     LDS buffer (one barrier per chunk) and chunk c + 3's window and chunk c + 2's
+//     weights are loaded into registers.
 //   * The chunk's 36 (tap, 16-channel block) MFMA steps are split over the 8 waves (wave w:
 //     steps w, w + 8, ...); their partial sums meet in LDS and are added in wave order, so
 //     every run gives the same result, with no atomics and no cleared output.
@@ -564,9 +565,10 @@ __global__ void __launch_bounds__(64 * kBandWaves) offset_conv_band_kernel(const
     bo[j] = (uint32_t)((u >> 2) * (p.C / 16) + (u & 3)) * 1024u + (uint32_t)lane * 16u;
   }
 
-  // Chunk c's window and weights are loaded into register stage c % 2 two chunks ahead;
-  // the window goes to LDS buffer c % 2. Every load is issued unconditionally (chunk
-  // indices past the end repeat the last chunk), so the vector-memory wait counts are exact.
+  // Chunk c's window is loaded into register stage c % 2 at step c - 3 and written to LDS
+  // buffer c % 2 at step c - 1; its weights are loaded into stage c % 2 at step c - 2.
+  // Every load is issued unconditionally (chunk indices past the end repeat the last
+  // chunk), so the vector-memory wait counts are exact.
   const int nch = p.C / 64;
   V xv[2][S::VPT];
   int4v wb[2][NU];
