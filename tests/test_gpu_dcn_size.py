@@ -136,3 +136,19 @@ def test_persistent_schedule_any_rows(shape, dtype):
                           weight.double(), bias.double(), 1, 1, 1, col_dtype=dtype,
                           coord_dtype=torch.float32)
     check(out[imgs].cpu(), ref, dtype, f"fused {shape}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+def test_empty_batch(dtype):
+    """A batch of 0 images: every forward entry point returns empty outputs of the right
+    shapes without launching (the C ABI returns before any kernel for zero rows)."""
+    from modulated_deform_conv import fused_tl, dcn_split_nhwc as dsn
+    x, w_off, b_off, weight, bias = _problem(0, 64, 192, 9, 7, dtype, seed=3)
+    dv = [t.to(DEV) for t in (x, w_off, b_off, weight, bias)]
+    out = fused_tl.fused_dcn_mega_forward_nhwc(*dv, 1, 1, 1)
+    out2, y = dsn.mega_forward(*dv, 1, 1, 1)
+    off, msk = fused_tl.offset_conv_forward_nhwc(dv[0], dv[1], dv[2], 3, 3, 1, 1, 1)
+    out3 = fused_tl.fused_dcn_forward_nhwc(dv[0], off, msk, dv[3], dv[4], 1, 1, 1)
+    torch.cuda.synchronize()
+    assert out.shape == out2.shape == out3.shape == (0, 9, 7, 192)
+    assert y.shape == (0, 9, 7, 27) and off.shape == (0, 9, 7, 18) and msk.shape == (0, 9, 7, 9)
