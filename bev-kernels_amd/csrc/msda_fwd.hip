@@ -46,6 +46,52 @@ template <> __device__ __forceinline__ void load_loc<float>(const float *p, floa
   y = v.y;
 }
 
+// Each x[k] summed over lanes i ^ m for m = G, 2G, ..., LPL / 2 (G, LPL powers of two;
+// lanes in aligned groups of LPL), i.e. over the lanes of i's group that share i % G; one
+// step at a time over all N values. Groups of 32 or more lanes sum on the vector ALU: row
+// rotations by 8, 4, ... G inside each 16-lane row (after them a lane holds the sum over
+// i + kG mod 16), then the gfx950 row swap (lanes i, i ^ 16) and half-wave swap (i, i ^ 32);
+// the swaps return both lanes' values, and their sum is the same in both lanes (against
+// LDS-pipe permutes: SCA fp16 242.5 -> 239.0 us, bf16 253.2 -> 250.8 us). Smaller
+// groups use LDS-pipe permutes: the rotations took the 16-bit four-point cached kernel
+// (16-lane groups) from 151 to 168 registers with spills (DETR fp16 89 -> 93 us).
+template <int M> __device__ __forceinline__ float row_ror(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x120 | M, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float swap16_sum(float x) {
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
+}
+__device__ __forceinline__ float swap32_sum(float x) {
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
+}
+template <int G, int LPL, int N> __device__ __forceinline__ void lane_group_sum(float (&x)[N]) {
+  static_assert((G & (G - 1)) == 0 && (LPL & (LPL - 1)) == 0 && LPL <= kWave, "lane groups");
+  if constexpr (LPL < 32) {
+#pragma unroll
+    for (int m = G; m < LPL; m <<= 1)
+#pragma unroll
+      for (int k = 0; k < N; ++k) x[k] += __shfl_xor(x[k], m);
+  } else {
+#pragma unroll
+    for (int k = 0; k < N; ++k) if constexpr (G <= 8) x[k] += row_ror<8>(x[k]);
+#pragma unroll
+    for (int k = 0; k < N; ++k) if constexpr (G <= 4) x[k] += row_ror<4>(x[k]);
+#pragma unroll
+    for (int k = 0; k < N; ++k) if constexpr (G <= 2) x[k] += row_ror<2>(x[k]);
+#pragma unroll
+    for (int k = 0; k < N; ++k) if constexpr (G <= 1) x[k] += row_ror<1>(x[k]);
+#pragma unroll
+    for (int k = 0; k < N; ++k) if constexpr (G <= 16 && LPL >= 32) x[k] = swap16_sum(x[k]);
+#pragma unroll
+    for (int k = 0; k < N; ++k) if constexpr (G <= 32 && LPL >= 64) x[k] = swap32_sum(x[k]);
+  }
+}
+
 struct WaveParams {
   const void *value;
   const int64_t *shapes;
@@ -226,11 +272,7 @@ __global__ void __launch_bounds__(kBlock) msda_wave_kernel(const WaveParams p) {
   }
 
   // Sum the lane groups of one unit (lanes that share a channel slice).
-#pragma unroll
-  for (int m = G; m < LPU; m <<= 1) {
-#pragma unroll
-    for (int k = 0; k < VEC; ++k) acc[k] += __shfl_xor(acc[k], m);
-  }
+  lane_group_sum<G, LPU>(acc);
 
   if (active && g == 0) {
     V o;
@@ -342,10 +384,7 @@ __global__ void __launch_bounds__(kBlock) msda_wave_lds_kernel(const WaveParams 
     for (int k = 0; k < VEC; ++k)
       acc[k] += w[it][0] * (float)v[it][0].v[k] + w[it][1] * (float)v[it][1].v[k] +
                 w[it][2] * (float)v[it][2].v[k] + w[it][3] * (float)v[it][3].v[k];
-#pragma unroll
-  for (int m = G; m < LPU; m <<= 1)
-#pragma unroll
-    for (int k = 0; k < VEC; ++k) acc[k] += __shfl_xor(acc[k], m);
+  lane_group_sum<G, LPU>(acc);
   if (q < p.NQ && gi == 0) {
     V o;
 #pragma unroll
@@ -629,12 +668,7 @@ __global__ void __launch_bounds__(WPB * kWave) msda_cached_kernel(const CachedPa
           acc[it / NL][k] = t;
         }
       // Sum over the points of each (unit, level) lane block.
-#pragma unroll
-      for (int m = G; m < LPL; m <<= 1)
-#pragma unroll
-        for (int a = 0; a < NACC; ++a)
-#pragma unroll
-          for (int k = 0; k < VEC; ++k) acc[a][k] += __shfl_xor(acc[a][k], m);
+      lane_group_sum<G, LPL>(*reinterpret_cast<float (*)[NACC * VEC]>(&acc[0][0]));
       if (pt == 0) {
 #pragma unroll
         for (int a = 0; a < NACC; ++a) {
