@@ -428,10 +428,39 @@ struct CachedParams {
   uint32_t batch_bytes;  // bytes of value per batch (buffer range; < 2^31)
 };
 
-// WPB waves per block, UPW (b, q, head) units per wave round, MIXL the one level that may
-// be cached in part (-1: none).
-template <typename T, int D, int NL, int NP, int WPB, int UPW, int MIXL>
-__global__ void __launch_bounds__(WPB * kWave) msda_cached_kernel(const CachedParams p) {
+// Level table and cache layout: row 0 of the cache is zeros, then levels from the
+// coarsest. Level MIXL keeps as many whole rows as still fit; every other level is cached
+// whole or not at all, so its reads take one path for the whole wave. R[l] = cached rows.
+template <int NL, int MIXL>
+__device__ __forceinline__ void cache_layout(const CachedParams &p, uint32_t row_bytes,
+                                             int cache_bytes, int (&H)[NL], int (&W)[NL],
+                                             int (&S)[NL], int (&R)[NL], uint32_t (&Off)[NL]) {
+  uint32_t used = row_bytes;
+#pragma unroll
+  for (int l = NL - 1; l >= 0; --l) {
+    H[l] = (int)p.shapes[2 * l];
+    W[l] = (int)p.shapes[2 * l + 1];
+    S[l] = (int)p.lsi[l];
+    const int64_t rowb = (int64_t)W[l] * row_bytes;
+    int64_t r = (H[l] > 0 && rowb > 0) ? ((int64_t)cache_bytes - used) / rowb : 0;
+    if (r > H[l]) r = H[l];
+    if (r < 0) r = 0;
+    if (l != MIXL && r < H[l]) r = 0;
+    R[l] = (int)r;
+    Off[l] = used;
+    used += (uint32_t)(r * rowb);
+  }
+}
+
+// The cached kernel's work, compiled per cache layout. FIX = 2: the two coarsest levels
+// are cached whole and the others not at all (SCA and DETR in 16-bit types), so each
+// level's path is known at compile time and phase 2 is straight-line code whose waits
+// name exactly the loads they need (with per-level run-time paths the merge points wait
+// for every load of the round before the first blend). FIX = -1: any layout, each level's
+// path chosen at run time.
+template <typename T, int D, int NL, int NP, int WPB, int UPW, int MIXL, int FIX>
+__device__ __forceinline__ void cached_body(const CachedParams &p, unsigned char *cache,
+                                            SampleGeo (*geo)[UPW * NL * NP]) {
   using V = Vec<T, 16 / sizeof(T)>;
   constexpr int VEC = 16 / sizeof(T);
   constexpr int G = D / VEC;           // lanes per sample
@@ -446,9 +475,6 @@ __global__ void __launch_bounds__(WPB * kWave) msda_cached_kernel(const CachedPa
   static_assert(G >= 1 && UPW * NS <= kWave && LPL <= kWave && kWave % LPL == 0 &&
                     UPW % UPI == 0, "unsupported MSDA geometry");
 
-  __shared__ __attribute__((aligned(16))) unsigned char cache[kCacheBytes];
-  __shared__ SampleGeo geo[WPB][UPW * NS];
-
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   // Block -> (group of xcd_group XCDs, rank in the group). Items of group gi are
@@ -461,28 +487,9 @@ __global__ void __launch_bounds__(WPB * kWave) msda_cached_kernel(const CachedPa
   const int pos_stride = p.NH * D;
   const uint32_t kOOB = p.batch_bytes;
 
-  // Level table and cache layout: row 0 of the cache is zeros, then levels from the
-  // coarsest. Level MIXL keeps as many whole rows as still fit; every other level is
-  // cached whole or not at all, so its reads take one path for the whole wave.
   int lvH[NL], lvW[NL], lvS[NL], lvR[NL];
   uint32_t lvOff[NL];
-  {
-    uint32_t used = ROW;
-#pragma unroll
-    for (int l = NL - 1; l >= 0; --l) {
-      lvH[l] = (int)p.shapes[2 * l];
-      lvW[l] = (int)p.shapes[2 * l + 1];
-      lvS[l] = (int)p.lsi[l];
-      const int64_t rowb = (int64_t)lvW[l] * ROW;
-      int64_t r = (lvH[l] > 0 && rowb > 0) ? ((int64_t)kCacheBytes - used) / rowb : 0;
-      if (r > lvH[l]) r = lvH[l];
-      if (r < 0) r = 0;
-      if (l != MIXL && r < lvH[l]) r = 0;
-      lvR[l] = (int)r;
-      lvOff[l] = used;
-      used += (uint32_t)(r * rowb);
-    }
-  }
+  cache_layout<NL, MIXL>(p, ROW, kCacheBytes, lvH, lvW, lvS, lvR, lvOff);
   if (threadIdx.x < (int)(ROW / 16)) {
     typedef int i4 __attribute__((ext_vector_type(4)));
     *reinterpret_cast<i4 *>(cache + threadIdx.x * 16) = i4{0, 0, 0, 0};
@@ -617,7 +624,7 @@ __global__ void __launch_bounds__(WPB * kWave) msda_cached_kernel(const CachedPa
 #pragma unroll
       for (int it = 0; it < NIT; ++it) {
         const int l = it % NL;
-        if (l == MIXL && lvR[l] > 0 && lvR[l] < lvH[l]) {
+        if (FIX < 0 && l == MIXL && lvR[l] > 0 && lvR[l] < lvH[l]) {
           // Each corner is in the cache or in the value buffer; the other read returns 0.
 #pragma unroll
           for (int c = 0; c < 4; ++c) {
@@ -626,21 +633,21 @@ __global__ void __launch_bounds__(WPB * kWave) msda_cached_kernel(const CachedPa
             v[it][c] = *reinterpret_cast<const V *>(cache + (in_lds ? (o & ~kLdsFlag) + cb : cb));
             vx[it / NL][c] = buffer_load_vec<T, VEC>(rsrc, in_lds ? kOOB : o + cb);
           }
-        } else if (lvR[l] > 0) {
+        } else if (FIX >= 0 ? l >= NL - FIX : lvR[l] > 0) {
 #pragma unroll
           for (int c = 0; c < 4; ++c) {
             v[it][c] = *reinterpret_cast<const V *>(cache + ((sg[it].o[c] & ~kLdsFlag) + cb));
-            if (l == MIXL) vx[it / NL][c] = V{};
+            if (FIX < 0 && l == MIXL) vx[it / NL][c] = V{};
           }
         } else {
 #pragma unroll
           for (int c = 0; c < 4; ++c) {
             v[it][c] = buffer_load_vec<T, VEC>(rsrc, sg[it].o[c] + cb);
-            if (l == MIXL) vx[it / NL][c] = V{};
+            if (FIX < 0 && l == MIXL) vx[it / NL][c] = V{};
           }
         }
       }
-      if constexpr (MIXL >= 0) {
+      if constexpr (MIXL >= 0 && FIX < 0) {
         // One of each pair is all-zero bits: OR keeps the other exactly.
 #pragma unroll
         for (int it = MIXL; it < NIT; it += NL)
@@ -692,6 +699,33 @@ __global__ void __launch_bounds__(WPB * kWave) msda_cached_kernel(const CachedPa
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
   }
+}
+
+// WPB waves per block, UPW (b, q, head) units per wave round, MIXL the one level that may
+// be cached in part (-1: none). The layout check is uniform over the grid. Only 16-bit
+// types get the fixed-layout body (SCA fp16 239.9 -> 237.7 us, bf16 252.0 -> 243.4 us,
+// DETR bf16 93.1 -> 91.2 us): fp32 layouts of the benchmark shapes are never fixed, and
+// with both bodies compiled DETR fp32 (run-time layout) measured 154.2 -> 157.5 us
+// (154.6 -> 156.0 us with the body alone, from the code the split produces).
+template <typename T, int D, int NL, int NP, int WPB, int UPW, int MIXL>
+__global__ void __launch_bounds__(WPB * kWave) msda_cached_kernel(const CachedParams p) {
+  constexpr int kCacheBytes = kLdsBytes - WPB * UPW * NL * NP * (int)sizeof(SampleGeo);
+  __shared__ __attribute__((aligned(16))) unsigned char cache[kCacheBytes];
+  __shared__ SampleGeo geo[WPB][UPW * NL * NP];
+  if constexpr (sizeof(T) == 2 && NL >= 2) {
+    int H[NL], W[NL], S[NL], R[NL];
+    uint32_t Off[NL];
+    cache_layout<NL, MIXL>(p, D * sizeof(T), kCacheBytes, H, W, S, R, Off);
+    bool fixed = true;
+#pragma unroll
+    for (int l = 0; l < NL; ++l)
+      fixed = fixed && (l >= NL - 2 ? H[l] > 0 && W[l] > 0 && R[l] == H[l] : R[l] == 0);
+    if (fixed) {
+      cached_body<T, D, NL, NP, WPB, UPW, MIXL, 2>(p, cache, geo);
+      return;
+    }
+  }
+  cached_body<T, D, NL, NP, WPB, UPW, MIXL, -1>(p, cache, geo);
 }
 
 // One thread per output element (b, q, h, c); any heads / channels / levels / points.
@@ -1183,8 +1217,8 @@ hipError_t launch_wave(const MsdaArgs &a, hipStream_t stream) {
       if (L == 4 && P == 8) {  // BEVFormer SCA
         // fp32: the per-sample gather kernel at high occupancy measured faster than the
         // cached kernel (whose partly cached level still costs a load per corner).
-        if (sizeof(T) == 2 && cached_worthwhile<T, 32, 4, 8>(a))
-          return launch_cached_t<T, 32, 4, 8, 12, 2>(a, stream);
+        if constexpr (sizeof(T) == 2)
+          if (cached_worthwhile<T, 32, 4, 8>(a)) return launch_cached_t<T, 32, 4, 8, 12, 2>(a, stream);
         return launch_wave_t<T, 32, 4, 8>(a, stream);
       }
       if (L == 1 && P == 4) {  // BEVFormer TSA
