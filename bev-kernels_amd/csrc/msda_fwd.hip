@@ -10,10 +10,10 @@
 //   * msda_wave_kernel / msda_wave_lds_kernel: one wavefront owns UPW (b, q, head)
 //     units. G = D/VEC lanes cover the head_dim channels of one sample with 16-byte
 //     loads; the other lane groups take other (level, point) samples at the same time
-//     and the partial sums meet in a butterfly over the lane groups. All corner loads of
-//     a unit are issued before the first use. Corner loads are buffer loads: an invalid
-//     corner gets an out-of-range offset and reads 0 without a memory request, so the
-//     zero padding is branch-free.
+//     and the partial sums meet in a butterfly over the lane groups (lane_group_sum). All
+//     corner loads of a unit are issued before the first use. Corner loads are buffer
+//     loads: an invalid corner gets an out-of-range offset and reads 0 without a memory
+//     request, so the zero padding is branch-free.
 //     The _lds variant (many samples per unit) computes each sample's geometry once,
 //     in one lane, with the attention weight folded into the four corner weights, and
 //     shares it with the sample's lane group through LDS; the plain variant (few
