@@ -55,6 +55,8 @@ template <> __device__ __forceinline__ void load_loc<float>(const float *p, floa
 // LDS-pipe permutes: SCA fp16 242.5 -> 239.0 us, bf16 253.2 -> 250.8 us). Smaller
 // groups use LDS-pipe permutes: the rotations took the 16-bit four-point cached kernel
 // (16-lane groups) from 151 to 168 registers with spills (DETR fp16 89 -> 93 us).
+// Call with every lane of the wave active: the rotations and swaps read other lanes'
+// registers (all call sites are outside divergent code).
 template <int M> __device__ __forceinline__ float row_ror(float x) {
   return __builtin_bit_cast(
       float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x120 | M, 0xf, 0xf, false));
