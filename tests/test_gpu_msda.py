@@ -234,3 +234,91 @@ def test_non_contiguous_rejected():
         _api().ms_deform_attn_forward(v, d["spatial_shapes"].to(dev),
                                       d["level_start_index"].to(dev),
                                       d["sampling_loc"].to(dev), d["attn_weight"].to(dev))
+
+
+def _exact_centre(n):
+    """Index i < n - 1 whose pixel centre (i + 0.5) / n is a dyadic fraction with at most
+    8 significant bits (exact in fp32, fp16 and bf16), so the sample lands on the centre."""
+    from fractions import Fraction
+    for i in range(n - 1):
+        fr = Fraction(2 * i + 1, 2 * n)
+        if fr.denominator & (fr.denominator - 1) == 0 and fr.numerator < 256:
+            return i, float(fr)
+    raise ValueError(f"no exact pixel centre for size {n}")
+
+
+def _poison(d, seed):
+    """NaN / +Inf in value, following the reference's read rule (ms_deform_attn_kernels.cuh
+    :7-49): a corner inside the level is read whatever its bilinear weight (0 * NaN = NaN,
+    0 * Inf = NaN), a corner outside it contributes exactly 0 and is never read.
+      * query 0, head 0 samples the exact centre of a level-0 pixel (y, x) at every point
+        (its other levels far outside); value is finite at the sample's weighted corner and
+        NaN at pixel (y + 1, x + 1), an in-bounds corner of weight 0 -> NaN;
+      * query 1, head 1 samples far outside every level; value is NaN at level-0 pixel
+        (0, 0) of head 1, where a clamped read would land -> output exactly 0;
+      * a few random (position, head) rows of every level hold NaN or +Inf."""
+    g = torch.Generator().manual_seed(seed)
+    v, loc = d["value"], d["sampling_loc"]
+    B, S, NH, D = v.shape
+    shapes = d["spatial_shapes"].tolist()
+    starts = d["level_start_index"].tolist()
+    H0, W0 = shapes[0]
+    for l, ((H, W), start) in enumerate(zip(shapes, starts)):
+        for b in range(B):
+            pos = start + torch.randint(0, H * W, (4,), generator=g)
+            heads = torch.randint(0, NH, (4,), generator=g)
+            for k in range(4):
+                v[b, pos[k], heads[k], :] = float("nan") if k < 2 else float("inf")
+    y, ly = _exact_centre(H0)
+    x, lx = _exact_centre(W0)
+    for p in (y * W0 + x, y * W0 + x + 1, (y + 1) * W0 + x):   # the sample's other corners
+        v[0, p, 0, :] = 1.0
+    v[0, (y + 1) * W0 + x + 1, 0, :] = float("nan")
+    loc[0, 0, 0] = -5.0                                          # other levels: outside
+    loc[0, 0, 0, 0, :, 0] = lx
+    loc[0, 0, 0, 0, :, 1] = ly
+    v[0, 0, 1, :] = float("nan")
+    loc[0, 1, 1] = -5.0
+    return d
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=["fp32", "fp16", "bf16"])
+@pytest.mark.parametrize("kind", ["wave", "generic", "cached", "cached_fixed", "tsa_tiled"])
+def test_nonfinite_value(kind, dtype):
+    """NaN and Inf in value give NaN / Inf exactly where the float64 oracle does, and the
+    finite outputs match it to tolerance. 'cached' has three levels in LDS (run-time
+    layout in 16-bit types, the per-sample kernel in fp32), 'cached_fixed' the two
+    coarsest (the fixed-layout body in 16-bit types)."""
+    force_generic = kind == "generic"
+    if kind in ("wave", "generic"):
+        d = inputs.msda_random(2, [(6, 8), (3, 5), (2, 3), (2, 2)], 50, 8, 32, 4, seed=31,
+                               loc_lo=-0.3, loc_hi=1.3)
+    elif kind == "cached":
+        d = inputs.msda_random(3, [(64, 90), (32, 45), (16, 23), (8, 12)], 11001, 2, 32, 8,
+                               seed=32, loc_lo=-0.25, loc_hi=1.25)
+    elif kind == "cached_fixed":
+        d = inputs.msda_random(1, [(116, 200), (58, 100), (29, 50), (15, 25)], 8192, 8, 32, 8,
+                               seed=33, loc_lo=-0.2, loc_hi=1.2)
+    else:
+        d = _tsa_like(2, 40, 37, 0.01, seed=34)
+    _poison(d, seed=35)
+    nq = d["sampling_loc"].shape[1]
+    out = _run(d, dtype, force_generic=force_generic).double()
+    if nq > 4000:
+        g = torch.Generator().manual_seed(36)
+        q_idx = torch.cat([torch.randperm(nq, generator=g)[:300],
+                           torch.tensor([0, 1, nq - 1])]).unique()
+        out = out[:, q_idx]
+        ref = _ref(d, dtype, q_idx)
+    else:
+        ref = _ref(d, dtype)
+    what = f"nonfinite {kind} {dtype}"
+    assert torch.equal(torch.isnan(out), torch.isnan(ref)), f"{what}: NaN pattern"
+    assert torch.equal(torch.isinf(out), torch.isinf(ref)), f"{what}: Inf pattern"
+    assert torch.equal(out[torch.isinf(ref)], ref[torch.isinf(ref)]), f"{what}: Inf sign"
+    fin = torch.isfinite(ref)
+    check(out[fin], ref[fin], dtype, what)
+    D = 32
+    assert torch.isnan(out[0, 0, :D]).all(), f"{what}: zero-weight NaN corner not read"
+    assert (out[0, 1, D:2 * D] == 0).all(), f"{what}: out-of-range sample not exactly 0"
+    assert 0.05 < fin.double().mean().item() < 0.999, f"{what}: degenerate poison pattern"
