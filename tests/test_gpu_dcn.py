@@ -727,3 +727,103 @@ def test_pack_cuda_channels_last(monkeypatch):
                           mod.bias.double().cpu(), (1, 1), (1, 1), (1, 1))
     check(out_cl.cpu(), ref, torch.float32, "channels_last")
     check(out.cpu(), ref, torch.float32, "contiguous")
+
+
+# ---------------------------------------------------------------------------------------
+# Non-finite input: the reference's corner read rule (modulated_deform_conv.py:184-213,
+# dcn_fused_nhwc_kernel.cuh:270-301): an in-bounds corner is read whatever its bilinear
+# weight (0 * NaN = NaN), an out-of-bounds corner contributes exactly 0.
+# ---------------------------------------------------------------------------------------
+
+def _poison_nhwc(x, off, seed):
+    """x [B, H, W, C], off [B, Ho, Wo, 18] (stride 1, pad 1, dilation 1, 3 x 3), in place:
+      * output pixel (1, 2) of image 0: every tap lands exactly on input pixel (1, 2), whose
+        corner of weight 1 is finite and whose weight-0 corners include NaN pixel (2, 3)
+        -> the whole output row is NaN;
+      * output pixel (Ho - 2, 1) of image 0: every tap far outside (offset +40), and NaN at
+        input pixel (H - 1, W - 1), where a clamped read would land -> output = bias;
+      * a few random pixels of every image hold NaN or +Inf in all channels."""
+    g = torch.Generator().manual_seed(seed)
+    B, H, W, C = x.shape
+    for b in range(B):
+        ys = torch.randint(0, H, (4,), generator=g)
+        xs = torch.randint(0, W, (4,), generator=g)
+        for k in range(4):
+            x[b, ys[k], xs[k], :] = float("nan") if k < 2 else float("inf")
+    for (py, px) in ((1, 2), (1, 3), (2, 2)):
+        x[0, py, px, :] = 1.0
+    x[0, 2, 3, :] = float("nan")
+    for t in range(9):
+        ki, kj = t // 3, t % 3
+        off[0, 1, 2, 2 * t] = 1 - ki        # h_im = 1 - 1 + ki + (1 - ki) = 1
+        off[0, 1, 2, 2 * t + 1] = 1 - kj    # w_im = 2 - 1 + kj + (1 - kj) = 2
+    x[0, H - 1, W - 1, :] = float("nan")
+    off[0, -2, 1, :] = 40.0
+
+
+def _nonfinite_check(out, ref, dtype, what):
+    out, ref = out.double().cpu(), ref.double().cpu()
+    assert torch.equal(torch.isnan(out), torch.isnan(ref)), f"{what}: NaN pattern"
+    assert torch.equal(torch.isinf(out), torch.isinf(ref)), f"{what}: Inf pattern"
+    assert torch.equal(out[torch.isinf(ref)], ref[torch.isinf(ref)]), f"{what}: Inf sign"
+    fin = torch.isfinite(ref)
+    check(out[fin], ref[fin], dtype, what)
+    assert 0.05 < fin.double().mean().item() < 0.999, f"{what}: degenerate poison pattern"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16],
+                         ids=["fp32", "fp16", "bf16"])
+@pytest.mark.parametrize("shape", [(2, 16, 32, 9, 11), (1, 64, 320, 90, 100)],
+                         ids=["tiled", "persistent"])
+def test_nonfinite_input_nhwc(shape, dtype):
+    """NaN / Inf in x give NaN / Inf exactly where the float64 oracle does (fused NHWC
+    forward: the tiled kernel, and in 16-bit types the persistent kernel with two column
+    halves), and every finite output matches it to tolerance."""
+    from modulated_deform_conv import fused_tl
+    b, cin, cout, h, w = shape
+    g = torch.Generator().manual_seed(41)
+    x = torch.randn(b, h, w, cin, generator=g)
+    off = 2.0 * torch.randn(b, h, w, 18, generator=g)
+    mask = torch.rand(b, h, w, 9, generator=g)
+    weight = 0.1 * torch.randn(cout, cin, 3, 3, generator=g)
+    bias = torch.randn(cout, generator=g)
+    _poison_nhwc(x, off, seed=42)
+    x, off, mask, weight, bias = (t.to(dtype) for t in (x, off, mask, weight, bias))
+    out = fused_tl.fused_dcn_forward_nhwc(x.to(DEV), off.to(DEV), mask.to(DEV),
+                                          weight.to(DEV), bias.to(DEV), 1, 1, 1)
+    torch.cuda.synchronize()
+    ref = od.forward_nhwc(x.double(), off.double(), mask.double(), weight.double(),
+                          bias.double(), 1, 1, 1, col_dtype=_cols_dtype(dtype))
+    what = f"nonfinite nhwc {shape} {dtype}"
+    _nonfinite_check(out, ref, dtype, what)
+    out = out.cpu()
+    assert torch.isnan(out[0, 1, 2].float()).all(), f"{what}: zero-weight NaN corner not read"
+    assert torch.equal(out[0, -2, 1], bias), f"{what}: out-of-range taps not exactly 0"
+
+
+@pytest.mark.parametrize("groups", [1, 2])
+def test_nonfinite_input_nchw(groups):
+    """The NCHW module forward (groups 1: NHWC fused kernel between transposes; groups 2:
+    NCHW column kernel + per-group GEMM) with NaN / Inf in x, against the float64 oracle."""
+    from modulated_deform_conv import modulated_deform_conv2d
+    g = torch.Generator().manual_seed(43)
+    b, cin, cout, h, w = 2, 16, 24, 11, 13
+    x = torch.randn(b, h, w, cin, generator=g)
+    off = 2.0 * torch.randn(b, h, w, 18, generator=g)
+    _poison_nhwc(x, off, seed=44)
+    x = x.permute(0, 3, 1, 2).contiguous()
+    off = off.permute(0, 3, 1, 2).contiguous()
+    mask = torch.rand(b, 9, h, w, generator=g)
+    weight = 0.1 * torch.randn(cout, cin // groups, 3, 3, generator=g)
+    bias = torch.randn(cout, generator=g)
+    out = modulated_deform_conv2d(x.to(DEV), off.to(DEV), mask.to(DEV), weight.to(DEV),
+                                  bias.to(DEV), 1, 1, 1, groups, 1)
+    torch.cuda.synchronize()
+    ref = od.forward_nchw(x.double(), off.double(), mask.double(), weight.double(),
+                          bias.double(), (1, 1), (1, 1), (1, 1), groups, 1)
+    what = f"nonfinite nchw groups {groups}"
+    _nonfinite_check(out, ref, torch.float32, what)
+    out = out.cpu()
+    if groups == 1:
+        assert torch.isnan(out[0, :, 1, 2]).all(), f"{what}: zero-weight NaN corner not read"
+    assert torch.equal(out[0, :, -2, 1], bias), f"{what}: out-of-range taps not exactly 0"
