@@ -541,8 +541,10 @@ __global__ void __launch_bounds__(kBlock) msda_grid_coord_kernel(
     if (live && far[pt]) {  // samples the owner pass does not take: atomics
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        if (wt[pt][k] == 0.f) continue;
+        // every corner inside the map, weight 0 included (0 * a non-finite grad_output is
+        // NaN in the reference's add, ms_deform_attn_kernels.cuh:445-480)
         const int yy = hls[pt] + (k >> 1), xx = wls[pt] + (k & 1);
+        if (yy < 0 || yy >= H || xx < 0 || xx >= W || (int64_t)yy * W + xx >= avail) continue;
         float *dst = gvb + ((int64_t)yy * W + xx) * row;
         const float ta = wt[pt][k] * av[pt];
 #pragma unroll
@@ -1734,7 +1736,8 @@ __global__ void __launch_bounds__(kCoWaves * kWave) msda_coord_kernel(const Coor
       float4 par = make_float4(0.f, 0.f, 0.f, 0.f);
       float him, wim;
       sample_coords<float>((float)xy.v[0], (float)xy.v[1], Hl, Wl, him, wim);
-      if (on && him > -1.f && wim > -1.f && him < Hf && wim < Wf) {
+      const bool win = on && him > -1.f && wim > -1.f && him < Hf && wim < Wf;
+      if (win) {
         const float fh = floorf(him), fw = floorf(wim);
         const int hl = (int)fh, wl = (int)fw;
         const uint32_t e1 = (uint32_t)((lbase + hl * Wl + wl) * row) * (uint32_t)sizeof(T);
@@ -1770,7 +1773,7 @@ __global__ void __launch_bounds__(kCoWaves * kWave) msda_coord_kernel(const Coor
           const float s1 = piece_dot<T, VEC>(top, cv[j][0]), s2 = piece_dot<T, VEC>(top, cv[j][1]);
           const float s3 = piece_dot<T, VEC>(top, cv[j][2]), s4 = piece_dot<T, VEC>(top, cv[j][3]);
           const float lh = pr[j].x, lw = pr[j].y, hh = 1.f - lh, hw = 1.f - lw;
-          // a sample outside the window has no valid corner: S_k = 0 and all three are 0
+          // a sample outside the window has no valid corner (its sums are discarded below)
           float gh = pr[j].z * (hw * (s3 - s1) + lw * (s4 - s2));
           float gw = pr[j].w * (hh * (s2 - s1) + lh * (s4 - s3));
           float ga = hh * hw * s1 + hh * lw * s2 + lh * hw * s3 + lh * lw * s4;
@@ -1781,9 +1784,10 @@ __global__ void __launch_bounds__(kCoWaves * kWave) msda_coord_kernel(const Coor
         }
       }
       wave_lds_handover();
-      // 3. sample lanes
+      // 3. sample lanes; a sample outside its level writes zeros whatever grad_output holds
+      // (the reference skips it: ms_deform_attn_kernels.cuh:252-259)
       if (on) {
-        const float4 rr = s_res[wave][lane];
+        const float4 rr = win ? s_res[wave][lane] : make_float4(0.f, 0.f, 0.f, 0.f);
         Vec<T, 2> gl;
         gl.v[0] = (T)rr.x;
         gl.v[1] = (T)rr.y;

@@ -652,3 +652,90 @@ def test_backward_workspace_cap(dtype, monkeypatch):
     _check3(got, ref, dtype, "capped from the environment")
     assert peak_full - peak_capped >= 0.9 * (full - least), (peak_full, peak_capped, full, least)
     assert peak_env == peak_capped
+
+
+def _exact_centre(n):
+    """Index i < n - 1 whose pixel centre (i + 0.5) / n is exact in fp32, fp16 and bf16."""
+    from fractions import Fraction
+    for i in range(n - 1):
+        fr = Fraction(2 * i + 1, 2 * n)
+        if fr.denominator & (fr.denominator - 1) == 0 and fr.numerator < 256:
+            return i, float(fr)
+    raise ValueError(f"no exact pixel centre for size {n}")
+
+
+def _poison_bwd(d, go, seed):
+    """Non-finite value / grad_output, following the reference's per-sample gradient
+    (ms_deform_attn_kernels.cuh:427-490): every in-bounds corner enters the position and
+    attention gradients and receives w * top * a in grad_value, whatever its weight w.
+    Units (batch 0, query 0, head 0) and (0, 1, head 1 % NH) sample the exact centre of
+    level-0 pixel (y, x) at every point (other levels far outside):
+      * value NaN at (y + 1, x + 1) of head 0, a corner of weight 0, the other corners
+        finite -> that unit's grad_sampling_loc and grad_attn_weight are NaN;
+      * grad_output NaN for the second unit -> grad_value NaN at all four corners of its
+        head, the three of weight 0 included;
+      * a few random (position, head) rows of value hold NaN or +Inf."""
+    g = torch.Generator().manual_seed(seed)
+    v, loc = d["value"], d["sampling_loc"]
+    B, S, NH, D = v.shape
+    shapes = d["spatial_shapes"].tolist()
+    starts = d["level_start_index"].tolist()
+    for (H, W), start in zip(shapes, starts):
+        for b in range(B):
+            pos = start + torch.randint(0, H * W, (4,), generator=g)
+            heads = torch.randint(0, NH, (4,), generator=g)
+            for k in range(4):
+                v[b, pos[k], heads[k], :] = float("nan") if k < 2 else float("inf")
+    H0, W0 = shapes[0]
+    y, ly = _exact_centre(H0)
+    x, lx = _exact_centre(W0)
+    h1 = 1 % NH
+    for q, h in ((0, 0), (1, h1)):
+        loc[0, q, h] = -5.0
+        loc[0, q, h, 0, :, 0] = lx
+        loc[0, q, h, 0, :, 1] = ly
+    for p in (y * W0 + x, y * W0 + x + 1, (y + 1) * W0 + x):
+        v[0, p, 0, :] = 1.0
+    v[0, (y + 1) * W0 + x + 1, 0, :] = float("nan")
+    go[0, 1, h1 * D:(h1 + 1) * D] = float("nan")
+    return [(y + dy) * W0 + x + dx for dy in (0, 1) for dx in (0, 1)], h1
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=IDS)
+@pytest.mark.parametrize("kind", ["sorted", "atomic", "owner", "generic"])
+def test_nonfinite_backward(kind, dtype):
+    """NaN / Inf in value and grad_output give NaN / Inf in all three gradients exactly where
+    the float64 oracle does, through each backward path (the API's sorted path, the D = 32
+    atomic kernels, the grid-query owner kernels, the generic kernels for D = 64); finite
+    entries match it to tolerance."""
+    if kind == "owner":
+        d = _grid_queries(1, 23, 37, 2, 4, 2.0, 0.05, seed=61)
+    elif kind == "generic":
+        d = inputs.msda_random(2, [(6, 8), (3, 5)], 40, 2, 64, 4, seed=62, loc_lo=-0.3,
+                               loc_hi=1.3)
+    else:
+        d = inputs.msda_random(2, [(12, 16), (6, 8), (3, 4), (2, 2)], 300, 4, 32, 8, seed=63,
+                               loc_lo=-0.3, loc_hi=1.3)
+    go = _grad_output(d, seed=64)
+    corners, h1 = _poison_bwd(d, go, seed=65)
+    if kind in ("atomic", "owner"):
+        got = _run_workspace(d, go, dtype, _accumulator_bytes(d, dtype))
+    else:
+        got = _run(d, go, dtype)
+    ref = _ref(d, go, dtype)
+    what = f"nonfinite backward {kind} {dtype}"
+    for name, x, r in zip(("grad_value", "grad_sampling_loc", "grad_attn_weight"), got, ref):
+        x, r = x.double(), r.double()
+        assert torch.equal(torch.isnan(x), torch.isnan(r)), f"{what} {name}: NaN pattern"
+        assert torch.equal(torch.isinf(x), torch.isinf(r)), f"{what} {name}: Inf pattern"
+        assert torch.equal(x[torch.isinf(r)], r[torch.isinf(r)]), f"{what} {name}: Inf sign"
+        fin = torch.isfinite(r)
+        check(x[fin], r[fin], dtype, f"{what} {name}")
+    gv, gl, ga = got
+    assert torch.isnan(gl[0, 0, 0, 0]).all() and torch.isnan(ga[0, 0, 0, 0]).all(), \
+        f"{what}: weight-0 NaN corner left out of the position gradient"
+    for p in corners:
+        assert torch.isnan(gv[0, p, h1].float()).all(), \
+            f"{what}: grad_value of a corner of weight 0 missed the NaN grad_output"
+    fin = torch.isfinite(ref[1]).double().mean().item()
+    assert 0.05 < fin < 0.999, f"{what}: degenerate poison pattern"
