@@ -739,3 +739,36 @@ def test_nonfinite_backward(kind, dtype):
             f"{what}: grad_value of a corner of weight 0 missed the NaN grad_output"
     fin = torch.isfinite(ref[1]).double().mean().item()
     assert 0.05 < fin < 0.999, f"{what}: degenerate poison pattern"
+
+
+@pytest.mark.parametrize("nq", [(1 << 22) - 4, (1 << 22) + 4], ids=["below", "above"])
+def test_sorted_path_query_limit(nq):
+    """fp16, one head, one 512 x 512 level, one point, about 2^22 queries: the API (the
+    sorted path below 2^22 queries, bkt_layout: its record word is query << 8 | position
+    in bucket; the atomic kernels from 2^22 on) against the D = 32 atomic kernels through
+    the C ABI, every output."""
+    import _bevk as bk
+    dt = torch.float16
+    H = W = 512
+    g = torch.Generator(device=DEV).manual_seed(71)
+    value = torch.randn(1, H * W, 1, 32, generator=g, device=DEV).to(dt)
+    loc = torch.rand(1, nq, 1, 1, 1, 2, generator=g, device=DEV).to(dt)
+    attn = torch.rand(1, nq, 1, 1, 1, generator=g, device=DEV).to(dt)
+    go = torch.randn(1, nq, 32, generator=g, device=DEV).to(dt)
+    shapes = torch.tensor([[H, W]], dtype=torch.int64, device=DEV)
+    lsi = torch.zeros(1, dtype=torch.int64, device=DEV)
+    api = _api().ms_deform_attn_backward(value, shapes, lsi, loc, attn, grad_output=go)
+    gv = torch.zeros_like(value)
+    gl = torch.empty_like(loc)
+    ga = torch.empty_like(attn)
+    ws_bytes = value.numel() * 4  # the fp32 grad_value accumulator only: atomic kernels
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
+    g4 = go.view(1, nq, 1, 32)
+    bk.call("bevk_msda_backward", bk.dtype_code(value), bk.ptr(value), bk.ptr(shapes),
+            bk.ptr(lsi), bk.ptr(loc), bk.ptr(attn), bk.ptr(g4), *g4.stride(), 1, H * W, 1, 32,
+            1, nq, 1, 64, 0, bk.ptr(gv), bk.ptr(gl), bk.ptr(ga), bk.ptr(ws), ws_bytes,
+            bk.stream_of(value))
+    torch.cuda.synchronize()
+    for name, x, r in zip(("grad_value", "grad_sampling_loc", "grad_attn_weight"), api,
+                          (gv, gl, ga)):
+        check(x.cpu(), r.cpu(), dt, f"{nq} queries {name}: API vs atomic kernels")
