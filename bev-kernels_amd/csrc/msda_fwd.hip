@@ -1226,11 +1226,12 @@ hipError_t launch_wave(const MsdaArgs &a, hipStream_t stream) {
       if (L == 1 && P == 4) {  // BEVFormer TSA
         // the tiled kernel (neighbourhood in LDS) measured faster than the per-sample
         // gather kernel: fp32 by 25%, fp16 74.0 -> 69.1 us, bf16 75.4 -> 73.6 us
-        if (a.num_query == a.spatial_size && device_cus() >= 8)
+        if (a.num_query == a.spatial_size && device_cus() >= 8) {
           if constexpr (sizeof(T) == 2)
             return launch_tile_t<T, 4, 16, 6, 8, 1, true>(a, stream);
           else
             return launch_tile_t<T, 4, 16, 6, 8, 1, false>(a, stream);
+        }
         return launch_wave_t<T, 32, 1, 4>(a, stream);
       }
       if (L == 4 && P == 4) {  // Deformable DETR
