@@ -1192,7 +1192,8 @@ struct SShape {
 template <typename T, int NRB, int NS>
 __device__ __forceinline__ void dcn_s_body(const HParams &p, const TapGeo *geo,
                                            T (*As)[NRB * 16 * kPLDA], T *stage, int n0, int nk,
-                                           int lane, int wave, int tid) {
+                                           int lane, int wave, int tid, int4v (&br0)[kPKH][2],
+                                           int4v (&br1)[kPKH][2]) {
   using V = Vec<T, 8>;
   constexpr int KV = kPBK / 8;
   constexpr int NF = 2 * NRB;        // A fragments per step (k-half x row block)
@@ -1302,9 +1303,6 @@ __device__ __forceinline__ void dcn_s_body(const HParams &p, const TapGeo *geo,
     __syncthreads();
   };
 
-  int4v br0[kPKH][2], br1[kPKH][2];
-  issue_b(0, br0);
-  issue_b(1, br1);
   // prologue: A(0) blended here; the loads of step 1 issued
 #pragma unroll
   for (int i = 0; i < NS; ++i) issue_slot(i, 0);
@@ -1388,6 +1386,23 @@ __global__ void __launch_bounds__(kSThreads) dcn_fused_s_kernel(const PParams pp
       dcn_p_producer<T, PSH::kSPT - 1, NRB, true, 2>(p, geo, As, nk, tid - kPProd);
     __syncthreads();  // y of every row in ys
   }
+  // B fragments of the first two K steps (br0 / br1 of dcn_s_body), issued before the
+  // geometry table, which they do not need: their latency runs under it (res4 fp16 61.6 ->
+  // 60.8 us, bf16 64.8 -> 64.1 us; in dcn_fused_p_kernel the same measured res5 fp16
+  // 74.1 -> 72.2 us but bf16 74.2 -> 75.0 us, and it spills at 2-3 row blocks: not there)
+  int4v br0[kPKH][2], br1[kPKH][2];
+  {
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, p.w_bytes);
+#pragma unroll
+    for (int kh = 0; kh < kPKH; ++kh)
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb) {
+        const uint32_t bo = b_frag_offset(n0 + wave * 32 + cb * 16 + (lane & 15), kh, lane,
+                                          p.nb_total, p.kb_total, p.w_bytes);
+        br0[kh][cb] = __builtin_amdgcn_raw_buffer_load_b128(wr, bo, 0u, 0);
+        br1[kh][cb] = __builtin_amdgcn_raw_buffer_load_b128(wr, bo, (uint32_t)(kPBK / 16) * 1024u, 0);
+      }
+  }
   for (int g = tid; g < kRows * TT; g += kSThreads) {
     const int row = g / TT, t = g - row * TT, m = m0 + row;
     TapGeo G = empty_geo(xoob);
@@ -1401,9 +1416,9 @@ __global__ void __launch_bounds__(kSThreads) dcn_fused_s_kernel(const PParams pp
   }
   __syncthreads();  // MEGA: ys is dead from here, the A ring is written again
   if (wave < SH::kFullWaves)
-    dcn_s_body<T, NRB, SH::kNS>(p, geo, As, stage, n0, nk, lane, wave, tid);
+    dcn_s_body<T, NRB, SH::kNS>(p, geo, As, stage, n0, nk, lane, wave, tid, br0, br1);
   else
-    dcn_s_body<T, NRB, SH::kNS - 1>(p, geo, As, stage, n0, nk, lane, wave, tid);
+    dcn_s_body<T, NRB, SH::kNS - 1>(p, geo, As, stage, n0, nk, lane, wave, tid, br0, br1);
   __syncthreads();
   T *out = static_cast<T *>(p.out);
   constexpr int kPieces = kPCols / 8;
