@@ -834,7 +834,8 @@ __device__ __forceinline__ uint32_t b_frag_offset(int n, int kh, int lane, int n
 // run-time conditions).
 template <typename T, int NRB, int CD>
 __device__ __forceinline__ void dcn_p_consumer(const HParams &p, T (*As)[NRB * 16 * kPLDA],
-                                               T *stage, int n0, int nk, int lane, int wave) {
+                                               T *stage, int n0, int nk, int lane, int wave,
+                                               const int4v (&b0)[kPKH][4], bool b0_loaded) {
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, p.w_bytes);
   uint32_t bo[kPKH][4];
 #pragma unroll
@@ -877,8 +878,16 @@ __device__ __forceinline__ void dcn_p_consumer(const HParams &p, T (*As)[NRB * 1
     issue_b(ks + CD, br);
     __syncthreads();
   };
+  if (b0_loaded) {  // B(0) loaded by the caller before the geometry table
 #pragma unroll
-  for (int d = 0; d < CD; ++d) issue_b(d, br[d]);
+    for (int kh = 0; kh < kPKH; ++kh)
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) br[0][kh][cb] = b0[kh][cb];
+  } else {
+    issue_b(0, br[0]);
+  }
+#pragma unroll
+  for (int d = 1; d < CD; ++d) issue_b(d, br[d]);
   __syncthreads();  // A(0) written by the producers
   int ks = 0;
   for (; ks + CD <= nk; ks += CD) {
@@ -1118,6 +1127,22 @@ __global__ void __launch_bounds__(kPThreads) dcn_fused_p_kernel(const PParams pp
     __syncthreads();  // y of every row in ys
   }
 
+  // The consumers' B fragments of K step 0, loaded before the geometry table (they do not
+  // need it) where the consumers keep two B sets (4-5 row blocks): res5 fp16 74.1 -> 71.7 us,
+  // bf16 74.4 -> 74.1 us, res5 one-launch fp16 84.6 -> 83.0 us. Loading both sets early
+  // measured res5 bf16 74.2 -> 75.0 us, and with four sets (2-3 row blocks) it spills.
+  constexpr bool kB0Early = SH::kCD == 2;
+  int4v b0[kPKH][4];
+  if (kB0Early && wave < 4) {
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, p.w_bytes);
+#pragma unroll
+    for (int kh = 0; kh < kPKH; ++kh)
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb)
+        b0[kh][cb] = __builtin_amdgcn_raw_buffer_load_b128(
+            wr, b_frag_offset(n0 + wave * 64 + cb * 16 + (lane & 15), kh, lane, p.nb_total,
+                              p.kb_total, p.w_bytes), 0u, 0);
+  }
   // Geometry table for all NRB * 16 rows (rows outside the range or past M: zero weights,
   // out-of-range offsets).
   for (int g = tid; g < kPRows * TT; g += kPThreads) {
@@ -1140,7 +1165,7 @@ __global__ void __launch_bounds__(kPThreads) dcn_fused_p_kernel(const PParams pp
   // 67.8 us; the consumers raised instead, 70.2 us).
   if (wave >= 4) __builtin_amdgcn_s_setprio(2);
   if (wave < 4)
-    dcn_p_consumer<T, NRB, SH::kCD>(p, As, stage, n0, nk, lane, wave);
+    dcn_p_consumer<T, NRB, SH::kCD>(p, As, stage, n0, nk, lane, wave, b0, kB0Early);
   else if (wave - 4 < SH::kLastWaves)
     dcn_p_producer<T, SH::kSPT, NRB, false, SH::kPD>(p, geo, As, nk, tid - kPProd);
   else if constexpr (SH::kLastWaves < 4)
@@ -1388,8 +1413,7 @@ __global__ void __launch_bounds__(kSThreads) dcn_fused_s_kernel(const PParams pp
   }
   // B fragments of the first two K steps (br0 / br1 of dcn_s_body), issued before the
   // geometry table, which they do not need: their latency runs under it (res4 fp16 61.6 ->
-  // 60.8 us, bf16 64.8 -> 64.1 us; in dcn_fused_p_kernel the same measured res5 fp16
-  // 74.1 -> 72.2 us but bf16 74.2 -> 75.0 us, and it spills at 2-3 row blocks: not there)
+  // 60.8 us, bf16 64.8 -> 64.1 us; dcn_fused_p_kernel loads its first B set the same way)
   int4v br0[kPKH][2], br1[kPKH][2];
   {
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, p.w_bytes);
