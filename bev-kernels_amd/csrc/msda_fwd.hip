@@ -794,11 +794,10 @@ __device__ __forceinline__ void cached_body(const CachedParams &p, unsigned char
 }
 
 // WPB waves per block, UPW (b, q, head) units per wave round, MIXL the one level that may
-// be cached in part (-1: none). The layout check is uniform over the grid. Only 16-bit
-// types get the fixed-layout body (SCA fp16 239.9 -> 237.7 us, bf16 252.0 -> 243.4 us,
-// DETR bf16 93.1 -> 91.2 us): fp32 layouts of the benchmark shapes are never fixed, and
-// with both bodies compiled DETR fp32 (run-time layout) measured 154.2 -> 157.5 us
-// (154.6 -> 156.0 us with the body alone, from the code the split produces).
+// be cached in part (-1: none). The layout check is uniform over the grid. The fixed-layout
+// body is compiled for 16-bit types (SCA fp16 239.9 -> 237.7 us, bf16 252.0 -> 243.4 us,
+// DETR bf16 93.1 -> 91.2 us), the only ones the dispatch sends here; the run-time body
+// serves any layout.
 template <typename T, int D, int NL, int NP, int WPB, int UPW, int MIXL>
 __global__ void __launch_bounds__(WPB * kWave) msda_cached_kernel(const CachedParams p) {
   constexpr int kCacheBytes = kLdsBytes - WPB * UPW * NL * NP * (int)sizeof(SampleGeo);
@@ -1325,8 +1324,11 @@ hipError_t launch_wave(const MsdaArgs &a, hipStream_t stream) {
         return launch_wave_t<T, 32, 1, 4>(a, stream);
       }
       if (L == 4 && P == 4) {  // Deformable DETR
-        if (cached_worthwhile<T, 32, 4, 4>(a))
-          return launch_cached_t<T, 32, 4, 4, 12, 2>(a, stream);
+        // 16-bit types: the LDS-cached kernel. fp32: the per-sample kernel, whose slice
+        // streaming (value lines and records) measured DETR fp32 cold 154.9 -> 152.8 us and
+        // warm 138.6 -> 132.2 us against the cached kernel (fp16: 119.6 against 87.7 us).
+        if constexpr (sizeof(T) == 2)
+          if (cached_worthwhile<T, 32, 4, 4>(a)) return launch_cached_t<T, 32, 4, 4, 12, 2>(a, stream);
         return launch_wave_t<T, 32, 4, 4>(a, stream);
       }
       return launch_wave_t<T, 32, 0, 0>(a, stream);

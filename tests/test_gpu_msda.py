@@ -67,6 +67,7 @@ def test_configs_full_size(cfg, dtype):
 @pytest.mark.parametrize("dtype", DTYPES, ids=["fp32", "fp16", "bf16"])
 @pytest.mark.parametrize("geom", [
     # batch, heads, num_query, shapes, points: large enough for the LDS-cached kernel
+    # (16-bit types; fp32 runs the per-sample kernel with slice streaming)
     (3, 2, 11001, [(64, 90), (32, 45), (16, 23), (8, 12)], 8),   # level 1 partly cached,
     #   6 slices -> each slice split into query ranges over the 8 XCDs
     (1, 8, 8193, [(40, 70), (20, 35), (10, 18), (5, 9)], 4),      # 8 slices, DETR points
