@@ -291,43 +291,19 @@ struct SampleGeo {
   uint32_t o[4];
 };
 
-// Reads the 128-byte value lines of positions [p0, p1) (byte column `col` of each
-// position's row of pos_bytes), 16 bytes per thread and NF loads in flight per thread, and
-// throws the data away: the lines land in the XCD's L2 (and the last-level cache) ahead of
-// the gathers that need them. The loaded words are folded into a value stored under a
-// condition that never holds, so the loads are kept.
-template <int THREADS, int NF>
-__device__ __forceinline__ void stream_lines(const __amdgpu_buffer_rsrc_t rs, int p0, int p1,
-                                             uint32_t pos_bytes, uint32_t col, uint32_t oob,
-                                             int never, void *sink_out) {
-  constexpr int PPR = THREADS / 8;  // positions per round
-  const uint32_t piece = col + (threadIdx.x % 8u) * 16u;
-  uint32_t sink = 0;
-  for (int r0 = p0; r0 < p1; r0 += NF * PPR) {
-    typedef int i4 __attribute__((ext_vector_type(4)));
-    i4 v[NF];
-#pragma unroll
-    for (int k = 0; k < NF; ++k) {
-      const int pos = r0 + k * PPR + (int)(threadIdx.x / 8u);
-      v[k] = __builtin_amdgcn_raw_buffer_load_b128(
-          rs, pos < p1 ? (uint32_t)pos * pos_bytes + piece : oob, 0, 0);
-    }
-#pragma unroll
-    for (int k = 0; k < NF; ++k) sink ^= (uint32_t)(v[k].x ^ v[k].w);
-  }
-  if (never < 0 && sink == 0x9e3779b9u) *static_cast<unsigned char *>(sink_out) = 0;
-}
-
 // Slice streaming for msda_wave_lds_kernel: the first kStreamBlocks blocks of a (batch,
-// head-group) slice each stream a 1 / kStreamBlocks share of the slice's value lines (one
-// 128-byte line per position) in position order before their own units. With the inputs
-// cold in HBM, the random first touches of the slice's gathers then find most lines
-// already in the XCD's L2: SCA fp32 cold 382.4 -> 375.0 us (32 / 128 / 256 streaming
-// blocks: 379.0 / 376.1 / 382.4 us; a share in every block: 425.5 us, too late and too much
-// texture-path work; blocks half-way through slice k streaming slice k + 1 instead: 375-376
-// us). The price is paid with warm inputs: back-to-back launches 318.5 -> 327.0 us (one
-// word per line, or wave 0 alone streaming, the same). Only slices of at least
-// 4 * kStreamBlocks blocks stream.
+// head-group) slice each touch one word of every 128-byte value line (one line per
+// position) of a 1 / kStreamBlocks share of the slice, in position order, before their own
+// units, and throw the words away. With the inputs cold in HBM, the random first touches
+// of the slice's gathers then find most lines already in the XCD's L2 or the last-level
+// cache: SCA fp32 cold 382.4 -> 375.0 us with full-line loads (32 / 128 / 256 streaming
+// blocks: 379.0 / 376.1 / 382.4 us; a share in every block: 425.5 us, too late and too
+// much texture-path work; blocks half-way through slice k streaming slice k + 1 instead:
+// 375-376 us), and with the record stream below in place one word per line instead of
+// full lines 346.8 -> 342.4 us (eight times fewer loads). The price is paid with warm
+// inputs: back-to-back launches 318.5 -> 327.0 us. Only slices of at least
+// 4 * kStreamBlocks blocks stream. The words are folded into a value stored under a
+// condition that never holds, so the loads are kept.
 constexpr int kStreamBlocks = 64;
 
 template <typename T, int D>
@@ -338,8 +314,20 @@ __device__ __forceinline__ void stream_slice_lines(const WaveParams &p, int b, i
       make_rsrc(static_cast<const T *>(p.value) + (int64_t)b * p.S * p.NH * D, p.batch_bytes);
   const int per = (p.S + kStreamBlocks - 1) / kStreamBlocks;
   const int p0 = min(p.S, chunk * per), p1 = min(p.S, p0 + per);
-  stream_lines<kBlock, 8>(rs, p0, p1, (uint32_t)(p.NH * D * sizeof(T)), (uint32_t)hg * line,
-                       p.batch_bytes, p.NQ, p.out);
+  const uint32_t pos_bytes = (uint32_t)(p.NH * D * sizeof(T)), col = (uint32_t)hg * line;
+  uint32_t sink = 0;
+  for (int r0 = p0; r0 < p1; r0 += 8 * kBlock) {  // 8 loads in flight per thread
+    int v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int pos = r0 + k * kBlock + (int)threadIdx.x;
+      v[k] = __builtin_amdgcn_raw_buffer_load_b32(
+          rs, pos < p1 ? (uint32_t)pos * pos_bytes + col : p.batch_bytes, 0, 0);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) sink ^= (uint32_t)v[k];
+  }
+  if (p.NQ < 0 && sink == 0x9e3779b9u) *static_cast<unsigned char *>(p.out) = 0;
 }
 
 // The same streaming blocks touch one word of every 128-byte line of their share of the
