@@ -96,6 +96,32 @@ def test_cached_kernel_whole_output(geom, dtype):
     check(out[:, q_idx], _ref(d, dtype, q_idx), dtype, f"cached {geom}")
 
 
+@pytest.mark.parametrize("dtype", DTYPES, ids=["fp32", "fp16", "bf16"])
+@pytest.mark.parametrize("geom", [
+    # batch, heads, num_query, shapes, points: below the LDS-cached kernel's size, so the
+    # per-sample kernel runs every dtype, with 1024-2048 workgroups per slice: its first 64
+    # workgroups per slice stream the slice's value lines and records (two heads per slice
+    # in 16-bit types); query counts off the 64-way split, a short slice (S < 64 * 8)
+    (1, 8, 4097, [(40, 52), (20, 26), (10, 13), (5, 7)], 8),
+    (2, 4, 2111, [(12, 20), (6, 10), (3, 5), (2, 3)], 4),
+])
+def test_streaming_slices_whole_output(geom, dtype):
+    """Every query against the one-thread-per-element kernel, a subset against the oracle,
+    on launches where the per-sample kernel streams each slice into the cache first."""
+    b, nh, nq, shapes, npnt = geom
+    d = inputs.msda_random(b, shapes, nq, nh, 32, npnt, seed=41, loc_lo=-0.2, loc_hi=1.2)
+    out = _run(d, dtype)
+    gen = _run(d, dtype, force_generic=True)
+    if dtype == torch.float32:
+        torch.testing.assert_close(out, gen, rtol=1e-5, atol=1e-5)
+    else:
+        check(out.double(), gen.double(), dtype, f"streaming vs generic {geom}")
+    g = torch.Generator().manual_seed(6)
+    q_idx = torch.randperm(nq, generator=g)[:200].sort().values
+    q_idx = torch.cat([q_idx, torch.tensor([0, nq - 1])]).unique()
+    check(out[:, q_idx], _ref(d, dtype, q_idx), dtype, f"streaming {geom}")
+
+
 def _tsa_like(b, H, W, sigma, seed, heads=8, points=4, extra=0):
     """Queries = the cells of one H x W grid (row-major), locations = cell centre + N(0, sigma)
     in normalised units, as BEVFormer temporal self-attention. extra > 0 appends unused value
